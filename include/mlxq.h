@@ -1,0 +1,133 @@
+/*
+ * mlxq.h — C ABI of libmlxq_hip.so, the MI355X (gfx950) implementation of mlx-gen's group-wise
+ * affine Q4/Q8 quantized-linear path.
+ *
+ * The reference reaches this arithmetic through three MLX ops and one MLX layer, all external to
+ * the reference (pmetal-mlx-rs 0.25.8 -> MLX 0.31.2, reference Cargo.toml:38,43):
+ *   mlx_rs::ops::quantize            called at src/quant.rs:140, src/nn.rs:91-93, and via
+ *                                    nn::QuantizedLinear::try_from_linear at src/adapters.rs:533-537
+ *   mlx_rs::ops::dequantize          called at src/nn.rs:55, mlx-gen-flux/src/text_encoder.rs:78
+ *   mlx_rs::ops::quantized_matmul    called at src/adapters.rs:309-317 (LinearBase::forward)
+ * Each entry point below replaces one of them; a Rust -sys crate binds these symbols one-to-one.
+ *
+ * Conventions
+ *   - All tensor pointers are DEVICE pointers owned by the caller; the library allocates nothing
+ *     on these paths except where a workspace size query says so.
+ *   - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the default stream).
+ *   - Row-major, contiguous.  Packing: 32/bits codes per uint32, element i of a word at bit offset
+ *     i*bits (low bits first); wq [N, K*bits/32]; scales/biases [N, K/group_size].
+ *   - group_size in {32, 64, 128}, bits in {4, 8}, K % group_size == 0.
+ *   - Every call returns an mlxq_status; on failure mlxq_last_error() (thread-local) describes
+ *     it.  Invalid shapes are rejected with MLXQ_EINVAL, never a crash (the reference's
+ *     packed_bits panics on malformed triples, src/quant.rs:38-41).
+ *   - Re-entrant per stream; no global mutable state besides the thread-local error string.
+ */
+#ifndef MLXQ_H
+#define MLXQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  MLXQ_FLOAT32 = 0,
+  MLXQ_BFLOAT16 = 1,
+} mlxq_dtype;
+
+typedef enum {
+  MLXQ_OK = 0,
+  MLXQ_EINVAL = 1,       /* bad shape / dtype / group_size / bits / null pointer */
+  MLXQ_EUNSUPPORTED = 2, /* valid for MLX but not implemented here (e.g. transpose=false) */
+  MLXQ_EDEVICE = 3,      /* HIP launch or runtime error */
+} mlxq_status;
+
+typedef enum {
+  MLXQ_ACT_NONE = 0,
+  MLXQ_ACT_GELU = 1, /* exact erf GELU, mlx-gen-flux/src/transformer.rs:975 */
+} mlxq_activation;
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char* mlxq_last_error(void);
+/* Library version string. */
+const char* mlxq_version(void);
+
+/*
+ * quantize — replaces mlx_rs::ops::quantize(w, group_size, bits) (src/quant.rs:140;
+ * src/adapters.rs:533-537 through QuantizedLinear::try_from_linear).
+ * w [N,K] in w_dtype; writes wq [N, K*bits/32] and scales/biases [N, K/group_size] in w_dtype.
+ */
+int mlxq_quantize(const void* w, int w_dtype, int64_t N, int64_t K, int group_size, int bits,
+                  uint32_t* wq, void* scales, void* biases, void* stream);
+
+/*
+ * dequantize — replaces mlx_rs::ops::dequantize(wq, scales, biases, group_size, bits)
+ * (src/nn.rs:55).  out [N,K] in sb_dtype (the scales dtype, as MLX returns).
+ */
+int mlxq_dequantize(const uint32_t* wq, const void* scales, const void* biases, int sb_dtype,
+                    int64_t N, int64_t K, int group_size, int bits, void* out, void* stream);
+
+/*
+ * quantized_matmul — replaces mlx_rs::ops::quantized_matmul(x, wq, scales, biases, transpose,
+ * group_size, bits) (src/adapters.rs:309-317).  x [M,K] in x_dtype (batch dims flattened into
+ * M); y [M,N] in x_dtype; fp32 accumulation.  Only transpose=1 (y = x . W^T, the only form the
+ * reference uses) is implemented; transpose=0 returns MLXQ_EUNSUPPORTED.
+ * Dispatch: bf16 x with M > 8 runs the MFMA GEMM (weights dequantized to bf16 tiles); bf16 x with
+ * M <= 8 runs the bandwidth-bound GEMV (weights dequantized exactly in f32, factored per group);
+ * f32 x runs the f32 kernel (exact f32 dequant).
+ */
+int mlxq_quantized_matmul(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
+                          const void* scales, const void* biases, int sb_dtype, int64_t N,
+                          int transpose, int group_size, int bits, void* y, void* stream);
+
+/* Forced-kernel variants of quantized_matmul (same arguments, transpose implied = 1). */
+/* MFMA GEMM; x must be bf16; any M >= 1. */
+int mlxq_qmm(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
+             const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
+             int bits, void* y, void* stream);
+/* GEMV; bf16 or f32 x; 1 <= M <= 8. */
+int mlxq_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
+             const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
+             int bits, void* y, void* stream);
+
+/*
+ * Fused AdaptableLinear forward over a quantized base — replaces the op sequence of
+ * LinearBase::forward's quantized arm plus AdaptableLinear::forward (src/adapters.rs:300-322,
+ * 543-549) for one LoRA adapter (Adapter::residual, src/adapters.rs:260-270), optionally followed
+ * by the caller's activation (FeedForward::forward, mlx-gen-flux/src/transformer.rs:970-977):
+ *   y = act( round(round(qmm(x) + bias) + round(round(round(x.A).B) * scale)) )
+ * with every round() to the activation dtype exactly where the reference's separate MLX ops
+ * round.  bias [N], lora_a [K,rank], lora_b [rank,N] are in x_dtype and nullable (rank 0 = no
+ * LoRA).  workspace must hold mlxq_linear_workspace_size(M, N, rank) bytes (NULL when that is
+ * 0); rank <= 256.
+ */
+typedef struct {
+  const void* bias;
+  const void* lora_a;
+  const void* lora_b;
+  int64_t lora_rank;
+  float lora_scale;
+  int activation; /* mlxq_activation */
+} mlxq_epilogue;
+
+size_t mlxq_linear_workspace_size(int64_t M, int64_t N, int64_t lora_rank);
+
+int mlxq_linear(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
+                const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
+                int bits, const mlxq_epilogue* epilogue, void* y, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/*
+ * Host-side shape helper — replaces quant::packed_bits (src/quant.rs:38-41): from the packed
+ * shapes infer bits = wq_cols*32 / (scales_cols*group_size).  Returns 4 or 8, or -1 (with
+ * mlxq_last_error set) for a malformed triple instead of panicking.
+ */
+int mlxq_packed_bits(int64_t wq_cols, int64_t scales_cols, int group_size);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLXQ_H */

@@ -1,0 +1,89 @@
+// epilogue.hip — LoRA prologue and the unfused linear epilogue.
+//
+// The adapter residual of the reference (Adapter::residual: scale * (x.A).B, each matmul and the
+// scale multiply rounded to the activation dtype) needs x.A once per call.  lora_prep computes it
+// together with the transposed, zero-padded up-projection so the GEMM epilogue can run the
+// rank-R product as one more MFMA K-step.  linear_epilogue applies bias / LoRA / activation to an
+// already computed y for the paths that do not fuse them (GEMV and f32 activations).
+#include "mlxq_common.h"
+
+namespace mlxq {
+
+// xa[M,R] = round(x[M,K] . A[K,rank]) (zero for r >= rank); lbt[N,R] = B[rank,N]^T (zero padded).
+// One thread per output element; rank <= 256 so the K-loop per thread is short relative to the GEMM.
+template <typename XT>
+__global__ void lora_prep_kernel(const XT* __restrict__ x, int64_t M, int64_t K,
+                                 const XT* __restrict__ A, const XT* __restrict__ B, int64_t N,
+                                 int rank, int R, XT* __restrict__ xa, XT* __restrict__ lbt) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nxa = M * R;
+  if (t < nxa) {
+    const int64_t m = t / R;
+    const int r = (int)(t % R);
+    float acc = 0.0f;
+    if (r < rank) {
+      for (int64_t k = 0; k < K; ++k) acc = fmaf(Act<XT>::ld(x, m * K + k), Act<XT>::ld(A, k * rank + r), acc);
+    }
+    Act<XT>::st(xa, t, acc);
+  } else if (t < nxa + N * R) {
+    const int64_t u = t - nxa;
+    const int64_t n = u / R;
+    const int r = (int)(u % R);
+    lbt[u] = r < rank ? B[(int64_t)r * N + n] : (XT)0;
+  }
+}
+
+int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* A, const void* B,
+                  int64_t N, int rank, int R, void* xa, void* lbt, hipStream_t st) {
+  const int64_t total = M * R + N * R;
+  if (total == 0) return MLXQ_OK;
+  const int64_t blocks = (total + 255) / 256;
+  if (x_dtype == MLXQ_BFLOAT16) {
+    hipLaunchKernelGGL(lora_prep_kernel<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const uint16_t*)x, M, K, (const uint16_t*)A, (const uint16_t*)B, N, rank, R,
+                       (uint16_t*)xa, (uint16_t*)lbt);
+  } else {
+    hipLaunchKernelGGL(lora_prep_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const float*)x, M, K, (const float*)A, (const float*)B, N, rank, R,
+                       (float*)xa, (float*)lbt);
+  }
+  return check_launch("lora_prep");
+}
+
+// In place on y[M,N]: y = act(rnd(rnd(y + bias) + rnd(rnd(xa . lbt^T) * scale))).
+template <typename XT>
+__global__ void linear_epilogue_kernel(XT* __restrict__ y, int64_t M, int64_t N,
+                                       const XT* __restrict__ bias, const XT* __restrict__ xa,
+                                       const XT* __restrict__ lbt, int R, float scale, int act) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= M * N) return;
+  const int64_t m = t / N, n = t % N;
+  float o = Act<XT>::ld(y, t);
+  if (bias) o = Act<XT>::rnd(o + Act<XT>::ld(bias, n));
+  if (R > 0) {
+    float r = 0.0f;
+    for (int k = 0; k < R; ++k) r = fmaf(Act<XT>::ld(xa, m * R + k), Act<XT>::ld(lbt, n * R + k), r);
+    o = Act<XT>::rnd(o + Act<XT>::rnd(Act<XT>::rnd(r) * scale));
+  }
+  if (act == MLXQ_ACT_GELU) o = gelu_erf(o);
+  Act<XT>::st(y, t, o);
+}
+
+int run_linear_epilogue(void* y, int x_dtype, int64_t M, int64_t N, const void* bias, const void* xa,
+                        const void* lbt, int R, float scale, int act, hipStream_t st) {
+  const int64_t total = M * N;
+  if (total == 0) return MLXQ_OK;
+  const int64_t blocks = (total + 255) / 256;
+  if (x_dtype == MLXQ_BFLOAT16) {
+    hipLaunchKernelGGL(linear_epilogue_kernel<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (uint16_t*)y, M, N, (const uint16_t*)bias, (const uint16_t*)xa,
+                       (const uint16_t*)lbt, R, scale, act);
+  } else {
+    hipLaunchKernelGGL(linear_epilogue_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (float*)y, M, N, (const float*)bias, (const float*)xa, (const float*)lbt, R,
+                       scale, act);
+  }
+  return check_launch("linear_epilogue");
+}
+
+}  // namespace mlxq

@@ -1,0 +1,77 @@
+// mlxq_common.h — shared device helpers for the gfx950 quantized-linear kernels.
+//
+// Storage conventions (identical to MLX's affine packing, which the reference consumes through
+// mlx_rs::ops::{quantize, dequantize, quantized_matmul}):
+//   * W [N, K] is packed row-major into uint32 words, 32/bits codes per word, element i of a word
+//     at bit offset i*bits (low bits first); a row holds K*bits/32 words.
+//   * scales / biases are [N, K/group_size] in the weight dtype (bf16 or f32).
+//   * bf16 travels as raw uint16 bits; conversions below are round-to-nearest-even.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mlxq.h"
+#include "mlxq_internal.h"
+
+namespace mlxq {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// Two f32 -> packed bf16 pair (lo in bits 0..15), RNE; lowers to v_cvt_pk_bf16_f32 on gfx950.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  return (uint16_t)(pack_bf16x2(f, 0.0f) & 0xffffu);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// Scale/bias element loaders for the two supported storage dtypes.
+template <typename SB>
+struct SBLoad;
+template <>
+struct SBLoad<uint16_t> {
+  static __device__ __forceinline__ float ld(const uint16_t* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+  static __device__ __forceinline__ void st(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16_bits(v); }
+  static __device__ __forceinline__ float rnd(float v) { return round_bf16(v); }
+};
+template <>
+struct SBLoad<float> {
+  static __device__ __forceinline__ float ld(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void st(float* p, int64_t i, float v) { p[i] = v; }
+  static __device__ __forceinline__ float rnd(float v) { return v; }
+};
+
+// Activation element access: bf16 (uint16 bits) or f32.
+template <typename T>
+struct Act;
+template <>
+struct Act<uint16_t> {
+  static __device__ __forceinline__ float ld(const uint16_t* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+  static __device__ __forceinline__ void st(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16_bits(v); }
+  static __device__ __forceinline__ float rnd(float v) { return round_bf16(v); }
+};
+template <>
+struct Act<float> {
+  static __device__ __forceinline__ float ld(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void st(float* p, int64_t i, float v) { p[i] = v; }
+  static __device__ __forceinline__ float rnd(float v) { return v; }
+};
+
+// Exact-erf GELU, 0.5*v*(1+erf(v/sqrt(2))), evaluated in f32 with the device erff.
+__device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+}  // namespace mlxq

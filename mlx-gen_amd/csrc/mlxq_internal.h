@@ -1,0 +1,36 @@
+// mlxq_internal.h — declarations shared between the ABI layer and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mlxq {
+
+// Fused GEMM epilogue operands (all bf16, device pointers, nullable).
+struct QmmEpilogue {
+  const uint16_t* bias;  // [N]
+  const uint16_t* xa;    // [M, rank16] = round_bf16(x . A), zero padded
+  const uint16_t* lbt;   // [N, rank16] = B^T, zero padded
+  int rank16;            // padded LoRA rank (multiple of 16), 0 = no LoRA
+  float lora_scale;      // already rounded to the activation dtype
+  int act;               // mlxq_activation
+};
+
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+int run_quantize(const void* w, int dtype, int64_t N, int64_t K, int gs, int bits, uint32_t* wq,
+                 void* s, void* b, hipStream_t st);
+int run_dequantize(const uint32_t* wq, const void* s, const void* b, int dtype, int64_t N, int64_t K,
+                   int gs, int bits, void* out, hipStream_t st);
+int run_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+            const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st);
+int run_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
+            int sb_dtype, int64_t N, int gs, int bits, void* y, const QmmEpilogue& epi,
+            hipStream_t st);
+int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* A, const void* B,
+                  int64_t N, int rank, int R, void* xa, void* lbt, hipStream_t st);
+int run_linear_epilogue(void* y, int x_dtype, int64_t M, int64_t N, const void* bias, const void* xa,
+                        const void* lbt, int R, float lora_scale, int act, hipStream_t st);
+
+}  // namespace mlxq

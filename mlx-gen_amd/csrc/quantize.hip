@@ -1,0 +1,200 @@
+// quantize.hip — affine group quantize / dequantize for gfx950.
+//
+// Both kernels are HBM-bound streaming passes: one thread owns 8 consecutive elements of a row
+// (one 16-byte bf16 load / one or two packed words), a group of gs elements is gs/8 adjacent
+// lanes, and the group's min/max is a butterfly over those lanes.  Every thread runs the same
+// straight-line code, so the launch is a flat 1-D grid over N*K/8 chunks.
+#include "mlxq_common.h"
+
+namespace mlxq {
+
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float (&v)[8]);
+
+template <>
+__device__ __forceinline__ void load8<uint16_t>(const uint16_t* p, float (&v)[8]) {
+  u32x4 r = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(r[i] << 16);
+    v[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+  }
+}
+
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float (&v)[8]) {
+  f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = a[i];
+    v[4 + i] = b[i];
+  }
+}
+
+// One code: clamp(round((w - bias) / s), 0, nb) with round half away from zero and an IEEE
+// quotient.  The quotient is formed as (w - bias) * (1/s); when that product lies within 2^-12 of
+// a half-integer (where the few-ulp difference to the exact quotient could flip the rounding) the
+// exact division is taken instead, so the result equals the exact-division form bit for bit.
+__device__ __forceinline__ uint32_t quant_code(float w, float bias, float s, float rs, float nb) {
+  float a = w - bias;
+  float t = a * rs;
+  float f = t - floorf(t);
+  if (__builtin_expect(fabsf(f - 0.5f) < 0x1p-12f, 0)) t = a / s;
+  float v = fminf(fmaxf(roundf(t), 0.0f), nb);
+  return (uint32_t)v;
+}
+
+// w [N,K] (bf16 bits or f32) -> wq [N, K*BITS/32], scales/biases [N, K/GS] in T.
+// Group parameters follow MLX's edge-exact affine scheme: the larger-magnitude end of the group
+// range is reproduced exactly (it becomes the bias) and the scale carries the sign.
+template <typename T, int BITS, int GS>
+__global__ __launch_bounds__(256) void quantize_kernel(const T* __restrict__ w, int64_t n_chunks,
+                                                       uint32_t* __restrict__ wq,
+                                                       T* __restrict__ scales, T* __restrict__ biases) {
+  constexpr int LANES = GS / 8;  // lanes per group
+  constexpr float nb = (float)((1 << BITS) - 1);
+  const int64_t chunk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // n_chunks is a multiple of LANES, so whole groups are either fully in or fully out.
+  const bool live = chunk < n_chunks;
+  float v[8];
+  if (live) {
+    load8<T>(w + chunk * 8, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+  }
+  float mx = v[0], mn = v[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) {
+    mx = fmaxf(mx, v[i]);
+    mn = fminf(mn, v[i]);
+  }
+#pragma unroll
+  for (int off = 1; off < LANES; off <<= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, off));
+    mn = fminf(mn, __shfl_xor(mn, off));
+  }
+  if (!live) return;
+  float s = fmaxf((mx - mn) / nb, 1e-7f);
+  const bool side = fabsf(mn) > fabsf(mx);
+  s = side ? s : -s;
+  const float edge = side ? mn : mx;
+  const float q0 = roundf(edge / s);
+  const bool at_zero = q0 == 0.0f;
+  s = at_zero ? s : edge / q0;
+  const float bias = at_zero ? 0.0f : edge;
+  const float rs = 1.0f / s;
+
+  if ((threadIdx.x & (LANES - 1)) == 0) {
+    const int64_t g = chunk / LANES;  // row-major group index == row*(K/GS) + group
+    SBLoad<T>::st(scales, g, s);
+    SBLoad<T>::st(biases, g, bias);
+  }
+  if constexpr (BITS == 4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) word |= quant_code(v[i], bias, s, rs, nb) << (4 * i);
+    wq[chunk] = word;
+  } else {
+    u32x2 words = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      words[0] |= quant_code(v[i], bias, s, rs, nb) << (8 * i);
+      words[1] |= quant_code(v[4 + i], bias, s, rs, nb) << (8 * i);
+    }
+    *reinterpret_cast<u32x2*>(wq + chunk * 2) = words;
+  }
+}
+
+// wq/scales/biases -> out [N,K] in the scales dtype: out = round(fma(code, scale, bias)).
+template <typename T, int BITS, int GS>
+__global__ __launch_bounds__(256) void dequantize_kernel(const uint32_t* __restrict__ wq,
+                                                         const T* __restrict__ scales,
+                                                         const T* __restrict__ biases,
+                                                         int64_t n_chunks, T* __restrict__ out) {
+  const int64_t chunk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (chunk >= n_chunks) return;
+  const int64_t g = (chunk * 8) / GS;
+  const float s = SBLoad<T>::ld(scales, g);
+  const float b = SBLoad<T>::ld(biases, g);
+  float o[8];
+  if constexpr (BITS == 4) {
+    const uint32_t word = wq[chunk];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = fmaf((float)((word >> (4 * i)) & 0xfu), s, b);
+  } else {
+    const u32x2 words = *reinterpret_cast<const u32x2*>(wq + chunk * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[i] = fmaf((float)((words[0] >> (8 * i)) & 0xffu), s, b);
+      o[4 + i] = fmaf((float)((words[1] >> (8 * i)) & 0xffu), s, b);
+    }
+  }
+  if constexpr (sizeof(T) == 2) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = pack_bf16x2(o[2 * i], o[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(out + chunk * 8) = r;
+  } else {
+    f32x4 a = {o[0], o[1], o[2], o[3]};
+    f32x4 c = {o[4], o[5], o[6], o[7]};
+    *reinterpret_cast<f32x4*>(out + chunk * 8) = a;
+    *reinterpret_cast<f32x4*>(out + chunk * 8 + 4) = c;
+  }
+}
+
+template <typename T, int BITS, int GS>
+static int launch_quantize(const void* w, int64_t N, int64_t K, uint32_t* wq, void* s, void* b,
+                           hipStream_t st) {
+  const int64_t n_chunks = N * K / 8;
+  if (n_chunks == 0) return MLXQ_OK;
+  const int64_t blocks = (n_chunks + 255) / 256;
+  hipLaunchKernelGGL((quantize_kernel<T, BITS, GS>), dim3((unsigned)blocks), dim3(256), 0, st,
+                     (const T*)w, n_chunks, wq, (T*)s, (T*)b);
+  return check_launch("quantize");
+}
+
+template <typename T, int BITS, int GS>
+static int launch_dequantize(const uint32_t* wq, const void* s, const void* b, int64_t N, int64_t K,
+                             void* out, hipStream_t st) {
+  const int64_t n_chunks = N * K / 8;
+  if (n_chunks == 0) return MLXQ_OK;
+  const int64_t blocks = (n_chunks + 255) / 256;
+  hipLaunchKernelGGL((dequantize_kernel<T, BITS, GS>), dim3((unsigned)blocks), dim3(256), 0, st, wq,
+                     (const T*)s, (const T*)b, n_chunks, (T*)out);
+  return check_launch("dequantize");
+}
+
+// Dispatch over (dtype, bits, group_size); arguments were validated by the ABI layer.
+int run_quantize(const void* w, int dtype, int64_t N, int64_t K, int gs, int bits, uint32_t* wq,
+                 void* s, void* b, hipStream_t st) {
+#define MLXQ_Q(T, B, G) \
+  if (bits == B && gs == G) return launch_quantize<T, B, G>(w, N, K, wq, s, b, st);
+  if (dtype == MLXQ_BFLOAT16) {
+    MLXQ_Q(uint16_t, 4, 32) MLXQ_Q(uint16_t, 4, 64) MLXQ_Q(uint16_t, 4, 128)
+    MLXQ_Q(uint16_t, 8, 32) MLXQ_Q(uint16_t, 8, 64) MLXQ_Q(uint16_t, 8, 128)
+  } else {
+    MLXQ_Q(float, 4, 32) MLXQ_Q(float, 4, 64) MLXQ_Q(float, 4, 128)
+    MLXQ_Q(float, 8, 32) MLXQ_Q(float, 8, 64) MLXQ_Q(float, 8, 128)
+  }
+#undef MLXQ_Q
+  return set_error(MLXQ_EINVAL, "quantize: unsupported bits=%d group_size=%d", bits, gs);
+}
+
+int run_dequantize(const uint32_t* wq, const void* s, const void* b, int dtype, int64_t N, int64_t K,
+                   int gs, int bits, void* out, hipStream_t st) {
+#define MLXQ_D(T, B, G) \
+  if (bits == B && gs == G) return launch_dequantize<T, B, G>(wq, s, b, N, K, out, st);
+  if (dtype == MLXQ_BFLOAT16) {
+    MLXQ_D(uint16_t, 4, 32) MLXQ_D(uint16_t, 4, 64) MLXQ_D(uint16_t, 4, 128)
+    MLXQ_D(uint16_t, 8, 32) MLXQ_D(uint16_t, 8, 64) MLXQ_D(uint16_t, 8, 128)
+  } else {
+    MLXQ_D(float, 4, 32) MLXQ_D(float, 4, 64) MLXQ_D(float, 4, 128)
+    MLXQ_D(float, 8, 32) MLXQ_D(float, 8, 64) MLXQ_D(float, 8, 128)
+  }
+#undef MLXQ_D
+  return set_error(MLXQ_EINVAL, "dequantize: unsupported bits=%d group_size=%d", bits, gs);
+}
+
+}  // namespace mlxq

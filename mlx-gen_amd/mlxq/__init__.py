@@ -1,0 +1,19 @@
+"""mlxq — MI355X (gfx950) group-wise affine Q4/Q8 quantized linear.
+
+Drop-in for mlx-gen's quantized-linear path: the op triple ``quantize`` / ``dequantize`` /
+``quantized_matmul`` (mlx_rs::ops as called from the reference's src/quant.rs and
+src/adapters.rs) and the ``QuantizedLinear`` / ``AdaptableLinear`` layer surface built on it.
+All compute runs in libmlxq_hip.so (hand-written HIP for gfx950) through its C ABI.
+"""
+from ._lib import (MLXQ_ACT_GELU, MLXQ_ACT_NONE, MLXQ_BFLOAT16, MLXQ_FLOAT32, MlxqError,
+                   LIB_PATH, load)
+from .ops import (DEFAULT_GROUP_SIZE, dequantize, linear, linear_workspace_size, packed_bits, qmm,
+                  qmv, quantize, quantized_matmul)
+from .nn import Adapter, AdaptableLinear, QuantizedLinear, quantize_map
+
+__all__ = [
+    "MLXQ_ACT_GELU", "MLXQ_ACT_NONE", "MLXQ_BFLOAT16", "MLXQ_FLOAT32", "MlxqError", "LIB_PATH",
+    "load", "DEFAULT_GROUP_SIZE", "dequantize", "linear", "linear_workspace_size", "packed_bits",
+    "qmm", "qmv", "quantize", "quantized_matmul", "Adapter", "AdaptableLinear", "QuantizedLinear",
+    "quantize_map",
+]

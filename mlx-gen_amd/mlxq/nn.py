@@ -1,0 +1,146 @@
+"""Layer surface over the mlxq ops, mirroring the reference's quantized-linear seam.
+
+  QuantizedLinear   ~ mlx_rs::nn::QuantizedLinear (try_from_linear used at src/adapters.rs:533-537)
+  Adapter           ~ src/adapters.rs:231-270 (LoRA arm; residual = scale * (x.A).B)
+  AdaptableLinear   ~ src/adapters.rs:330-549 (dense / quantized base + adapter stack)
+  quantize_map      ~ src/quant.rs:125-149 (offline converter primitive)
+
+Only the quantized base runs on libmlxq_hip.so.  The dense base (before ``quantize``) is the
+reference's plain ``addmm``/``matmul`` and is evaluated with torch; it is not part of the
+quantized path.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Callable, Dict, List, Optional
+
+import torch
+
+from . import ops
+from ._lib import MLXQ_ACT_NONE
+
+
+@dataclass
+class QuantizedLinear:
+    """Packed triple + optional dense bias (MLX nn.QuantizedLinear)."""
+    weight: torch.Tensor          # int32 storage of the uint32 packed codes [out, in*bits/32]
+    scales: torch.Tensor          # [out, in/group_size]
+    biases: torch.Tensor          # [out, in/group_size]
+    bias: Optional[torch.Tensor]  # dense bias [out] or None
+    group_size: int = ops.DEFAULT_GROUP_SIZE
+    bits: int = 4
+
+    @classmethod
+    def try_from_linear(cls, weight: torch.Tensor, bias: Optional[torch.Tensor],
+                        group_size: int = ops.DEFAULT_GROUP_SIZE, bits: int = 4):
+        wq, s, b = ops.quantize(weight, group_size, bits)
+        return cls(wq, s, b, bias, group_size, bits)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        # src/adapters.rs:309-320: quantized_matmul, then the dense bias as a separate add.
+        if self.bias is None:
+            return ops.quantized_matmul(x, self.weight, self.scales, self.biases, True,
+                                        self.group_size, self.bits)
+        return ops.linear(x, self.weight, self.scales, self.biases, self.group_size, self.bits,
+                          bias=self.bias.to(x.dtype))
+
+    def in_features(self) -> int:
+        # AdaptableLinear::base_shape (src/adapters.rs:491-502): in = scales.cols * group_size.
+        return self.scales.shape[1] * self.group_size
+
+
+@dataclass
+class Adapter:
+    """LoRA adapter: residual = scale * (x.A).B, A [in, r], B [r, out] (alpha/rank folded in B)."""
+    a: torch.Tensor
+    b: torch.Tensor
+    scale: float = 1.0
+
+    def residual(self, x: torch.Tensor) -> torch.Tensor:
+        # src/adapters.rs:260-270 — each op in the activation dtype.
+        r = (x @ self.a.to(x.dtype)) @ self.b.to(x.dtype)
+        return r * torch.tensor(self.scale, dtype=r.dtype, device=r.device)
+
+
+@dataclass
+class AdaptableLinear:
+    """A linear base (dense or quantized) plus a stack of adapters: base(x) + sum residual(x)."""
+    dense_weight: Optional[torch.Tensor] = None
+    dense_bias: Optional[torch.Tensor] = None
+    quantized: Optional[QuantizedLinear] = None
+    adapters: List[Adapter] = field(default_factory=list)
+
+    @classmethod
+    def dense(cls, weight: torch.Tensor, bias: Optional[torch.Tensor] = None):
+        return cls(dense_weight=weight, dense_bias=bias)
+
+    @classmethod
+    def from_quantized_parts(cls, weight, scales, biases, bias, group_size: int, bits: int):
+        return cls(quantized=QuantizedLinear(weight, scales, biases, bias, group_size, bits))
+
+    def push(self, adapter: Adapter) -> None:
+        self.adapters.append(adapter)
+
+    def set_adapters(self, adapters: List[Adapter]) -> None:
+        self.adapters = list(adapters)
+
+    def is_quantized(self) -> bool:
+        return self.quantized is not None
+
+    def base_shape(self):
+        if self.quantized is not None:
+            q = self.quantized
+            return [q.scales.shape[0], q.in_features()]
+        return list(self.dense_weight.shape)
+
+    def quantize(self, bits: int, group_size: Optional[int] = None) -> None:
+        """src/adapters.rs:508-541: cast weight and bias to bf16, then pack (no-op if packed)."""
+        if self.quantized is not None:
+            return
+        w = self.dense_weight.to(torch.bfloat16)
+        b = None if self.dense_bias is None else self.dense_bias.to(torch.bfloat16)
+        gs = ops.DEFAULT_GROUP_SIZE if group_size is None else group_size
+        self.quantized = QuantizedLinear.try_from_linear(w, b, gs, bits)
+        self.dense_weight = None
+        self.dense_bias = None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.quantized is not None:
+            q = self.quantized
+            # Single-LoRA stacks fuse into the library's epilogue with the reference's roundings.
+            if len(self.adapters) == 1 and self.adapters[0].a.shape[1] <= 256:
+                ad = self.adapters[0]
+                return ops.linear(x, q.weight, q.scales, q.biases, q.group_size, q.bits,
+                                  bias=None if q.bias is None else q.bias.to(x.dtype),
+                                  lora_a=ad.a.to(x.dtype), lora_b=ad.b.to(x.dtype),
+                                  lora_scale=ad.scale, activation=MLXQ_ACT_NONE)
+            out = q.forward(x)
+        else:
+            w = self.dense_weight
+            if self.dense_bias is not None:
+                out = torch.addmm(self.dense_bias.to(x.dtype), x.reshape(-1, x.shape[-1]),
+                                  w.to(x.dtype).t()).reshape(*x.shape[:-1], w.shape[0])
+            else:
+                out = x @ w.to(x.dtype).t()
+        for ad in self.adapters:
+            out = out + ad.residual(x)
+        return out
+
+
+def quantize_map(tensors: Dict[str, torch.Tensor], bits: int, group_size: int,
+                 is_target: Callable[[str], bool]) -> Dict[str, torch.Tensor]:
+    """src/quant.rs:125-149: pack every targeted, group-divisible 2-D `{base}.weight` (cast to
+    bf16 first) into `{base}.weight/.scales/.biases`; pass everything else through."""
+    out: Dict[str, torch.Tensor] = {}
+    for k, v in tensors.items():
+        base = k[: -len(".weight")] if k.endswith(".weight") else None
+        packable = (base is not None and is_target(base) and v.dim() == 2
+                    and v.shape[1] % group_size == 0 and v.shape[1] >= group_size)
+        if packable:
+            wq, s, b = ops.quantize(v.to(torch.bfloat16), group_size, bits)
+            out[f"{base}.weight"] = wq
+            out[f"{base}.scales"] = s
+            out[f"{base}.biases"] = b
+        else:
+            out[k] = v
+    return out

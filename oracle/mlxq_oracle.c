@@ -1,0 +1,304 @@
+/*
+ * mlxq_oracle.c — CPU restatement of mlx-gen's group-wise affine Q4/Q8 quantized-linear path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker the HIP path is compared against; only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The product
+ * library (libmlxq_hip.so) never links or calls it, and there is no CPU fallback.
+ *
+ * The arithmetic being restated lives in MLX 0.31.2 (C++/Metal), reached through the git-pinned
+ * crate pmetal-mlx-rs 0.25.8 (rev 38e1cc1730a11b1e40c2c8ecda01606763a12d51, reference
+ * Cargo.toml:38,43, Cargo.lock:1120-1147).  That source is not present, so each function restates
+ * MLX's published affine-quantization algorithm and cites the reference call site it serves.
+ *
+ * Pinning (what fixes each function besides its own text):
+ *   oracle_quantize    pinned: reference tests/fixtures/quant_q4q8.safetensors (q4/q8 .wq, .scales,
+ *                      .biases, bit-exact, f32 input); closed forms for all-zero and constant
+ *                      groups; row-split commutation (mlx-gen-sdxl/src/quant.rs:89-110).
+ *                      Parity unpinned for: the bf16-input scale rounding point, the tie rule of
+ *                      round() (fixture holds no exact .5 ties), eps for near-constant groups.
+ *   oracle_dequantize  pinned: fixture q4/q8 .deq (single-rounded fma, 0 mismatches).
+ *   oracle_qmm         pinned: fixture q4/q8 .qmm (f32 activations, exact dequant); textbook
+ *                      matmul over the dequantized matrix for the bf16-tile variant.
+ *   oracle_linear      pinned by composition: qmm + the reference op sequence of
+ *                      src/adapters.rs:300-322,543-549 (bias add, then LoRA residual); its
+ *                      rounding points follow MLX's per-op bf16 rounding (not pinned by a golden).
+ *   oracle_gelu_erf / oracle_silu: textbook closed forms (special values tested).
+ *
+ * Data convention: every float tensor crosses this interface as f32.  A bf16 tensor is passed as
+ * the f32 values it represents (exact), and the `*_bf16` flags say where results are rounded to
+ * bf16 (round-to-nearest-even), as the reference does when its arrays have dtype bf16.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+#include <stdlib.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORACLE_OK 0
+#define ORACLE_EINVAL 1
+
+/* Round-to-nearest-even f32 -> bf16, returned widened back to f32 (NaN kept quiet). */
+float oracle_bf16_round(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
+        u |= 0x00400000u;
+        u &= 0xffff0000u;
+    } else {
+        uint32_t lsb = (u >> 16) & 1u;
+        u += 0x7fffu + lsb;
+        u &= 0xffff0000u;
+    }
+    float r;
+    memcpy(&r, &u, 4);
+    return r;
+}
+
+static inline float rnd(float x, int to_bf16) { return to_bf16 ? oracle_bf16_round(x) : x; }
+
+static int valid_shape(int64_t N, int64_t K, int gs, int bits) {
+    if (N < 0 || K <= 0) return 0;
+    if (bits != 4 && bits != 8) return 0;
+    if (gs != 32 && gs != 64 && gs != 128) return 0;
+    if (K % gs) return 0;
+    return 1;
+}
+
+/*
+ * Affine group quantization, MLX `quantize(w, group_size, bits)` (affine mode), as called at
+ * reference src/quant.rs:140, src/adapters.rs:533-537 (QuantizedLinear::try_from_linear) and
+ * src/nn.rs:91-93, with the fixture produced by tools/dump_quant.py:25 and checked by
+ * tests/quant_parity.rs:34-51.
+ *
+ * Per row n and per group g of `gs` consecutive elements along K:
+ *   mx, mn   = max, min of the group
+ *   s        = max((mx - mn) / (2^bits - 1), eps)            eps = 1e-7
+ *   side     = |mn| > |mx|;  s = side ? s : -s;  edge = side ? mn : mx
+ *   q0       = round(edge / s)
+ *   s        = q0 != 0 ? edge / q0 : s;   bias = q0 != 0 ? edge : 0
+ *   code[k]  = clamp(round((w[k] - bias) / s), 0, 2^bits - 1)
+ * so one end of the group range (the larger-magnitude one) is reproduced exactly and the scale
+ * may be negative.  Codes are computed from the f32 scale; the stored scale/bias are rounded to
+ * the weight dtype (bf16 when sb_bf16).  Packing: 32/bits codes per uint32 word, element i of the
+ * word at bit offset i*bits (low bits first); words row-major, K/(32/bits) words per row.
+ * round() is half-away-from-zero (the Metal stdlib rule).
+ */
+int oracle_quantize(const float* w, int64_t N, int64_t K, int gs, int bits, int sb_bf16,
+                    uint32_t* wq, float* scales, float* biases) {
+    if (!valid_shape(N, K, gs, bits)) return ORACLE_EINVAL;
+    const float eps = 1e-7f;
+    const float nb = (float)((1 << bits) - 1);
+    const int per = 32 / bits;
+    const int64_t G = K / gs;
+    const int64_t W = K / per;
+#pragma omp parallel for schedule(static)
+    for (int64_t n = 0; n < N; ++n) {
+        for (int64_t g = 0; g < G; ++g) {
+            const float* src = w + n * K + g * gs;
+            float mx = src[0], mn = src[0];
+            for (int i = 1; i < gs; ++i) {
+                mx = fmaxf(mx, src[i]);
+                mn = fminf(mn, src[i]);
+            }
+            float s = fmaxf((mx - mn) / nb, eps);
+            int side = fabsf(mn) > fabsf(mx);
+            s = side ? s : -s;
+            float edge = side ? mn : mx;
+            float q0 = roundf(edge / s);
+            int at_zero = (q0 == 0.0f);
+            s = at_zero ? s : edge / q0;
+            float bias = at_zero ? 0.0f : edge;
+            scales[n * G + g] = rnd(s, sb_bf16);
+            biases[n * G + g] = rnd(bias, sb_bf16);
+            for (int i = 0; i < gs; i += per) {
+                uint32_t word = 0;
+                for (int j = 0; j < per; ++j) {
+                    float v = roundf((src[i + j] - bias) / s);
+                    v = fminf(fmaxf(v, 0.0f), nb);
+                    word |= ((uint32_t)v) << (j * bits);
+                }
+                wq[n * W + (g * gs + i) / per] = word;
+            }
+        }
+    }
+    return ORACLE_OK;
+}
+
+static inline uint32_t code_at(const uint32_t* row, int64_t k, int bits) {
+    const int per = 32 / bits;
+    return (row[k / per] >> ((k % per) * bits)) & ((1u << bits) - 1u);
+}
+
+/*
+ * MLX `dequantize(wq, scales, biases, group_size, bits)` (reference src/nn.rs:55,
+ * mlx-gen-flux/src/text_encoder.rs:78): w = fma(code, scale, bias) in f32, rounded once, then to
+ * the scales dtype (bf16 when out_bf16).  The single-rounding form is pinned by the fixture's
+ * q*.deq (tests/quant_parity.rs:53-57).
+ */
+int oracle_dequantize(const uint32_t* wq, const float* scales, const float* biases, int64_t N,
+                      int64_t K, int gs, int bits, int out_bf16, float* out) {
+    if (!valid_shape(N, K, gs, bits)) return ORACLE_EINVAL;
+    const int per = 32 / bits;
+    const int64_t G = K / gs, W = K / per;
+#pragma omp parallel for schedule(static)
+    for (int64_t n = 0; n < N; ++n) {
+        const uint32_t* row = wq + n * W;
+        for (int64_t k = 0; k < K; ++k) {
+            float s = scales[n * G + k / gs], b = biases[n * G + k / gs];
+            out[n * K + k] = rnd(fmaf((float)code_at(row, k, bits), s, b), out_bf16);
+        }
+    }
+    return ORACLE_OK;
+}
+
+/*
+ * MLX `quantized_matmul(x, wq, scales, biases, transpose=true, group_size, bits)` as called from
+ * LinearBase::forward (reference src/adapters.rs:309-317): y[M,N] = x[M,K] . What[N,K]^T with
+ * What = dequantize(...).  w_bf16 selects the dequantized-weight precision (1: each weight rounded
+ * to bf16 as in a bf16-tile GEMM; 0: exact f32 fma as in the factored small-M form).  Products
+ * are accumulated in double; out_bf16 rounds y to bf16 (activation dtype bf16), else y is rounded
+ * to f32.
+ */
+int oracle_qmm(const float* x, int64_t M, int64_t K, const uint32_t* wq, const float* scales,
+               const float* biases, int64_t N, int gs, int bits, int w_bf16, int out_bf16,
+               float* y) {
+    if (!valid_shape(N, K, gs, bits) || M < 0) return ORACLE_EINVAL;
+    const int per = 32 / bits;
+    const int64_t G = K / gs, W = K / per;
+#pragma omp parallel
+    {
+        double* wrow = (double*)malloc(sizeof(double) * (size_t)K);
+#pragma omp for schedule(static)
+        for (int64_t n = 0; n < N; ++n) {
+            const uint32_t* row = wq + n * W;
+            for (int64_t k = 0; k < K; ++k) {
+                float s = scales[n * G + k / gs], b = biases[n * G + k / gs];
+                wrow[k] = (double)rnd(fmaf((float)code_at(row, k, bits), s, b), w_bf16);
+            }
+            for (int64_t m = 0; m < M; ++m) {
+                const float* xr = x + m * K;
+                double acc = 0.0;
+                for (int64_t k = 0; k < K; ++k) acc += (double)xr[k] * wrow[k];
+                y[m * N + n] = rnd((float)acc, out_bf16);
+            }
+        }
+        free(wrow);
+    }
+    return ORACLE_OK;
+}
+
+/* Dense y[M,N] = x[M,K] . B[K,N] (row-major B), double accumulate, rounded per out_bf16. */
+static void dense_mm(const float* x, int64_t M, int64_t K, const float* B, int64_t N, int out_bf16,
+                     float* y) {
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t n = 0; n < N; ++n) {
+            double acc = 0.0;
+            for (int64_t k = 0; k < K; ++k) acc += (double)x[m * K + k] * (double)B[k * N + n];
+            y[m * N + n] = rnd((float)acc, out_bf16);
+        }
+    }
+}
+
+/*
+ * Exact-erf GELU, MLX `gelu` as applied in FLUX's FeedForward (reference
+ * mlx-gen-flux/src/transformer.rs:975): 0.5 * v * (1 + erf(v / sqrt(2))), evaluated in double and
+ * rounded to the activation dtype.
+ */
+float oracle_gelu_erf(float v, int out_bf16) {
+    double d = (double)v;
+    return rnd((float)(0.5 * d * (1.0 + erf(d / sqrt(2.0)))), out_bf16);
+}
+
+/* SiLU v * sigmoid(v), as in the SwiGLU of reference mlx-gen-sensenova/src/qwen3.rs:179. */
+float oracle_silu(float v, int out_bf16) {
+    double d = (double)v;
+    return rnd((float)(d / (1.0 + exp(-d))), out_bf16);
+}
+
+/*
+ * AdaptableLinear::forward over a quantized base (reference src/adapters.rs:543-549 and the
+ * quantized arm of LinearBase::forward, :300-322), with every intermediate rounded to the
+ * activation dtype the way separate MLX ops round it (act_bf16 = 1 for bf16 activations):
+ *   y1 = qmm(x)                                  (src/adapters.rs:309-317)
+ *   y2 = y1 + bias            if bias            (:318-320)
+ *   xa = x . A                A [K,r]            (Adapter::residual, :260-270; A = lora_down^T,
+ *   r  = xa . B               B [r,N]             B = lora_up^T with alpha/rank folded in,
+ *   r2 = r * scale            scale in act dtype  src/adapters/loader.rs:568-569,597)
+ *   y  = y2 + r2              if lora
+ *   y  = act(y)               act: 0 none, 1 exact-erf GELU (mlx-gen-flux/src/transformer.rs:975)
+ * The activation is the caller's next op (FeedForward::forward, transformer.rs:970-977), listed
+ * here so a fused epilogue has a checker.  w_bf16 as in oracle_qmm.
+ */
+int oracle_linear(const float* x, int64_t M, int64_t K, const uint32_t* wq, const float* scales,
+                  const float* biases, int64_t N, int gs, int bits, int w_bf16, int act_bf16,
+                  const float* bias, const float* lora_a, const float* lora_b, int64_t rank,
+                  float lora_scale, int act, float* y) {
+    int rc = oracle_qmm(x, M, K, wq, scales, biases, N, gs, bits, w_bf16, act_bf16, y);
+    if (rc) return rc;
+    if (bias) {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < M * N; ++i) y[i] = rnd(y[i] + bias[i % N], act_bf16);
+    }
+    if (lora_a && lora_b && rank > 0) {
+        float* xa = (float*)malloc(sizeof(float) * (size_t)(M * rank));
+        float* r = (float*)malloc(sizeof(float) * (size_t)(M * N));
+        if (!xa || !r) {
+            free(xa);
+            free(r);
+            return ORACLE_EINVAL;
+        }
+        dense_mm(x, M, K, lora_a, rank, act_bf16, xa);
+        dense_mm(xa, M, rank, lora_b, N, act_bf16, r);
+        float sc = rnd(lora_scale, act_bf16);
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < M * N; ++i) y[i] = rnd(y[i] + rnd(r[i] * sc, act_bf16), act_bf16);
+        free(xa);
+        free(r);
+    }
+    if (act == 1) {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < M * N; ++i) y[i] = oracle_gelu_erf(y[i], act_bf16);
+    }
+    return ORACLE_OK;
+}
+
+/*
+ * SwiGLU decode MLP of reference mlx-gen-sensenova/src/qwen3.rs:178-181:
+ *   h = silu(gate(x)) * up(x)   (each op rounded to the activation dtype),  y = down(h).
+ * gate/up are [F,K] packs; down is an [Nd,F] pack.  h [M,F] and y [M,Nd] are outputs.
+ */
+int oracle_swiglu_mlp(const float* x, int64_t M, int64_t K, const uint32_t* wq_g,
+                      const float* s_g, const float* b_g, const uint32_t* wq_u, const float* s_u,
+                      const float* b_u, int64_t F, const uint32_t* wq_d, const float* s_d,
+                      const float* b_d, int64_t Nd, int gs, int bits, int w_bf16, int act_bf16,
+                      float* h, float* y) {
+    float* g = (float*)malloc(sizeof(float) * (size_t)(M * F));
+    float* u = (float*)malloc(sizeof(float) * (size_t)(M * F));
+    if (!g || !u) {
+        free(g);
+        free(u);
+        return ORACLE_EINVAL;
+    }
+    int rc = oracle_qmm(x, M, K, wq_g, s_g, b_g, F, gs, bits, w_bf16, act_bf16, g);
+    if (!rc) rc = oracle_qmm(x, M, K, wq_u, s_u, b_u, F, gs, bits, w_bf16, act_bf16, u);
+    if (!rc) {
+        for (int64_t i = 0; i < M * F; ++i)
+            h[i] = rnd(oracle_silu(g[i], act_bf16) * u[i], act_bf16);
+        rc = oracle_qmm(h, M, F, wq_d, s_d, b_d, Nd, gs, bits, w_bf16, act_bf16, y);
+    }
+    free(g);
+    free(u);
+    return rc;
+}
+
+int oracle_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

@@ -1,0 +1,221 @@
+"""GPU parity: libmlxq_hip.so (through its C ABI) against the CPU oracle and the reference's golden.
+
+Mirrors the reference's tests/quant_parity.rs (byte-level packing parity, dequant and
+quantized_matmul within tolerance) and extends it to bf16 inputs, all six (bits, group_size)
+pairs, both kernels (MFMA GEMM, GEMV), ragged shapes and the fused linear epilogue.
+Bars: bit-exact for quantize / dequantize; relFro <= 2e-3 and |delta| <= 1e-2*max|y| for matmuls.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+from safetensors.numpy import load_file
+
+from gpu_util import (assert_close, banner, bf16_normal, errors, to_gpu, to_np, wq_to_gpu)
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+GOLD = load_file(os.path.join(os.path.dirname(__file__), "golden", "quant_q4q8.safetensors"))
+
+
+@pytest.fixture(scope="module")
+def mlxq():
+    import mlxq as m
+    m.load()
+    return m
+
+
+# ---------------------------------------------------------------- golden (tests/quant_parity.rs)
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_golden_quantize_dequantize_qmm(mlxq, bits):
+    banner("golden f32 fixture", f"bits={bits}")
+    w = to_gpu(GOLD["w"], torch.float32)
+    wq, s, b = mlxq.quantize(w, 64, bits)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(wq), GOLD[f"q{bits}.wq"])
+    assert np.array_equal(to_np(s), GOLD[f"q{bits}.scales"])
+    assert np.array_equal(to_np(b), GOLD[f"q{bits}.biases"])
+    deq = mlxq.dequantize(wq, s, b, 64, bits)
+    assert np.array_equal(to_np(deq), GOLD[f"q{bits}.deq"])
+    x = to_gpu(GOLD["x"], torch.float32)
+    y = to_np(mlxq.quantized_matmul(x, wq, s, b, True, 64, bits))
+    ref = GOLD[f"q{bits}.qmm"]
+    # tests/quant_parity.rs:59-64 (rtol=atol=1e-2); the f32 kernel is far inside it.
+    assert np.allclose(y, ref, rtol=1e-4, atol=1e-4)
+
+
+# ---------------------------------------------------------------- quantize / dequantize
+
+QUANT_CASES = [
+    # (N, K, gs, bits)
+    (96, 256, 32, 4), (96, 256, 64, 4), (96, 256, 128, 4),
+    (96, 256, 32, 8), (96, 256, 64, 8), (96, 256, 128, 8),
+    (1, 64, 64, 4), (3, 128, 128, 8), (257, 96, 32, 4),
+]
+
+
+@pytest.mark.parametrize("N,K,gs,bits", QUANT_CASES)
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_quantize_bit_exact(mlxq, N, K, gs, bits, dtype):
+    banner("quantize", dtype, N, K, gs, bits)
+    rng = np.random.default_rng(N * 7 + K + gs + bits)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    if dtype == "bf16":
+        w = oracle.bf16_round(w)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    wq, s, b = mlxq.quantize(to_gpu(w, tdt), gs, bits)
+    rwq, rs, rb = oracle.quantize(w, gs, bits, sb_bf16=(dtype == "bf16"))
+    assert np.array_equal(to_np(wq), rwq)
+    assert np.array_equal(to_np(s), rs)
+    assert np.array_equal(to_np(b), rb)
+    deq = to_np(mlxq.dequantize(wq, s, b, gs, bits))
+    assert np.array_equal(deq, oracle.dequantize(rwq, rs, rb, gs, bits, out_bf16=(dtype == "bf16")))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantize_special_groups(mlxq, bits):
+    """Zero, constant, all-negative, tiny-range and huge-range groups."""
+    banner("quantize special groups", bits)
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal((6, 512)) * 0.02).astype(np.float32)
+    w[0, :64] = 0.0
+    w[1, 64:128] = 0.375
+    w[2, :] = -np.abs(w[2, :]) - 0.01
+    w[3, 128:192] = 1e-9 * rng.standard_normal(64)
+    w[4, 192:256] *= 1e4
+    w[5, ::2] = 0.0
+    w = oracle.bf16_round(w)
+    wq, s, b = mlxq.quantize(to_gpu(w), 64, bits)
+    rwq, rs, rb = oracle.quantize(w, 64, bits, sb_bf16=True)
+    assert np.array_equal(to_np(wq), rwq)
+    assert np.array_equal(to_np(s), rs)
+    assert np.array_equal(to_np(b), rb)
+
+
+def test_quantize_config1_full_size(mlxq):
+    """Config 1: W [3072,3072] bf16 ~ N(0,0.02), seed 0, Q4 g64 — bit-exact against the oracle."""
+    banner("quantize config1 [3072,3072] q4 g64")
+    rng = np.random.default_rng(0)
+    w = bf16_normal(rng, (3072, 3072), 0.02)
+    wq, s, b = mlxq.quantize(to_gpu(w), 64, 4)
+    rwq, rs, rb = oracle.quantize(w, 64, 4, sb_bf16=True)
+    assert np.array_equal(to_np(wq), rwq)
+    assert np.array_equal(to_np(s), rs) and np.array_equal(to_np(b), rb)
+    deq = to_np(mlxq.dequantize(wq, s, b, 64, 4))
+    assert np.array_equal(deq, oracle.dequantize(rwq, rs, rb, 64, 4, out_bf16=True))
+
+
+# ---------------------------------------------------------------- GEMM (MFMA, bf16 tiles)
+
+GEMM_CASES = [
+    # (M, K, N, gs, bits)
+    (256, 3072, 3072, 64, 4),   # config 1 shape
+    (64, 256, 128, 64, 4),
+    (200, 320, 136, 32, 4),     # ragged M, N; K % 64 == 0
+    (77, 96, 40, 32, 8),        # K % 64 == 32, tiny N
+    (300, 512, 520, 128, 8),
+    (129, 384, 264, 64, 8),
+    (9, 256, 256, 32, 4),       # smallest GEMM M
+    (600, 1024, 1280, 64, 4),   # big-tile path
+]
+
+
+@pytest.mark.parametrize("M,K,N,gs,bits", GEMM_CASES)
+def test_qmm_gemm_vs_oracle(mlxq, M, K, N, gs, bits):
+    banner("qmm gemm", M, K, N, gs, bits)
+    rng = np.random.default_rng(M + K + N)
+    x = bf16_normal(rng, (M, K))
+    w = bf16_normal(rng, (N, K), 0.02)
+    rwq, rs, rb = oracle.quantize(w, gs, bits, sb_bf16=True)
+    y = to_np(mlxq.qmm(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), gs, bits))
+    ref = oracle.quantized_matmul(x, rwq, rs, rb, gs, bits, w_bf16=True, out_bf16=True)
+    assert_close(y, ref, f"gemm M={M} K={K} N={N} gs={gs} b={bits}")
+
+
+def test_qmm_dispatch_matches_forced_kernels(mlxq):
+    banner("dispatch")
+    rng = np.random.default_rng(5)
+    w = bf16_normal(rng, (256, 512), 0.02)
+    wq, s, b = mlxq.quantize(to_gpu(w), 64, 4)
+    for M, forced in ((8, mlxq.qmv), (9, mlxq.qmm), (64, mlxq.qmm), (1, mlxq.qmv)):
+        x = to_gpu(bf16_normal(rng, (M, 512)))
+        a = mlxq.quantized_matmul(x, wq, s, b, True, 64, 4)
+        c = forced(x, wq, s, b, 64, 4)
+        assert torch.equal(a, c), M
+
+
+# ---------------------------------------------------------------- GEMV (exact f32 dequant)
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 3])
+@pytest.mark.parametrize("K,N,gs,bits", [(3072, 512, 64, 4), (256, 96, 32, 8), (384, 40, 128, 4)])
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_qmv_vs_oracle(mlxq, M, K, N, gs, bits, dtype):
+    banner("qmv", dtype, M, K, N, gs, bits)
+    rng = np.random.default_rng(M * 1000 + K + N)
+    x = bf16_normal(rng, (M, K))
+    if dtype == "f32":
+        x = rng.standard_normal((M, K)).astype(np.float32)
+    w = bf16_normal(rng, (N, K), 0.02)
+    rwq, rs, rb = oracle.quantize(w, gs, bits, sb_bf16=True)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    y = to_np(mlxq.qmv(to_gpu(x, tdt), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), gs, bits))
+    ref = oracle.quantized_matmul(x, rwq, rs, rb, gs, bits, w_bf16=False, out_bf16=(dtype == "bf16"))
+    rel, peak = assert_close(y, ref, f"gemv {dtype} M={M}")
+    if dtype == "f32":
+        assert rel < 1e-5
+
+
+def test_f32_activations_large_m(mlxq):
+    """f32 activations at GEMM-sized M keep exact-f32 semantics (the FLUX.1 f32 stream)."""
+    banner("f32 large M")
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((40, 256)).astype(np.float32)
+    w = (rng.standard_normal((72, 256)) * 0.02).astype(np.float32)
+    wq, s, b = mlxq.quantize(to_gpu(w, torch.float32), 64, 8)
+    y = to_np(mlxq.quantized_matmul(to_gpu(x, torch.float32), wq, s, b, True, 64, 8))
+    rwq, rs, rb = oracle.quantize(w, 64, 8)
+    ref = oracle.quantized_matmul(x, rwq, rs, rb, 64, 8, w_bf16=False, out_bf16=False)
+    assert errors(y, ref)[0] < 1e-5
+
+
+# ---------------------------------------------------------------- fused linear epilogue
+
+@pytest.mark.parametrize("M", [4, 300])
+@pytest.mark.parametrize("act", [0, 1])
+def test_linear_bias_lora_act(mlxq, M, act):
+    banner("linear epilogue", M, act)
+    rng = np.random.default_rng(21 + M + act)
+    K, N, r = 512, 264, 16
+    x = bf16_normal(rng, (M, K))
+    w = bf16_normal(rng, (N, K), 0.02)
+    bias = bf16_normal(rng, (N,), 0.5)
+    A = bf16_normal(rng, (K, r), 0.01)
+    B = bf16_normal(rng, (r, N), 0.01)
+    rwq, rs, rb = oracle.quantize(w, 64, 4, sb_bf16=True)
+    y = to_np(mlxq.linear(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), 64, 4,
+                          bias=to_gpu(bias), lora_a=to_gpu(A), lora_b=to_gpu(B), lora_scale=0.75,
+                          activation=act))
+    ref = oracle.linear(x, rwq, rs, rb, 64, 4, w_bf16=(M > 8), act_bf16=True, bias=bias,
+                        lora_a=A, lora_b=B, lora_scale=0.75, act=act)
+    assert_close(y, ref, f"linear M={M} act={act}")
+
+
+# ---------------------------------------------------------------- errors never crash
+
+def test_invalid_arguments_return_errors(mlxq):
+    banner("invalid arguments")
+    w = torch.zeros((4, 100), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(mlxq.MlxqError, match="multiple of group_size"):
+        mlxq.quantize(w, 64, 4)
+    w = torch.zeros((4, 128), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(mlxq.MlxqError, match="bits"):
+        mlxq.quantize(w, 64, 3)
+    wq, s, b = mlxq.quantize(w, 64, 4)
+    x = torch.zeros((2, 128), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(mlxq.MlxqError, match="transpose"):
+        mlxq.quantized_matmul(x, wq, s, b, False, 64, 4)
+    with pytest.raises(mlxq.MlxqError, match="GEMV limit"):
+        mlxq.qmv(torch.zeros((9, 128), dtype=torch.bfloat16, device="cuda"), wq, s, b, 64, 4)

@@ -1,0 +1,186 @@
+"""Pins the CPU oracle (oracle/mlxq_oracle.c) before anything is compared against it.
+
+Each check is chosen so a plausible slip in the oracle (a dropped term, the simplified
+``scale=(max-min)/15, bias=min`` scheme, high-bits-first packing, a mul-then-add dequant, a
+transposed operand) fails at least one of them:
+
+* the reference's golden fixture (tests/golden/quant_q4q8.safetensors, from the reference's
+  tools/dump_quant.py and tests/quant_parity.rs:30-66) — bit-exact packing, scales, biases and
+  dequant, and the fixture's quantized_matmul;
+* closed forms (all-zero and constant groups, a hand-computed packed word);
+* invariants the reference relies on (row-split commutation, mlx-gen-sdxl/src/quant.rs:89-110;
+  the quantization-error envelope of tests/quant_parity.rs:99-127);
+* library routines for what is textbook (numpy float64 matmul, torch bf16 rounding, math.erf).
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+from safetensors.numpy import load_file
+
+from oracle import oracle
+
+GOLD = load_file(os.path.join(os.path.dirname(__file__), "golden", "quant_q4q8.safetensors"))
+GS = 64
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_quantize_matches_golden_bit_exact(bits):
+    wq, s, b = oracle.quantize(GOLD["w"], GS, bits)
+    assert np.array_equal(wq, GOLD[f"q{bits}.wq"]), "packed words diverge from MLX 0.31"
+    assert np.array_equal(s, GOLD[f"q{bits}.scales"])
+    assert np.array_equal(b, GOLD[f"q{bits}.biases"])
+    # The edge-exact scheme yields negative scales for about half of the N(0,1) groups.
+    assert 0.3 < (s < 0).mean() < 0.7
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_simplified_scheme_is_rejected_by_golden(bits):
+    """The (max-min)/nb, bias=min scheme would fail the same bit-exact check."""
+    w = GOLD["w"].reshape(128, -1, GS)
+    nb = np.float32(2 ** bits - 1)
+    mn, mx = w.min(-1), w.max(-1)
+    s = ((mx - mn) / nb).astype(np.float32)
+    assert not np.array_equal(s, GOLD[f"q{bits}.scales"])
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_dequantize_matches_golden_bit_exact(bits):
+    deq = oracle.dequantize(GOLD[f"q{bits}.wq"], GOLD[f"q{bits}.scales"], GOLD[f"q{bits}.biases"],
+                            GS, bits)
+    assert np.array_equal(deq, GOLD[f"q{bits}.deq"])
+    # A mul-then-add dequant (two roundings) is distinguishable by the same golden.
+    codes = _codes(GOLD[f"q{bits}.wq"], bits).reshape(128, -1, GS).astype(np.float32)
+    two_round = (codes * GOLD[f"q{bits}.scales"][..., None]).astype(np.float32) + \
+        GOLD[f"q{bits}.biases"][..., None]
+    assert not np.array_equal(two_round.reshape(128, 256), GOLD[f"q{bits}.deq"])
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_qmm_matches_golden(bits):
+    y = oracle.quantized_matmul(GOLD["x"], GOLD[f"q{bits}.wq"], GOLD[f"q{bits}.scales"],
+                                GOLD[f"q{bits}.biases"], GS, bits, w_bf16=False, out_bf16=False)
+    ref = GOLD[f"q{bits}.qmm"]
+    # tests/quant_parity.rs:60-64 allows 1e-2; the f32 restatement is far inside that.
+    assert np.abs(y - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max())
+    # A transposed weight operand is caught.
+    wrong = GOLD["x"] @ GOLD[f"q{bits}.deq"][:, ::-1].T
+    assert np.abs(wrong - ref).max() > 1e-1
+
+
+def _codes(wq, bits):
+    per = 32 // bits
+    sh = (np.arange(per, dtype=np.uint32) * bits)
+    return ((wq[..., None] >> sh) & ((1 << bits) - 1)).reshape(wq.shape[0], -1)
+
+
+def test_low_bits_first_hand_computed_word():
+    # One Q8 group holding 0..63: mx=63 wins the edge (|0| > |63| is false) so the scale is
+    # negative and code(k) = round((k-63) / (63/-255)) = round((63-k)*255/63).
+    w = np.arange(64, dtype=np.float32)[None, :]
+    wq, s, b = oracle.quantize(w, 64, 8)
+    assert b[0, 0] == 63.0 and s[0, 0] < 0
+    word0 = int(wq[0, 0])
+    assert word0 & 0xFF == 255            # element 0 in the lowest byte
+    assert (word0 >> 24) & 0xFF == round(60 * 255 / 63)
+    # Q4 of 0..15 * 2 (range 30, nb 15 -> scale -2, edge 30): code(k) = 15 - k.
+    w4 = np.tile(np.arange(16, dtype=np.float32) * 2, 4)[None, :]
+    wq4, s4, b4 = oracle.quantize(w4, 64, 4)
+    assert s4[0, 0] == -2.0 and b4[0, 0] == 30.0
+    assert int(wq4[0, 0]) == 0x89ABCDEF     # codes 15,14,...,8 from low nibble up
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_zero_and_constant_groups(bits):
+    w = np.zeros((3, 128), np.float32)
+    w[1, :64] = 0.75          # constant group
+    w[2, 64:] = -1.5          # constant negative group
+    wq, s, b = oracle.quantize(w, 64, bits)
+    assert np.all(wq == 0)
+    assert s[0, 0] == np.float32(-1e-7) and b[0, 0] == 0.0
+    assert b[1, 0] == 0.75 and b[2, 1] == -1.5
+    deq = oracle.dequantize(wq, s, b, 64, bits)
+    assert np.array_equal(deq, w)
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (8, 128)])
+def test_row_split_commutes(bits, gs):
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((48, 256)) * 0.02).astype(np.float32)
+    full = oracle.quantize(w, gs, bits)
+    top = oracle.quantize(w[:20], gs, bits)
+    bot = oracle.quantize(w[20:], gs, bits)
+    for f, t, bt in zip(full, top, bot):
+        assert np.array_equal(f, np.concatenate([t, bt]))
+
+
+@pytest.mark.parametrize("bits,max_rel", [(8, 0.02), (4, 0.12)])
+def test_quantization_error_envelope(bits, max_rel):
+    """tests/quant_parity.rs:99-127: bf16-cast quantize then qmm stays near the dense output."""
+    w, x = GOLD["w"], GOLD["x"]
+    dense = x.astype(np.float64) @ w.astype(np.float64).T
+    wq, s, b = oracle.quantize(oracle.bf16_round(w), GS, bits, sb_bf16=True)
+    y = oracle.quantized_matmul(x, wq, s, b, GS, bits, w_bf16=False, out_bf16=False)
+    rel = np.abs(y - dense).max() / np.abs(dense).max()
+    assert rel < max_rel
+
+
+@pytest.mark.parametrize("w_bf16", [False, True])
+def test_qmm_against_numpy_matmul(w_bf16):
+    rng = np.random.default_rng(2)
+    x = oracle.bf16_round(rng.standard_normal((5, 192)).astype(np.float32))
+    w = oracle.bf16_round((rng.standard_normal((24, 192)) * 0.02).astype(np.float32))
+    wq, s, b = oracle.quantize(w, 64, 4, sb_bf16=True)
+    deq = oracle.dequantize(wq, s, b, 64, 4, out_bf16=w_bf16)
+    ref = oracle.bf16_round((x.astype(np.float64) @ deq.astype(np.float64).T).astype(np.float32))
+    y = oracle.quantized_matmul(x, wq, s, b, 64, 4, w_bf16=w_bf16, out_bf16=True)
+    assert np.array_equal(y, ref)
+
+
+def test_bf16_round_matches_torch():
+    rng = np.random.default_rng(3)
+    v = np.concatenate([rng.standard_normal(10000).astype(np.float32) * 10.0 ** rng.integers(-6, 6, 10000),
+                        np.array([0.0, -0.0, 1.0, 65504.0, 3.0e38, np.inf, -np.inf], np.float32)])
+    v = v.astype(np.float32)
+    ref = torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(oracle.bf16_round(v), ref)
+    assert all(oracle.lib().oracle_bf16_round(float(a)) == r for a, r in zip(v[:200], ref[:200]))
+
+
+def test_gelu_and_silu_closed_forms():
+    for v in (-3.0, -0.5, 0.0, 0.25, 1.0, 4.0):
+        want = 0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0)))
+        assert oracle.gelu_erf(v, out_bf16=False) == pytest.approx(want, rel=1e-6, abs=1e-12)
+        assert oracle.silu(v, out_bf16=False) == pytest.approx(v / (1 + math.exp(-v)), rel=1e-6,
+                                                               abs=1e-12)
+    assert oracle.gelu_erf(0.0) == 0.0 and oracle.gelu_erf(30.0) == 30.0
+
+
+def test_linear_sequence_rounds_like_separate_ops():
+    """bias then LoRA residual, each rounded to bf16, equals composing the pieces by hand."""
+    rng = np.random.default_rng(4)
+    M, K, N, r = 6, 128, 40, 16
+    x = oracle.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    w = oracle.bf16_round((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    bias = oracle.bf16_round(rng.standard_normal(N).astype(np.float32))
+    A = oracle.bf16_round((rng.standard_normal((K, r)) * 0.01).astype(np.float32))
+    B = oracle.bf16_round((rng.standard_normal((r, N)) * 0.01).astype(np.float32))
+    wq, s, b = oracle.quantize(w, 64, 4, sb_bf16=True)
+    y = oracle.linear(x, wq, s, b, 64, 4, bias=bias, lora_a=A, lora_b=B, lora_scale=0.5, act=1)
+    rb = oracle.bf16_round
+    y1 = oracle.quantized_matmul(x, wq, s, b, 64, 4)
+    y2 = rb(y1 + bias)
+    xa = rb((x.astype(np.float64) @ A.astype(np.float64)).astype(np.float32))
+    rr = rb((xa.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+    y3 = rb(y2 + rb(rr * np.float32(0.5)))
+    want = np.vectorize(lambda v: oracle.gelu_erf(v))(y3).astype(np.float32)
+    assert np.array_equal(y, want)
+
+
+def test_invalid_shapes_rejected():
+    with pytest.raises(ValueError):
+        oracle.quantize(np.zeros((2, 100), np.float32), 64, 4)
+    with pytest.raises(ValueError):
+        oracle.quantize(np.zeros((2, 128), np.float32), 64, 3)
