@@ -69,8 +69,30 @@ struct Act<float> {
   static __device__ __forceinline__ float rnd(float v) { return v; }
 };
 
-// Exact-erf GELU, 0.5*v*(1+erf(v/sqrt(2))), evaluated in f32 with the device erff.
-__device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+// Exact-erf GELU, 0.5*v*(1+erf(v/sqrt(2))), branch-free so it can run on values held in the
+// MFMA accumulators without forcing them out of registers.  With z = |v|/sqrt(2):
+//   v >= 0:  0.5*v*(2 - erfc(z)),   v < 0:  0.5*v*erfc(z),
+// where erfc(z) = t*exp(-z^2 + P(t)), t = 1/(1 + z/2), P the degree-9 Chebyshev-fitted
+// polynomial of Press et al., Numerical Recipes 2nd ed. sec. 6.2 ("erfcc"; fractional error
+// below 1.2e-7 for all z >= 0).  Evaluated with the hardware reciprocal and exp2.
+__device__ __forceinline__ float gelu_erf(float v) {
+  const float z = fabsf(v) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = fmaf(p, t, -0.82215223f);
+  p = fmaf(p, t, 1.48851587f);
+  p = fmaf(p, t, -1.13520398f);
+  p = fmaf(p, t, 0.27886807f);
+  p = fmaf(p, t, -0.18628806f);
+  p = fmaf(p, t, 0.09678418f);
+  p = fmaf(p, t, 0.37409196f);
+  p = fmaf(p, t, 1.00002368f);
+  p = fmaf(p, t, -1.26551223f);
+  const float e = fmaf(-z, z, p);
+  const float erfc_z = t * __builtin_amdgcn_exp2f(e * 1.44269504088896341f);
+  const float g = v >= 0.0f ? 2.0f - erfc_z : erfc_z;
+  return 0.5f * v * g;
+}
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 

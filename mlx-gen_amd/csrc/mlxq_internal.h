@@ -28,6 +28,9 @@ int run_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq
 int run_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
             int sb_dtype, int64_t N, int gs, int bits, void* y, const QmmEpilogue& epi,
             hipStream_t st);
+int run_qmm_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
+                 int sb_dtype, int64_t N, int gs, int bits, void* y, const QmmEpilogue& epi,
+                 hipStream_t st);
 int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* A, const void* B,
                   int64_t N, int rank, int R, void* xa, void* lbt, hipStream_t st);
 int run_linear_epilogue(void* y, int x_dtype, int64_t M, int64_t N, const void* bias, const void* xa,

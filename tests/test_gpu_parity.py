@@ -135,6 +135,72 @@ def test_qmm_gemm_vs_oracle(mlxq, M, K, N, gs, bits):
     assert_close(y, ref, f"gemm M={M} K={K} N={N} gs={gs} b={bits}")
 
 
+WIDE_CASES = [
+    # Shapes with >= 128 256x256 tiles take the wide kernel (weights dequantized in registers).
+    (2304, 256, 4096, 64, 4),
+    (2000, 192, 4136, 32, 8),   # ragged M and N
+    (2048, 384, 4096, 128, 4),
+    (2304, 128, 4096, 64, 8),
+]
+
+
+@pytest.mark.parametrize("M,K,N,gs,bits", WIDE_CASES)
+def test_qmm_wide_vs_oracle(mlxq, M, K, N, gs, bits):
+    banner("qmm wide", M, K, N, gs, bits)
+    rng = np.random.default_rng(M + K + N + bits)
+    x = bf16_normal(rng, (M, K))
+    w = bf16_normal(rng, (N, K), 0.02)
+    rwq, rs, rb = oracle.quantize(w, gs, bits, sb_bf16=True)
+    y = to_np(mlxq.qmm(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), gs, bits))
+    ref = oracle.quantized_matmul(x, rwq, rs, rb, gs, bits, w_bf16=True, out_bf16=True)
+    assert_close(y, ref, f"wide M={M} K={K} N={N} gs={gs} b={bits}")
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_linear_wide_bias_lora_act(mlxq, act):
+    banner("linear wide epilogue", act)
+    rng = np.random.default_rng(77 + act)
+    M, K, N, r = 2100, 256, 4200, 16
+    x = bf16_normal(rng, (M, K))
+    w = bf16_normal(rng, (N, K), 0.02)
+    bias = bf16_normal(rng, (N,), 0.5)
+    A = bf16_normal(rng, (K, r), 0.01)
+    B = bf16_normal(rng, (r, N), 0.01)
+    rwq, rs, rb = oracle.quantize(w, 64, 4, sb_bf16=True)
+    y = to_np(mlxq.linear(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), 64, 4,
+                          bias=to_gpu(bias), lora_a=to_gpu(A), lora_b=to_gpu(B), lora_scale=1.0,
+                          activation=act))
+    ref = oracle.linear(x, rwq, rs, rb, 64, 4, w_bf16=True, act_bf16=True, bias=bias,
+                        lora_a=A, lora_b=B, lora_scale=1.0, act=act)
+    assert_close(y, ref, f"linear wide act={act}")
+
+
+def test_flux_mlp_full_size_sampled_rows(mlxq):
+    """Config 2 at full size: every output row depends only on its own input row, so a seeded
+    sample of rows checked against the oracle covers the full-size launch (all tiles ran)."""
+    banner("config2 full size: up+gelu, down")
+    M, K, F = 4608, 3072, 12288
+    rng = np.random.default_rng(0)
+    x = bf16_normal(rng, (M, K))
+    wu = bf16_normal(rng, (F, K), 0.02)
+    wd = bf16_normal(rng, (K, F), 0.02)
+    qu = oracle.quantize(wu, 64, 4, sb_bf16=True)
+    qd = oracle.quantize(wd, 64, 4, sb_bf16=True)
+    gu = [wq_to_gpu(qu[0]), to_gpu(qu[1]), to_gpu(qu[2])]
+    gd = [wq_to_gpu(qd[0]), to_gpu(qd[1]), to_gpu(qd[2])]
+    h = mlxq.linear(to_gpu(x), *gu, 64, 4, activation=mlxq.MLXQ_ACT_GELU)
+    y = mlxq.quantized_matmul(h, *gd, True, 64, 4)
+    torch.cuda.synchronize()
+    rows = np.sort(rng.choice(M, 40, replace=False))
+    rows = np.concatenate([[0, 255, 256, M - 1], rows])
+    h_np = to_np(h)
+    ref_h = oracle.linear(x[rows], *qu, 64, 4, w_bf16=True, act_bf16=True, act=1)
+    assert_close(h_np[rows], ref_h, "config2 up+gelu rows")
+    ref_y = oracle.quantized_matmul(h_np[rows], *qd, 64, 4, w_bf16=True, out_bf16=True)
+    assert_close(to_np(y)[rows], ref_y, "config2 down rows")
+    assert np.isfinite(h_np).all()
+
+
 def test_qmm_dispatch_matches_forced_kernels(mlxq):
     banner("dispatch")
     rng = np.random.default_rng(5)
