@@ -28,6 +28,7 @@ int run_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq
 int run_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
             int sb_dtype, int64_t N, int gs, int bits, void* y, const QmmEpilogue& epi,
             hipStream_t st);
+bool qmm_wide_fits(int64_t M, int64_t K, int64_t N, int gs, int bits, int sb_bytes);
 int run_qmm_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
                  int sb_dtype, int64_t N, int gs, int bits, void* y, const QmmEpilogue& epi,
                  hipStream_t st);

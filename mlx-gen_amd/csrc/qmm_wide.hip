@@ -3,20 +3,25 @@
 // y[M,N] = x[M,K] . W^T with W dequantized to bf16 (round_bf16(fma(code, scale, bias))) and
 // v_mfma_f32_32x32x16_bf16 accumulating in f32.
 //
-// Workgroup: 256 threads = 4 waves, block tile 256 (M) x 256 (N), K advanced 64 per step.
-// The waves split the tile along N only (wave w owns columns [64w, 64w+64) of all 256 rows):
-//   * weights: every lane loads its own packed words straight into registers (one 16-byte load
-//     per 32-column sub-tile per K step for Q4, two for Q8) and dequantizes them into the MFMA
-//     operand registers — no LDS round trip, and each weight is dequantized exactly once per
-//     workgroup because no two waves share columns;
-//   * activations: the 256x64 bf16 tile is staged global -> registers -> LDS (double buffered,
-//     XOR-swizzled 16-byte chunks so fragment reads and tile writes are bank-conflict free) and
-//     every wave reads all of it;
+// Workgroup: WAVES waves (8 by default: two per SIMD, so one wave's VALU/LDS work overlaps the
+// other's MFMAs), block tile 256 (M) x 256 (N), K advanced 64 per step.  The waves split the tile
+// along N only: wave w owns columns [w*256/WAVES, (w+1)*256/WAVES) of all 256 rows.
+//   * weights: every lane loads its own packed words straight into registers (one 16-byte
+//     buffer load per 32-column sub-tile per K step for Q4, two for Q8) and dequantizes them into
+//     the MFMA operand registers — no LDS round trip, and each weight is dequantized exactly once
+//     per workgroup because no two waves share columns;
+//   * activations: the 256x64 bf16 tile is staged global -> registers -> LDS through a 3-deep
+//     ring (one barrier per K step) and every wave reads all of it.  16-byte chunks are
+//     XOR-swizzled by f(row) = (row & 7) ^ ((row >> 3) & 1), which keeps both the 16-lane
+//     fragment reads (16 rows, one chunk) and the row-wise tile writes on distinct banks;
 //   * the MFMA takes the weight fragment as its A operand (rows = n) and the activation fragment
 //     as B (columns = m), so each lane's f32x16 result holds 4 runs of 4 consecutive n for one m
 //     and the epilogue writes 8-byte (4 x bf16) row segments directly.
 // Within a K step, lane half h (lane >> 5) covers k in [8(4h+kk), 8(4h+kk)+8) for MFMA kk = 0..3,
 // i.e. packed words 4h..4h+3 of the row's 8-word (Q4) K step — one contiguous load.
+// Q4 dequant: lo = w & 0x0f0f0f0f holds the even codes in its bytes, w & 0xf0f0f0f0 the odd codes
+// times 16, so each code is one v_cvt_f32_ubyteN and one FMA (with scale/16 for the odd codes —
+// an exact power-of-two rescale, so fma(16c, s/16, b) == fma(c, s, b) bit for bit).
 //
 // Tile order is XCD-aware: workgroups are dispatched round-robin over the 8 XCDs, so consecutive
 // ids are remapped to give each XCD a contiguous slice of a grouped (4 M-tiles x all N-tiles)
@@ -32,6 +37,7 @@ namespace {
 constexpr int kBM = 256;
 constexpr int kBN = 256;
 constexpr int kGroupM = 4;
+constexpr int kBufferFlags = 0x00020000;  // raw buffer resource word 3 for gfx9-family loads
 
 __device__ __forceinline__ void tile_coords(int64_t bid, int64_t tiles_m, int64_t tiles_n,
                                             int64_t& tm, int64_t& tn) {
@@ -48,43 +54,63 @@ __device__ __forceinline__ void tile_coords(int64_t bid, int64_t tiles_m, int64_
   tn = idx / gsz;
 }
 
+__device__ __forceinline__ int swz_f(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+template <int B>
+__device__ __forceinline__ float ubyte(uint32_t v) {
+  float r;
+  if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+  if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+  if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+  if constexpr (B == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
 // Dequantize the 8 codes of k-run [8(4h+kk), +8) into a bf16x8 MFMA operand.
+// s16 = s/16 (exact) pairs with the odd Q4 codes, which are extracted still shifted left by 4.
 template <int BITS>
-__device__ __forceinline__ bf16x8 dequant8(const uint32_t* w, int kk, float s, float z) {
+__device__ __forceinline__ bf16x8 dequant8(const uint32_t* w, int kk, float s, float s16, float z) {
   u32x4 o;
   if constexpr (BITS == 4) {
     const uint32_t v = w[kk];
-    const uint32_t lo = v & 0x0f0f0f0fu, hi = (v >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float c0 = (float)((lo >> (8 * e)) & 0xffu);
-      const float c1 = (float)((hi >> (8 * e)) & 0xffu);
-      o[e] = pack_bf16x2(fmaf(c0, s, z), fmaf(c1, s, z));
-    }
+    const uint32_t lo = v & 0x0f0f0f0fu, hi = v & 0xf0f0f0f0u;
+    o[0] = pack_bf16x2(fmaf(ubyte<0>(lo), s, z), fmaf(ubyte<0>(hi), s16, z));
+    o[1] = pack_bf16x2(fmaf(ubyte<1>(lo), s, z), fmaf(ubyte<1>(hi), s16, z));
+    o[2] = pack_bf16x2(fmaf(ubyte<2>(lo), s, z), fmaf(ubyte<2>(hi), s16, z));
+    o[3] = pack_bf16x2(fmaf(ubyte<3>(lo), s, z), fmaf(ubyte<3>(hi), s16, z));
   } else {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint32_t v = w[2 * kk + h];
-      const float c0 = (float)(v & 0xffu), c1 = (float)((v >> 8) & 0xffu);
-      const float c2 = (float)((v >> 16) & 0xffu), c3 = (float)(v >> 24);
-      o[2 * h] = pack_bf16x2(fmaf(c0, s, z), fmaf(c1, s, z));
-      o[2 * h + 1] = pack_bf16x2(fmaf(c2, s, z), fmaf(c3, s, z));
+      o[2 * h] = pack_bf16x2(fmaf(ubyte<0>(v), s, z), fmaf(ubyte<1>(v), s, z));
+      o[2 * h + 1] = pack_bf16x2(fmaf(ubyte<2>(v), s, z), fmaf(ubyte<3>(v), s, z));
     }
   }
   return __builtin_bit_cast(bf16x8, o);
 }
 
+template <typename SB>
+__device__ __forceinline__ float load_sb(__amdgpu_buffer_rsrc_t r, uint32_t idx) {
+  if constexpr (sizeof(SB) == 2)
+    return bf16_bits_to_f32((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, idx * 2u, 0, 0));
+  else
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, idx * 4u, 0, 0));
+}
+
 }  // namespace
 
-template <typename SB, int BITS, int GS, bool FUSED>
-__global__ __launch_bounds__(256, 1) void qmm_wide_kernel(const uint16_t* __restrict__ x, int64_t M,
-                                                          int64_t K, const uint32_t* __restrict__ wq,
-                                                          const SB* __restrict__ scales,
-                                                          const SB* __restrict__ biases, int64_t N,
-                                                          uint16_t* __restrict__ y, QmmEpilogue epi) {
-  constexpr int TMW = kBM / 32;     // 8 m sub-tiles per wave
-  constexpr int TNW = 2;            // 2 n sub-tiles per wave (64 columns)
-  constexpr int WPL = BITS;         // packed words per lane per n sub-tile per K step (4 or 8)
+template <typename SB, int BITS, int GS, int WAVES, bool FUSED>
+__global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
+    const uint16_t* __restrict__ x, int64_t M, int64_t K, const uint32_t* __restrict__ wq,
+    const SB* __restrict__ scales, const SB* __restrict__ biases, int64_t N,
+    uint16_t* __restrict__ y, QmmEpilogue epi) {
+  constexpr int NT = WAVES * 64;
+  constexpr int TMW = kBM / 32;          // m sub-tiles per wave (all 256 rows)
+  constexpr int TNW = kBN / WAVES / 32;  // n sub-tiles per wave
+  constexpr int WPL = BITS;              // packed words per lane per n sub-tile per K step (4 or 8)
+  constexpr int A_PER = kBM * 8 / NT;    // 16-byte activation chunks per thread per K step
+  constexpr int A_ROWS = NT / 8;         // row stride between a thread's chunks
+  static_assert(TNW >= 1 && A_PER >= 1 && A_ROWS % 16 == 0, "tile/wave shape");
   __shared__ __attribute__((aligned(16))) unsigned char smem[3][kBM * 128];
 
   const int tid = threadIdx.x;
@@ -96,37 +122,46 @@ __global__ __launch_bounds__(256, 1) void qmm_wide_kernel(const uint16_t* __rest
   const int64_t kwords = K * BITS / 32;
   const int64_t groups = K / GS;
   const int KT = (int)(K / 64);
+  const int64_t wn0 = bn0 + (int64_t)wave * (kBN / WAVES);
 
-  // ---- activation staging: thread owns chunk (tid & 7) of rows (tid >> 3) + 32 i.  Rows past M
-  // are clamped to M-1: they only feed output rows that are never stored, so no branch is needed.
-  // Offsets are 32-bit byte offsets (the host checks the operands fit in 4 GiB).
+  // Buffer resources: 32-bit offsets (the host checks every operand fits in 4 GiB).  Rows past
+  // M / N are clamped so every offset stays inside its operand.
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(x), (short)0, (int)(uint32_t)(M * K * 2), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(wq), (short)0, (int)(uint32_t)(N * kwords * 4), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<SB*>(scales), (short)0, (int)(uint32_t)(N * groups * sizeof(SB)), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<SB*>(biases), (short)0, (int)(uint32_t)(N * groups * sizeof(SB)), kBufferFlags);
+
+  // ---- activation staging: thread owns chunk (tid & 7) of rows (tid >> 3) + A_ROWS * i.
   const int a_row0 = tid >> 3, a_c = tid & 7;
-  const char* xb = reinterpret_cast<const char*>(x);
-  uint32_t a_goff[8];
+  uint32_t a_goff[A_PER];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int64_t r = bm0 + a_row0 + 32 * i < M ? bm0 + a_row0 + 32 * i : M - 1;
+  for (int i = 0; i < A_PER; ++i) {
+    const int64_t r = bm0 + a_row0 + A_ROWS * i < M ? bm0 + a_row0 + A_ROWS * i : M - 1;
     a_goff[i] = (uint32_t)((r * K + a_c * 8) * 2);
   }
-  const int a_lds = a_row0 * 128 + ((a_c ^ (a_row0 & 7)) << 4);
-  u32x4 areg[8];
+  const int a_lds = a_row0 * 128 + ((a_c ^ swz_f(a_row0)) << 4);
+  u32x4 areg[A_PER];
   auto load_a = [&](int kt) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      areg[i] = *reinterpret_cast<const u32x4*>(xb + a_goff[i] + (uint32_t)kt * 128u);
+    for (int i = 0; i < A_PER; ++i)
+      areg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, a_goff[i] + (uint32_t)kt * 128u, 0, 0));
   };
   auto store_a = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(smem[buf] + a_lds + i * 4096) = areg[i];
+    for (int i = 0; i < A_PER; ++i)
+      *reinterpret_cast<u32x4*>(smem[buf] + a_lds + i * A_ROWS * 128) = areg[i];
   };
 
-  // ---- weight rows of this lane: n = bn0 + 64 wave + 32 j + r32 (clamped to N-1 like A rows)
-  const char* wb = reinterpret_cast<const char*>(wq);
+  // ---- weight rows of this lane: n = wn0 + 32 j + r32 (clamped to N-1 like A rows)
   uint32_t w_goff[TNW], g_base[TNW];
   bool n_ok[TNW];
 #pragma unroll
   for (int j = 0; j < TNW; ++j) {
-    const int64_t n = bn0 + wave * 64 + j * 32 + r32;
+    const int64_t n = wn0 + j * 32 + r32;
     n_ok[j] = n < N;
     const int64_t nn = n_ok[j] ? n : N - 1;
     w_goff[j] = (uint32_t)((nn * kwords + half * WPL) * 4);
@@ -140,19 +175,20 @@ __global__ __launch_bounds__(256, 1) void qmm_wide_kernel(const uint16_t* __rest
     for (int j = 0; j < TNW; ++j) {
 #pragma unroll
       for (int q = 0; q < WPL / 4; ++q) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(wb + w_goff[j] + (uint32_t)kt * (8u * WPL) + 16u * q);
+        const u32x4 v = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, w_goff[j] + (uint32_t)kt * (8u * WPL) + 16u * q, 0, 0));
 #pragma unroll
         for (int e = 0; e < 4; ++e) braw[j][4 * q + e] = v[e];
       }
-      bs[j] = SBLoad<SB>::ld(scales, g_base[j] + g);
-      bz[j] = SBLoad<SB>::ld(biases, g_base[j] + g);
+      bs[j] = load_sb<SB>(rs, g_base[j] + g);
+      bz[j] = load_sb<SB>(rz, g_base[j] + g);
     }
   };
 
-  // ---- fragment read offsets (LDS): row i*32 + r32, chunk 4h + kk, swizzled by r32 & 7
+  // ---- fragment read offsets (LDS): row i*32 + r32, chunk 4h + kk
   int a_off[4];
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) a_off[kk] = r32 * 128 + (((4 * half + kk) ^ (r32 & 7)) << 4);
+  for (int kk = 0; kk < 4; ++kk) a_off[kk] = r32 * 128 + (((4 * half + kk) ^ swz_f(r32)) << 4);
 
   f32x16 acc[TMW][TNW];
 #pragma unroll
@@ -167,15 +203,16 @@ __global__ __launch_bounds__(256, 1) void qmm_wide_kernel(const uint16_t* __rest
   // registers.  One barrier per step, between the tile write and the first read of it (the
   // prefetch of step kt+1's first fragments during MFMA group kk=3).  Within a step, the next
   // group's activation fragments (LDS) and weight fragments (dequantized in registers) are
-  // prepared while the current group's 16 MFMAs run.
+  // prepared while the current group's MFMAs run.
   uint32_t bcur[TNW][WPL];
-  float scur[TNW], zcur[TNW];
+  float scur[TNW], s16cur[TNW], zcur[TNW];
   auto take_b = [&]() {
 #pragma unroll
     for (int j = 0; j < TNW; ++j) {
 #pragma unroll
       for (int e = 0; e < WPL; ++e) bcur[j][e] = braw[j][e];
       scur[j] = bs[j];
+      s16cur[j] = bs[j] * 0.0625f;
       zcur[j] = bz[j];
     }
   };
@@ -186,7 +223,7 @@ __global__ __launch_bounds__(256, 1) void qmm_wide_kernel(const uint16_t* __rest
   };
   auto deq_b = [&](int slot, int kk) {
 #pragma unroll
-    for (int j = 0; j < TNW; ++j) bfr[slot][j] = dequant8<BITS>(bcur[j], kk, scur[j], zcur[j]);
+    for (int j = 0; j < TNW; ++j) bfr[slot][j] = dequant8<BITS>(bcur[j], kk, scur[j], s16cur[j], zcur[j]);
   };
   auto mfma_group = [&](int slot) {
 #pragma unroll
@@ -195,6 +232,7 @@ __global__ __launch_bounds__(256, 1) void qmm_wide_kernel(const uint16_t* __rest
       for (int j = 0; j < TNW; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[slot][j], af[slot][i], acc[i][j], 0, 0, 0);
   };
+  constexpr int MF = TMW * TNW;  // MFMAs per group
 
   load_a(0);
   load_b(0);
@@ -223,19 +261,13 @@ __global__ __launch_bounds__(256, 1) void qmm_wide_kernel(const uint16_t* __rest
     read_a(0, As, 2);
     deq_b(0, 2);
     mfma_group(1);
-    if constexpr (next) __builtin_amdgcn_sched_group_barrier(0x200, 8, 0);   // tile writes first
+    if constexpr (next) __builtin_amdgcn_sched_group_barrier(0x200, A_PER, 0);  // tile writes first
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA
-      if (q < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);           // LDS read
-      if (next2 && q < 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                      // VALU
-    }
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (q < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+    for (int q = 0; q < 2 * MF; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                          // MFMA
+      if (q % MF < TMW) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // LDS read
+      if (next2 && q < A_PER) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // global load
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);                          // VALU
     }
     __syncthreads();
     read_a(1, As, 3);
@@ -249,17 +281,13 @@ __global__ __launch_bounds__(256, 1) void qmm_wide_kernel(const uint16_t* __rest
     }
     mfma_group(1);
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
+    for (int q = 0; q < 2 * MF; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (q < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-    }
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (next && q < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (next2 && q < 6) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      if (q < MF || next) {
+        if (q % MF < TMW) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      if (next2 && q >= MF && q < MF + 2 + TNW * WPL / 4) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
     }
   };
   using T_ = std::true_type;
@@ -272,7 +300,7 @@ __global__ __launch_bounds__(256, 1) void qmm_wide_kernel(const uint16_t* __rest
   }
   step(kt, F_{}, F_{});
 
-  // ---- epilogue: lane holds m = bm0 + 32 i + r32 and n = bn0 + 64 wave + 32 j + 8 a + 4 h + b.
+  // ---- epilogue: lane holds m = bm0 + 32 i + r32 and n = wn0 + 32 j + 8 a + 4 h + b.
   const bool vec_ok = (N % 4) == 0;
   bf16x8 xa[TMW], lb[TNW];
   const bool lora = FUSED && epi.rank16 > 0;
@@ -287,13 +315,13 @@ __global__ __launch_bounds__(256, 1) void qmm_wide_kernel(const uint16_t* __rest
     for (int j = 0; j < TNW; ++j) {
       lb[j] = bf16x8{};
       if (lora && n_ok[j])
-        lb[j] = *reinterpret_cast<const bf16x8*>(epi.lbt + (bn0 + wave * 64 + j * 32 + r32) * 16 + half * 8);
+        lb[j] = *reinterpret_cast<const bf16x8*>(epi.lbt + (wn0 + j * 32 + r32) * 16 + half * 8);
     }
   }
   // One 32-column sub-tile per call; J is a compile-time index so acc stays in registers.
   auto epilogue_cols = [&](auto J) {
     constexpr int j = decltype(J)::value;
-    const int64_t nb = bn0 + wave * 64 + j * 32 + 4 * half;
+    const int64_t nb = wn0 + j * 32 + 4 * half;
     float bias_v[16];
     if constexpr (FUSED) {
 #pragma unroll
@@ -337,9 +365,24 @@ __global__ __launch_bounds__(256, 1) void qmm_wide_kernel(const uint16_t* __rest
       }
     }
   };
-  static_assert(TNW == 2, "epilogue unrolls two column sub-tiles");
   epilogue_cols(std::integral_constant<int, 0>{});
-  epilogue_cols(std::integral_constant<int, 1>{});
+  if constexpr (TNW > 1) epilogue_cols(std::integral_constant<int, 1>{});
+}
+
+template <typename SB, int BITS, int GS, int WAVES>
+static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+                         const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st,
+                         int64_t tiles) {
+  const bool fused = epi.bias || epi.rank16 || epi.act != MLXQ_ACT_NONE;
+  if (fused)
+    hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, true>), dim3((unsigned)tiles),
+                       dim3(WAVES * 64), 0, st, (const uint16_t*)x, M, K, wq, (const SB*)s,
+                       (const SB*)b, N, (uint16_t*)y, epi);
+  else
+    hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, false>), dim3((unsigned)tiles),
+                       dim3(WAVES * 64), 0, st, (const uint16_t*)x, M, K, wq, (const SB*)s,
+                       (const SB*)b, N, (uint16_t*)y, epi);
+  return check_launch("qmm_wide");
 }
 
 template <typename SB, int BITS, int GS>
@@ -348,14 +391,13 @@ static int launch_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, 
   const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
   if (tiles == 0) return MLXQ_OK;
   if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm: problem too large");
-  const bool fused = epi.bias || epi.rank16 || epi.act != MLXQ_ACT_NONE;
-  if (fused)
-    hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, true>), dim3((unsigned)tiles), dim3(256), 0, st,
-                       (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi);
-  else
-    hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, false>), dim3((unsigned)tiles), dim3(256), 0, st,
-                       (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi);
-  return check_launch("qmm_wide");
+  // 8 waves (two per SIMD) measured faster than 4 waves with twice the columns per wave.
+  return launch_wide_w<SB, BITS, GS, 8>(x, M, K, wq, s, b, N, y, epi, st, tiles);
+}
+
+bool qmm_wide_fits(int64_t M, int64_t K, int64_t N, int gs, int bits, int sb_bytes) {
+  const int64_t lim = (int64_t)1 << 32;
+  return M * K * 2 < lim && N * (K * bits / 32) * 4 < lim && N * (K / gs) * sb_bytes < lim;
 }
 
 int run_qmm_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
