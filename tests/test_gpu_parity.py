@@ -234,6 +234,21 @@ def test_qmv_vs_oracle(mlxq, M, K, N, gs, bits, dtype):
         assert rel < 1e-5
 
 
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+@pytest.mark.parametrize("K,N,gs,bits", [(3072, 8192, 64, 4), (8192, 3072, 64, 4), (512, 2064, 64, 8),
+                                         (1024, 520, 128, 8)])
+def test_qmv_config4_shapes(mlxq, M, K, N, gs, bits):
+    """Config 4 decode shapes (gate/up [8192,3072], down [3072,8192]) plus Q8 and ragged N."""
+    banner("qmv config4", M, K, N, gs, bits)
+    rng = np.random.default_rng(M * 31 + K + N + bits)
+    x = bf16_normal(rng, (M, K))
+    w = bf16_normal(rng, (N, K), 0.02)
+    rwq, rs, rb = oracle.quantize(w, gs, bits, sb_bf16=True)
+    y = to_np(mlxq.quantized_matmul(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), True, gs, bits))
+    ref = oracle.quantized_matmul(x, rwq, rs, rb, gs, bits, w_bf16=False, out_bf16=True)
+    assert_close(y, ref, f"qmv M={M} K={K} N={N} gs={gs} b={bits}")
+
+
 def test_f32_activations_large_m(mlxq):
     """f32 activations at GEMM-sized M keep exact-f32 semantics (the FLUX.1 f32 stream)."""
     banner("f32 large M")
