@@ -17,6 +17,8 @@
  *   - Row-major, contiguous.  Packing: 32/bits codes per uint32, element i of a word at bit offset
  *     i*bits (low bits first); wq [N, K*bits/32]; scales/biases [N, K/group_size].
  *   - group_size in {32, 64, 128}, bits in {4, 8}, K % group_size == 0.
+ *   - Alignment: activations, packed weights, outputs and workspaces 16 bytes; scales and biases
+ *     4 bytes.  Misaligned pointers are rejected with MLXQ_EINVAL.
  *   - Every call returns an mlxq_status; on failure mlxq_last_error() (thread-local) describes
  *     it.  Invalid shapes are rejected with MLXQ_EINVAL, never a crash (the reference's
  *     packed_bits panics on malformed triples, src/quant.rs:38-41).

@@ -44,10 +44,10 @@ static int check_dtype(const char* op, const char* what, int dt) {
   return MLXQ_OK;
 }
 
-static int check_aligned(const char* op, const char* what, const void* p) {
+static int check_aligned(const char* op, const char* what, const void* p, uintptr_t align = 16) {
   if (p == nullptr) return set_error(MLXQ_EINVAL, "%s: %s is null", op, what);
-  if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
-    return set_error(MLXQ_EINVAL, "%s: %s must be 16-byte aligned", op, what);
+  if (reinterpret_cast<uintptr_t>(p) % align != 0)
+    return set_error(MLXQ_EINVAL, "%s: %s must be %d-byte aligned", op, what, (int)align);
   return MLXQ_OK;
 }
 
@@ -62,7 +62,8 @@ static int check_mm(const char* op, const void* x, int x_dtype, int64_t M, int64
   if ((rc = check_aligned(op, "x", x)) || (rc = check_aligned(op, "wq", wq)) ||
       (rc = check_aligned(op, "y", y)))
     return rc;
-  if (s == nullptr || b == nullptr) return set_error(MLXQ_EINVAL, "%s: scales/biases are null", op);
+  // scales/biases are read as whole dwords (16-byte chunks in the GEMV)
+  if ((rc = check_aligned(op, "scales", s, 4)) || (rc = check_aligned(op, "biases", b, 4))) return rc;
   return MLXQ_OK;
 }
 

@@ -2,7 +2,8 @@
 //
 // The path is HBM-bound and small (a few MB per call), so what matters is latency: every load a
 // wave needs is issued up front, the packed weights go straight into MFMA operand registers, and
-// the only other phase is one coalesced copy of the activations into LDS.
+// each K step is folded as soon as its weights arrive (the step code is branch-free, so the
+// compiler waits for exactly one load per step instead of the whole stream).
 //
 // Semantics are the exact-f32 factored form (no bf16 rounding of dequantized weights):
 //   y[m,n] = sum_g ( s[n,g] * sum_{k in g} x[m,k]*c[n,k]  +  b[n,g] * X[m,g] ),  X = sum_{k in g} x.
@@ -12,14 +13,14 @@
 // Q8 codes enter as bf16(c) (exact for c < 256) and fold as y += s*acc + b*X.
 // X comes from the same activation fragments multiplied by an all-ones operand on the MFMA.
 //
-// v_mfma_f32_32x32x16_bf16 with A = activations (rows m = lane&31, rows >= M zeroed) and
-// B = weights (columns n = lane&31).  Lane half h = lane>>5 supplies k-run 4h+kk for MFMA kk, i.e.
-// packed words 4h..4h+3 of the row's 64-wide K step (one 16-byte load for Q4, two for Q8); each
-// MFMA stays inside one group (group_size 64 or 128).  The result holds column n for rows
-// m = 8a + 4h + b; rows 0..7 (a = 0) are folded.
-// A workgroup owns 32 weight rows; its SPLIT waves split K and reduce through LDS at the end.
+// v_mfma_f32_16x16x32_bf16 with A = activations (rows m = lane&15; rows >= M read row 0 and are
+// never stored) and B = weights (columns n = lane&15).  Lane quarter q = lane>>4 supplies the
+// 16 codes [16q, 16q+16) of the row's 64-wide K step (one 8-byte load for Q4, 16 bytes for Q8);
+// MFMA j takes codes [16q+8j, 16q+8j+8), so every MFMA stays inside one group (group_size 64 or
+// 128).  The 16x16 result holds column n = lane&15 for rows m = 4q + e.
+// A workgroup owns 16 weight rows; its SPLIT waves split K and reduce through LDS at the end.
 // Q4 k-order inside an 8-run is [0,4,1,5,2,6,3,7] (how the and-or pairs nibbles i and i+4); the
-// activation fragment is permuted to match with v_perm_b32 as it comes out of LDS.
+// activation rows are permuted to match with v_perm_b32 as they are copied into LDS.
 #include "mlxq_common.h"
 
 namespace mlxq {
@@ -27,12 +28,13 @@ namespace mlxq {
 namespace {
 
 constexpr int kBufferFlags = 0x00020000;
-constexpr int kMaxSteps = 8;  // K steps per wave (all loads issued at once)
-constexpr int kCopyPer = 9;   // 16-byte operand chunks per thread in the LDS copy
+constexpr int kMaxSteps = 8;   // K steps per wave (all loads issued at once)
+constexpr int kMaxRows = 8;    // activation rows
 constexpr int kMaxLds = 160 * 1024;
+constexpr uint32_t kOob = 0x7ffffff0u;  // buffer offset past every resource: loads return zero
 
-// LDS: activations [M][K] (rows padded by 16 bytes), then the workgroup's 16 scale rows and
-// 16 bias rows [16][G] in the scales dtype.
+// LDS: activations [M][K] (rows padded by 16 bytes so rows start on different banks), then the
+// workgroup's 16 scale rows and 16 bias rows [16][G] in the scales dtype.
 struct QmvLds {
   int x_stride, sb_off, sb_bytes, total;
 };
@@ -75,14 +77,20 @@ __device__ __forceinline__ bf16x8 cvt_q8(uint32_t w0, uint32_t w1) {
   return __builtin_bit_cast(bf16x8, o);
 }
 
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
 }  // namespace
 
+// Launch contract (checked on the host by qmv_mfma_applicable): 1 <= M <= 8, K % 64 == 0,
+// K/8 <= SPLIT*64 (one activation chunk per thread and row), G*sizeof(SB) <= SPLIT*64 (one scale
+// chunk and one bias chunk per thread), ceil(K/64 / SPLIT) == STEPS, every buffer < 2 GiB.
 template <typename SB, int BITS, int SPLIT, int STEPS>
 __global__ __launch_bounds__(SPLIT * 64) void qmv_mfma_kernel(
-    const uint16_t* __restrict__ x, int M, int64_t K, const uint32_t* __restrict__ wq,
-    const SB* __restrict__ scales, const SB* __restrict__ biases, int64_t N, int gs,
+    const uint16_t* __restrict__ x, int M, int K, const uint32_t* __restrict__ wq,
+    const SB* __restrict__ scales, const SB* __restrict__ biases, int N, int gs,
     uint16_t* __restrict__ y) {
-  constexpr int NT = SPLIT * 64;
   constexpr int WW = BITS == 4 ? 2 : 4;  // packed words per lane per K step
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
 
@@ -90,45 +98,49 @@ __global__ __launch_bounds__(SPLIT * 64) void qmv_mfma_kernel(
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c16 = lane & 15, q = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const int64_t n = n0 + c16;
-  const int64_t nn = n < N ? n : N - 1;
-  const int64_t kwords = K * BITS / 32;
-  const int G = (int)K / gs;
-  const int KT = (int)(K / 64);
+  const int n0 = blockIdx.x * 16;
+  const int n = n0 + c16;
+  const int nn = n < N ? n : N - 1;
+  const int kwords = K * BITS / 32;
+  const int gshift = gs == 128 ? 1 : 0;  // 64-wide K steps per group: 1 or 2
+  const int G = (K >> 6) >> gshift;
+  const int KT = K / 64;
   const int kt0 = wave * STEPS;  // this wave's K steps: [kt0, min(kt0 + STEPS, KT))
-  const QmvLds L = qmv_lds_layout(M, K, gs, sizeof(SB));
+  QmvLds L;  // qmv_lds_layout without the division
+  L.x_stride = K * 2 + 16;
+  L.sb_off = M * L.x_stride;
+  L.sb_bytes = 16 * G * (int)sizeof(SB);
 
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(x), (short)0, (int)(uint32_t)((int64_t)M * K * 2), kBufferFlags);
+      const_cast<uint16_t*>(x), (short)0, M * K * 2, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(wq), (short)0, (int)(uint32_t)(N * kwords * 4), kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<SB*>(scales), (short)0, (int)(uint32_t)(N * G * sizeof(SB)), kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<SB*>(biases), (short)0, (int)(uint32_t)(N * G * sizeof(SB)), kBufferFlags);
+      const_cast<uint32_t*>(wq), (short)0, (int)((uint32_t)N * (uint32_t)kwords * 4u), kBufferFlags);
+  // Rounded up to whole dwords: buffer range checks are per dword, and the last bf16 scale may
+  // share its dword with 2 bytes past the end (same aligned dword, so never another page; the
+  // extra value lands in the LDS slot of a row >= N, which is never stored).
+  const int sb_total = (int)(((uint32_t)N * (uint32_t)G * sizeof(SB) + 3u) & ~3u);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<SB*>(scales), (short)0, sb_total, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rz =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<SB*>(biases), (short)0, sb_total, kBufferFlags);
 
-  // 1. Workgroup operands first (they are small and return before the weight stream): the
-  //    activations, and the contiguous scale / bias rows of this workgroup's 16 weight rows.
-  //    Everything is read as 16-byte chunks; past-the-end bytes come back as zero.
-  const int x_chunks = (int)((int64_t)M * K / 8);
+  // 1. Workgroup operands first (small; they return before the weight stream): one 16-byte chunk
+  //    per thread of each activation row, and of the contiguous scale and bias rows of this
+  //    workgroup's 16 weight rows.  Threads past the end read at an out-of-range offset (zero).
+  const int x_chunks = K / 8;
   const int sb_chunks = L.sb_bytes / 16;
-  const uint32_t sb_base = (uint32_t)(n0 * G * sizeof(SB));
-  u32x4 ct[kCopyPer];
+  const uint32_t x_off = tid < x_chunks ? (uint32_t)tid * 16u : kOob;
+  const uint32_t sb_off = tid < sb_chunks ? (uint32_t)n0 * (uint32_t)G * sizeof(SB) + (uint32_t)tid * 16u : kOob;
+  u32x4 cx[kMaxRows];
 #pragma unroll
-  for (int i = 0; i < kCopyPer; ++i) {
-    const int c = tid + i * NT;
-    if (c < x_chunks)
-      ct[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)c * 16u, 0, 0));
-    else if (c < x_chunks + sb_chunks)
-      ct[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, sb_base + (uint32_t)(c - x_chunks) * 16u, 0, 0));
-    else if (c < x_chunks + 2 * sb_chunks)
-      ct[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rz, sb_base + (uint32_t)(c - x_chunks - sb_chunks) * 16u, 0, 0));
-  }
+  for (int m = 0; m < kMaxRows; ++m)
+    if (m < M) cx[m] = load16(rx, x_off + (uint32_t)(m * K * 2));
+  const u32x4 cs = load16(rs, sb_off);
+  const u32x4 cz = load16(rz, sb_off);
 
   // 2. The wave's whole weight stream (branch-free: steps past KT, only possible in the last
-  //    wave, re-read step KT-1 and are not folded).
-  const uint32_t w_base = (uint32_t)((nn * kwords + q * WW) * 4);
+  //    wave, re-read step KT-1 and are folded with weight zero).
+  const uint32_t w_base = ((uint32_t)nn * (uint32_t)kwords + (uint32_t)(q * WW)) * 4u;
   uint32_t wv[STEPS][WW];
 #pragma unroll
   for (int d = 0; d < STEPS; ++d) {
@@ -146,21 +158,20 @@ __global__ __launch_bounds__(SPLIT * 64) void qmv_mfma_kernel(
 
   // 3. Operands into LDS.  Q4 activation runs are stored permuted to [0,4,1,5,2,6,3,7] so they
   //    pair with the and-or code layout without per-wave work.
+  if (tid < x_chunks) {
 #pragma unroll
-  for (int i = 0; i < kCopyPer; ++i) {
-    const int c = tid + i * NT;
-    if (c < x_chunks) {
-      const int m = c / (int)(K / 8), kc = c - m * (int)(K / 8);
-      const u32x4 v = BITS == 4 ? perm_q4(ct[i]) : ct[i];
-      *reinterpret_cast<u32x4*>(lds + m * L.x_stride + kc * 16) = v;
-    } else if (c < x_chunks + 2 * sb_chunks) {
-      *reinterpret_cast<u32x4*>(lds + L.sb_off + (c - x_chunks) * 16) = ct[i];
-    }
+    for (int m = 0; m < kMaxRows; ++m)
+      if (m < M)
+        *reinterpret_cast<u32x4*>(lds + m * L.x_stride + tid * 16) = BITS == 4 ? perm_q4(cx[m]) : cx[m];
+  }
+  if (tid < sb_chunks) {
+    *reinterpret_cast<u32x4*>(lds + L.sb_off + tid * 16) = cs;
+    *reinterpret_cast<u32x4*>(lds + L.sb_off + L.sb_bytes + tid * 16) = cz;
   }
   __syncthreads();
 
-  // 4. Per K step: 2 MFMAs x . codes and 2 MFMAs x . ones (group sums), then the fold.
-  //    Rows m >= M use row 0's activations; their results are never stored.
+  // 4. Per K step: 2 MFMAs x . codes and 2 MFMAs x . ones (group sums), then the fold.  Steps
+  //    past KT recompute step KT-1 with scale and bias zero.
   const unsigned char* xrow = lds + (c16 < M ? c16 : 0) * L.x_stride + q * 32;
   const SB* s_lds = reinterpret_cast<const SB*>(lds + L.sb_off) + c16 * G;
   const SB* z_lds = reinterpret_cast<const SB*>(lds + L.sb_off + L.sb_bytes) + c16 * G;
@@ -170,23 +181,23 @@ __global__ __launch_bounds__(SPLIT * 64) void qmv_mfma_kernel(
   f32x4 yacc = {0.0f, 0.0f, 0.0f, 0.0f};  // rows m = 4q + e, column n
 #pragma unroll
   for (int d = 0; d < STEPS; ++d) {
-    const int kt = kt0 + d;
-    if (kt < KT) {
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, xsum = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool valid = kt0 + d < KT;
+    const int kt = valid ? kt0 + d : KT - 1;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, xsum = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(xrow + kt * 128 + j * 16);
-        const bf16x8 b = BITS == 4 ? magic_q4(wv[d][j]) : cvt_q8(wv[d][2 * j], wv[d][2 * j + 1]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
-        xsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xsum, 0, 0, 0);
-      }
-      const int g = kt * 64 / gs;
-      const float s = SBLoad<SB>::ld(s_lds, g);
-      const float z = SBLoad<SB>::ld(z_lds, g);
-      const float zc = BITS == 4 ? fmaf(-128.0f, s, z) : z;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) yacc[e] = fmaf(s, acc[e], fmaf(zc, xsum[e], yacc[e]));
+    for (int j = 0; j < 2; ++j) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(xrow + kt * 128 + j * 16);
+      const bf16x8 b = BITS == 4 ? magic_q4(wv[d][j]) : cvt_q8(wv[d][2 * j], wv[d][2 * j + 1]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+      xsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xsum, 0, 0, 0);
     }
+    const int g = kt >> gshift;
+    const float s_raw = SBLoad<SB>::ld(s_lds, g), z_raw = SBLoad<SB>::ld(z_lds, g);
+    const float s = valid ? s_raw : 0.0f;
+    const float z = valid ? z_raw : 0.0f;
+    const float zc = BITS == 4 ? fmaf(-128.0f, s, z) : z;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) yacc[e] = fmaf(s, acc[e], fmaf(zc, xsum[e], yacc[e]));
   }
 
   // 5. Split-K reduction through LDS (reuses the operand area): [wave][m 0..15][n 0..15].
@@ -212,13 +223,14 @@ static int launch_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* 
   const int red = SPLIT * 16 * 17 * 4;
   static bool attr_set = false;
   if (!attr_set) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_mfma_kernel<SB, BITS, SPLIT, STEPS>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_mfma_kernel<SB, BITS, SPLIT, STEPS>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds) != hipSuccess)
+      return set_error(MLXQ_EDEVICE, "qmv: hipFuncSetAttribute failed");
     attr_set = true;
   }
   hipLaunchKernelGGL((qmv_mfma_kernel<SB, BITS, SPLIT, STEPS>), dim3((unsigned)blocks),
                      dim3(SPLIT * 64), L.total > red ? L.total : red, st, (const uint16_t*)x, (int)M,
-                     K, wq, (const SB*)s, (const SB*)b, N, gs, (uint16_t*)y);
+                     (int)K, wq, (const SB*)s, (const SB*)b, (int)N, gs, (uint16_t*)y);
   return check_launch("qmv_mfma");
 }
 
@@ -244,15 +256,16 @@ static int qmv_mfma_dispatch(const void* x, int64_t M, int64_t K, const uint32_t
 }
 
 bool qmv_mfma_applicable(int x_dtype, int64_t M, int64_t K, int64_t N, int gs) {
-  const int64_t lim = (int64_t)1 << 32;
-  if (x_dtype != MLXQ_BFLOAT16 || M < 1 || M > 8 || (gs != 64 && gs != 128) || K % 64 != 0) return false;
-  if (N * K >= lim) return false;
+  const int64_t lim = (int64_t)1 << 31;
+  if (x_dtype != MLXQ_BFLOAT16 || M < 1 || M > kMaxRows || (gs != 64 && gs != 128) || K % 64 != 0)
+    return false;
+  // every buffer (Q8 weights are the largest, N*K bytes; f32 scales N*G*4) under 2 GiB
+  if (N * K >= lim || M * K * 2 >= lim || N * (K / gs) * 4 >= lim) return false;
   int split, steps;
   qmv_shape(K, split, steps);
-  if (steps > kMaxSteps || M * K * 2 >= lim) return false;
-  const QmvLds L = qmv_lds_layout((int)M, K, gs, 4);
-  const int64_t chunks = M * K / 8 + 2 * L.sb_bytes / 16;
-  return chunks <= (int64_t)kCopyPer * split * 64 && L.total <= kMaxLds;
+  const int64_t threads = (int64_t)split * 64;
+  if (steps > kMaxSteps || K / 8 > threads || (K / gs) * 4 > threads) return false;
+  return qmv_lds_layout((int)M, K, gs, 4).total <= kMaxLds;
 }
 
 int run_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,

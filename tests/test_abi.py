@@ -79,6 +79,9 @@ def test_validation_rejects_before_device_work(lib):
     st = lib.mlxq_qmm(ctypes.c_void_p(8), 1, 16, 128, ctypes.c_void_p(16), ctypes.c_void_p(16),
                       ctypes.c_void_p(16), 1, 8, 64, 4, ctypes.c_void_p(16), null)
     assert st == _lib.MLXQ_EINVAL and b"aligned" in lib.mlxq_last_error()
+    st = lib.mlxq_qmv(ctypes.c_void_p(16), 1, 4, 128, ctypes.c_void_p(16), ctypes.c_void_p(18),
+                      ctypes.c_void_p(16), 1, 8, 64, 4, ctypes.c_void_p(16), null)
+    assert st == _lib.MLXQ_EINVAL and b"scales must be 4-byte aligned" in lib.mlxq_last_error()
     # Empty problems are successful no-ops.
     assert lib.mlxq_quantize(null, 1, 0, 128, 64, 4, null, null, null, null) == _lib.MLXQ_OK
 
