@@ -106,8 +106,12 @@ def bench_flux_mlp(mlxq, torch, steps, warmup):
     }
 
 
-def bench_gemv(mlxq, torch, iters=50):
-    """Config 4: decode MLP GEMVs (Q4 g64), weights rotated over 8 copies."""
+def bench_gemv(mlxq, torch, reps=20):
+    """Config 4: decode MLP GEMVs (Q4 g64) gate/up [8192,3072] and down [3072,8192].
+
+    The weights are rotated over 8 MLP copies (340 MB, more than the 256 MB Infinity Cache), and
+    one replay of a captured HIP graph runs 8 MLPs (24 GEMV launches) back to back, so the rate
+    is GPU time including the gaps between kernels but without host launch overhead."""
     dev = torch.device("cuda:0")
     K, F = 3072, 8192
     copies = []
@@ -117,35 +121,48 @@ def bench_gemv(mlxq, torch, iters=50):
         d = mlxq.quantize(gen_bf16((K, F), 0.02, 102 + 3 * c, dev), 64, 4)
         copies.append((g, u, d))
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
     out = {}
     wbytes_gu = F * K // 2 + F * (K // 64) * 4  # codes + bf16 scales and biases
     wbytes_d = K * F // 2 + K * (F // 64) * 4
     for M in (1, 2, 4, 8):
         x = gen_bf16((M, K), 1.0, 7, dev)
         hh = gen_bf16((M, F), 1.0, 8, dev)
-        for _ in range(3):
+        yg = torch.empty((M, F), dtype=torch.bfloat16, device=dev)
+        yu = torch.empty((M, F), dtype=torch.bfloat16, device=dev)
+        yd = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+
+        def mlps():
             for (g, u, d) in copies:
-                mlxq.qmv(x, *g, 64, 4)
-                mlxq.qmv(x, *u, 64, 4)
-                mlxq.qmv(hh, *d, 64, 4)
+                mlxq.qmv(x, *g, 64, 4, out=yg)
+                mlxq.qmv(x, *u, 64, 4, out=yu)
+                mlxq.qmv(hh, *d, 64, 4, out=yd)
+
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            mlps()  # warm-up outside capture (one-time kernel attribute setup)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            mlps()
+        for _ in range(3):
+            graph.replay()
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(iters):
-            g, u, d = copies[i % 8]
-            mlxq.qmv(x, *g, 64, 4)
-            mlxq.qmv(x, *u, 64, 4)
-            mlxq.qmv(hh, *d, 64, 4)
-        e1.record(stream)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / iters
+        us = e0.elapsed_time(e1) * 1e3 / (reps * len(copies))
         nbytes = 2 * wbytes_gu + wbytes_d + 2 * (2 * M * K) + 2 * (2 * M * F) + 2 * M * F + 2 * M * K
-        out[f"M{M}"] = {"us_per_mlp": ms * 1e3, "GBs": nbytes / (ms * 1e-3) / 1e9,
+        out[f"M{M}"] = {"us_per_mlp": round(us, 3), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
                         "bytes_per_mlp": nbytes}
-    out["note"] = ("3 GEMV launches per MLP (gate, up, down), event-timed back to back, so the "
-                   "rate includes launch gaps; rocprof kernel durations are in profiles/")
+        del graph
+    out["note"] = ("3 GEMV launches per decode MLP (gate, up, down) replayed from a HIP graph, "
+                   "so the rate includes inter-kernel gaps; per-kernel durations are in profiles/")
     return out
 
 

@@ -178,8 +178,8 @@ int run_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq
             const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st) {
   // bf16 activations with 64/128 groups take the matrix-core GEMV; f32 activations and
   // group_size 32 take the VALU kernel below (same exact-f32 dequant semantics).
-  if (qmv_mfma_applicable(x_dtype, M, K, N, gs))
-    return run_qmv_mfma(x, M, K, wq, s, b, sb_dtype, N, gs, bits, y, st);
+  if (qmv_mfma_applicable(x_dtype, sb_dtype, M, K, N, gs, bits))
+    return run_qmv_mfma(x, M, K, wq, s, b, N, gs, bits, y, st);
   if (x_dtype == MLXQ_BFLOAT16) {
     if (sb_dtype == MLXQ_BFLOAT16) return qmv_bits_gs<uint16_t, uint16_t>(x, M, K, wq, s, b, N, gs, bits, y, st);
     return qmv_bits_gs<uint16_t, float>(x, M, K, wq, s, b, N, gs, bits, y, st);

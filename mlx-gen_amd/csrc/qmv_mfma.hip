@@ -1,25 +1,32 @@
 // qmv_mfma.hip — decode GEMV y[M,N] = x[M,K] . W^T for M <= 8 on gfx950 matrix cores.
 //
-// The path is HBM-bound and small (a few MB per call), so what matters is latency: every load a
-// wave needs is issued up front, the packed weights go straight into MFMA operand registers, and
-// each K step is folded as soon as its weights arrive (the step code is branch-free, so the
-// compiler waits for exactly one load per step instead of the whole stream).
+// The path is HBM-bound and small (a few MB per call), so the kernel is built around the load
+// shape the memory system streams best and around latency: every 16-byte weight load a wave
+// needs is issued up front, each load covers 16 rows x 64 contiguous bytes (4 lanes per row), the
+// packed codes go straight into MFMA operand registers, and each load step is folded as soon as
+// its data arrives (the step code is branch-free, so the compiler waits for one load per step).
 //
 // Semantics are the exact-f32 factored form (no bf16 rounding of dequantized weights):
 //   y[m,n] = sum_g ( s[n,g] * sum_{k in g} x[m,k]*c[n,k]  +  b[n,g] * X[m,g] ),  X = sum_{k in g} x.
-// Q4 codes enter the MFMA as the exact bf16 value 128+c (bf16 bits 0x4300|c, built with one
-// and-or per code pair), so acc = sum x*(128+c) and the fold per 64-wide K step is
+// Q4 codes enter the MFMA as the exact bf16 value 128+c (bf16 bits 0x4300|c, built with byte
+// permutes), so acc = sum x*(128+c) and the fold per group is
 //   y += s*acc + (b - 128*s)*X.
 // Q8 codes enter as bf16(c) (exact for c < 256) and fold as y += s*acc + b*X.
 // X comes from the same activation fragments multiplied by an all-ones operand on the MFMA.
 //
 // v_mfma_f32_16x16x32_bf16 with A = activations (rows m = lane&15; rows >= M read row 0 and are
-// never stored) and B = weights (columns n = lane&15).  Lane quarter q = lane>>4 supplies the
-// 16 codes [16q, 16q+16) of the row's 64-wide K step (one 8-byte load for Q4, 16 bytes for Q8);
-// MFMA j takes codes [16q+8j, 16q+8j+8), so every MFMA stays inside one group (group_size 64 or
-// 128).  The 16x16 result holds column n = lane&15 for rows m = 4q + e.
-// A workgroup owns 16 weight rows; its SPLIT waves split K and reduce through LDS at the end.
-// Q4 k-order inside an 8-run is [0,4,1,5,2,6,3,7] (how the and-or pairs nibbles i and i+4); the
+// never stored) and B = weights (columns n = lane&15).  Lane quarter q = lane>>4 holds the 16
+// bytes [16q, 16q+16) of the row's 64-byte load step: 32 Q4 codes (4 words) or 16 Q8 codes.
+// Each MFMA takes one 8-code run per lane, and all four runs of one MFMA must lie in one group:
+//   * Q8 (64 codes per step): MFMA j takes words 2j, 2j+1 of every lane — one 64-code block.
+//   * Q4, group 128 (128 codes per step, one group): MFMA i takes word i of every lane.
+//   * Q4, group 64: lanes q = 0,1 hold group 2t and lanes q = 2,3 group 2t+1.  Two
+//     v_permlane32_swap ops exchange words 2,3 of the low lane half with words 0,1 of the high
+//     half, after which words 0,1 of every lane belong to group 2t and words 2,3 to group 2t+1.
+// Each lane reads the activation run matching its code run from LDS (per-lane offsets below).
+// The 16x16 result holds column n = lane&15 for rows m = 4q + e.
+// A workgroup owns 16 weight rows; its waves split K and reduce through LDS at the end.
+// Q4 k-order inside an 8-run is [0,2,4,6,1,3,5,7] (low nibbles first, see unpack_q4); the
 // activation rows are permuted to match with v_perm_b32 as they are copied into LDS.
 #include "mlxq_common.h"
 
@@ -28,42 +35,33 @@ namespace mlxq {
 namespace {
 
 constexpr int kBufferFlags = 0x00020000;
-constexpr int kMaxSteps = 8;   // K steps per wave (all loads issued at once)
-constexpr int kMaxRows = 8;    // activation rows
+constexpr int kMaxSteps = 8;   // 64-byte load steps per wave (all issued at once)
+constexpr int kMaxWaves = 16;  // waves per workgroup (they split K)
+constexpr int kCopySlots = 8;  // 16-byte activation chunks per thread in the LDS copy
 constexpr int kMaxLds = 160 * 1024;
 constexpr uint32_t kOob = 0x7ffffff0u;  // buffer offset past every resource: loads return zero
 
-// LDS: activations [M][K] (rows padded by 16 bytes so rows start on different banks), then the
-// workgroup's 16 scale rows and 16 bias rows [16][G] in the scales dtype.
-struct QmvLds {
-  int x_stride, sb_off, sb_bytes, total;
-};
-__host__ __device__ inline QmvLds qmv_lds_layout(int M, int64_t K, int gs, int sb_size) {
-  QmvLds L;
-  L.x_stride = (int)(K * 2 + 16);
-  L.sb_off = M * L.x_stride;
-  L.sb_bytes = 16 * (int)(K / gs) * sb_size;
-  L.total = L.sb_off + 2 * L.sb_bytes;
-  return L;
-}
-
-// Q4 word -> bf16 pairs (128+c_i, 128+c_{i+4}), i = 0..3.
-__device__ __forceinline__ bf16x8 magic_q4(uint32_t w) {
+// Q4 word (codes c0..c7, c_i at bits 4i) -> bf16 pairs (128+c0, 128+c2), (128+c4, 128+c6),
+// (128+c1, 128+c3), (128+c5, 128+c7): bf16 bits 0x4300|c are exactly 128+c.  The low and high
+// nibbles are split into bytes once, then v_perm_b32 pairs two code bytes with two 0x43 bytes.
+__device__ __forceinline__ bf16x8 unpack_q4(uint32_t w) {
+  const uint32_t lo = w & 0x0f0f0f0fu;          // bytes c0, c2, c4, c6
+  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;   // bytes c1, c3, c5, c7
   u32x4 o;
-  o[0] = (w & 0x000f000fu) | 0x43004300u;
-  o[1] = ((w >> 4) & 0x000f000fu) | 0x43004300u;
-  o[2] = ((w >> 8) & 0x000f000fu) | 0x43004300u;
-  o[3] = ((w >> 12) & 0x000f000fu) | 0x43004300u;
+  o[0] = __builtin_amdgcn_perm(0x43434343u, lo, 0x04010400u);
+  o[1] = __builtin_amdgcn_perm(0x43434343u, lo, 0x04030402u);
+  o[2] = __builtin_amdgcn_perm(0x43434343u, hi, 0x04010400u);
+  o[3] = __builtin_amdgcn_perm(0x43434343u, hi, 0x04030402u);
   return __builtin_bit_cast(bf16x8, o);
 }
 
-// Activation run x0..x7 (raw bf16 pairs r0..r3) -> order [0,4,1,5,2,6,3,7].
+// Activation run x0..x7 (raw bf16 pairs r0..r3) -> order [0,2,4,6,1,3,5,7], matching unpack_q4.
 __device__ __forceinline__ u32x4 perm_q4(u32x4 r) {
   u32x4 o;
-  o[0] = __builtin_amdgcn_perm(r[2], r[0], 0x05040100u);
-  o[1] = __builtin_amdgcn_perm(r[2], r[0], 0x07060302u);
-  o[2] = __builtin_amdgcn_perm(r[3], r[1], 0x05040100u);
-  o[3] = __builtin_amdgcn_perm(r[3], r[1], 0x07060302u);
+  o[0] = __builtin_amdgcn_perm(r[1], r[0], 0x05040100u);
+  o[1] = __builtin_amdgcn_perm(r[3], r[2], 0x05040100u);
+  o[2] = __builtin_amdgcn_perm(r[1], r[0], 0x07060302u);
+  o[3] = __builtin_amdgcn_perm(r[3], r[2], 0x07060302u);
   return o;
 }
 
@@ -81,19 +79,34 @@ __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+// v_permlane32_swap_b32: lanes 32..63 of `lo_keep` trade places with lanes 0..31 of `hi_keep`.
+// Afterwards lanes 0..31 still hold their own `lo_keep` and lanes 32..63 their own `hi_keep`.
+__device__ __forceinline__ void swap_lane_halves(uint32_t& lo_keep, uint32_t& hi_keep) {
+  const auto r = __builtin_amdgcn_permlane32_swap(lo_keep, hi_keep, false, false);
+  lo_keep = r[0];
+  hi_keep = r[1];
+}
+
 }  // namespace
 
-// Launch contract (checked on the host by qmv_mfma_applicable): 1 <= M <= 8, K % 64 == 0,
-// K/8 <= SPLIT*64 (one activation chunk per thread and row), G*sizeof(SB) <= SPLIT*64 (one scale
-// chunk and one bias chunk per thread), ceil(K/64 / SPLIT) == STEPS, every buffer < 2 GiB.
-template <typename SB, int BITS, int SPLIT, int STEPS>
-__global__ __launch_bounds__(SPLIT * 64) void qmv_mfma_kernel(
+// Launch contract (checked on the host by qmv_plan): 1 <= M <= MR, K % (512/BITS) == 0,
+// bf16 scales and biases, LS = K*BITS/512 load steps per row with LS % STEPS == 0 and
+// blockDim.x = 64 * LS/STEPS <= 1024, at most kCopySlots/MR activation chunks per thread per
+// row, at most one scale chunk per thread, dynamic LDS as computed by qmv_plan, every buffer
+// < 2 GiB.
+template <int BITS, bool G64, int STEPS, int MR>
+__global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
     const uint16_t* __restrict__ x, int M, int K, const uint32_t* __restrict__ wq,
-    const SB* __restrict__ scales, const SB* __restrict__ biases, int N, int gs,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases, int N,
     uint16_t* __restrict__ y) {
-  constexpr int WW = BITS == 4 ? 2 : 4;  // packed words per lane per K step
+  constexpr int CPL = 512 / BITS;          // codes per row in one 64-byte load step
+  constexpr int GS = G64 ? 64 : 128;       // group size
+  constexpr int NM = BITS == 4 ? 4 : 2;    // MFMAs per load step
+  constexpr int E = MR < 4 ? MR : 4;       // result registers per lane that can hold a row < M
+  constexpr int SLOTS = kCopySlots / MR;   // activation chunks per thread per row
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
 
+  const int NT = blockDim.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -101,181 +114,253 @@ __global__ __launch_bounds__(SPLIT * 64) void qmv_mfma_kernel(
   const int n0 = blockIdx.x * 16;
   const int n = n0 + c16;
   const int nn = n < N ? n : N - 1;
-  const int kwords = K * BITS / 32;
-  const int gshift = gs == 128 ? 1 : 0;  // 64-wide K steps per group: 1 or 2
-  const int G = (K >> 6) >> gshift;
-  const int KT = K / 64;
-  const int kt0 = wave * STEPS;  // this wave's K steps: [kt0, min(kt0 + STEPS, KT))
-  QmvLds L;  // qmv_lds_layout without the division
-  L.x_stride = K * 2 + 16;
-  L.sb_off = M * L.x_stride;
-  L.sb_bytes = 16 * G * (int)sizeof(SB);
+  const int rowbytes = K * BITS / 8;
+  const int G = K / GS;
+  const int ls0 = wave * STEPS;     // this wave's load steps: [ls0, ls0 + STEPS)
+  const int x_stride = 2 * K + 16;  // LDS row pitch: rows start on different banks
+  const int sz_lds = M * x_stride;  // then (s, b - 128 s) or (s, b) as f32 pairs, [16 rows][G]
 
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(x), (short)0, M * K * 2, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(wq), (short)0, (int)((uint32_t)N * (uint32_t)kwords * 4u), kBufferFlags);
-  // Rounded up to whole dwords: buffer range checks are per dword, and the last bf16 scale may
-  // share its dword with 2 bytes past the end (same aligned dword, so never another page; the
-  // extra value lands in the LDS slot of a row >= N, which is never stored).
-  const int sb_total = (int)(((uint32_t)N * (uint32_t)G * sizeof(SB) + 3u) & ~3u);
-  const __amdgpu_buffer_rsrc_t rs =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<SB*>(scales), (short)0, sb_total, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rz =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<SB*>(biases), (short)0, sb_total, kBufferFlags);
+      const_cast<uint32_t*>(wq), (short)0, (int)((uint32_t)N * (uint32_t)rowbytes), kBufferFlags);
+  // Rounded up to whole dwords: buffer range checks are per dword, and the last scale may share
+  // its dword with 2 bytes past the end (same aligned dword, so never another page; the extra
+  // value belongs to a row >= N, which is never stored).
+  const int sb_total = (int)(((uint32_t)N * (uint32_t)G * 2u + 3u) & ~3u);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(scales), (short)0, sb_total, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(biases), (short)0, sb_total, kBufferFlags);
 
-  // 1. Workgroup operands first (small; they return before the weight stream): one 16-byte chunk
-  //    per thread of each activation row, and of the contiguous scale and bias rows of this
-  //    workgroup's 16 weight rows.  Threads past the end read at an out-of-range offset (zero).
-  const int x_chunks = K / 8;
-  const int sb_chunks = L.sb_bytes / 16;
-  const uint32_t x_off = tid < x_chunks ? (uint32_t)tid * 16u : kOob;
-  const uint32_t sb_off = tid < sb_chunks ? (uint32_t)n0 * (uint32_t)G * sizeof(SB) + (uint32_t)tid * 16u : kOob;
-  u32x4 cx[kMaxRows];
+  // 1. Workgroup operands first (small; they return before the weight stream): the activation
+  //    rows as 16-byte chunks, and the contiguous scale and bias rows of this workgroup's 16
+  //    weight rows (one 8-value chunk of each per thread).  Out-of-range chunks read as zero.
+  const int KC = K / 8;
+  u32x4 cx[MR][SLOTS];
 #pragma unroll
-  for (int m = 0; m < kMaxRows; ++m)
-    if (m < M) cx[m] = load16(rx, x_off + (uint32_t)(m * K * 2));
-  const u32x4 cs = load16(rs, sb_off);
-  const u32x4 cz = load16(rz, sb_off);
-
-  // 2. The wave's whole weight stream (branch-free: steps past KT, only possible in the last
-  //    wave, re-read step KT-1 and are folded with weight zero).
-  const uint32_t w_base = ((uint32_t)nn * (uint32_t)kwords + (uint32_t)(q * WW)) * 4u;
-  uint32_t wv[STEPS][WW];
+  for (int m = 0; m < MR; ++m) {
+    if (m < M) {
 #pragma unroll
-  for (int d = 0; d < STEPS; ++d) {
-    const int kt = kt0 + d < KT ? kt0 + d : KT - 1;
-    if constexpr (BITS == 4) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rw, w_base + (uint32_t)kt * 32u, 0, 0);
-      wv[d][0] = v[0];
-      wv[d][1] = v[1];
-    } else {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rw, w_base + (uint32_t)kt * 64u, 0, 0);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) wv[d][e] = v[e];
+      for (int i = 0; i < SLOTS; ++i) {
+        if (i * NT < KC) {
+          const int kc = tid + i * NT;
+          cx[m][i] = load16(rx, kc < KC ? (uint32_t)(m * K * 2 + kc * 16) : kOob);
+        }
+      }
     }
   }
+  const int sb_chunks = 2 * G;  // 16 rows x G bf16 = 2G chunks of 16 bytes
+  const uint32_t sb_src = tid < sb_chunks ? (uint32_t)n0 * (uint32_t)G * 2u + (uint32_t)tid * 16u : kOob;
+  const u32x4 cs = load16(rs, sb_src);
+  const u32x4 cz = load16(rz, sb_src);
 
-  // 3. Operands into LDS.  Q4 activation runs are stored permuted to [0,4,1,5,2,6,3,7] so they
-  //    pair with the and-or code layout without per-wave work.
-  if (tid < x_chunks) {
+  // 2. The wave's whole weight stream.
+  const uint32_t w_base = (uint32_t)nn * (uint32_t)rowbytes + (uint32_t)(ls0 * 64 + q * 16);
+  u32x4 wv[STEPS];
 #pragma unroll
-    for (int m = 0; m < kMaxRows; ++m)
-      if (m < M)
-        *reinterpret_cast<u32x4*>(lds + m * L.x_stride + tid * 16) = BITS == 4 ? perm_q4(cx[m]) : cx[m];
+  for (int d = 0; d < STEPS; ++d) wv[d] = load16(rw, w_base + (uint32_t)d * 64u);
+
+  // 3. Operands into LDS.  Q4 activation runs are stored permuted to [0,2,4,6,1,3,5,7] so they
+  //    pair with the unpacked code layout without per-wave work.  Scales and biases become f32
+  //    pairs (s, b - 128 s) for Q4 and (s, b) for Q8, ready for the fold.
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    if (m < M) {
+#pragma unroll
+      for (int i = 0; i < SLOTS; ++i) {
+        if (i * NT < KC) {
+          const int kc = tid + i * NT;
+          if (kc < KC)
+            *reinterpret_cast<u32x4*>(lds + m * x_stride + kc * 16) = BITS == 4 ? perm_q4(cx[m][i]) : cx[m][i];
+        }
+      }
+    }
   }
   if (tid < sb_chunks) {
-    *reinterpret_cast<u32x4*>(lds + L.sb_off + tid * 16) = cs;
-    *reinterpret_cast<u32x4*>(lds + L.sb_off + L.sb_bytes + tid * 16) = cz;
+    f32x4 pr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float s0 = __uint_as_float(cs[j] << 16), s1 = __uint_as_float(cs[j] & 0xffff0000u);
+      const float z0 = __uint_as_float(cz[j] << 16), z1 = __uint_as_float(cz[j] & 0xffff0000u);
+      pr[j] = f32x4{s0, BITS == 4 ? fmaf(-128.0f, s0, z0) : z0, s1, BITS == 4 ? fmaf(-128.0f, s1, z1) : z1};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<f32x4*>(lds + sz_lds + tid * 64 + j * 16) = pr[j];
   }
   __syncthreads();
 
-  // 4. Per K step: 2 MFMAs x . codes and 2 MFMAs x . ones (group sums), then the fold.  Steps
-  //    past KT recompute step KT-1 with scale and bias zero.
-  const unsigned char* xrow = lds + (c16 < M ? c16 : 0) * L.x_stride + q * 32;
-  const SB* s_lds = reinterpret_cast<const SB*>(lds + L.sb_off) + c16 * G;
-  const SB* z_lds = reinterpret_cast<const SB*>(lds + L.sb_off + L.sb_bytes) + c16 * G;
+  // 4. Per load step: NM MFMAs x . codes and NM MFMAs x . ones (group sums), then the fold of
+  //    each group, y += s*acc + zc*X.
+  const unsigned char* xa[NM];  // this lane's activation run for MFMA i at load step ls0
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    int k;
+    if constexpr (BITS == 8) k = 16 * q + 8 * i;
+    else if constexpr (!G64) k = 32 * q + 8 * i;
+    else if (i < 2) k = (q < 2 ? 32 * q : 32 * (q - 2) + 16) + 8 * i;
+    else k = (q < 2 ? 64 + 32 * q : 32 * q + 16) + 8 * (i - 2);
+    xa[i] = lds + (c16 < M ? c16 : 0) * x_stride + (ls0 * CPL + k) * 2;
+  }
+  const float* sz = reinterpret_cast<const float*>(lds + sz_lds) + 2 * c16 * G;
   bf16x8 ones;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
-  f32x4 yacc = {0.0f, 0.0f, 0.0f, 0.0f};  // rows m = 4q + e, column n
+  float yacc[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) yacc[e] = 0.0f;
+
+  auto fold = [&](const f32x4& acc, const f32x4& xsum, float s, float zc) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) yacc[e] = fmaf(s, acc[e], fmaf(zc, xsum[e], yacc[e]));
+  };
+
 #pragma unroll
   for (int d = 0; d < STEPS; ++d) {
-    const bool valid = kt0 + d < KT;
-    const int kt = valid ? kt0 + d : KT - 1;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, xsum = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(xrow + kt * 128 + j * 16);
-      const bf16x8 b = BITS == 4 ? magic_q4(wv[d][j]) : cvt_q8(wv[d][2 * j], wv[d][2 * j + 1]);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
-      xsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xsum, 0, 0, 0);
+    const int ls = ls0 + d;
+    uint32_t w[4] = {wv[d][0], wv[d][1], wv[d][2], wv[d][3]};
+    if constexpr (BITS == 4 && G64) {
+      swap_lane_halves(w[0], w[2]);
+      swap_lane_halves(w[1], w[3]);
     }
-    const int g = kt >> gshift;
-    const float s_raw = SBLoad<SB>::ld(s_lds, g), z_raw = SBLoad<SB>::ld(z_lds, g);
-    const float s = valid ? s_raw : 0.0f;
-    const float z = valid ? z_raw : 0.0f;
-    const float zc = BITS == 4 ? fmaf(-128.0f, s, z) : z;
+    f32x4 acc[2], xsum[2];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) yacc[e] = fmaf(s, acc[e], fmaf(zc, xsum[e], yacc[e]));
+    for (int h = 0; h < 2; ++h) {
+      acc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      xsum[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      const int h = (BITS == 4 && G64) ? i >> 1 : 0;
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(xa[i] + d * (CPL * 2));
+      const bf16x8 b = BITS == 4 ? unpack_q4(w[i]) : cvt_q8(w[2 * i], w[2 * i + 1]);
+      acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[h], 0, 0, 0);
+      xsum[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xsum[h], 0, 0, 0);
+    }
+    if constexpr (BITS == 4 && G64) {
+      const f32x4 p = *reinterpret_cast<const f32x4*>(sz + 4 * ls);  // groups 2ls, 2ls+1
+      fold(acc[0], xsum[0], p[0], p[1]);
+      fold(acc[1], xsum[1], p[2], p[3]);
+    } else {
+      const int g = (BITS == 4 || G64) ? ls : ls >> 1;  // Q4/128: one group per step; Q8: 64 codes
+      const f32x2 p = *reinterpret_cast<const f32x2*>(sz + 2 * g);
+      fold(acc[0], xsum[0], p[0], p[1]);
+    }
   }
 
   // 5. Split-K reduction through LDS (reuses the operand area): [wave][m 0..15][n 0..15].
+  //    Only rows 4q + e with e < E can be < M; the rest are never written or read.
   __syncthreads();
   float* red = reinterpret_cast<float*>(lds);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) red[(wave * 16 + 4 * q + e) * 17 + c16] = yacc[e];
+  for (int e = 0; e < E; ++e) red[(wave * 16 + 4 * q + e) * 17 + c16] = yacc[e];
   __syncthreads();
-  if (tid < 128) {
-    const int m = tid >> 4, nl = tid & 15;
+  const int W = NT >> 6;
+  for (int idx = tid; idx < 16 * M; idx += NT) {  // a one-wave workgroup has 64 < 16*M threads
+    const int m = idx >> 4, nl = idx & 15;
     float v = 0.0f;
-#pragma unroll
-    for (int w = 0; w < SPLIT; ++w) v += red[(w * 16 + m) * 17 + nl];
-    if (m < M && n0 + nl < N) y[(int64_t)m * N + n0 + nl] = f32_to_bf16_bits(v);
+    for (int w = 0; w < W; ++w) v += red[(w * 16 + m) * 17 + nl];
+    if (n0 + nl < N) y[m * N + n0 + nl] = f32_to_bf16_bits(v);
   }
 }
 
-template <typename SB, int BITS, int SPLIT, int STEPS>
+namespace {
+
+struct QmvPlan {
+  int waves, steps, mr, lds;
+};
+
+constexpr int kStepChoices[] = {8, 6, 4, 3, 2, 1};
+
+// Picks the most load steps per wave (<= kMaxSteps) that divide the row's load-step count, fit a
+// workgroup, and keep the activation copy within kCopySlots chunks per thread.  Long streams per
+// wave in small workgroups measured best: at 100 MB, 8 steps x 3 waves streams 5.4 TB/s against
+// 3.6 TB/s for 2 steps x 12 waves, and the decode shapes are no slower.
+bool qmv_plan(int64_t M, int64_t K, int gs, int bits, QmvPlan& p) {
+  if (M < 1 || M > 8 || (bits != 4 && bits != 8) || (gs != 64 && gs != 128)) return false;
+  const int64_t cpl = 512 / bits;
+  if (K <= 0 || K % cpl != 0 || K % gs != 0) return false;
+  const int64_t LS = K / cpl, KC = K / 8, G = K / gs;
+  const int mr = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
+  for (int steps : kStepChoices) {
+    if (LS % steps != 0) continue;
+    const int64_t waves = LS / steps;
+    if (waves > kMaxWaves) continue;
+    const int64_t nt = waves * 64;
+    if ((KC + nt - 1) / nt > kCopySlots / mr) continue;
+    if (2 * G > nt) continue;  // one scale chunk per thread
+    const int64_t operands = M * (2 * K + 16) + 16 * G * 8;
+    const int64_t red = waves * 16 * 17 * 4;
+    const int64_t lds = operands > red ? operands : red;
+    if (lds > kMaxLds) continue;
+    p = {(int)waves, steps, mr, (int)lds};
+    return true;
+  }
+  return false;
+}
+
+}  // namespace
+
+template <int BITS, bool G64, int STEPS, int MR>
 static int launch_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
-                           const void* b, int64_t N, int gs, void* y, hipStream_t st) {
-  const int64_t blocks = (N + 15) / 16;
-  const QmvLds L = qmv_lds_layout((int)M, K, gs, sizeof(SB));
-  const int red = SPLIT * 16 * 17 * 4;
+                           const void* b, int64_t N, const QmvPlan& p, void* y, hipStream_t st) {
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_mfma_kernel<SB, BITS, SPLIT, STEPS>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_mfma_kernel<BITS, G64, STEPS, MR>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds) != hipSuccess)
       return set_error(MLXQ_EDEVICE, "qmv: hipFuncSetAttribute failed");
     attr_set = true;
   }
-  hipLaunchKernelGGL((qmv_mfma_kernel<SB, BITS, SPLIT, STEPS>), dim3((unsigned)blocks),
-                     dim3(SPLIT * 64), L.total > red ? L.total : red, st, (const uint16_t*)x, (int)M,
-                     (int)K, wq, (const SB*)s, (const SB*)b, (int)N, gs, (uint16_t*)y);
+  hipLaunchKernelGGL((qmv_mfma_kernel<BITS, G64, STEPS, MR>), dim3((unsigned)((N + 15) / 16)),
+                     dim3(p.waves * 64), p.lds, st, (const uint16_t*)x, (int)M, (int)K, wq,
+                     (const uint16_t*)s, (const uint16_t*)b, (int)N, (uint16_t*)y);
   return check_launch("qmv_mfma");
 }
 
-// 16 waves split K (fewer when K is short); each wave gets STEPS = ceil(KT/16) <= 8 steps.
-static void qmv_shape(int64_t K, int& split, int& steps) {
-  const int64_t KT = K / 64;
-  split = KT >= 16 ? 16 : (KT >= 8 ? 8 : (KT >= 4 ? 4 : (KT >= 2 ? 2 : 1)));
-  steps = (int)((KT + split - 1) / split);
+template <int BITS, bool G64, int STEPS>
+static int qmv_rows(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+                    const void* b, int64_t N, const QmvPlan& p, void* y, hipStream_t st) {
+  switch (p.mr) {
+    case 1: return launch_qmv_mfma<BITS, G64, STEPS, 1>(x, M, K, wq, s, b, N, p, y, st);
+    case 2: return launch_qmv_mfma<BITS, G64, STEPS, 2>(x, M, K, wq, s, b, N, p, y, st);
+    case 4: return launch_qmv_mfma<BITS, G64, STEPS, 4>(x, M, K, wq, s, b, N, p, y, st);
+    default: return launch_qmv_mfma<BITS, G64, STEPS, 8>(x, M, K, wq, s, b, N, p, y, st);
+  }
 }
 
-template <typename SB, int BITS>
-static int qmv_mfma_dispatch(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
-                             const void* b, int64_t N, int gs, void* y, hipStream_t st) {
-  int split, steps;
-  qmv_shape(K, split, steps);
-#define MLXQ_S(SP, ST) \
-  if (split == SP && steps == ST) return launch_qmv_mfma<SB, BITS, SP, ST>(x, M, K, wq, s, b, N, gs, y, st);
-  MLXQ_S(16, 1) MLXQ_S(16, 2) MLXQ_S(16, 3) MLXQ_S(16, 4) MLXQ_S(16, 5) MLXQ_S(16, 6) MLXQ_S(16, 7)
-  MLXQ_S(16, 8) MLXQ_S(8, 1) MLXQ_S(8, 2) MLXQ_S(4, 1) MLXQ_S(4, 2) MLXQ_S(2, 1) MLXQ_S(2, 2)
-  MLXQ_S(1, 1)
-#undef MLXQ_S
-  return set_error(MLXQ_EINVAL, "qmv: no GEMV shape for K=%lld", (long long)K);
+template <int BITS, bool G64>
+static int qmv_steps(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+                     const void* b, int64_t N, const QmvPlan& p, void* y, hipStream_t st) {
+  switch (p.steps) {
+    case 1: return qmv_rows<BITS, G64, 1>(x, M, K, wq, s, b, N, p, y, st);
+    case 2: return qmv_rows<BITS, G64, 2>(x, M, K, wq, s, b, N, p, y, st);
+    case 3: return qmv_rows<BITS, G64, 3>(x, M, K, wq, s, b, N, p, y, st);
+    case 4: return qmv_rows<BITS, G64, 4>(x, M, K, wq, s, b, N, p, y, st);
+    case 6: return qmv_rows<BITS, G64, 6>(x, M, K, wq, s, b, N, p, y, st);
+    default: return qmv_rows<BITS, G64, 8>(x, M, K, wq, s, b, N, p, y, st);
+  }
 }
 
-bool qmv_mfma_applicable(int x_dtype, int64_t M, int64_t K, int64_t N, int gs) {
+bool qmv_mfma_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int64_t N, int gs, int bits) {
   const int64_t lim = (int64_t)1 << 31;
-  if (x_dtype != MLXQ_BFLOAT16 || M < 1 || M > kMaxRows || (gs != 64 && gs != 128) || K % 64 != 0)
-    return false;
-  // every buffer (Q8 weights are the largest, N*K bytes; f32 scales N*G*4) under 2 GiB
-  if (N * K >= lim || M * K * 2 >= lim || N * (K / gs) * 4 >= lim) return false;
-  int split, steps;
-  qmv_shape(K, split, steps);
-  const int64_t threads = (int64_t)split * 64;
-  if (steps > kMaxSteps || K / 8 > threads || (K / gs) * 4 > threads) return false;
-  return qmv_lds_layout((int)M, K, gs, 4).total <= kMaxLds;
+  if (x_dtype != MLXQ_BFLOAT16 || sb_dtype != MLXQ_BFLOAT16) return false;
+  // every buffer (Q8 weights are the largest, N*K bytes) under 2 GiB
+  if (N * K >= lim || M * K * 2 >= lim) return false;
+  QmvPlan p;
+  return qmv_plan(M, K, gs, bits, p);
 }
 
 int run_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
-                 int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st) {
-  if (sb_dtype == MLXQ_BFLOAT16) {
-    if (bits == 4) return qmv_mfma_dispatch<uint16_t, 4>(x, M, K, wq, s, b, N, gs, y, st);
-    return qmv_mfma_dispatch<uint16_t, 8>(x, M, K, wq, s, b, N, gs, y, st);
+                 int64_t N, int gs, int bits, void* y, hipStream_t st) {
+  QmvPlan p;
+  if (!qmv_plan(M, K, gs, bits, p))
+    return set_error(MLXQ_EINVAL, "qmv: no GEMV plan for M=%lld K=%lld", (long long)M, (long long)K);
+  if (bits == 8) {
+    if (gs == 64) return qmv_steps<8, true>(x, M, K, wq, s, b, N, p, y, st);
+    return qmv_steps<8, false>(x, M, K, wq, s, b, N, p, y, st);
   }
-  if (bits == 4) return qmv_mfma_dispatch<float, 4>(x, M, K, wq, s, b, N, gs, y, st);
-  return qmv_mfma_dispatch<float, 8>(x, M, K, wq, s, b, N, gs, y, st);
+  if (gs == 64) return qmv_steps<4, true>(x, M, K, wq, s, b, N, p, y, st);
+  return qmv_steps<4, false>(x, M, K, wq, s, b, N, p, y, st);
 }
 
 }  // namespace mlxq

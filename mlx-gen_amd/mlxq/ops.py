@@ -81,14 +81,19 @@ def dequantize(wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: i
     return out
 
 
-def _mm(entry, x, wq, scales, biases, group_size, bits, *extra):
+def _mm(entry, x, wq, scales, biases, group_size, bits, *extra, out=None):
     _need_gpu(x, wq, scales, biases)
     K = x.shape[-1]
     lead = x.shape[:-1]
     x2 = x.reshape(-1, K).contiguous()
     wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
     M, N = x2.shape[0], wq.shape[0]
-    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    if out is None:
+        y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    else:
+        if out.dtype != x.dtype or out.device != x.device or out.numel() != M * N or not out.is_contiguous():
+            raise ValueError(f"out must be a contiguous {x.dtype} tensor of {M * N} elements on {x.device}")
+        y = out
     args = [_ptr(x2), _dt(x2), M, K, _ptr(wq), _ptr(scales), _ptr(biases), _dt(scales), N]
     if entry == "mlxq_quantized_matmul":
         args.append(int(extra[0]))
@@ -98,19 +103,19 @@ def _mm(entry, x, wq, scales, biases, group_size, bits, *extra):
 
 
 def quantized_matmul(x, wq, scales, biases, transpose: bool = True,
-                     group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4):
+                     group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4, out=None):
     """y = x . dequantize(W)^T (transpose=True, the only form the reference uses)."""
-    return _mm("mlxq_quantized_matmul", x, wq, scales, biases, group_size, bits, transpose)
+    return _mm("mlxq_quantized_matmul", x, wq, scales, biases, group_size, bits, transpose, out=out)
 
 
-def qmm(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4):
+def qmm(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4, out=None):
     """Force the MFMA GEMM kernel (bf16 activations)."""
-    return _mm("mlxq_qmm", x, wq, scales, biases, group_size, bits)
+    return _mm("mlxq_qmm", x, wq, scales, biases, group_size, bits, out=out)
 
 
-def qmv(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4):
+def qmv(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4, out=None):
     """Force the GEMV kernel (M <= 8)."""
-    return _mm("mlxq_qmv", x, wq, scales, biases, group_size, bits)
+    return _mm("mlxq_qmv", x, wq, scales, biases, group_size, bits, out=out)
 
 
 def linear_workspace_size(M: int, N: int, rank: int) -> int:

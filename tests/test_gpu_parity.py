@@ -237,12 +237,13 @@ def test_qmv_vs_oracle(mlxq, M, K, N, gs, bits, dtype):
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
 @pytest.mark.parametrize("K,N,gs,bits", [(3072, 8192, 64, 4), (8192, 3072, 64, 4), (512, 2064, 64, 8),
                                          (1024, 520, 128, 8), (192, 17, 64, 4), (320, 33, 64, 8),
-                                         (640, 45, 128, 4)])
+                                         (640, 45, 128, 4), (512, 40, 64, 4), (256, 24, 128, 8)])
 def test_qmv_config4_shapes(mlxq, M, K, N, gs, bits):
     """Config 4 decode shapes (gate/up [8192,3072], down [3072,8192]) plus Q8 and ragged N.
 
-    The last three have an odd number of bf16 scales in total, so the final scale sits in a
-    half-filled dword at the end of its buffer."""
+    (192,17), (320,33), (640,45) have an odd number of bf16 scales in total, so the final scale
+    sits in a half-filled dword at the end of its buffer; (512,40) and (256,24) run on a one-wave
+    workgroup, where 64 threads store the 16*M outputs."""
     banner("qmv config4", M, K, N, gs, bits)
     rng = np.random.default_rng(M * 31 + K + N + bits)
     x = bf16_normal(rng, (M, K))
