@@ -39,6 +39,12 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extras", action="store_true", help="headline GEMM only")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--only", choices=("all", "mlp", "gemv", "quantize", "copy"), default="all",
+                   help="run one leg only (for profiling); 'copy' is the plain-copy calibration "
+                        "kernel for the HBM byte counters")
+    p.add_argument("--summarize-pmc", metavar="DIR",
+                   help="print the HBM traffic summary from rocprofv3 --pmc runs under DIR "
+                        "(subdirectories fetch/, write/, copy_fetch/, copy_write/) and exit")
     return p.parse_args()
 
 
@@ -223,8 +229,73 @@ def cpu_baseline(budget_s):
                       f"{dt:.1f} s"}
 
 
+COPY_BYTES = 1 << 30  # plain-copy calibration: 1 GiB read + 1 GiB written per launch
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qmm_wide_flux_mlp_hbm_traffic.txt")
+
+
+def run_copy(torch, reps=5):
+    dev = torch.device("cuda:0")
+    src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "reps": reps}))
+
+
+def _pmc_values(d, counter):
+    """{kernel name: [per-dispatch counter values]} from a rocprofv3 --pmc csv directory."""
+    import csv
+    import glob
+    out = {}
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] == counter:
+                out.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return out
+
+
+def summarize_pmc(d):
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the qmm kernels, scaled by what the same
+    counters read for a plain copy of COPY_BYTES."""
+    med = lambda v: sorted(v)[len(v) // 2]
+    cal = {}
+    for c, sub in (("FETCH_SIZE", "copy_fetch"), ("WRITE_SIZE", "copy_write")):
+        vals = [med(v) for k, v in _pmc_values(os.path.join(d, sub), c).items() if "copy" in k]
+        cal[c] = (COPY_BYTES / 1024.0) / max(vals)
+    lines = [f"calibration (1 GiB plain copy): FETCH_SIZE x{cal['FETCH_SIZE']:.4f}, "
+             f"WRITE_SIZE x{cal['WRITE_SIZE']:.4f} (expected KiB / counted KiB)"]
+    total = []
+    fetch = _pmc_values(os.path.join(d, "fetch"), "FETCH_SIZE")
+    write = _pmc_values(os.path.join(d, "write"), "WRITE_SIZE")
+    for k in sorted(fetch):
+        if "qmm" not in k:
+            continue
+        f = med(fetch[k]) * 1024 * cal["FETCH_SIZE"]
+        w = med(write.get(k, [0.0])) * 1024 * cal["WRITE_SIZE"]
+        total.append(f + w)
+        lines.append(f"{k.split('(')[0]}: fetch {f / 1e6:.1f} MB  write {w / 1e6:.1f} MB  "
+                     f"({len(fetch[k])} dispatches)")
+    lines.append(f"traffic_bytes_per_launch: {int(sum(total) / max(len(total), 1))}")
+    print("\n".join(lines))
+
+
+def read_traffic():
+    """HBM bytes per qmm launch from the committed rocprofv3 --pmc summary, or None."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     args = parse()
+    if args.summarize_pmc:
+        summarize_pmc(args.summarize_pmc)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the quantized-linear "
               "path is single-device by design, so multi-GPU runs are not supported.", file=sys.stderr)
@@ -234,6 +305,15 @@ def main():
     mlxq.load()
     assert torch.cuda.is_available(), "bench.py needs a GPU"
 
+    if args.only == "copy":
+        run_copy(torch)
+        return
+    if args.only == "gemv":
+        print(json.dumps({"gemv": bench_gemv(mlxq, torch)}))
+        return
+    if args.only == "quantize":
+        print(json.dumps({"quantize": bench_quantize(mlxq, torch)}))
+        return
     g = bench_flux_mlp(mlxq, torch, args.steps, args.warmup)
     achieved = g["qmm_flop_per_launch"] / (g["qmm_launch_ms"] * 1e-3) / 1e12
     res = {
@@ -255,14 +335,14 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "traffic": None,
-                     "kernel": "qmm_kernel (up: fused GELU epilogue, down: plain)",
+                     "traffic": read_traffic(),
+                     "kernel": "qmm_wide_kernel (up: fused GELU epilogue, down: plain)",
                      "launch_ms": {"up": round(g["up_ms"], 4), "down": round(g["down_ms"], 4)}},
     }
-    if not args.no_extras:
+    if not args.no_extras and args.only == "all":
         res["gemv"] = bench_gemv(mlxq, torch)
         res["quantize"] = bench_quantize(mlxq, torch)
-    if not args.no_cpu:
+    if not args.no_cpu and args.only == "all":
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(res))
 
