@@ -89,12 +89,20 @@ __device__ __forceinline__ bf16x8 dequant8(const uint32_t* w, int kk, float s, f
   return __builtin_bit_cast(bf16x8, o);
 }
 
+// Scale/bias element as raw bits.  The conversion to f32 happens one K step later (sb_to_f32 in
+// take_b): converting right after the load would make the loop wait for it at the end of the
+// step it was issued in.
 template <typename SB>
-__device__ __forceinline__ float load_sb(__amdgpu_buffer_rsrc_t r, uint32_t idx) {
+__device__ __forceinline__ uint32_t load_sb_bits(__amdgpu_buffer_rsrc_t r, uint32_t idx) {
   if constexpr (sizeof(SB) == 2)
-    return bf16_bits_to_f32((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, idx * 2u, 0, 0));
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, idx * 2u, 0, 0);
   else
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, idx * 4u, 0, 0));
+    return __builtin_amdgcn_raw_buffer_load_b32(r, idx * 4u, 0, 0);
+}
+template <typename SB>
+__device__ __forceinline__ float sb_to_f32(uint32_t bits) {
+  if constexpr (sizeof(SB) == 2) return bf16_bits_to_f32(bits & 0xffffu);
+  else return __uint_as_float(bits);
 }
 
 }  // namespace
@@ -168,7 +176,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     g_base[j] = (uint32_t)(nn * groups);
   }
   uint32_t braw[TNW][WPL];
-  float bs[TNW], bz[TNW];
+  uint32_t bs[TNW], bz[TNW];  // raw scale/bias bits
   auto load_b = [&](int kt) {
     const uint32_t g = (uint32_t)((kt * 64 + half * 32) / GS);
 #pragma unroll
@@ -180,8 +188,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) braw[j][4 * q + e] = v[e];
       }
-      bs[j] = load_sb<SB>(rs, g_base[j] + g);
-      bz[j] = load_sb<SB>(rz, g_base[j] + g);
+      bs[j] = load_sb_bits<SB>(rs, g_base[j] + g);
+      bz[j] = load_sb_bits<SB>(rz, g_base[j] + g);
     }
   };
 
@@ -211,9 +219,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     for (int j = 0; j < TNW; ++j) {
 #pragma unroll
       for (int e = 0; e < WPL; ++e) bcur[j][e] = braw[j][e];
-      scur[j] = bs[j];
-      s16cur[j] = bs[j] * 0.0625f;
-      zcur[j] = bz[j];
+      scur[j] = sb_to_f32<SB>(bs[j]);
+      s16cur[j] = scur[j] * 0.0625f;
+      zcur[j] = sb_to_f32<SB>(bz[j]);
     }
   };
   bf16x8 af[2][TMW], bfr[2][TNW];
