@@ -84,6 +84,18 @@ int mlxq_quantized_matmul(const void* x, int x_dtype, int64_t M, int64_t K, cons
                           const void* scales, const void* biases, int sb_dtype, int64_t N,
                           int transpose, int group_size, int bits, void* y, void* stream);
 
+/*
+ * Quantized token-embedding lookup — replaces TokenEmbedding::forward's quantized arm
+ * (src/nn.rs:42-58: take_axis of wq/scales/biases by ids, dequantize, cast to f32) in one pass.
+ * ids [T] int32 device array; table wq [vocab, hidden*bits/32] with scales/biases
+ * [vocab, hidden/group_size] in sb_dtype; out [T, hidden] in out_dtype (MLXQ_FLOAT32 reproduces
+ * the reference's cast).  Each value is dequantize()'s, i.e. rounded to sb_dtype first.  Ids
+ * outside [0, vocab) produce a row of NaN.
+ */
+int mlxq_embedding(const int32_t* ids, int64_t T, const uint32_t* wq, const void* scales,
+                   const void* biases, int sb_dtype, int64_t vocab, int64_t hidden, int group_size,
+                   int bits, void* out, int out_dtype, void* stream);
+
 /* Forced-kernel variants of quantized_matmul (same arguments, transpose implied = 1). */
 /* MFMA GEMM; x must be bf16; any M >= 1. */
 int mlxq_qmm(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,

@@ -127,6 +127,25 @@ int mlxq_dequantize(const uint32_t* wq, const void* scales, const void* biases, 
   return run_dequantize(wq, scales, biases, sb_dtype, N, K, group_size, bits, out, (hipStream_t)stream);
 }
 
+int mlxq_embedding(const int32_t* ids, int64_t T, const uint32_t* wq, const void* scales,
+                   const void* biases, int sb_dtype, int64_t vocab, int64_t hidden, int group_size,
+                   int bits, void* out, int out_dtype, void* stream) {
+  g_err[0] = 0;
+  int rc;
+  if ((rc = check_pack("embedding", vocab, hidden, group_size, bits))) return rc;
+  if ((rc = check_dtype("embedding", "scales", sb_dtype)) || (rc = check_dtype("embedding", "out", out_dtype)))
+    return rc;
+  if (T < 0) return set_error(MLXQ_EINVAL, "embedding: T=%lld < 0", (long long)T);
+  if (T == 0 || hidden == 0) return MLXQ_OK;
+  if (vocab == 0) return set_error(MLXQ_EINVAL, "embedding: empty table");
+  if ((rc = check_aligned("embedding", "ids", ids, 4)) || (rc = check_aligned("embedding", "wq", wq)) ||
+      (rc = check_aligned("embedding", "scales", scales, 4)) ||
+      (rc = check_aligned("embedding", "biases", biases, 4)) || (rc = check_aligned("embedding", "out", out)))
+    return rc;
+  return run_embedding(ids, T, wq, scales, biases, sb_dtype, vocab, hidden, group_size, bits, out,
+                       out_dtype, (hipStream_t)stream);
+}
+
 int mlxq_qmm(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
              const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
              int bits, void* y, void* stream) {

@@ -35,6 +35,9 @@ int run_qmm_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, const 
 bool qmv_mfma_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int64_t N, int gs, int bits);
 int run_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
                  int64_t N, int gs, int bits, void* y, hipStream_t st);
+int run_embedding(const int32_t* ids, int64_t T, const uint32_t* wq, const void* s, const void* b,
+                  int sb_dtype, int64_t vocab, int64_t hidden, int gs, int bits, void* out,
+                  int out_dtype, hipStream_t st);
 int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* A, const void* B,
                   int64_t N, int rank, int R, void* xa, void* lbt, hipStream_t st);
 int run_linear_epilogue(void* y, int x_dtype, int64_t M, int64_t N, const void* bias, const void* xa,

@@ -4,6 +4,8 @@
   Adapter           ~ src/adapters.rs:231-270 (LoRA arm; residual = scale * (x.A).B)
   AdaptableLinear   ~ src/adapters.rs:330-549 (dense / quantized base + adapter stack)
   quantize_map      ~ src/quant.rs:125-149 (offline converter primitive)
+  TokenEmbedding    ~ src/nn.rs:20-101 (dense or packed table; forward gathers + dequantizes)
+  lin / embedding   ~ src/quant.rs:49-90 (packed when `{base}.scales` is present, else dense)
 
 Only the quantized base runs on libmlxq_hip.so.  The dense base (before ``quantize``) is the
 reference's plain ``addmm``/``matmul`` and is evaluated with torch; it is not part of the
@@ -144,3 +146,73 @@ def quantize_map(tensors: Dict[str, torch.Tensor], bits: int, group_size: int,
         else:
             out[k] = v
     return out
+
+
+@dataclass
+class TokenEmbedding:
+    """Dense `[vocab, hidden]` table or a packed triple (src/nn.rs:20-101)."""
+    weight: Optional[torch.Tensor] = None   # dense table
+    wq: Optional[torch.Tensor] = None       # packed codes (int32 storage of uint32)
+    scales: Optional[torch.Tensor] = None
+    biases: Optional[torch.Tensor] = None
+    group_size: int = ops.DEFAULT_GROUP_SIZE
+    bits: int = 4
+
+    @classmethod
+    def dense(cls, weight: torch.Tensor):
+        return cls(weight=weight)
+
+    @classmethod
+    def from_quantized_parts(cls, wq, scales, biases, group_size: int, bits: int):
+        """src/nn.rs:60-81: adopt an already-packed table as is (no re-quantization)."""
+        return cls(wq=wq, scales=scales, biases=biases, group_size=group_size, bits=bits)
+
+    def is_quantized(self) -> bool:
+        return self.wq is not None
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        """src/nn.rs:42-58: rows of ids ([b, s] -> [b, s, hidden]), cast to f32."""
+        if self.wq is not None:
+            return ops.embedding(ids, self.wq, self.scales, self.biases, self.group_size, self.bits,
+                                 torch.float32)
+        return self.weight[ids.long()].to(torch.float32)
+
+    def quantize(self, bits: int, cast_to_bf16: bool) -> None:
+        """src/nn.rs:83-101: pack with group size 64 (bf16 first when cast_to_bf16); no-op if
+        already packed."""
+        if self.wq is not None:
+            return
+        w = self.weight.to(torch.bfloat16) if cast_to_bf16 else self.weight
+        self.wq, self.scales, self.biases = ops.quantize(w, 64, bits)
+        self.group_size, self.bits = 64, bits
+        self.weight = None
+
+
+def _require(w: Dict[str, torch.Tensor], key: str) -> torch.Tensor:
+    if key not in w:
+        raise KeyError(f"missing tensor {key!r}")  # Weights::require (reference src/weights.rs)
+    return w[key]
+
+
+def lin(w: Dict[str, torch.Tensor], base: str, bias: bool, group_size: int) -> AdaptableLinear:
+    """src/quant.rs:49-68: `{base}` as a packed AdaptableLinear when `{base}.scales` exists (bits
+    inferred by packed_bits), else dense; `bias` also loads the dense `{base}.bias`."""
+    b = _require(w, f"{base}.bias") if bias else None
+    scales = w.get(f"{base}.scales")
+    if scales is not None:
+        wq = _require(w, f"{base}.weight")
+        bits = ops.packed_bits(wq, scales, group_size)
+        return AdaptableLinear.from_quantized_parts(wq, scales, _require(w, f"{base}.biases"), b,
+                                                    group_size, bits)
+    return AdaptableLinear.dense(_require(w, f"{base}.weight"), b)
+
+
+def embedding(w: Dict[str, torch.Tensor], base: str, group_size: int) -> TokenEmbedding:
+    """src/quant.rs:70-90: the embedding analogue of lin."""
+    scales = w.get(f"{base}.scales")
+    if scales is not None:
+        wq = _require(w, f"{base}.weight")
+        bits = ops.packed_bits(wq, scales, group_size)
+        return TokenEmbedding.from_quantized_parts(wq, scales, _require(w, f"{base}.biases"),
+                                                   group_size, bits)
+    return TokenEmbedding.dense(_require(w, f"{base}.weight"))

@@ -118,6 +118,26 @@ def qmv(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int =
     return _mm("mlxq_qmv", x, wq, scales, biases, group_size, bits, out=out)
 
 
+def embedding(ids, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4,
+              out_dtype=torch.float32):
+    """TokenEmbedding::forward's quantized arm (src/nn.rs:42-58): gather the packed rows of ids
+    (any shape, int32/int64), dequantize, cast to out_dtype (f32 like the reference).  Ids outside
+    [0, vocab) give NaN rows."""
+    _need_gpu(ids, wq, scales, biases)
+    wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
+    flat = ids.reshape(-1).to(torch.int32).contiguous()
+    vocab = wq.shape[0]
+    hidden = _k_of(wq, bits)
+    out = torch.empty((flat.numel(), hidden), dtype=out_dtype, device=wq.device)
+    odt = MLXQ_BFLOAT16 if out_dtype == torch.bfloat16 else MLXQ_FLOAT32
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"embedding: out_dtype must be bfloat16 or float32, got {out_dtype}")
+    check(_lib.load().mlxq_embedding(_ptr(flat), flat.numel(), _ptr(wq), _ptr(scales), _ptr(biases),
+                                     _dt(scales), vocab, hidden, group_size, bits, _ptr(out), odt,
+                                     _stream(wq.device)))
+    return out.reshape(*ids.shape, hidden)
+
+
 def linear_workspace_size(M: int, N: int, rank: int) -> int:
     return int(_lib.load().mlxq_linear_workspace_size(M, N, rank))
 
