@@ -134,6 +134,24 @@ int mlxq_linear(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
                 size_t workspace_bytes, void* stream);
 
 /*
+ * One more LoRA adapter on an already computed output — the `out + adapter.residual(x)` step of
+ * AdaptableLinear::forward (src/adapters.rs:543-549, Adapter::residual :260-270) for adapter
+ * stacks beyond the one mlxq_linear fuses:
+ *   y = round(y + round(round(round(x.A).B) * scale))   (round() to x_dtype, y in x_dtype)
+ * A [K,rank], B [rank,N] in x_dtype, 1 <= rank <= 256; workspace as for mlxq_linear.
+ */
+int mlxq_lora_residual(const void* x, int x_dtype, int64_t M, int64_t K, const void* lora_a,
+                       const void* lora_b, int64_t N, int64_t rank, float lora_scale, void* y,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Element-wise dtype conversion f32 <-> bf16 (round to nearest even) — the `as_dtype(Bfloat16)`
+ * casts that precede packing in AdaptableLinear::quantize (src/adapters.rs:508-521) and
+ * quant::quantize_map (src/quant.rs:140).  src/dst 4-byte aligned.
+ */
+int mlxq_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream);
+
+/*
  * Host-side shape helper — replaces quant::packed_bits (src/quant.rs:38-41): from the packed
  * shapes infer bits = wq_cols*32 / (scales_cols*group_size).  Returns 4 or 8, or -1 (with
  * mlxq_last_error set) for a malformed triple instead of panicking.

@@ -86,4 +86,27 @@ int run_linear_epilogue(void* y, int x_dtype, int64_t M, int64_t N, const void* 
   return check_launch("linear_epilogue");
 }
 
+// dst[i] = src[i] converted between f32 and bf16 (round to nearest even) or copied.
+template <typename ST, typename DT>
+__global__ void cast_kernel(const ST* __restrict__ src, DT* __restrict__ dst, int64_t n) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < n) Act<DT>::st(dst, t, Act<ST>::ld(src, t));
+}
+
+int run_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, hipStream_t st) {
+  if (n == 0) return MLXQ_OK;
+  const int64_t blocks = (n + 255) / 256;
+  if (blocks > 0x7fffffff) return set_error(MLXQ_EINVAL, "cast: %lld elements is too many", (long long)n);
+  const dim3 g((unsigned)blocks), b(256);
+  if (src_dtype == MLXQ_BFLOAT16 && dst_dtype == MLXQ_BFLOAT16)
+    hipLaunchKernelGGL((cast_kernel<uint16_t, uint16_t>), g, b, 0, st, (const uint16_t*)src, (uint16_t*)dst, n);
+  else if (src_dtype == MLXQ_BFLOAT16)
+    hipLaunchKernelGGL((cast_kernel<uint16_t, float>), g, b, 0, st, (const uint16_t*)src, (float*)dst, n);
+  else if (dst_dtype == MLXQ_BFLOAT16)
+    hipLaunchKernelGGL((cast_kernel<float, uint16_t>), g, b, 0, st, (const float*)src, (uint16_t*)dst, n);
+  else
+    hipLaunchKernelGGL((cast_kernel<float, float>), g, b, 0, st, (const float*)src, (float*)dst, n);
+  return check_launch("cast");
+}
+
 }  // namespace mlxq

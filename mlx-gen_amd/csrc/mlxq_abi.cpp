@@ -198,6 +198,48 @@ size_t mlxq_linear_workspace_size(int64_t M, int64_t N, int64_t lora_rank) {
   return (size_t)(xa + N * R * 4);
 }
 
+int mlxq_lora_residual(const void* x, int x_dtype, int64_t M, int64_t K, const void* lora_a,
+                       const void* lora_b, int64_t N, int64_t rank, float lora_scale, void* y,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc;
+  if ((rc = check_dtype("lora_residual", "x", x_dtype))) return rc;
+  if (M < 0 || K <= 0 || N < 0) return set_error(MLXQ_EINVAL, "lora_residual: bad shape M=%lld K=%lld N=%lld",
+                                                  (long long)M, (long long)K, (long long)N);
+  if (rank < 1 || rank > 256)
+    return set_error(MLXQ_EINVAL, "lora_residual: rank %lld outside [1, 256]", (long long)rank);
+  if (M == 0 || N == 0) return MLXQ_OK;
+  if (!x || !lora_a || !lora_b || !y) return set_error(MLXQ_EINVAL, "lora_residual: null operand");
+  const size_t need = mlxq_linear_workspace_size(M, N, rank);
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error(MLXQ_EINVAL, "lora_residual: workspace of %zu bytes is smaller than the %zu required",
+                     workspace_bytes, need);
+  if ((rc = check_aligned("lora_residual", "workspace", workspace))) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const int R = (int)round16(rank);
+  void* xa = workspace;
+  void* lbt = (char*)workspace + (M * R * 4 + 255) / 256 * 256;
+  if ((rc = run_lora_prep(x, x_dtype, M, K, lora_a, lora_b, N, (int)rank, R, xa, lbt, st))) return rc;
+  float scale = lora_scale;
+  if (x_dtype == MLXQ_BFLOAT16) {
+    uint32_t u;
+    memcpy(&u, &scale, 4);
+    u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+    memcpy(&scale, &u, 4);
+  }
+  return run_linear_epilogue(y, x_dtype, M, N, nullptr, xa, lbt, R, scale, MLXQ_ACT_NONE, st);
+}
+
+int mlxq_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream) {
+  g_err[0] = 0;
+  int rc;
+  if ((rc = check_dtype("cast", "src", src_dtype)) || (rc = check_dtype("cast", "dst", dst_dtype))) return rc;
+  if (n < 0) return set_error(MLXQ_EINVAL, "cast: n=%lld < 0", (long long)n);
+  if (n == 0) return MLXQ_OK;
+  if ((rc = check_aligned("cast", "src", src, 4)) || (rc = check_aligned("cast", "dst", dst, 4))) return rc;
+  return run_cast(src, src_dtype, dst, dst_dtype, n, (hipStream_t)stream);
+}
+
 int mlxq_linear(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
                 const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
                 int bits, const mlxq_epilogue* ep, void* y, void* workspace, size_t workspace_bytes,

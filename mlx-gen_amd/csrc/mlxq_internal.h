@@ -40,6 +40,7 @@ int run_embedding(const int32_t* ids, int64_t T, const uint32_t* wq, const void*
                   int out_dtype, hipStream_t st);
 int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* A, const void* B,
                   int64_t N, int rank, int R, void* xa, void* lbt, hipStream_t st);
+int run_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, hipStream_t st);
 int run_linear_epilogue(void* y, int x_dtype, int64_t M, int64_t N, const void* bias, const void* xa,
                         const void* lbt, int R, float lora_scale, int act, hipStream_t st);
 

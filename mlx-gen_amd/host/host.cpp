@@ -1,0 +1,366 @@
+// host.cpp — Array, the op triple and the layer types of the C++ host API (see mlxq.hpp).
+// Every computation goes through the C ABI of libmlxq_hip.so; this file only allocates device
+// memory, checks shapes the way the reference's callers rely on, and sequences ABI calls.
+#include "mlxq.hpp"
+
+#include <cstring>
+
+#include "../../include/mlxq.h"
+
+namespace mlxq {
+
+namespace {
+
+void check(int status) {
+  if (status != MLXQ_OK) throw Error(status, mlxq_last_error());
+}
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw Error(MLXQ_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int abi_dtype(Dtype dt, const char* op) {
+  if (dt == Dtype::Float32) return MLXQ_FLOAT32;
+  if (dt == Dtype::Bfloat16) return MLXQ_BFLOAT16;
+  throw Error(MLXQ_EINVAL, std::string(op) + ": expected a float32 or bfloat16 array, got " + dtype_name(dt));
+}
+
+void need_packed(const Array& wq, const char* op) {
+  if (wq.dtype() != Dtype::Uint32 && wq.dtype() != Dtype::Int32)
+    throw Error(MLXQ_EINVAL, std::string(op) + ": packed weights must be uint32");
+  if (wq.ndim() != 2) throw Error(MLXQ_EINVAL, std::string(op) + ": packed weights must be 2-D");
+}
+
+// Workspace for mlxq_linear / mlxq_lora_residual (nullptr-free empty array when none is needed).
+Array workspace(int64_t M, int64_t N, int64_t rank) {
+  const size_t need = mlxq_linear_workspace_size(M, N, rank);
+  return Array::empty({(int64_t)((need + 3) / 4)}, Dtype::Uint32);
+}
+
+}  // namespace
+
+size_t dtype_size(Dtype dt) {
+  switch (dt) {
+    case Dtype::Float32: case Dtype::Uint32: case Dtype::Int32: return 4;
+    case Dtype::Bfloat16: case Dtype::Float16: return 2;
+    case Dtype::Int64: case Dtype::Float64: return 8;
+    case Dtype::Uint8: case Dtype::Int8: case Dtype::Bool: return 1;
+  }
+  return 0;
+}
+
+const char* dtype_name(Dtype dt) {
+  switch (dt) {
+    case Dtype::Float32: return "F32";
+    case Dtype::Bfloat16: return "BF16";
+    case Dtype::Uint32: return "U32";
+    case Dtype::Int32: return "I32";
+    case Dtype::Float16: return "F16";
+    case Dtype::Int64: return "I64";
+    case Dtype::Uint8: return "U8";
+    case Dtype::Int8: return "I8";
+    case Dtype::Float64: return "F64";
+    case Dtype::Bool: return "BOOL";
+  }
+  return "?";
+}
+
+Dtype dtype_from_name(const std::string& n) {
+  static const std::pair<const char*, Dtype> table[] = {
+      {"F32", Dtype::Float32}, {"BF16", Dtype::Bfloat16}, {"U32", Dtype::Uint32},
+      {"I32", Dtype::Int32},   {"F16", Dtype::Float16},   {"I64", Dtype::Int64},
+      {"U8", Dtype::Uint8},    {"I8", Dtype::Int8},       {"F64", Dtype::Float64},
+      {"BOOL", Dtype::Bool}};
+  for (const auto& e : table)
+    if (n == e.first) return e.second;
+  throw Error(MLXQ_EUNSUPPORTED, "unsupported tensor dtype " + n);
+}
+
+// ---- Array ------------------------------------------------------------------------------------
+
+int64_t Array::size() const {
+  int64_t n = 1;
+  for (int64_t d : shape_) n *= d;
+  return n;
+}
+
+Array Array::empty(std::vector<int64_t> shape, Dtype dt) {
+  Array a;
+  a.shape_ = std::move(shape);
+  a.dtype_ = dt;
+  for (int64_t d : a.shape_)
+    if (d < 0) throw Error(MLXQ_EINVAL, "Array: negative dimension");
+  if (a.nbytes() > 0) {
+    void* p = nullptr;
+    hip_check(hipMalloc(&p, a.nbytes()), "hipMalloc");
+    a.buf_ = std::shared_ptr<void>(p, [](void* q) { (void)hipFree(q); });
+    a.ptr_ = p;
+  }
+  return a;
+}
+
+Array Array::from_host(const void* data, std::vector<int64_t> shape, Dtype dt) {
+  Array a = empty(std::move(shape), dt);
+  if (a.nbytes() > 0) hip_check(hipMemcpy(a.ptr_, data, a.nbytes(), hipMemcpyHostToDevice), "hipMemcpy");
+  return a;
+}
+
+Array Array::borrow(void* device_ptr, std::vector<int64_t> shape, Dtype dt) {
+  Array a;
+  a.shape_ = std::move(shape);
+  a.dtype_ = dt;
+  a.ptr_ = device_ptr;
+  return a;
+}
+
+void Array::to_host(void* dst) const {
+  if (nbytes() == 0) return;
+  hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  hip_check(hipMemcpy(dst, ptr_, nbytes(), hipMemcpyDeviceToHost), "hipMemcpy");
+}
+
+Array Array::reshape(std::vector<int64_t> shape) const {
+  Array a = *this;
+  a.shape_ = std::move(shape);
+  if (a.size() != size()) throw Error(MLXQ_EINVAL, "reshape: element count changes");
+  return a;
+}
+
+// ---- ops --------------------------------------------------------------------------------------
+
+Array as_dtype(const Array& a, Dtype dt, hipStream_t s) {
+  if (a.dtype() == dt) return a;
+  const int src = abi_dtype(a.dtype(), "as_dtype"), dst = abi_dtype(dt, "as_dtype");
+  Array out = Array::empty(a.shape(), dt);
+  check(mlxq_cast(a.data(), src, out.data(), dst, a.size(), s));
+  return out;
+}
+
+Packed quantize(const Array& w, int group_size, int bits, hipStream_t s) {
+  if (w.ndim() != 2) throw Error(MLXQ_EINVAL, "quantize: expected a 2-D weight");
+  const int dt = abi_dtype(w.dtype(), "quantize");
+  const int64_t N = w.dim(0), K = w.dim(1);
+  const int64_t gcols = group_size > 0 ? K / group_size : 0;
+  Packed p{Array::empty({N, bits > 0 ? K * bits / 32 : 0}, Dtype::Uint32),
+           Array::empty({N, gcols}, w.dtype()), Array::empty({N, gcols}, w.dtype())};
+  check(mlxq_quantize(w.data(), dt, N, K, group_size, bits, (uint32_t*)p.wq.data(), p.scales.data(),
+                      p.biases.data(), s));
+  return p;
+}
+
+Array dequantize(const Array& wq, const Array& scales, const Array& biases, int group_size, int bits,
+                 hipStream_t s) {
+  need_packed(wq, "dequantize");
+  if (bits <= 0) throw Error(MLXQ_EINVAL, "dequantize: bits must be 4 or 8");
+  const int64_t N = wq.dim(0), K = wq.dim(1) * 32 / bits;
+  Array out = Array::empty({N, K}, scales.dtype());
+  check(mlxq_dequantize((const uint32_t*)wq.data(), scales.data(), biases.data(),
+                        abi_dtype(scales.dtype(), "dequantize"), N, K, group_size, bits, out.data(), s));
+  return out;
+}
+
+Array quantized_matmul(const Array& x, const Array& wq, const Array& scales, const Array& biases,
+                       bool transpose, int group_size, int bits, hipStream_t s) {
+  need_packed(wq, "quantized_matmul");
+  if (x.ndim() < 1) throw Error(MLXQ_EINVAL, "quantized_matmul: x must have a last dimension");
+  const int64_t K = x.dim(-1), N = wq.dim(0), M = K > 0 ? x.size() / K : 0;
+  std::vector<int64_t> shape = x.shape();
+  shape.back() = N;
+  Array y = Array::empty(shape, x.dtype());
+  check(mlxq_quantized_matmul(x.data(), abi_dtype(x.dtype(), "quantized_matmul"), M, K,
+                              (const uint32_t*)wq.data(), scales.data(), biases.data(),
+                              abi_dtype(scales.dtype(), "quantized_matmul"), N, transpose ? 1 : 0,
+                              group_size, bits, y.data(), s));
+  return y;
+}
+
+int packed_bits(const Array& wq, const Array& scales, int group_size) {
+  if (wq.ndim() != 2 || scales.ndim() != 2) throw Error(MLXQ_EINVAL, "packed_bits: expected 2-D arrays");
+  const int b = mlxq_packed_bits(wq.dim(1), scales.dim(1), group_size);
+  if (b < 0) throw Error(MLXQ_EINVAL, mlxq_last_error());
+  return b;
+}
+
+// ---- layers -----------------------------------------------------------------------------------
+
+QuantizedLinear QuantizedLinear::try_from_linear(const Array& weight, std::optional<Array> bias,
+                                                 int group_size, int bits, hipStream_t s) {
+  Packed p = quantize(weight, group_size, bits, s);
+  return QuantizedLinear{p.wq, p.scales, p.biases, std::move(bias), group_size, bits};
+}
+
+Array QuantizedLinear::forward(const Array& x, hipStream_t s) const {
+  if (!bias) return quantized_matmul(x, weight, scales, biases, true, group_size, bits, s);
+  // src/adapters.rs:309-320: quantized_matmul, then the dense bias as a separate, rounded add.
+  const Array b = as_dtype(*bias, x.dtype(), s);
+  const int64_t K = x.dim(-1), N = weight.dim(0), M = K > 0 ? x.size() / K : 0;
+  std::vector<int64_t> shape = x.shape();
+  shape.back() = N;
+  Array y = Array::empty(shape, x.dtype());
+  mlxq_epilogue e = {b.data(), nullptr, nullptr, 0, 1.0f, MLXQ_ACT_NONE};
+  check(mlxq_linear(x.data(), abi_dtype(x.dtype(), "linear"), M, K, (const uint32_t*)weight.data(),
+                    scales.data(), biases.data(), abi_dtype(scales.dtype(), "linear"), N, group_size,
+                    bits, &e, y.data(), nullptr, 0, s));
+  return y;
+}
+
+AdaptableLinear AdaptableLinear::dense(Array weight, std::optional<Array> bias) {
+  AdaptableLinear l;
+  l.dense_weight_ = std::move(weight);
+  l.dense_bias_ = std::move(bias);
+  return l;
+}
+
+AdaptableLinear AdaptableLinear::from_quantized_parts(Array weight, Array scales, Array biases,
+                                                      std::optional<Array> bias, int group_size,
+                                                      int bits) {
+  AdaptableLinear l;
+  l.quantized_ = QuantizedLinear{std::move(weight), std::move(scales), std::move(biases), std::move(bias),
+                                 group_size, bits};
+  return l;
+}
+
+std::array<int64_t, 2> AdaptableLinear::base_shape() const {
+  if (quantized_) return {quantized_->scales.dim(0), quantized_->in_features()};
+  return {dense_weight_->dim(0), dense_weight_->dim(1)};
+}
+
+void AdaptableLinear::quantize(int bits, std::optional<int> group_size, hipStream_t s) {
+  if (quantized_) return;
+  const Array w = as_dtype(*dense_weight_, Dtype::Bfloat16, s);
+  std::optional<Array> b;
+  if (dense_bias_) b = as_dtype(*dense_bias_, Dtype::Bfloat16, s);
+  quantized_ = QuantizedLinear::try_from_linear(w, b, group_size.value_or(64), bits, s);
+  dense_weight_.reset();
+  dense_bias_.reset();
+}
+
+Array AdaptableLinear::forward(const Array& x, hipStream_t s) const {
+  if (!quantized_)
+    throw Error(MLXQ_EUNSUPPORTED,
+                "AdaptableLinear: the dense base is not on the quantized path; call quantize() first");
+  const QuantizedLinear& q = *quantized_;
+  if (adapters_.empty()) return q.forward(x, s);
+  const int xdt = abi_dtype(x.dtype(), "AdaptableLinear::forward");
+  const int64_t K = x.dim(-1), N = q.weight.dim(0), M = K > 0 ? x.size() / K : 0;
+  std::vector<int64_t> shape = x.shape();
+  shape.back() = N;
+  Array y = Array::empty(shape, x.dtype());
+  std::optional<Array> b;
+  if (q.bias) b = as_dtype(*q.bias, x.dtype(), s);
+  // The first adapter rides in mlxq_linear's epilogue, later ones are added one at a time with
+  // the same rounding points (out = out + residual, src/adapters.rs:545-547).
+  for (size_t i = 0; i < adapters_.size(); ++i) {
+    const Adapter& ad = adapters_[i];
+    const int64_t rank = ad.a.dim(1);
+    if (rank > 256) throw Error(MLXQ_EUNSUPPORTED, "AdaptableLinear: LoRA rank above 256");
+    const Array A = as_dtype(ad.a, x.dtype(), s), B = as_dtype(ad.b, x.dtype(), s);
+    Array ws = workspace(M, N, rank);
+    if (i == 0) {
+      mlxq_epilogue e = {b ? b->data() : nullptr, A.data(), B.data(), rank, ad.scale, MLXQ_ACT_NONE};
+      check(mlxq_linear(x.data(), xdt, M, K, (const uint32_t*)q.weight.data(), q.scales.data(),
+                        q.biases.data(), abi_dtype(q.scales.dtype(), "linear"), N, q.group_size,
+                        q.bits, &e, y.data(), ws.data(), ws.nbytes(), s));
+    } else {
+      check(mlxq_lora_residual(x.data(), xdt, M, K, A.data(), B.data(), N, rank, ad.scale, y.data(),
+                               ws.data(), ws.nbytes(), s));
+    }
+    // The workspace must outlive the kernels that read it.
+    hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+  }
+  return y;
+}
+
+TokenEmbedding TokenEmbedding::dense(Array weight) {
+  TokenEmbedding e;
+  e.dense_ = std::move(weight);
+  return e;
+}
+
+TokenEmbedding TokenEmbedding::from_quantized_parts(Array wq, Array scales, Array biases,
+                                                    int group_size, int bits) {
+  TokenEmbedding e;
+  e.packed_ = Packed{std::move(wq), std::move(scales), std::move(biases)};
+  e.group_size_ = group_size;
+  e.bits_ = bits;
+  return e;
+}
+
+Array TokenEmbedding::forward(const Array& ids, hipStream_t s) const {
+  if (!packed_)
+    throw Error(MLXQ_EUNSUPPORTED, "TokenEmbedding: the dense table is not on the quantized path");
+  if (ids.dtype() != Dtype::Int32) throw Error(MLXQ_EINVAL, "TokenEmbedding: ids must be int32");
+  const Packed& p = *packed_;
+  const int64_t vocab = p.wq.dim(0), hidden = p.wq.dim(1) * 32 / bits_;
+  std::vector<int64_t> shape = ids.shape();
+  shape.push_back(hidden);
+  Array out = Array::empty(shape, Dtype::Float32);
+  check(mlxq_embedding((const int32_t*)ids.data(), ids.size(), (const uint32_t*)p.wq.data(),
+                       p.scales.data(), p.biases.data(), abi_dtype(p.scales.dtype(), "embedding"),
+                       vocab, hidden, group_size_, bits_, out.data(), MLXQ_FLOAT32, s));
+  return out;
+}
+
+void TokenEmbedding::quantize(int bits, bool cast_to_bf16, hipStream_t s) {
+  if (packed_) return;
+  const Array w = cast_to_bf16 ? as_dtype(*dense_, Dtype::Bfloat16, s) : *dense_;
+  packed_ = mlxq::quantize(w, 64, bits, s);
+  group_size_ = 64;
+  bits_ = bits;
+  dense_.reset();
+}
+
+// ---- quant.rs ---------------------------------------------------------------------------------
+
+const Array& require(const Weights& w, const std::string& key) {
+  auto it = w.find(key);
+  if (it == w.end()) throw Error(MLXQ_EINVAL, "missing tensor " + key);
+  return it->second;
+}
+
+AdaptableLinear lin(const Weights& w, const std::string& base, bool bias, int group_size) {
+  std::optional<Array> b;
+  if (bias) b = require(w, base + ".bias");
+  auto sc = w.find(base + ".scales");
+  if (sc != w.end()) {
+    const Array& wq = require(w, base + ".weight");
+    const int bits = packed_bits(wq, sc->second, group_size);
+    return AdaptableLinear::from_quantized_parts(wq, sc->second, require(w, base + ".biases"), b,
+                                                 group_size, bits);
+  }
+  return AdaptableLinear::dense(require(w, base + ".weight"), b);
+}
+
+TokenEmbedding embedding(const Weights& w, const std::string& base, int group_size) {
+  auto sc = w.find(base + ".scales");
+  if (sc != w.end()) {
+    const Array& wq = require(w, base + ".weight");
+    const int bits = packed_bits(wq, sc->second, group_size);
+    return TokenEmbedding::from_quantized_parts(wq, sc->second, require(w, base + ".biases"),
+                                                group_size, bits);
+  }
+  return TokenEmbedding::dense(require(w, base + ".weight"));
+}
+
+Weights quantize_map(const Weights& map, int bits, int group_size,
+                     const std::function<bool(const std::string&)>& is_target, hipStream_t s) {
+  static const std::string suffix = ".weight";
+  Weights out;
+  for (const auto& [k, v] : map) {
+    const bool is_weight = k.size() > suffix.size() && k.compare(k.size() - suffix.size(), suffix.size(), suffix) == 0;
+    const std::string base = is_weight ? k.substr(0, k.size() - suffix.size()) : std::string();
+    const bool packable = is_weight && is_target(base) && v.ndim() == 2 &&
+                          group_size > 0 && v.dim(1) % group_size == 0 && v.dim(1) >= group_size;
+    if (packable) {
+      Packed p = quantize(as_dtype(v, Dtype::Bfloat16, s), group_size, bits, s);
+      out[base + ".weight"] = p.wq;
+      out[base + ".scales"] = p.scales;
+      out[base + ".biases"] = p.biases;
+    } else {
+      out[k] = v;
+    }
+  }
+  return out;
+}
+
+}  // namespace mlxq

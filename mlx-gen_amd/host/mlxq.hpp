@@ -1,0 +1,175 @@
+// mlxq.hpp — C++ host API of the MI355X quantized-linear path, layered on the C ABI of
+// libmlxq_hip.so (include/mlxq.h).
+//
+// It mirrors the reference's Rust surface for this path with the same names, argument meanings
+// and error behaviour, so a caller ports line for line:
+//   mlx_rs::ops::{quantize, dequantize, quantized_matmul}  (src/quant.rs:140, src/nn.rs:55,
+//                                                           src/adapters.rs:309-317)
+//   quant::{packed_bits, lin, embedding, load_dir_map, save_map, quantize_map}
+//                                                          (src/quant.rs:38-149)
+//   nn::QuantizedLinear, adapters::{Adapter, AdaptableLinear} (src/adapters.rs:231-549)
+//   nn::TokenEmbedding                                     (src/nn.rs:20-101)
+//   convert::write_quantized_config                        (mlx-gen-flux/src/convert.rs:46-63)
+// Errors are thrown as mlxq::Error (the reference returns Result<_, Error>); a status code and
+// the library's message travel with it.  Arrays are ref-counted device buffers: copying an Array
+// copies the handle, as cloning an mlx_rs::Array does (src/quant.rs:92-94).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <array>
+#include <cstdint>
+#include <functional>
+#include <map>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace mlxq {
+
+// The first two values are the C ABI's mlxq_dtype; the others are storage types the loaders carry.
+enum class Dtype : int {
+  Float32 = 0, Bfloat16 = 1, Uint32 = 2, Int32 = 3, Float16 = 4, Int64 = 5, Uint8 = 6, Int8 = 7,
+  Float64 = 8, Bool = 9
+};
+size_t dtype_size(Dtype dt);
+const char* dtype_name(Dtype dt);       // safetensors spelling: F32, BF16, U32, I32, ...
+Dtype dtype_from_name(const std::string& name);  // throws on an unknown spelling
+
+class Error : public std::runtime_error {
+ public:
+  Error(int status, const std::string& msg) : std::runtime_error(msg), status(status) {}
+  int status;  // mlxq_status
+};
+
+// Device array: shared ownership of a HIP allocation (or a borrowed pointer), row-major.
+class Array {
+ public:
+  Array() = default;
+  static Array empty(std::vector<int64_t> shape, Dtype dt);
+  static Array from_host(const void* data, std::vector<int64_t> shape, Dtype dt);
+  // Wraps memory owned elsewhere (e.g. a framework tensor); the caller keeps it alive.
+  static Array borrow(void* device_ptr, std::vector<int64_t> shape, Dtype dt);
+
+  void to_host(void* dst) const;  // synchronous device-to-host copy of nbytes()
+  Array reshape(std::vector<int64_t> shape) const;  // same buffer, new shape (same size)
+
+  bool valid() const { return ptr_ != nullptr || size() == 0; }
+  void* data() const { return ptr_; }
+  const std::vector<int64_t>& shape() const { return shape_; }
+  int ndim() const { return (int)shape_.size(); }
+  int64_t dim(int i) const { return shape_.at(i < 0 ? shape_.size() + i : i); }
+  int64_t size() const;
+  size_t nbytes() const { return (size_t)size() * dtype_size(dtype_); }
+  Dtype dtype() const { return dtype_; }
+
+ private:
+  std::shared_ptr<void> buf_;
+  void* ptr_ = nullptr;
+  std::vector<int64_t> shape_;
+  Dtype dtype_ = Dtype::Float32;
+};
+
+// ---- ops (mlx_rs::ops) ----------------------------------------------------------------------
+struct Packed {
+  Array wq, scales, biases;
+};
+// `as_dtype` between f32 and bf16 (round to nearest even); returns `a` itself when equal.
+Array as_dtype(const Array& a, Dtype dt, hipStream_t s = nullptr);
+Packed quantize(const Array& w, int group_size, int bits, hipStream_t s = nullptr);
+Array dequantize(const Array& wq, const Array& scales, const Array& biases, int group_size, int bits,
+                 hipStream_t s = nullptr);
+// x [..., K] -> [..., N]; only transpose = true exists in the reference and here.
+Array quantized_matmul(const Array& x, const Array& wq, const Array& scales, const Array& biases,
+                       bool transpose, int group_size, int bits, hipStream_t s = nullptr);
+int packed_bits(const Array& wq, const Array& scales, int group_size);
+
+// ---- layers ---------------------------------------------------------------------------------
+// LoRA adapter: residual = scale * (x.A).B with A [in, r], B [r, out] (alpha/rank folded in B,
+// src/adapters/loader.rs:568-599).
+struct Adapter {
+  Array a, b;
+  float scale = 1.0f;
+};
+
+struct QuantizedLinear {
+  Array weight, scales, biases;  // packed triple (weight in U32)
+  std::optional<Array> bias;     // dense bias
+  int group_size = 64;
+  int bits = 4;
+
+  static QuantizedLinear try_from_linear(const Array& weight, std::optional<Array> bias,
+                                         int group_size, int bits, hipStream_t s = nullptr);
+  Array forward(const Array& x, hipStream_t s = nullptr) const;
+  int64_t in_features() const { return scales.dim(1) * group_size; }
+};
+
+class AdaptableLinear {
+ public:
+  static AdaptableLinear dense(Array weight, std::optional<Array> bias);
+  static AdaptableLinear from_quantized_parts(Array weight, Array scales, Array biases,
+                                              std::optional<Array> bias, int group_size, int bits);
+  void push(Adapter a) { adapters_.push_back(std::move(a)); }
+  void set_adapters(std::vector<Adapter> a) { adapters_ = std::move(a); }
+  const std::vector<Adapter>& adapters() const { return adapters_; }
+  bool is_quantized() const { return quantized_.has_value(); }
+  const QuantizedLinear& quantized() const { return quantized_.value(); }
+  std::array<int64_t, 2> base_shape() const;
+  // src/adapters.rs:508-541: cast weight and bias to bf16, then pack; no-op when packed.
+  void quantize(int bits, std::optional<int> group_size, hipStream_t s = nullptr);
+  // src/adapters.rs:300-322,543-549: base(x) (+ bias) + sum of adapter residuals, every step
+  // rounded to the activation dtype.  The dense base is not on this library's path and throws.
+  Array forward(const Array& x, hipStream_t s = nullptr) const;
+
+ private:
+  std::optional<Array> dense_weight_, dense_bias_;
+  std::optional<QuantizedLinear> quantized_;
+  std::vector<Adapter> adapters_;
+};
+
+class TokenEmbedding {
+ public:
+  static TokenEmbedding dense(Array weight);
+  static TokenEmbedding from_quantized_parts(Array wq, Array scales, Array biases, int group_size,
+                                             int bits);
+  bool is_quantized() const { return packed_.has_value(); }
+  int group_size() const { return group_size_; }
+  int bits() const { return bits_; }
+  const Packed& packed() const { return packed_.value(); }
+  // ids (int32, any shape) -> [..., hidden] f32.  Only the packed table runs here.
+  Array forward(const Array& ids, hipStream_t s = nullptr) const;
+  // Pack with group size 64 (bf16 first when cast_to_bf16); no-op when packed.
+  void quantize(int bits, bool cast_to_bf16, hipStream_t s = nullptr);
+
+ private:
+  std::optional<Array> dense_;
+  std::optional<Packed> packed_;
+  int group_size_ = 64, bits_ = 4;
+};
+
+// ---- quant.rs --------------------------------------------------------------------------------
+using Weights = std::map<std::string, Array>;
+const Array& require(const Weights& w, const std::string& key);  // throws on a missing key
+AdaptableLinear lin(const Weights& w, const std::string& base, bool bias, int group_size);
+TokenEmbedding embedding(const Weights& w, const std::string& base, int group_size);
+Weights quantize_map(const Weights& map, int bits, int group_size,
+                     const std::function<bool(const std::string&)>& is_target,
+                     hipStream_t s = nullptr);
+
+// ---- snapshot I/O ----------------------------------------------------------------------------
+struct HostTensor {
+  Dtype dtype = Dtype::Float32;
+  std::vector<int64_t> shape;
+  std::vector<uint8_t> data;
+};
+using HostMap = std::map<std::string, HostTensor>;
+HostMap read_safetensors(const std::string& path);
+void write_safetensors(const std::string& path, const HostMap& tensors);
+Weights load_dir_map(const std::string& dir);                 // every *.safetensors in dir
+void save_map(const std::string& path, const Weights& map);   // one file
+void write_quantized_config(const std::string& src_dir, const std::string& dst_dir, int bits,
+                            int group_size);
+
+}  // namespace mlxq

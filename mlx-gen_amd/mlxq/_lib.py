@@ -35,6 +35,8 @@ EXPORTS = (
     "mlxq_linear",
     "mlxq_packed_bits",
     "mlxq_embedding",
+    "mlxq_lora_residual",
+    "mlxq_cast",
 )
 
 
@@ -88,10 +90,14 @@ def load():
     lib.mlxq_linear.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _vp, _int, _i64, _int, _int,
                                 ctypes.POINTER(Epilogue), _vp, _vp, ctypes.c_size_t, _vp]
     lib.mlxq_packed_bits.argtypes = [_i64, _i64, _int]
+    lib.mlxq_lora_residual.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _i64, _i64, ctypes.c_float,
+                                       _vp, _vp, ctypes.c_size_t, _vp]
+    lib.mlxq_cast.argtypes = [_vp, _int, _vp, _int, _i64, _vp]
     lib.mlxq_embedding.argtypes = [_vp, _i64, _vp, _vp, _vp, _int, _i64, _i64, _int, _int, _vp, _int,
                                    _vp]
     for name in ("mlxq_quantize", "mlxq_dequantize", "mlxq_quantized_matmul", "mlxq_qmm",
-                 "mlxq_qmv", "mlxq_linear", "mlxq_packed_bits"):
+                 "mlxq_qmv", "mlxq_linear", "mlxq_packed_bits", "mlxq_embedding",
+                 "mlxq_lora_residual", "mlxq_cast"):
         getattr(lib, name).restype = _int
     _lib = lib
     return lib

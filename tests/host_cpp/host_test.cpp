@@ -1,0 +1,355 @@
+// host_test.cpp — tests of the C++ host API (mlx-gen_amd/host/mlxq.hpp), run by pytest.
+//
+//   host_test cpu   file formats and host logic only (no device work)
+//   host_test gpu   the API end to end on the GPU, checked against the reference's golden fixture
+//                   (tests/golden/quant_q4q8.safetensors, read through the API's own reader) and
+//                   the CPU oracle (oracle/liboracle.so; test infrastructure, linked here only)
+//
+// Mirrors the reference's tests/quant_parity.rs (packing bit-exact, dequantize bit-exact,
+// quantized_matmul within tolerance) and adds the layer and loader seams of src/adapters.rs,
+// src/nn.rs and src/quant.rs.  Prints one line per case and exits non-zero on the first failure.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <filesystem>
+#include <fstream>
+#include <random>
+#include <string>
+#include <vector>
+
+#include <unistd.h>
+
+#include "../../mlx-gen_amd/host/mlxq.hpp"
+
+extern "C" {
+float oracle_bf16_round(float x);
+int oracle_quantize(const float* w, int64_t N, int64_t K, int gs, int bits, int sb_bf16, uint32_t* wq,
+                    float* scales, float* biases);
+int oracle_dequantize(const uint32_t* wq, const float* scales, const float* biases, int64_t N, int64_t K,
+                      int gs, int bits, int out_bf16, float* out);
+int oracle_qmm(const float* x, int64_t M, int64_t K, const uint32_t* wq, const float* scales,
+               const float* biases, int64_t N, int gs, int bits, int w_bf16, int out_bf16, float* y);
+int oracle_linear(const float* x, int64_t M, int64_t K, const uint32_t* wq, const float* scales,
+                  const float* biases, int64_t N, int gs, int bits, int w_bf16, int act_bf16,
+                  const float* bias, const float* lora_a, const float* lora_b, int64_t rank,
+                  float lora_scale, int act, float* y);
+}
+
+namespace fs = std::filesystem;
+using namespace mlxq;
+
+static int g_failures = 0;
+#define EXPECT(cond, ...)                                            \
+  do {                                                               \
+    if (!(cond)) {                                                   \
+      fprintf(stderr, "FAIL %s:%d: %s: ", __FILE__, __LINE__, #cond); \
+      fprintf(stderr, __VA_ARGS__);                                  \
+      fprintf(stderr, "\n");                                         \
+      ++g_failures;                                                  \
+    }                                                                \
+  } while (0)
+
+static void banner(const char* name) {
+  printf("[case] %s\n", name);
+  fflush(stdout);
+}
+
+// ---- host-side helpers ---------------------------------------------------------------------------
+static std::vector<float> bf16_normal(std::mt19937& rng, size_t n, float std_) {
+  std::normal_distribution<float> d(0.0f, std_);
+  std::vector<float> v(n);
+  for (auto& x : v) x = oracle_bf16_round(d(rng));
+  return v;
+}
+static std::vector<uint16_t> to_bf16_bits(const std::vector<float>& v) {
+  std::vector<uint16_t> o(v.size());
+  for (size_t i = 0; i < v.size(); ++i) {
+    uint32_t u;
+    memcpy(&u, &v[i], 4);
+    o[i] = (uint16_t)(u >> 16);  // values are already bf16-exact
+  }
+  return o;
+}
+static std::vector<float> from_bf16_bits(const uint16_t* p, size_t n) {
+  std::vector<float> o(n);
+  for (size_t i = 0; i < n; ++i) {
+    uint32_t u = (uint32_t)p[i] << 16;
+    memcpy(&o[i], &u, 4);
+  }
+  return o;
+}
+template <typename T>
+static std::vector<T> host(const Array& a) {
+  std::vector<T> v(a.nbytes() / sizeof(T));
+  a.to_host(v.data());
+  return v;
+}
+static std::vector<float> host_f32(const Array& a) {
+  if (a.dtype() == Dtype::Bfloat16) {
+    auto b = host<uint16_t>(a);
+    return from_bf16_bits(b.data(), b.size());
+  }
+  return host<float>(a);
+}
+static Array bf16_array(const std::vector<float>& v, std::vector<int64_t> shape) {
+  auto b = to_bf16_bits(v);
+  return Array::from_host(b.data(), shape, Dtype::Bfloat16);
+}
+static double rel_fro(const std::vector<float>& y, const std::vector<float>& r) {
+  double num = 0, den = 0;
+  for (size_t i = 0; i < y.size(); ++i) {
+    num += ((double)y[i] - r[i]) * ((double)y[i] - r[i]);
+    den += (double)r[i] * r[i];
+  }
+  return std::sqrt(num / std::max(den, 1e-300));
+}
+static fs::path repo_root(const char* argv0) {
+  return fs::absolute(fs::path(argv0)).parent_path().parent_path().parent_path();
+}
+
+// ---- CPU cases -------------------------------------------------------------------------------------
+static void cpu_cases(const fs::path& root) {
+  const fs::path tmp = fs::temp_directory_path() / ("mlxq_host_test_" + std::to_string(::getpid()));
+  fs::create_directories(tmp);
+
+  banner("safetensors round trip, every dtype");
+  {
+    HostMap m;
+    const Dtype dts[] = {Dtype::Float32, Dtype::Bfloat16, Dtype::Uint32, Dtype::Int32, Dtype::Float16,
+                         Dtype::Int64, Dtype::Uint8, Dtype::Int8, Dtype::Float64, Dtype::Bool};
+    int k = 0;
+    for (Dtype dt : dts) {
+      HostTensor t;
+      t.dtype = dt;
+      t.shape = {3, 5};
+      t.data.resize(15 * dtype_size(dt));
+      for (size_t i = 0; i < t.data.size(); ++i) t.data[i] = (uint8_t)(i * 7 + k);
+      m["t." + std::string(dtype_name(dt))] = t;
+      ++k;
+    }
+    HostTensor empty;
+    empty.dtype = Dtype::Float32;
+    empty.shape = {0, 4};
+    m["empty"] = empty;
+    write_safetensors((tmp / "a.safetensors").string(), m);
+    HostMap back = read_safetensors((tmp / "a.safetensors").string());
+    EXPECT(back.size() == m.size(), "%zu tensors back", back.size());
+    for (const auto& [name, t] : m) {
+      EXPECT(back.count(name) == 1, "%s missing", name.c_str());
+      EXPECT(back[name].dtype == t.dtype && back[name].shape == t.shape && back[name].data == t.data,
+             "%s differs", name.c_str());
+    }
+    // the data section starts 8-byte aligned
+    std::ifstream f(tmp / "a.safetensors", std::ios::binary);
+    uint64_t n = 0;
+    f.read((char*)&n, 8);
+    EXPECT(n % 8 == 0, "header length %llu", (unsigned long long)n);
+  }
+
+  banner("golden fixture through read_safetensors");
+  {
+    HostMap g = read_safetensors((root / "tests" / "golden" / "quant_q4q8.safetensors").string());
+    EXPECT(g.at("w").dtype == Dtype::Float32 && g.at("w").shape == std::vector<int64_t>({128, 256}), "w");
+    EXPECT(g.at("q4.wq").dtype == Dtype::Uint32 && g.at("q4.wq").shape == std::vector<int64_t>({128, 32}), "q4.wq");
+    EXPECT(g.at("q8.wq").shape == std::vector<int64_t>({128, 64}), "q8.wq");
+    EXPECT(g.at("q4.scales").shape == std::vector<int64_t>({128, 4}), "q4.scales");
+    // codes recomputed on the CPU from the fixture's own w match its packed words
+    std::vector<uint32_t> wq(128 * 32);
+    std::vector<float> s(128 * 4), b(128 * 4);
+    EXPECT(oracle_quantize((const float*)g.at("w").data.data(), 128, 256, 64, 4, 0, wq.data(), s.data(),
+                           b.data()) == 0, "oracle_quantize");
+    EXPECT(memcmp(wq.data(), g.at("q4.wq").data.data(), wq.size() * 4) == 0, "q4 words");
+  }
+
+  banner("malformed files are errors");
+  {
+    std::ofstream(tmp / "short.safetensors", std::ios::binary) << "abc";
+    bool threw = false;
+    try { read_safetensors((tmp / "short.safetensors").string()); } catch (const Error&) { threw = true; }
+    EXPECT(threw, "short file accepted");
+    std::string bad = std::string("\x10\0\0\0\0\0\0\0", 8) + "{\"x\":{\"dtype\":\"Q9\"}}";
+    bad.resize(8 + 16);
+    std::ofstream(tmp / "bad.safetensors", std::ios::binary) << bad;
+    threw = false;
+    try { read_safetensors((tmp / "bad.safetensors").string()); } catch (const Error&) { threw = true; }
+    EXPECT(threw, "malformed header accepted");
+    threw = false;
+    try { dtype_from_name("C64"); } catch (const Error&) { threw = true; }
+    EXPECT(threw, "unknown dtype accepted");
+  }
+
+  banner("write_quantized_config merges into an existing config");
+  {
+    fs::create_directories(tmp / "src");
+    std::ofstream(tmp / "src" / "config.json")
+        << "{\"hidden_size\": 3072, \"name\": \"a\\\"b\", \"ratio\": 0.5, \"layers\": [1, 2],"
+           " \"nested\": {\"ok\": true, \"none\": null}, \"quantization\": {\"bits\": 8}}";
+    write_quantized_config((tmp / "src").string(), (tmp / "dst").string(), 4, 64);
+    std::ifstream f(tmp / "dst" / "config.json");
+    std::string text((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+    EXPECT(text.find("\"hidden_size\": 3072") != std::string::npos, "%s", text.c_str());
+    EXPECT(text.find("\"name\": \"a\\\"b\"") != std::string::npos, "%s", text.c_str());
+    EXPECT(text.find("\"layers\": [1,2]") != std::string::npos, "%s", text.c_str());
+    EXPECT(text.find("\"bits\": 4") != std::string::npos && text.find("\"group_size\": 64") != std::string::npos &&
+               text.find("\"bits\": 8") == std::string::npos, "%s", text.c_str());
+    write_quantized_config((tmp / "nothing").string(), (tmp / "dst2").string(), 8, 32);
+    std::ifstream f2(tmp / "dst2" / "config.json");
+    std::string t2((std::istreambuf_iterator<char>(f2)), std::istreambuf_iterator<char>());
+    EXPECT(t2.find("\"quantization\"") != std::string::npos && t2.find("\"group_size\": 32") != std::string::npos,
+           "%s", t2.c_str());
+  }
+  fs::remove_all(tmp);
+}
+
+// ---- GPU cases -------------------------------------------------------------------------------------
+static void gpu_cases(const fs::path& root) {
+  const HostMap g = read_safetensors((root / "tests" / "golden" / "quant_q4q8.safetensors").string());
+  const auto& hw = g.at("w");
+  const auto& hx = g.at("x");
+
+  for (int bits : {4, 8}) {
+    banner(bits == 4 ? "golden quantize/dequantize/qmm Q4" : "golden quantize/dequantize/qmm Q8");
+    const std::string p = "q" + std::to_string(bits) + ".";
+    Array w = Array::from_host(hw.data.data(), hw.shape, hw.dtype);
+    Packed q = quantize(w, 64, bits);
+    EXPECT(q.wq.dtype() == Dtype::Uint32 && q.wq.shape() == g.at(p + "wq").shape, "wq shape");
+    EXPECT(host<uint8_t>(q.wq) == g.at(p + "wq").data, "packed words differ from the fixture");
+    EXPECT(host<uint8_t>(q.scales) == g.at(p + "scales").data, "scales differ from the fixture");
+    EXPECT(host<uint8_t>(q.biases) == g.at(p + "biases").data, "biases differ from the fixture");
+    Array deq = dequantize(q.wq, q.scales, q.biases, 64, bits);
+    EXPECT(host<uint8_t>(deq) == g.at(p + "deq").data, "dequantize differs from the fixture");
+    Array x = Array::from_host(hx.data.data(), hx.shape, hx.dtype);
+    Array y = quantized_matmul(x, q.wq, q.scales, q.biases, true, 64, bits);
+    const auto ref = g.at(p + "qmm");
+    std::vector<float> r(ref.data.size() / 4);
+    memcpy(r.data(), ref.data.data(), ref.data.size());
+    const double e = rel_fro(host<float>(y), r);
+    EXPECT(e < 1e-5, "relFro %.3e", e);
+    EXPECT(packed_bits(q.wq, q.scales, 64) == bits, "packed_bits");
+    bool threw = false;
+    try { quantized_matmul(x, q.wq, q.scales, q.biases, false, 64, bits); } catch (const Error& err) {
+      threw = err.status == 2;  // MLXQ_EUNSUPPORTED
+    }
+    EXPECT(threw, "transpose=false accepted");
+  }
+
+  banner("AdaptableLinear: bf16 cast + quantize, bias, two LoRA adapters");
+  {
+    std::mt19937 rng(7);
+    const int64_t M = 37, K = 256, N = 192, R1 = 16, R2 = 24;
+    std::vector<float> wf(N * K);
+    std::normal_distribution<float> nd(0.0f, 0.02f);
+    for (auto& v : wf) v = nd(rng);  // f32 weights: quantize() casts to bf16 first
+    std::vector<float> bias = bf16_normal(rng, N, 0.1f), x = bf16_normal(rng, M * K, 1.0f);
+    std::vector<float> a1 = bf16_normal(rng, K * R1, 0.01f), b1 = bf16_normal(rng, R1 * N, 0.01f);
+    std::vector<float> a2 = bf16_normal(rng, K * R2, 0.01f), b2 = bf16_normal(rng, R2 * N, 0.01f);
+    AdaptableLinear l = AdaptableLinear::dense(Array::from_host(wf.data(), {N, K}, Dtype::Float32),
+                                               Array::from_host(bias.data(), {N}, Dtype::Float32));
+    bool threw = false;
+    try { l.forward(bf16_array(x, {M, K})); } catch (const Error&) { threw = true; }
+    EXPECT(threw, "dense forward should be refused");
+    l.quantize(4, std::nullopt);
+    EXPECT(l.is_quantized() && l.quantized().group_size == 64 && l.base_shape()[1] == K, "quantize");
+    l.push(Adapter{bf16_array(a1, {K, R1}), bf16_array(b1, {R1, N}), 0.75f});
+    l.push(Adapter{bf16_array(a2, {K, R2}), bf16_array(b2, {R2, N}), 1.5f});
+    Array y = l.forward(bf16_array(x, {M, K}).reshape({1, M, K}));
+    EXPECT(y.shape() == std::vector<int64_t>({1, M, N}) && y.dtype() == Dtype::Bfloat16, "output shape");
+    // reference: bf16-cast weights, quantize, linear with bias + adapter 1, then + adapter 2
+    std::vector<float> wb(wf.size());
+    for (size_t i = 0; i < wf.size(); ++i) wb[i] = oracle_bf16_round(wf[i]);
+    std::vector<uint32_t> wq(N * K / 8);
+    std::vector<float> s(N * K / 64), z(N * K / 64), ref(M * N);
+    oracle_quantize(wb.data(), N, K, 64, 4, 1, wq.data(), s.data(), z.data());
+    EXPECT(host<uint32_t>(l.quantized().weight) == wq, "packed words");
+    std::vector<float> bias_b(N);
+    for (int64_t n = 0; n < N; ++n) bias_b[n] = oracle_bf16_round(bias[n]);
+    oracle_linear(x.data(), M, K, wq.data(), s.data(), z.data(), N, 64, 4, M > 8, 1, bias_b.data(),
+                  a1.data(), b1.data(), R1, 0.75f, 0, ref.data());
+    std::vector<float> xa(M * R2);
+    for (int64_t m = 0; m < M; ++m)
+      for (int64_t r = 0; r < R2; ++r) {
+        double acc = 0;
+        for (int64_t k = 0; k < K; ++k) acc += (double)x[m * K + k] * a2[k * R2 + r];
+        xa[m * R2 + r] = oracle_bf16_round((float)acc);
+      }
+    const float sc2 = oracle_bf16_round(1.5f);
+    for (int64_t m = 0; m < M; ++m)
+      for (int64_t n = 0; n < N; ++n) {
+        double acc = 0;
+        for (int64_t r = 0; r < R2; ++r) acc += (double)xa[m * R2 + r] * b2[r * N + n];
+        const float res = oracle_bf16_round(oracle_bf16_round((float)acc) * sc2);
+        ref[m * N + n] = oracle_bf16_round(ref[m * N + n] + res);
+      }
+    const double e = rel_fro(host_f32(y), ref);
+    EXPECT(e < 2e-3, "relFro %.3e", e);
+  }
+
+  banner("TokenEmbedding quantize + forward, and the snapshot round trip");
+  {
+    std::mt19937 rng(11);
+    const int64_t vocab = 300, hidden = 128;
+    std::vector<float> table = bf16_normal(rng, vocab * hidden, 0.02f);
+    TokenEmbedding e = TokenEmbedding::dense(bf16_array(table, {vocab, hidden}));
+    e.quantize(8, true);
+    std::vector<int32_t> ids = {0, 299, 5, 5, 123, 42};
+    Array out = e.forward(Array::from_host(ids.data(), {2, 3}, Dtype::Int32));
+    EXPECT(out.shape() == std::vector<int64_t>({2, 3, hidden}) && out.dtype() == Dtype::Float32, "shape");
+    std::vector<uint32_t> wq(vocab * hidden / 4);
+    std::vector<float> s(vocab * hidden / 64), z(vocab * hidden / 64), deq(vocab * hidden);
+    oracle_quantize(table.data(), vocab, hidden, 64, 8, 1, wq.data(), s.data(), z.data());
+    oracle_dequantize(wq.data(), s.data(), z.data(), vocab, hidden, 64, 8, 1, deq.data());
+    auto got = host<float>(out);
+    bool same = true;
+    for (size_t t = 0; t < ids.size(); ++t)
+      same &= memcmp(&got[t * hidden], &deq[ids[t] * hidden], hidden * 4) == 0;
+    EXPECT(same, "embedding rows differ from dequantize");
+
+    // quantize_map -> save_map -> load_dir_map -> lin / embedding
+    const fs::path dir = fs::temp_directory_path() / ("mlxq_snap_" + std::to_string(::getpid()));
+    Weights m;
+    std::vector<float> wlin = bf16_normal(rng, 96 * 256, 0.02f);
+    m["blk.q.weight"] = bf16_array(wlin, {96, 256});
+    m["blk.norm.weight"] = bf16_array(std::vector<float>(256, 1.0f), {256});
+    m["embed.weight"] = bf16_array(table, {vocab, hidden});
+    Weights packed = quantize_map(m, 4, 32, [](const std::string& b) { return b != "blk.norm"; });
+    EXPECT(packed.count("blk.q.scales") && packed.count("embed.biases") && !packed.count("blk.norm.scales"),
+           "quantize_map keys");
+    save_map((dir / "model.safetensors").string(), packed);
+    HostMap raw = read_safetensors((dir / "model.safetensors").string());
+    EXPECT(raw.at("blk.q.weight").dtype == Dtype::Uint32, "codes stored as U32");
+    Weights back = load_dir_map(dir.string());
+    AdaptableLinear q = lin(back, "blk.q", false, 32);
+    EXPECT(q.is_quantized() && q.quantized().bits == 4, "lin packed");
+    EXPECT(!lin(back, "blk.norm", false, 32).is_quantized(), "lin dense");
+    TokenEmbedding te = embedding(back, "embed", 32);
+    EXPECT(te.is_quantized() && te.bits() == 4 && te.group_size() == 32, "embedding packed");
+    std::vector<float> xq = bf16_normal(rng, 3 * 256, 1.0f);
+    auto y1 = host_f32(q.forward(bf16_array(xq, {3, 256})));
+    AdaptableLinear orig = AdaptableLinear::from_quantized_parts(
+        packed["blk.q.weight"], packed["blk.q.scales"], packed["blk.q.biases"], std::nullopt, 32, 4);
+    auto y2 = host_f32(orig.forward(bf16_array(xq, {3, 256})));
+    EXPECT(y1 == y2, "reloaded linear differs");
+    fs::remove_all(dir);
+  }
+}
+
+int main(int argc, char** argv) {
+  if (argc < 2 || (strcmp(argv[1], "cpu") && strcmp(argv[1], "gpu"))) {
+    fprintf(stderr, "usage: %s cpu|gpu\n", argv[0]);
+    return 2;
+  }
+  const fs::path root = repo_root(argv[0]);
+  try {
+    if (!strcmp(argv[1], "cpu")) cpu_cases(root);
+    else gpu_cases(root);
+  } catch (const std::exception& e) {
+    fprintf(stderr, "FAIL: uncaught exception: %s\n", e.what());
+    return 1;
+  }
+  if (g_failures) {
+    fprintf(stderr, "%d check(s) failed\n", g_failures);
+    return 1;
+  }
+  printf("ALL PASS (%s)\n", argv[1]);
+  return 0;
+}

@@ -116,3 +116,16 @@ def test_quantize_component_roundtrip(mlxq, tmp_path):
     ids = torch.tensor([[0, 95, 7]], device="cuda")
     table = oracle.dequantize(*ref, 32, 4, out_bf16=True)
     assert np.array_equal(to_np(e.forward(ids))[0], table[[0, 95, 7]])
+
+
+def test_cpp_host_api_gpu_cases():
+    """The C++ host API end to end (tests/host_cpp/host_test.cpp, `gpu`): golden fixture bit-exact,
+    AdaptableLinear with bias and two LoRA adapters vs the oracle, TokenEmbedding, and the
+    quantize_map -> save_map -> load_dir_map -> lin snapshot round trip."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(__file__), "host_cpp", "host_test")
+    assert os.path.exists(exe), "build() compiles tests/host_cpp/host_test"
+    banner("C++ host API gpu cases")
+    r = subprocess.run([exe, "gpu"], capture_output=True, text=True, timeout=120)
+    print(r.stdout, flush=True)
+    assert r.returncode == 0 and "ALL PASS" in r.stdout, r.stdout + r.stderr

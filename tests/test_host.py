@@ -66,3 +66,14 @@ def test_golden_fixture_through_load_dir_map(tmp_path):
     for bits in (4, 8):
         assert np.array_equal(m[f"q{bits}.wq"].numpy().view(np.uint32), gold[f"q{bits}.wq"])
         assert np.array_equal(m[f"q{bits}.scales"].numpy(), gold[f"q{bits}.scales"])
+
+
+HOST_TEST = os.path.join(os.path.dirname(__file__), "host_cpp", "host_test")
+
+
+def test_cpp_host_api_cpu_cases():
+    """The C++ host API's file formats and host logic (tests/host_cpp/host_test.cpp, `cpu`)."""
+    import subprocess
+    assert os.path.exists(HOST_TEST), "build() compiles tests/host_cpp/host_test"
+    r = subprocess.run([HOST_TEST, "cpu"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "ALL PASS" in r.stdout, r.stdout + r.stderr
