@@ -1,9 +1,10 @@
 // quantize.hip — affine group quantize / dequantize for gfx950.
 //
-// Both kernels are HBM-bound streaming passes: one thread owns 8 consecutive elements of a row
-// (one 16-byte bf16 load / one or two packed words), a group of gs elements is gs/8 adjacent
-// lanes, and the group's min/max is a butterfly over those lanes.  Every thread runs the same
-// straight-line code, so the launch is a flat 1-D grid over N*K/8 chunks.
+// Both kernels are HBM-bound streaming passes over a flat 1-D grid.  quantize: one thread owns 16
+// consecutive elements of a row (two 16-byte bf16 loads; two or four packed words out), a group
+// of gs elements is gs/16 adjacent lanes, and the group's min/max is a butterfly over those
+// lanes.  dequantize: one thread owns 8 elements (one or two packed words in, one 16-byte bf16
+// store out).
 #include "mlxq_common.h"
 
 namespace mlxq {
@@ -32,41 +33,48 @@ __device__ __forceinline__ void load8<float>(const float* p, float (&v)[8]) {
   }
 }
 
-// One code: clamp(round((w - bias) / s), 0, nb) with round half away from zero and an IEEE
-// quotient.  The quotient is formed as (w - bias) * (1/s); when that product lies within 2^-12 of
-// a half-integer (where the few-ulp difference to the exact quotient could flip the rounding) the
-// exact division is taken instead, so the result equals the exact-division form bit for bit.
-__device__ __forceinline__ uint32_t quant_code(float w, float bias, float s, float rs, float nb) {
-  float a = w - bias;
-  float t = a * rs;
-  float f = t - floorf(t);
-  if (__builtin_expect(fabsf(f - 0.5f) < 0x1p-12f, 0)) t = a / s;
-  float v = fminf(fmaxf(roundf(t), 0.0f), nb);
-  return (uint32_t)v;
+// Codes: clamp(round((w - bias) / s), 0, nb) with round half away from zero and an IEEE
+// quotient, as MLX computes them.  The fast form is t = (w - bias) * (1/s) and
+// clamp(floor(t + 0.5), 0, nb): away from half-integers the few-ulp difference between t and the
+// exact quotient, and the rounding of t + 0.5, cannot change the result.  A code whose t lies
+// within 2^-12 of a half-integer is recomputed with the exact division and roundf (about one
+// element in 2000, handled in a rarely taken second pass).
+__device__ __forceinline__ uint32_t code_fast(float a, float rs, float nb, bool& near) {
+  const float t = a * rs;
+  near = fabsf((t - floorf(t)) - 0.5f) < 0x1p-12f;
+  return (uint32_t)fminf(fmaxf(floorf(t + 0.5f), 0.0f), nb);
+}
+__device__ __forceinline__ uint32_t code_exact(float a, float s, float nb) {
+  return (uint32_t)fminf(fmaxf(roundf(a / s), 0.0f), nb);
 }
 
 // w [N,K] (bf16 bits or f32) -> wq [N, K*BITS/32], scales/biases [N, K/GS] in T.
 // Group parameters follow MLX's edge-exact affine scheme: the larger-magnitude end of the group
 // range is reproduced exactly (it becomes the bias) and the scale carries the sign.
+// A thread owns EPT = 16 consecutive elements (two 16-byte bf16 loads), so a group is GS/16
+// lanes (2, 4 or 8) and its min/max is a butterfly over those lanes.
 template <typename T, int BITS, int GS>
 __global__ __launch_bounds__(256) void quantize_kernel(const T* __restrict__ w, int64_t n_chunks,
                                                        uint32_t* __restrict__ wq,
                                                        T* __restrict__ scales, T* __restrict__ biases) {
-  constexpr int LANES = GS / 8;  // lanes per group
+  constexpr int EPT = 16;
+  constexpr int LANES = GS / EPT;  // lanes per group
+  constexpr int WPT = EPT * BITS / 32;  // packed words per thread: 2 (Q4) or 4 (Q8)
   constexpr float nb = (float)((1 << BITS) - 1);
   const int64_t chunk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   // n_chunks is a multiple of LANES, so whole groups are either fully in or fully out.
   const bool live = chunk < n_chunks;
-  float v[8];
+  float v[EPT];
   if (live) {
-    load8<T>(w + chunk * 8, v);
+    load8<T>(w + chunk * EPT, *reinterpret_cast<float(*)[8]>(&v[0]));
+    load8<T>(w + chunk * EPT + 8, *reinterpret_cast<float(*)[8]>(&v[8]));
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    for (int i = 0; i < EPT; ++i) v[i] = 0.0f;
   }
   float mx = v[0], mn = v[0];
 #pragma unroll
-  for (int i = 1; i < 8; ++i) {
+  for (int i = 1; i < EPT; ++i) {
     mx = fmaxf(mx, v[i]);
     mn = fminf(mn, v[i]);
   }
@@ -91,19 +99,30 @@ __global__ __launch_bounds__(256) void quantize_kernel(const T* __restrict__ w, 
     SBLoad<T>::st(scales, g, s);
     SBLoad<T>::st(biases, g, bias);
   }
-  if constexpr (BITS == 4) {
-    uint32_t word = 0;
+  uint32_t words[WPT];
+  uint32_t near_mask = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) word |= quant_code(v[i], bias, s, rs, nb) << (4 * i);
-    wq[chunk] = word;
-  } else {
-    u32x2 words = {0u, 0u};
+  for (int j = 0; j < WPT; ++j) words[j] = 0u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      words[0] |= quant_code(v[i], bias, s, rs, nb) << (8 * i);
-      words[1] |= quant_code(v[4 + i], bias, s, rs, nb) << (8 * i);
+  for (int i = 0; i < EPT; ++i) {
+    bool near;
+    const uint32_t c = code_fast(v[i] - bias, rs, nb, near);
+    near_mask |= (uint32_t)near << i;
+    words[i * BITS / 32] |= c << ((i * BITS) % 32);
+  }
+  if (__builtin_expect(near_mask != 0u, 0)) {
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      if (near_mask & (1u << i)) {
+        const uint32_t sh = (i * BITS) % 32, m = ((1u << BITS) - 1u) << sh;
+        words[i * BITS / 32] = (words[i * BITS / 32] & ~m) | (code_exact(v[i] - bias, s, nb) << sh);
+      }
     }
-    *reinterpret_cast<u32x2*>(wq + chunk * 2) = words;
+  }
+  if constexpr (WPT == 2) {
+    *reinterpret_cast<u32x2*>(wq + chunk * 2) = u32x2{words[0], words[1]};
+  } else {
+    *reinterpret_cast<u32x4*>(wq + chunk * 4) = u32x4{words[0], words[1], words[2], words[3]};
   }
 }
 
@@ -147,7 +166,7 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const uint32_t* __restr
 template <typename T, int BITS, int GS>
 static int launch_quantize(const void* w, int64_t N, int64_t K, uint32_t* wq, void* s, void* b,
                            hipStream_t st) {
-  const int64_t n_chunks = N * K / 8;
+  const int64_t n_chunks = N * K / 16;  // K % GS == 0 and GS >= 32, so K % 16 == 0
   if (n_chunks == 0) return MLXQ_OK;
   const int64_t blocks = (n_chunks + 255) / 256;
   hipLaunchKernelGGL((quantize_kernel<T, BITS, GS>), dim3((unsigned)blocks), dim3(256), 0, st,

@@ -95,6 +95,38 @@ def test_quantize_special_groups(mlxq, bits):
     assert np.array_equal(to_np(b), rb)
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_quantize_half_integer_ties(mlxq, bits, dtype):
+    """Groups whose quotients (w - bias)/s land exactly on half-integers, and one ulp either side.
+
+    With min 0 and max nb*d (d a power of two) the scale is -d and the bias nb*d exactly, so
+    w = (k + 0.5) d gives the quotient nb - k - 0.5: a tie, which MLX's round() sends away from
+    zero.  These are the codes the kernel recomputes with an exact division."""
+    banner("quantize ties", bits, dtype)
+    nb = (1 << bits) - 1
+    gs = 64
+    rows = []
+    for e in (-6, -3, 0, 2):
+        d = np.float32(2.0 ** e)
+        k = np.arange(gs - 2) % nb
+        ties = ((k + 0.5) * d).astype(np.float32)
+        for nudge in (0, 1, -1):  # exact ties, then one ulp above and below
+            w = ties.copy()
+            if nudge:
+                w = np.nextafter(w, np.float32(np.inf) if nudge > 0 else np.float32(-np.inf)).astype(np.float32)
+            rows.append(np.concatenate([[0.0, nb * d], w]).astype(np.float32))
+    w = np.stack(rows)
+    if dtype == "bf16":
+        w = oracle.bf16_round(w)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    wq, s, b = mlxq.quantize(to_gpu(w, tdt), gs, bits)
+    rwq, rs, rb = oracle.quantize(w, gs, bits, sb_bf16=(dtype == "bf16"))
+    assert np.array_equal(to_np(wq), rwq)
+    assert np.array_equal(to_np(s), rs)
+    assert np.array_equal(to_np(b), rb)
+
+
 def test_quantize_config1_full_size(mlxq):
     """Config 1: W [3072,3072] bf16 ~ N(0,0.02), seed 0, Q4 g64 — bit-exact against the oracle."""
     banner("quantize config1 [3072,3072] q4 g64")
