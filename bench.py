@@ -39,7 +39,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extras", action="store_true", help="headline GEMM only")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
-    p.add_argument("--only", choices=("all", "mlp", "gemv", "quantize", "copy"), default="all",
+    p.add_argument("--only", choices=("all", "mlp", "gemv", "quantize", "copy", "configs"),
+                   default="all",
                    help="run one leg only (for profiling); 'copy' is the plain-copy calibration "
                         "kernel for the HBM byte counters")
     p.add_argument("--summarize-pmc", metavar="DIR",
@@ -204,6 +205,104 @@ def bench_quantize(mlxq, torch, iters=10):
             "frac_of_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+def graph_ms(torch, fn, inner=8, reps=5):
+    """Mean milliseconds of fn() on the GPU: `inner` calls captured in one HIP graph, replayed
+    `reps` times between events (no host launch overhead in the measurement)."""
+    dev = torch.device("cuda:0")
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        fn()  # warm-up outside capture
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(inner):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del graph
+    return e0.elapsed_time(e1) / (reps * inner)
+
+
+def bench_config1(mlxq, torch):
+    """Config 1 round trip: W[3072,3072] bf16 -> Q4 g64, dequantize, x[256,3072] . W^T."""
+    dev = torch.device("cuda:0")
+    w = gen_bf16((3072, 3072), 0.02, 300, dev)
+    x = gen_bf16((256, 3072), 1.0, 301, dev)
+    q = mlxq.quantize(w, 64, 4)
+    qbytes = 3072 * 3072 * 2 + 3072 * 3072 // 2 + 3072 * 48 * 4
+    t_q = graph_ms(torch, lambda: mlxq.quantize(w, 64, 4))
+    t_d = graph_ms(torch, lambda: mlxq.dequantize(*q, 64, 4))
+    t_m = graph_ms(torch, lambda: mlxq.quantized_matmul(x, *q, True, 64, 4))
+    flop = 2.0 * 256 * 3072 * 3072
+    return {"quantize_us": round(t_q * 1e3, 2), "quantize_GBs": round(qbytes / (t_q * 1e-3) / 1e9, 1),
+            "dequantize_us": round(t_d * 1e3, 2), "dequantize_GBs": round(qbytes / (t_d * 1e-3) / 1e9, 1),
+            "qmm_us": round(t_m * 1e3, 2), "qmm_TFLOPs": round(flop / (t_m * 1e-3) / 1e12, 1),
+            "note": "24.2 MB per quantize/dequantize: latency-bound at this size"}
+
+
+def bench_config3(mlxq, torch):
+    """Config 3: Wan2.2 self-attention projections, x[32760,5120] bf16 . 4 x Q8-g64 W[5120,5120],
+    including the quantize pass over all four weights."""
+    dev = torch.device("cuda:0")
+    M, D = 32760, 5120
+    x = gen_bf16((M, D), 1.0, 400, dev)
+    ws = [gen_bf16((D, D), 0.02, 401 + i, dev) for i in range(4)]
+    qs = [mlxq.quantize(w, 64, 8) for w in ws]
+    ys = [torch.empty((M, D), dtype=torch.bfloat16, device=dev) for _ in range(4)]
+
+    def proj():
+        for q, y in zip(qs, ys):
+            mlxq.quantized_matmul(x, *q, True, 64, 8, out=y)
+
+    def quant():
+        for w in ws:
+            mlxq.quantize(w, 64, 8)
+    t_p = graph_ms(torch, proj, inner=2, reps=3)
+    t_q = graph_ms(torch, quant, inner=4, reps=3)
+    flop = 4 * 2.0 * M * D * D
+    qbytes = 4 * (D * D * 2 + D * D + D * (D // 64) * 4)
+    return {"qmm_ms": round(t_p, 3), "qmm_TFLOPs": round(flop / (t_p * 1e-3) / 1e12, 1),
+            "qmm_frac_of_mfma_peak": round(flop / (t_p * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "quantize_ms": round(t_q, 4), "quantize_GBs": round(qbytes / (t_q * 1e-3) / 1e9, 1),
+            "quantize_frac_of_hbm_peak": round(qbytes / (t_q * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "total_ms": round(t_p + t_q, 3)}
+
+
+def bench_config5(mlxq, torch):
+    """Config 5: FLUX.1-dev double-stream block linear sweep at 4608 tokens, {Q4,Q8} x group
+    {32,64,128}, each with a bf16 rank-16 LoRA residual (A, B ~ N(0, 0.01)) fused in the epilogue."""
+    dev = torch.device("cuda:0")
+    M = 4608
+    shapes = [(9216, 3072), (3072, 3072), (12288, 3072), (3072, 12288), (18432, 3072)]
+    xs = {K: gen_bf16((M, K), 1.0, 500 + K, dev) for K in (3072, 12288)}
+    cells, total_flop, total_ms = {}, 0.0, 0.0
+    for bits in (4, 8):
+        for gs in (32, 64, 128):
+            for (N, K) in shapes:
+                q = mlxq.quantize(gen_bf16((N, K), 0.02, 600 + N + K, dev), gs, bits)
+                a = gen_bf16((K, 16), 0.01, 700 + K, dev)
+                b = gen_bf16((16, N), 0.01, 701 + N, dev)
+                ws = torch.empty(mlxq.linear_workspace_size(M, N, 16), dtype=torch.uint8, device=dev)
+                ms = graph_ms(torch, lambda: mlxq.linear(xs[K], *q, gs, bits, lora_a=a, lora_b=b,
+                                                         workspace=ws), inner=4, reps=3)
+                flop = 2.0 * M * K * N + 2.0 * M * 16 * (K + N)
+                cells[f"Q{bits}g{gs} {N}x{K}"] = round(flop / (ms * 1e-3) / 1e12, 1)
+                total_flop += flop
+                total_ms += ms
+                del q
+    return {"sweep_TFLOPs": round(total_flop / (total_ms * 1e-3) / 1e12, 1),
+            "sweep_ms": round(total_ms, 3), "cells_TFLOPs": cells}
+
+
 def cpu_baseline(budget_s):
     """The CPU oracle on a bounded row sample of the config-2 up projection."""
     import numpy as np
@@ -314,6 +413,10 @@ def main():
     if args.only == "quantize":
         print(json.dumps({"quantize": bench_quantize(mlxq, torch)}))
         return
+    if args.only == "configs":
+        print(json.dumps({"config1": bench_config1(mlxq, torch), "config3": bench_config3(mlxq, torch),
+                          "config5": bench_config5(mlxq, torch)}))
+        return
     g = bench_flux_mlp(mlxq, torch, args.steps, args.warmup)
     achieved = g["qmm_flop_per_launch"] / (g["qmm_launch_ms"] * 1e-3) / 1e12
     res = {
@@ -342,6 +445,9 @@ def main():
     if not args.no_extras and args.only == "all":
         res["gemv"] = bench_gemv(mlxq, torch)
         res["quantize"] = bench_quantize(mlxq, torch)
+        res["config1"] = bench_config1(mlxq, torch)
+        res["config3"] = bench_config3(mlxq, torch)
+        res["config5"] = bench_config5(mlxq, torch)
     if not args.no_cpu and args.only == "all":
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(res))

@@ -337,3 +337,63 @@ def test_invalid_arguments_return_errors(mlxq):
         mlxq.quantized_matmul(x, wq, s, b, False, 64, 4)
     with pytest.raises(mlxq.MlxqError, match="GEMV limit"):
         mlxq.qmv(torch.zeros((9, 128), dtype=torch.bfloat16, device="cuda"), wq, s, b, 64, 4)
+
+
+# ---------------------------------------------------------------- configs 3 and 5 at full size
+
+def test_config3_wan_projection_full_size_sampled_rows(mlxq):
+    """Config 3: x[32760,5120] bf16 . Q8-g64 W[5120,5120]^T at full size (sampled rows), with the
+    full-size quantize bit-exact against the oracle."""
+    banner("config3 full size")
+    rng = np.random.default_rng(33)
+    M, D = 32760, 5120
+    x = bf16_normal(rng, (M, D))
+    w = bf16_normal(rng, (D, D), 0.02)
+    wq, s, b = mlxq.quantize(to_gpu(w), 64, 8)
+    y = mlxq.quantized_matmul(to_gpu(x), wq, s, b, True, 64, 8)
+    torch.cuda.synchronize()
+    rwq, rs, rb = oracle.quantize(w, 64, 8, sb_bf16=True)
+    assert np.array_equal(to_np(wq), rwq)
+    assert np.array_equal(to_np(s), rs) and np.array_equal(to_np(b), rb)
+    rows = np.concatenate([[0, 255, 256, 32511, 32512, M - 1], np.sort(rng.choice(M, 26, replace=False))])
+    ref = oracle.quantized_matmul(x[rows], rwq, rs, rb, 64, 8, w_bf16=True, out_bf16=True)
+    assert_close(to_np(y)[rows], ref, "config3 rows")
+
+
+CONFIG5_SHAPES = [(9216, 3072), (3072, 3072), (12288, 3072), (3072, 12288), (18432, 3072)]
+_CONFIG5_X = {}
+
+
+def _config5_x(K):
+    """Activations x[4608, K] shared by the cells with the same K (host copy and device copy)."""
+    if K not in _CONFIG5_X:
+        x = bf16_normal(np.random.default_rng(K), (4608, K))
+        _CONFIG5_X.clear()
+        _CONFIG5_X[K] = (x, to_gpu(x))
+    return _CONFIG5_X[K]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("N,K", sorted(CONFIG5_SHAPES, key=lambda nk: nk[1]))
+def test_config5_block_sweep_with_lora_sampled_rows(mlxq, bits, gs, N, K):
+    """Config 5 cell at full size: M=4608, rank-16 bf16 LoRA (A, B ~ N(0,0.01)) fused into the
+    epilogue, checked on sampled rows against the oracle's op-by-op linear.  The packed codes the
+    GPU produced are checked bit-exact on a slice and then fed to the oracle."""
+    banner("config5", bits, gs, N, K)
+    rng = np.random.default_rng(bits * 1000 + gs + N + K)
+    M = 4608
+    x, gx = _config5_x(K)
+    w = bf16_normal(rng, (N, K), 0.02)
+    a = bf16_normal(rng, (K, 16), 0.01)
+    bb = bf16_normal(rng, (16, N), 0.01)
+    wq, s, b = mlxq.quantize(to_gpu(w), gs, bits)
+    y = mlxq.linear(gx, wq, s, b, gs, bits, lora_a=to_gpu(a), lora_b=to_gpu(bb))
+    torch.cuda.synchronize()
+    gwq, gs_, gb = to_np(wq), to_np(s), to_np(b)
+    rwq, rs, rb = oracle.quantize(w[:64], gs, bits, sb_bf16=True)
+    assert np.array_equal(gwq[:64], rwq) and np.array_equal(gs_[:64], rs) and np.array_equal(gb[:64], rb)
+    rows = np.concatenate([[0, 255, 256, M - 1], np.sort(rng.choice(M, 12, replace=False))])
+    ref = oracle.linear(x[rows], gwq, gs_, gb, gs, bits, w_bf16=True, act_bf16=True, lora_a=a,
+                        lora_b=bb, lora_scale=1.0)
+    assert_close(to_np(y)[rows], ref, f"config5 Q{bits} g{gs} {N}x{K}")
