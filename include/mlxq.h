@@ -134,6 +134,20 @@ int mlxq_linear(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
                 size_t workspace_bytes, void* stream);
 
 /*
+ * Fused SwiGLU gate/up for decode — the first two ops of Mlp::forward
+ * (mlx-gen-sensenova/src/qwen3.rs:178-181): h = multiply(silu(gate.forward(x)), up.forward(x))
+ * with gate/up quantized linears [F,K] sharing x [M,K]; one launch streams both weight matrices:
+ *   h = round(round(silu(round(x.Wg^T))) * round(x.Wu^T))      (round() to bf16)
+ * Decode form only: bf16 x and scales, 1 <= M <= 8, group_size 64 or 128, K a multiple of
+ * 512/bits; anything else returns MLXQ_EUNSUPPORTED (callers then run the two linears).
+ * This entry point has no single counterpart in the reference; it replaces a three-op sequence.
+ */
+int mlxq_swiglu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq_gate,
+                const void* scales_gate, const void* biases_gate, const uint32_t* wq_up,
+                const void* scales_up, const void* biases_up, int sb_dtype, int64_t F,
+                int group_size, int bits, void* h, void* stream);
+
+/*
  * One more LoRA adapter on an already computed output — the `out + adapter.residual(x)` step of
  * AdaptableLinear::forward (src/adapters.rs:543-549, Adapter::residual :260-270) for adapter
  * stacks beyond the one mlxq_linear fuses:

@@ -198,6 +198,28 @@ size_t mlxq_linear_workspace_size(int64_t M, int64_t N, int64_t lora_rank) {
   return (size_t)(xa + N * R * 4);
 }
 
+int mlxq_swiglu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq_gate,
+                const void* scales_gate, const void* biases_gate, const uint32_t* wq_up,
+                const void* scales_up, const void* biases_up, int sb_dtype, int64_t F,
+                int group_size, int bits, void* h, void* stream) {
+  g_err[0] = 0;
+  int rc;
+  if ((rc = check_mm("swiglu", x, x_dtype, M, K, wq_gate, scales_gate, biases_gate, sb_dtype, F,
+                     group_size, bits, h)))
+    return rc;
+  if (M == 0 || F == 0) return MLXQ_OK;
+  if ((rc = check_aligned("swiglu", "wq_up", wq_up)) || (rc = check_aligned("swiglu", "scales_up", scales_up, 4)) ||
+      (rc = check_aligned("swiglu", "biases_up", biases_up, 4)))
+    return rc;
+  if (!swiglu_qmv_applicable(x_dtype, sb_dtype, M, K, F, group_size, bits))
+    return set_error(MLXQ_EUNSUPPORTED,
+                     "swiglu: the fused decode form takes bf16 x and scales, 1 <= M <= 8, group_size "
+                     "64 or 128 and K a multiple of %d (got M=%lld K=%lld)", 512 / bits, (long long)M,
+                     (long long)K);
+  return run_swiglu_qmv(x, M, K, wq_gate, scales_gate, biases_gate, wq_up, scales_up, biases_up, F,
+                        group_size, bits, h, (hipStream_t)stream);
+}
+
 int mlxq_lora_residual(const void* x, int x_dtype, int64_t M, int64_t K, const void* lora_a,
                        const void* lora_b, int64_t N, int64_t rank, float lora_scale, void* y,
                        void* workspace, size_t workspace_bytes, void* stream) {

@@ -35,7 +35,6 @@ namespace mlxq {
 namespace {
 
 constexpr int kBufferFlags = 0x00020000;
-constexpr int kMaxSteps = 8;   // 64-byte load steps per wave (all issued at once)
 constexpr int kMaxWaves = 16;  // waves per workgroup (they split K)
 constexpr int kCopySlots = 8;  // 16-byte activation chunks per thread in the LDS copy
 constexpr int kMaxLds = 160 * 1024;
@@ -91,14 +90,17 @@ __device__ __forceinline__ void swap_lane_halves(uint32_t& lo_keep, uint32_t& hi
 
 // Launch contract (checked on the host by qmv_plan): 1 <= M <= MR, K % (512/BITS) == 0,
 // bf16 scales and biases, LS = K*BITS/512 load steps per row with LS % STEPS == 0 and
-// blockDim.x = 64 * LS/STEPS <= 1024, at most kCopySlots/MR activation chunks per thread per
-// row, at most one scale chunk per thread, dynamic LDS as computed by qmv_plan, every buffer
+// blockDim.x = 64 * NMAT * LS/STEPS <= 1024, at most kCopySlots/MR activation chunks per thread
+// per row, at most one scale chunk per thread, dynamic LDS as computed by qmv_plan, every buffer
 // < 2 GiB.
-template <int BITS, bool G64, int STEPS, int MR>
+// NMAT = 2 is the SwiGLU decode form: the second wave half streams the same 16 rows of a second
+// matrix (up) and the output is round(round(silu(round(x.Wg^T))) * round(x.Wu^T)).
+template <int BITS, bool G64, int STEPS, int MR, int NMAT>
 __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
     const uint16_t* __restrict__ x, int M, int K, const uint32_t* __restrict__ wq,
-    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases, int N,
-    uint16_t* __restrict__ y) {
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const uint32_t* __restrict__ wq2, const uint16_t* __restrict__ scales2,
+    const uint16_t* __restrict__ biases2, int N, uint16_t* __restrict__ y) {
   constexpr int CPL = 512 / BITS;          // codes per row in one 64-byte load step
   constexpr int GS = G64 ? 64 : 128;       // group size
   constexpr int NM = BITS == 4 ? 4 : 2;    // MFMAs per load step
@@ -109,7 +111,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   const int NT = blockDim.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int W = (NT >> 6) / NMAT;  // waves per matrix
+  const int mat = NMAT == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave_all / W);
+  const int wave = wave_all - mat * W;  // index within this wave's matrix
   const int c16 = lane & 15, q = lane >> 4;
   const int n0 = blockIdx.x * 16;
   const int n = n0 + c16;
@@ -118,20 +123,24 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   const int G = K / GS;
   const int ls0 = wave * STEPS;     // this wave's load steps: [ls0, ls0 + STEPS)
   const int x_stride = 2 * K + 16;  // LDS row pitch: rows start on different banks
-  const int sz_lds = M * x_stride;  // then (s, b - 128 s) or (s, b) as f32 pairs, [16 rows][G]
+  const int sz_lds = M * x_stride;  // then (s, b - 128 s) or (s, b) as f32 pairs, [mat][16 rows][G]
 
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(x), (short)0, M * K * 2, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(wq), (short)0, (int)((uint32_t)N * (uint32_t)rowbytes), kBufferFlags);
+      const_cast<uint32_t*>(mat ? wq2 : wq), (short)0, (int)((uint32_t)N * (uint32_t)rowbytes), kBufferFlags);
   // Rounded up to whole dwords: buffer range checks are per dword, and the last scale may share
   // its dword with 2 bytes past the end (same aligned dword, so never another page; the extra
   // value belongs to a row >= N, which is never stored).
   const int sb_total = (int)(((uint32_t)N * (uint32_t)G * 2u + 3u) & ~3u);
+  // Scale/bias chunks: threads [0, 2G) copy the first matrix's, [2G, 4G) the second's.
+  const int sb_chunks = 2 * G;  // 16 rows x G bf16 = 2G chunks of 16 bytes per matrix
+  const int smat = NMAT == 2 && tid >= sb_chunks ? 1 : 0;
+  const int stid = tid - smat * sb_chunks;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(scales), (short)0, sb_total, kBufferFlags);
+      const_cast<uint16_t*>(smat ? scales2 : scales), (short)0, sb_total, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(biases), (short)0, sb_total, kBufferFlags);
+      const_cast<uint16_t*>(smat ? biases2 : biases), (short)0, sb_total, kBufferFlags);
 
   // 1. Workgroup operands first (small; they return before the weight stream): the activation
   //    rows as 16-byte chunks, and the contiguous scale and bias rows of this workgroup's 16
@@ -150,8 +159,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
       }
     }
   }
-  const int sb_chunks = 2 * G;  // 16 rows x G bf16 = 2G chunks of 16 bytes
-  const uint32_t sb_src = tid < sb_chunks ? (uint32_t)n0 * (uint32_t)G * 2u + (uint32_t)tid * 16u : kOob;
+  const uint32_t sb_src = stid < sb_chunks ? (uint32_t)n0 * (uint32_t)G * 2u + (uint32_t)stid * 16u : kOob;
   const u32x4 cs = load16(rs, sb_src);
   const u32x4 cz = load16(rz, sb_src);
 
@@ -177,7 +185,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
       }
     }
   }
-  if (tid < sb_chunks) {
+  if (stid < sb_chunks) {
     f32x4 pr[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -186,7 +194,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
       pr[j] = f32x4{s0, BITS == 4 ? fmaf(-128.0f, s0, z0) : z0, s1, BITS == 4 ? fmaf(-128.0f, s1, z1) : z1};
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<f32x4*>(lds + sz_lds + tid * 64 + j * 16) = pr[j];
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<f32x4*>(lds + sz_lds + smat * 128 * G + stid * 64 + j * 16) = pr[j];
   }
   __syncthreads();
 
@@ -202,7 +211,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
     else k = (q < 2 ? 64 + 32 * q : 32 * q + 16) + 8 * (i - 2);
     xa[i] = lds + (c16 < M ? c16 : 0) * x_stride + (ls0 * CPL + k) * 2;
   }
-  const float* sz = reinterpret_cast<const float*>(lds + sz_lds) + 2 * c16 * G;
+  const float* sz = reinterpret_cast<const float*>(lds + sz_lds + mat * 128 * G) + 2 * c16 * G;
   bf16x8 ones;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
@@ -253,13 +262,20 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   __syncthreads();
   float* red = reinterpret_cast<float*>(lds);
 #pragma unroll
-  for (int e = 0; e < E; ++e) red[(wave * 16 + 4 * q + e) * 17 + c16] = yacc[e];
+  for (int e = 0; e < E; ++e) red[(wave_all * 16 + 4 * q + e) * 17 + c16] = yacc[e];
   __syncthreads();
-  const int W = NT >> 6;
   for (int idx = tid; idx < 16 * M; idx += NT) {  // a one-wave workgroup has 64 < 16*M threads
     const int m = idx >> 4, nl = idx & 15;
     float v = 0.0f;
     for (int w = 0; w < W; ++w) v += red[(w * 16 + m) * 17 + nl];
+    if constexpr (NMAT == 2) {
+      float u = 0.0f;
+      for (int w = 0; w < W; ++w) u += red[((W + w) * 16 + m) * 17 + nl];
+      // each op rounded to bf16 as the reference's separate ops are (qwen3.rs:178-181)
+      const float g = round_bf16(v);
+      const float sg = round_bf16(g / (1.0f + expf(-g)));
+      v = sg * round_bf16(u);
+    }
     if (n0 + nl < N) y[m * N + n0 + nl] = f32_to_bf16_bits(v);
   }
 }
@@ -267,16 +283,16 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
 namespace {
 
 struct QmvPlan {
-  int waves, steps, mr, lds;
+  int waves, steps, mr, lds;  // waves: all waves of the workgroup (per matrix x matrices)
 };
 
 constexpr int kStepChoices[] = {8, 6, 4, 3, 2, 1};
 
-// Picks the most load steps per wave (<= kMaxSteps) that divide the row's load-step count, fit a
+// Picks the most load steps per wave (at most 8) that divide the row's load-step count, fit a
 // workgroup, and keep the activation copy within kCopySlots chunks per thread.  Long streams per
 // wave in small workgroups measured best: at 100 MB, 8 steps x 3 waves streams 5.4 TB/s against
 // 3.6 TB/s for 2 steps x 12 waves, and the decode shapes are no slower.
-bool qmv_plan(int64_t M, int64_t K, int gs, int bits, QmvPlan& p) {
+bool qmv_plan(int64_t M, int64_t K, int gs, int bits, int nmat, QmvPlan& p) {
   if (M < 1 || M > 8 || (bits != 4 && bits != 8) || (gs != 64 && gs != 128)) return false;
   const int64_t cpl = 512 / bits;
   if (K <= 0 || K % cpl != 0 || K % gs != 0) return false;
@@ -284,12 +300,12 @@ bool qmv_plan(int64_t M, int64_t K, int gs, int bits, QmvPlan& p) {
   const int mr = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
   for (int steps : kStepChoices) {
     if (LS % steps != 0) continue;
-    const int64_t waves = LS / steps;
+    const int64_t waves = nmat * (LS / steps);
     if (waves > kMaxWaves) continue;
     const int64_t nt = waves * 64;
     if ((KC + nt - 1) / nt > kCopySlots / mr) continue;
-    if (2 * G > nt) continue;  // one scale chunk per thread
-    const int64_t operands = M * (2 * K + 16) + 16 * G * 8;
+    if (nmat * 2 * G > nt) continue;  // one scale chunk per thread
+    const int64_t operands = M * (2 * K + 16) + nmat * 16 * G * 8;
     const int64_t red = waves * 16 * 17 * 4;
     const int64_t lds = operands > red ? operands : red;
     if (lds > kMaxLds) continue;
@@ -299,68 +315,102 @@ bool qmv_plan(int64_t M, int64_t K, int gs, int bits, QmvPlan& p) {
   return false;
 }
 
+// Device operands of one launch (the second matrix is used by the SwiGLU form only).
+struct QmvArgs {
+  const void* x;
+  int64_t M, K, N;
+  const uint32_t* wq;
+  const void *s, *b;
+  const uint32_t* wq2;
+  const void *s2, *b2;
+  void* y;
+};
+
 }  // namespace
 
-template <int BITS, bool G64, int STEPS, int MR>
-static int launch_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
-                           const void* b, int64_t N, const QmvPlan& p, void* y, hipStream_t st) {
+template <int BITS, bool G64, int STEPS, int MR, int NMAT>
+static int launch_qmv_mfma(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_mfma_kernel<BITS, G64, STEPS, MR>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_mfma_kernel<BITS, G64, STEPS, MR, NMAT>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds) != hipSuccess)
       return set_error(MLXQ_EDEVICE, "qmv: hipFuncSetAttribute failed");
     attr_set = true;
   }
-  hipLaunchKernelGGL((qmv_mfma_kernel<BITS, G64, STEPS, MR>), dim3((unsigned)((N + 15) / 16)),
-                     dim3(p.waves * 64), p.lds, st, (const uint16_t*)x, (int)M, (int)K, wq,
-                     (const uint16_t*)s, (const uint16_t*)b, (int)N, (uint16_t*)y);
-  return check_launch("qmv_mfma");
+  hipLaunchKernelGGL((qmv_mfma_kernel<BITS, G64, STEPS, MR, NMAT>), dim3((unsigned)((a.N + 15) / 16)),
+                     dim3(p.waves * 64), p.lds, st, (const uint16_t*)a.x, (int)a.M, (int)a.K, a.wq,
+                     (const uint16_t*)a.s, (const uint16_t*)a.b, a.wq2, (const uint16_t*)a.s2,
+                     (const uint16_t*)a.b2, (int)a.N, (uint16_t*)a.y);
+  return check_launch(NMAT == 2 ? "swiglu_qmv" : "qmv_mfma");
 }
 
-template <int BITS, bool G64, int STEPS>
-static int qmv_rows(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
-                    const void* b, int64_t N, const QmvPlan& p, void* y, hipStream_t st) {
+template <int BITS, bool G64, int STEPS, int NMAT>
+static int qmv_rows(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
   switch (p.mr) {
-    case 1: return launch_qmv_mfma<BITS, G64, STEPS, 1>(x, M, K, wq, s, b, N, p, y, st);
-    case 2: return launch_qmv_mfma<BITS, G64, STEPS, 2>(x, M, K, wq, s, b, N, p, y, st);
-    case 4: return launch_qmv_mfma<BITS, G64, STEPS, 4>(x, M, K, wq, s, b, N, p, y, st);
-    default: return launch_qmv_mfma<BITS, G64, STEPS, 8>(x, M, K, wq, s, b, N, p, y, st);
+    case 1: return launch_qmv_mfma<BITS, G64, STEPS, 1, NMAT>(a, p, st);
+    case 2: return launch_qmv_mfma<BITS, G64, STEPS, 2, NMAT>(a, p, st);
+    case 4: return launch_qmv_mfma<BITS, G64, STEPS, 4, NMAT>(a, p, st);
+    default: return launch_qmv_mfma<BITS, G64, STEPS, 8, NMAT>(a, p, st);
   }
 }
 
-template <int BITS, bool G64>
-static int qmv_steps(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
-                     const void* b, int64_t N, const QmvPlan& p, void* y, hipStream_t st) {
+template <int BITS, bool G64, int NMAT>
+static int qmv_steps(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
   switch (p.steps) {
-    case 1: return qmv_rows<BITS, G64, 1>(x, M, K, wq, s, b, N, p, y, st);
-    case 2: return qmv_rows<BITS, G64, 2>(x, M, K, wq, s, b, N, p, y, st);
-    case 3: return qmv_rows<BITS, G64, 3>(x, M, K, wq, s, b, N, p, y, st);
-    case 4: return qmv_rows<BITS, G64, 4>(x, M, K, wq, s, b, N, p, y, st);
-    case 6: return qmv_rows<BITS, G64, 6>(x, M, K, wq, s, b, N, p, y, st);
-    default: return qmv_rows<BITS, G64, 8>(x, M, K, wq, s, b, N, p, y, st);
+    case 1: return qmv_rows<BITS, G64, 1, NMAT>(a, p, st);
+    case 2: return qmv_rows<BITS, G64, 2, NMAT>(a, p, st);
+    case 3: return qmv_rows<BITS, G64, 3, NMAT>(a, p, st);
+    case 4: return qmv_rows<BITS, G64, 4, NMAT>(a, p, st);
+    case 6: return qmv_rows<BITS, G64, 6, NMAT>(a, p, st);
+    default: return qmv_rows<BITS, G64, 8, NMAT>(a, p, st);
   }
+}
+
+template <int NMAT>
+static int qmv_kind(const QmvArgs& a, int gs, int bits, const QmvPlan& p, hipStream_t st) {
+  if (bits == 8) {
+    if (gs == 64) return qmv_steps<8, true, NMAT>(a, p, st);
+    return qmv_steps<8, false, NMAT>(a, p, st);
+  }
+  if (gs == 64) return qmv_steps<4, true, NMAT>(a, p, st);
+  return qmv_steps<4, false, NMAT>(a, p, st);
+}
+
+static bool buffers_fit(int64_t M, int64_t K, int64_t N) {
+  const int64_t lim = (int64_t)1 << 31;  // every buffer (Q8 weights: N*K bytes) under 2 GiB
+  return N * K < lim && M * K * 2 < lim;
 }
 
 bool qmv_mfma_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int64_t N, int gs, int bits) {
-  const int64_t lim = (int64_t)1 << 31;
-  if (x_dtype != MLXQ_BFLOAT16 || sb_dtype != MLXQ_BFLOAT16) return false;
-  // every buffer (Q8 weights are the largest, N*K bytes) under 2 GiB
-  if (N * K >= lim || M * K * 2 >= lim) return false;
+  if (x_dtype != MLXQ_BFLOAT16 || sb_dtype != MLXQ_BFLOAT16 || !buffers_fit(M, K, N)) return false;
   QmvPlan p;
-  return qmv_plan(M, K, gs, bits, p);
+  return qmv_plan(M, K, gs, bits, 1, p);
 }
 
 int run_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
                  int64_t N, int gs, int bits, void* y, hipStream_t st) {
   QmvPlan p;
-  if (!qmv_plan(M, K, gs, bits, p))
+  if (!qmv_plan(M, K, gs, bits, 1, p))
     return set_error(MLXQ_EINVAL, "qmv: no GEMV plan for M=%lld K=%lld", (long long)M, (long long)K);
-  if (bits == 8) {
-    if (gs == 64) return qmv_steps<8, true>(x, M, K, wq, s, b, N, p, y, st);
-    return qmv_steps<8, false>(x, M, K, wq, s, b, N, p, y, st);
-  }
-  if (gs == 64) return qmv_steps<4, true>(x, M, K, wq, s, b, N, p, y, st);
-  return qmv_steps<4, false>(x, M, K, wq, s, b, N, p, y, st);
+  const QmvArgs a = {x, M, K, N, wq, s, b, nullptr, nullptr, nullptr, y};
+  return qmv_kind<1>(a, gs, bits, p, st);
+}
+
+bool swiglu_qmv_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int64_t F, int gs, int bits) {
+  if (x_dtype != MLXQ_BFLOAT16 || sb_dtype != MLXQ_BFLOAT16 || !buffers_fit(M, K, F)) return false;
+  QmvPlan p;
+  return qmv_plan(M, K, gs, bits, 2, p);
+}
+
+int run_swiglu_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq_g, const void* s_g,
+                   const void* b_g, const uint32_t* wq_u, const void* s_u, const void* b_u, int64_t F,
+                   int gs, int bits, void* h, hipStream_t st) {
+  QmvPlan p;
+  if (!qmv_plan(M, K, gs, bits, 2, p))
+    return set_error(MLXQ_EUNSUPPORTED, "swiglu: no fused GEMV plan for M=%lld K=%lld", (long long)M,
+                     (long long)K);
+  const QmvArgs a = {x, M, K, F, wq_g, s_g, b_g, wq_u, s_u, b_u, h};
+  return qmv_kind<2>(a, gs, bits, p, st);
 }
 
 }  // namespace mlxq

@@ -8,13 +8,13 @@ All compute runs in libmlxq_hip.so (hand-written HIP for gfx950) through its C A
 from ._lib import (MLXQ_ACT_GELU, MLXQ_ACT_NONE, MLXQ_BFLOAT16, MLXQ_FLOAT32, MlxqError,
                    LIB_PATH, load)
 from .ops import (DEFAULT_GROUP_SIZE, dequantize, embedding, linear, linear_workspace_size,
-                  packed_bits, qmm, qmv, quantize, quantized_matmul)
+                  packed_bits, qmm, qmv, quantize, quantized_matmul, swiglu)
 from .nn import Adapter, AdaptableLinear, QuantizedLinear, TokenEmbedding, lin, quantize_map
 from . import io
 
 __all__ = [
     "MLXQ_ACT_GELU", "MLXQ_ACT_NONE", "MLXQ_BFLOAT16", "MLXQ_FLOAT32", "MlxqError", "LIB_PATH",
     "load", "DEFAULT_GROUP_SIZE", "dequantize", "embedding", "linear", "linear_workspace_size",
-    "packed_bits", "qmm", "qmv", "quantize", "quantized_matmul", "Adapter", "AdaptableLinear",
+    "packed_bits", "qmm", "qmv", "quantize", "quantized_matmul", "swiglu", "Adapter", "AdaptableLinear",
     "QuantizedLinear", "TokenEmbedding", "lin", "quantize_map", "io",
 ]

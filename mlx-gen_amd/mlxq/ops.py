@@ -138,6 +138,24 @@ def embedding(ids, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bit
     return out.reshape(*ids.shape, hidden)
 
 
+def swiglu(x, gate, up, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4, out=None):
+    """Fused decode SwiGLU h = silu(gate(x)) * up(x) (mlx-gen-sensenova/src/qwen3.rs:178-181), gate
+    and up given as packed (wq, scales, biases) triples of shape [F, K].  Decode form only (bf16,
+    M <= 8); other shapes raise MlxqError with status MLXQ_EUNSUPPORTED."""
+    _need_gpu(x, *gate, *up)
+    K = x.shape[-1]
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K).contiguous()
+    g = [t.contiguous() for t in gate]
+    u = [t.contiguous() for t in up]
+    M, F = x2.shape[0], g[0].shape[0]
+    h = out if out is not None else torch.empty((M, F), dtype=x.dtype, device=x.device)
+    check(_lib.load().mlxq_swiglu(_ptr(x2), _dt(x2), M, K, _ptr(g[0]), _ptr(g[1]), _ptr(g[2]), _ptr(u[0]),
+                                  _ptr(u[1]), _ptr(u[2]), _dt(g[1]), F, group_size, bits, _ptr(h),
+                                  _stream(x.device)))
+    return h.reshape(*lead, F)
+
+
 def linear_workspace_size(M: int, N: int, rank: int) -> int:
     return int(_lib.load().mlxq_linear_workspace_size(M, N, rank))
 

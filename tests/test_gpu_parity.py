@@ -286,6 +286,55 @@ def test_qmv_config4_shapes(mlxq, M, K, N, gs, bits):
     assert_close(y, ref, f"qmv M={M} K={K} N={N} gs={gs} b={bits}")
 
 
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+@pytest.mark.parametrize("K,F,Nd,gs,bits", [(3072, 8192, 3072, 64, 4), (1024, 640, 256, 128, 8),
+                                            (512, 192, 64, 64, 4)])
+def test_swiglu_decode_mlp_vs_oracle(mlxq, M, K, F, Nd, gs, bits):
+    """Decode MLP of qwen3.rs:178-181 as two launches: the fused gate/up SwiGLU GEMV, then the
+    down GEMV; h and y against the oracle's op-by-op MLP (exact-f32 dequant, bf16 rounding per op)."""
+    banner("swiglu mlp", M, K, F, Nd, gs, bits)
+    rng = np.random.default_rng(M * 7 + K + F + bits)
+    x = bf16_normal(rng, (M, K))
+    trip = [oracle.quantize(bf16_normal(rng, shape, 0.02), gs, bits, sb_bf16=True)
+            for shape in ((F, K), (F, K), (Nd, F))]
+    g, u, d = [(wq_to_gpu(t[0]), to_gpu(t[1]), to_gpu(t[2])) for t in trip]
+    h = mlxq.swiglu(to_gpu(x), g, u, gs, bits)
+    y = mlxq.quantized_matmul(h, *d, True, gs, bits)
+    ref_h, ref_y = oracle.swiglu_mlp(x, trip[0], trip[1], trip[2], gs, bits, w_bf16=False, act_bf16=True)
+    assert_close(to_np(h), ref_h, f"swiglu h M={M}")
+    assert_close(to_np(y), oracle.quantized_matmul(to_np(h), *trip[2], gs, bits, w_bf16=False,
+                                                   out_bf16=True), f"swiglu y M={M}")
+    assert_close(to_np(y), ref_y, f"swiglu y vs oracle mlp M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_swiglu_ragged_rows(mlxq, M):
+    """F = 40 rows (not a multiple of the 16-row workgroup): h against silu(g) * u op by op."""
+    banner("swiglu ragged", M)
+    rng = np.random.default_rng(40 + M)
+    x = bf16_normal(rng, (M, 512))
+    tg, tu = [oracle.quantize(bf16_normal(rng, (40, 512), 0.02), 64, 4, sb_bf16=True) for _ in range(2)]
+    h = mlxq.swiglu(to_gpu(x), [wq_to_gpu(tg[0]), to_gpu(tg[1]), to_gpu(tg[2])],
+                    [wq_to_gpu(tu[0]), to_gpu(tu[1]), to_gpu(tu[2])], 64, 4)
+    gr = oracle.quantized_matmul(x, *tg, 64, 4, w_bf16=False, out_bf16=True)
+    ur = oracle.quantized_matmul(x, *tu, 64, 4, w_bf16=False, out_bf16=True)
+    ref = oracle.bf16_round(np.vectorize(oracle.silu)(gr).astype(np.float32) * ur)
+    assert_close(to_np(h), ref, f"swiglu ragged M={M}")
+
+
+def test_swiglu_outside_the_decode_form_is_unsupported(mlxq):
+    banner("swiglu unsupported")
+    rng = np.random.default_rng(9)
+    t = oracle.quantize(bf16_normal(rng, (64, 256), 0.02), 64, 4, sb_bf16=True)
+    g = (wq_to_gpu(t[0]), to_gpu(t[1]), to_gpu(t[2]))
+    with pytest.raises(mlxq.MlxqError) as e:
+        mlxq.swiglu(to_gpu(bf16_normal(rng, (9, 256))), g, g, 64, 4)
+    assert e.value.status == 2
+    with pytest.raises(mlxq.MlxqError) as e:
+        mlxq.swiglu(to_gpu(bf16_normal(rng, (2, 256)), torch.float32), g, g, 64, 4)
+    assert e.value.status == 2
+
+
 def test_f32_activations_large_m(mlxq):
     """f32 activations at GEMM-sized M keep exact-f32 semantics (the FLUX.1 f32 stream)."""
     banner("f32 large M")
