@@ -117,8 +117,10 @@ def bench_gemv(mlxq, torch, reps=20):
     """Config 4: decode MLP GEMVs (Q4 g64) gate/up [8192,3072] and down [3072,8192].
 
     The weights are rotated over 8 MLP copies (340 MB, more than the 256 MB Infinity Cache), and
-    one replay of a captured HIP graph runs 8 MLPs (24 GEMV launches) back to back, so the rate
-    is GPU time including the gaps between kernels but without host launch overhead."""
+    one replay of a captured HIP graph runs 8 MLPs back to back, so the rate is GPU time
+    including the gaps between kernels but without host launch overhead.  Two forms: three GEMV
+    launches per MLP (gate, up, down, then silu(g)*u left to the caller) and the fused form
+    (one SwiGLU launch reading gate and up, then down), which also does the activation."""
     dev = torch.device("cuda:0")
     K, F = 3072, 8192
     copies = []
@@ -136,6 +138,7 @@ def bench_gemv(mlxq, torch, reps=20):
         hh = gen_bf16((M, F), 1.0, 8, dev)
         yg = torch.empty((M, F), dtype=torch.bfloat16, device=dev)
         yu = torch.empty((M, F), dtype=torch.bfloat16, device=dev)
+        h = torch.empty((M, F), dtype=torch.bfloat16, device=dev)
         yd = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
 
         def mlps():
@@ -144,32 +147,22 @@ def bench_gemv(mlxq, torch, reps=20):
                 mlxq.qmv(x, *u, 64, 4, out=yu)
                 mlxq.qmv(hh, *d, 64, 4, out=yd)
 
-        side = torch.cuda.Stream(dev)
-        side.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(side):
-            mlps()  # warm-up outside capture (one-time kernel attribute setup)
-        torch.cuda.current_stream(dev).wait_stream(side)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            mlps()
-        for _ in range(3):
-            graph.replay()
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            graph.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (reps * len(copies))
-        nbytes = 2 * wbytes_gu + wbytes_d + 2 * (2 * M * K) + 2 * (2 * M * F) + 2 * M * F + 2 * M * K
-        out[f"M{M}"] = {"us_per_mlp": round(us, 3), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
-                        "bytes_per_mlp": nbytes}
-        del graph
-    out["note"] = ("3 GEMV launches per decode MLP (gate, up, down) replayed from a HIP graph, "
-                   "so the rate includes inter-kernel gaps; per-kernel durations are in profiles/")
+        def fused():
+            for (g, u, d) in copies:
+                mlxq.swiglu(x, g, u, 64, 4, out=h)
+                mlxq.qmv(h, *d, 64, 4, out=yd)
+
+        us3 = graph_ms(torch, mlps, inner=1, reps=reps) * 1e3 / len(copies)
+        us2 = graph_ms(torch, fused, inner=1, reps=reps) * 1e3 / len(copies)
+        nbytes3 = 2 * wbytes_gu + wbytes_d + 2 * (2 * M * K) + 2 * (2 * M * F) + 2 * M * F + 2 * M * K
+        nbytes2 = 2 * wbytes_gu + wbytes_d + 2 * M * K + 2 * M * F + 2 * M * F + 2 * M * K
+        out[f"M{M}"] = {"us_per_mlp": round(us3, 3), "GBs": round(nbytes3 / (us3 * 1e-6) / 1e9, 1),
+                        "bytes_per_mlp": nbytes3,
+                        "fused_us_per_mlp": round(us2, 3),
+                        "fused_GBs": round(nbytes2 / (us2 * 1e-6) / 1e9, 1)}
+    out["note"] = ("per decode MLP, replayed from a HIP graph (rates include inter-kernel gaps): "
+                   "3 GEMV launches (gate, up, down) and the fused form (SwiGLU gate/up launch + "
+                   "down launch); per-kernel durations are in profiles/")
     return out
 
 
