@@ -86,6 +86,15 @@ __device__ __forceinline__ void swap_lane_halves(uint32_t& lo_keep, uint32_t& hi
   hi_keep = r[1];
 }
 
+// Row pitch in floats of the per-row (s, zc) pair table in LDS: at least 2G, a multiple of 4 (the
+// fold reads 16 bytes) and an odd multiple of 4, so the 16 rows read in one step (one per lane)
+// land on 16 distinct 16-byte bank quads.  A pitch of exactly 2G puts every row on the same banks
+// whenever 2G is a multiple of 64 (K = 8192, group 64: a 16-way conflict on every fold).
+__host__ __device__ constexpr int sz_pitch(int G) {
+  const int p = (2 * G + 3) & ~3;
+  return (p & 4) ? p : p + 4;
+}
+
 }  // namespace
 
 // Launch contract (checked on the host by qmv_plan): 1 <= M <= MR, K % (512/BITS) == 0,
@@ -123,7 +132,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   const int G = K / GS;
   const int ls0 = wave * STEPS;     // this wave's load steps: [ls0, ls0 + STEPS)
   const int x_stride = 2 * K + 16;  // LDS row pitch: rows start on different banks
-  const int sz_lds = M * x_stride;  // then (s, b - 128 s) or (s, b) as f32 pairs, [mat][16 rows][G]
+  const int sz_lds = M * x_stride;  // then (s, b - 128 s) or (s, b) as f32 pairs, [mat][16 rows][P]
+  const int P = sz_pitch(G);
 
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(x), (short)0, M * K * 2, kBufferFlags);
@@ -186,16 +196,22 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
     }
   }
   if (stid < sb_chunks) {
-    f32x4 pr[4];
+    // Chunk stid holds entries [8 stid, 8 stid + 8) of the workgroup's [16 rows][G] scales; the
+    // run may cross into the next row when G is not a multiple of 8.
+    int r = (stid * 8) / G;
+    int c = stid * 8 - r * G;
+    float* szw = reinterpret_cast<float*>(lds + sz_lds) + smat * 16 * P;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float s0 = __uint_as_float(cs[j] << 16), s1 = __uint_as_float(cs[j] & 0xffff0000u);
-      const float z0 = __uint_as_float(cz[j] << 16), z1 = __uint_as_float(cz[j] & 0xffff0000u);
-      pr[j] = f32x4{s0, BITS == 4 ? fmaf(-128.0f, s0, z0) : z0, s1, BITS == 4 ? fmaf(-128.0f, s1, z1) : z1};
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t sw = cs[j >> 1], zw = cz[j >> 1];
+      const float sv = __uint_as_float((j & 1) ? (sw & 0xffff0000u) : (sw << 16));
+      const float zv = __uint_as_float((j & 1) ? (zw & 0xffff0000u) : (zw << 16));
+      *reinterpret_cast<f32x2*>(szw + r * P + 2 * c) = f32x2{sv, BITS == 4 ? fmaf(-128.0f, sv, zv) : zv};
+      if (++c == G) {
+        c = 0;
+        ++r;
+      }
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<f32x4*>(lds + sz_lds + smat * 128 * G + stid * 64 + j * 16) = pr[j];
   }
   __syncthreads();
 
@@ -211,7 +227,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
     else k = (q < 2 ? 64 + 32 * q : 32 * q + 16) + 8 * (i - 2);
     xa[i] = lds + (c16 < M ? c16 : 0) * x_stride + (ls0 * CPL + k) * 2;
   }
-  const float* sz = reinterpret_cast<const float*>(lds + sz_lds + mat * 128 * G) + 2 * c16 * G;
+  const float* sz = reinterpret_cast<const float*>(lds + sz_lds) + (mat * 16 + c16) * P;
   bf16x8 ones;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
@@ -305,7 +321,7 @@ bool qmv_plan(int64_t M, int64_t K, int gs, int bits, int nmat, QmvPlan& p) {
     const int64_t nt = waves * 64;
     if ((KC + nt - 1) / nt > kCopySlots / mr) continue;
     if (nmat * 2 * G > nt) continue;  // one scale chunk per thread
-    const int64_t operands = M * (2 * K + 16) + nmat * 16 * G * 8;
+    const int64_t operands = M * (2 * K + 16) + nmat * 16 * sz_pitch((int)G) * 4;
     const int64_t red = waves * 16 * 17 * 4;
     const int64_t lds = operands > red ? operands : red;
     if (lds > kMaxLds) continue;
