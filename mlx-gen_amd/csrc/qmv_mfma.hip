@@ -36,7 +36,7 @@ namespace {
 
 constexpr int kBufferFlags = 0x00020000;
 constexpr int kMaxWaves = 16;  // waves per workgroup (they split K)
-constexpr int kCopySlots = 8;  // 16-byte activation chunks per thread in the LDS copy
+constexpr int kCopySlots = 8;  // 16-byte activation chunks a lane stages (registers), all rows
 constexpr int kMaxLds = 160 * 1024;
 constexpr uint32_t kOob = 0x7ffffff0u;  // buffer offset past every resource: loads return zero
 
@@ -97,13 +97,27 @@ __host__ __device__ constexpr int sz_pitch(int G) {
 
 }  // namespace
 
+// Scale/bias group slots one wave keeps: the groups its load steps touch (a group 128 of Q8 spans
+// two steps and may straddle two waves, hence the spare slot).
+__host__ __device__ constexpr int qmv_wave_groups(int bits, bool g64, int steps) {
+  return bits == 8 && !g64 ? (steps + 2) / 2 : (bits == 4 && g64 ? 2 * steps : steps);
+}
+
+// Bytes of LDS one wave owns: its activation rows (M rows of steps * 64 bytes of codes' worth of
+// activations, padded so rows start on different banks) and its (s, zc) table.
+__host__ __device__ constexpr int qmv_wave_lds(int bits, bool g64, int steps, int M) {
+  return M * (steps * (512 / bits) * 2 + 16) + 16 * sz_pitch(qmv_wave_groups(bits, g64, steps)) * 4;
+}
+
 // Launch contract (checked on the host by qmv_plan): 1 <= M <= MR, K % (512/BITS) == 0,
-// bf16 scales and biases, LS = K*BITS/512 load steps per row with LS % STEPS == 0 and
-// blockDim.x = 64 * NMAT * LS/STEPS <= 1024, at most kCopySlots/MR activation chunks per thread
-// per row, at most one scale chunk per thread, dynamic LDS as computed by qmv_plan, every buffer
-// < 2 GiB.
+// K % group == 0, bf16 scales and biases, LS = K*BITS/512 load steps per row with
+// LS % STEPS == 0 and blockDim.x = 64 * NMAT * LS/STEPS <= 1024, dynamic LDS of at least
+// max(waves * qmv_wave_lds, waves * 16 * 17 * 4) bytes, every buffer < 2 GiB.
 // NMAT = 2 is the SwiGLU decode form: the second wave half streams the same 16 rows of a second
 // matrix (up) and the output is round(round(silu(round(x.Wg^T))) * round(x.Wu^T)).
+// Each wave stages only its own operands (its K range of the activations, the scales and biases
+// of its groups) into its own LDS region, so it starts on its weights as soon as its own operands
+// land; the only workgroup barrier is the final split-K reduction.
 template <int BITS, bool G64, int STEPS, int MR, int NMAT>
 __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
     const uint16_t* __restrict__ x, int M, int K, const uint32_t* __restrict__ wq,
@@ -114,7 +128,12 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   constexpr int GS = G64 ? 64 : 128;       // group size
   constexpr int NM = BITS == 4 ? 4 : 2;    // MFMAs per load step
   constexpr int E = MR < 4 ? MR : 4;       // result registers per lane that can hold a row < M
-  constexpr int SLOTS = kCopySlots / MR;   // activation chunks per thread per row
+  constexpr int XCH = STEPS * CPL / 8;     // 16-byte activation chunks per row in the wave's range
+  constexpr int XSL = (XCH + 63) / 64;     // ... per lane
+  constexpr int NGW = qmv_wave_groups(BITS, G64, STEPS);
+  constexpr int PW = sz_pitch(NGW);        // (s, zc) table row pitch, floats
+  constexpr int SBL = (16 * NGW + 63) / 64;  // scale entries per lane
+  constexpr int XW = STEPS * CPL * 2 + 16;   // LDS pitch of the wave's activation rows
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
 
   const int NT = blockDim.x;
@@ -130,94 +149,90 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   const int nn = n < N ? n : N - 1;
   const int rowbytes = K * BITS / 8;
   const int G = K / GS;
-  const int ls0 = wave * STEPS;     // this wave's load steps: [ls0, ls0 + STEPS)
-  const int x_stride = 2 * K + 16;  // LDS row pitch: rows start on different banks
-  const int sz_lds = M * x_stride;  // then (s, b - 128 s) or (s, b) as f32 pairs, [mat][16 rows][P]
-  const int P = sz_pitch(G);
+  const int ls0 = wave * STEPS;  // this wave's load steps: [ls0, ls0 + STEPS)
+  const int kb = ls0 * CPL;      // its first activation index
+  const int g0 = kb / GS;        // its first group
+  unsigned char* const wl = lds + wave_all * (M * XW + 16 * PW * 4);  // this wave's LDS region
+  float* const szw = reinterpret_cast<float*>(wl + M * XW);
 
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(x), (short)0, M * K * 2, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(mat ? wq2 : wq), (short)0, (int)((uint32_t)N * (uint32_t)rowbytes), kBufferFlags);
   // Rounded up to whole dwords: buffer range checks are per dword, and the last scale may share
-  // its dword with 2 bytes past the end (same aligned dword, so never another page; the extra
-  // value belongs to a row >= N, which is never stored).
+  // its dword with 2 bytes past the end (same aligned dword, so never another page).
   const int sb_total = (int)(((uint32_t)N * (uint32_t)G * 2u + 3u) & ~3u);
-  // Scale/bias chunks: threads [0, 2G) copy the first matrix's, [2G, 4G) the second's.
-  const int sb_chunks = 2 * G;  // 16 rows x G bf16 = 2G chunks of 16 bytes per matrix
-  const int smat = NMAT == 2 && tid >= sb_chunks ? 1 : 0;
-  const int stid = tid - smat * sb_chunks;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(smat ? scales2 : scales), (short)0, sb_total, kBufferFlags);
+      const_cast<uint16_t*>(mat ? scales2 : scales), (short)0, sb_total, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(smat ? biases2 : biases), (short)0, sb_total, kBufferFlags);
+      const_cast<uint16_t*>(mat ? biases2 : biases), (short)0, sb_total, kBufferFlags);
 
-  // 1. Workgroup operands first (small; they return before the weight stream): the activation
-  //    rows as 16-byte chunks, and the contiguous scale and bias rows of this workgroup's 16
-  //    weight rows (one 8-value chunk of each per thread).  Out-of-range chunks read as zero.
-  const int KC = K / 8;
-  u32x4 cx[MR][SLOTS];
+  // 1. The wave's own operands first (they return before its weight stream): its activation
+  //    range as 16-byte chunks, and the scale and bias of each (row, group) slot it folds.
+  //    Out-of-range loads read as zero.
+  u32x4 cx[MR][XSL];
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     if (m < M) {
 #pragma unroll
-      for (int i = 0; i < SLOTS; ++i) {
-        if (i * NT < KC) {
-          const int kc = tid + i * NT;
-          cx[m][i] = load16(rx, kc < KC ? (uint32_t)(m * K * 2 + kc * 16) : kOob);
-        }
+      for (int j = 0; j < XSL; ++j) {
+        const int c = lane + 64 * j;
+        cx[m][j] = load16(rx, c < XCH ? (uint32_t)((m * K + kb + c * 8) * 2) : kOob);
       }
     }
   }
-  const uint32_t sb_src = stid < sb_chunks ? (uint32_t)n0 * (uint32_t)G * 2u + (uint32_t)stid * 16u : kOob;
-  const u32x4 cs = load16(rs, sb_src);
-  const u32x4 cz = load16(rz, sb_src);
+  uint32_t cs[SBL], cz[SBL];
+#pragma unroll
+  for (int j = 0; j < SBL; ++j) {
+    const int e = lane + 64 * j;
+    const int r = e / NGW, gl = e - r * NGW;  // constant divisor
+    const bool ok = e < 16 * NGW && n0 + r < N && g0 + gl < G;
+    const uint32_t off = ok ? ((uint32_t)(n0 + r) * (uint32_t)G + (uint32_t)(g0 + gl)) * 2u : kOob;
+    cs[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+    cz[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rz, off, 0, 0);
+  }
 
-  // 2. The wave's whole weight stream.
+  // 2. The wave's whole weight stream, issued once every wave of the workgroup has issued its
+  //    operand loads: a CU's vector memory requests are served in order, and a wave whose small
+  //    operand loads queue behind its neighbours' weight streams waits microseconds for them.
+  //    (A bare s_barrier: nothing here waits for the loads themselves.)
+  __builtin_amdgcn_s_barrier();
   const uint32_t w_base = (uint32_t)nn * (uint32_t)rowbytes + (uint32_t)(ls0 * 64 + q * 16);
   u32x4 wv[STEPS];
 #pragma unroll
   for (int d = 0; d < STEPS; ++d) wv[d] = load16(rw, w_base + (uint32_t)d * 64u);
 
-  // 3. Operands into LDS.  Q4 activation runs are stored permuted to [0,2,4,6,1,3,5,7] so they
-  //    pair with the unpacked code layout without per-wave work.  Scales and biases become f32
-  //    pairs (s, b - 128 s) for Q4 and (s, b) for Q8, ready for the fold.
+  // 3. Operands into the wave's LDS region.  Q4 activation runs are stored permuted to
+  //    [0,2,4,6,1,3,5,7] so they pair with the unpacked code layout; scales and biases become
+  //    f32 pairs (s, b - 128 s) for Q4 and (s, b) for Q8, ready for the fold.  Only this wave
+  //    reads them back, so a wave-level ordering point replaces a workgroup barrier.
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     if (m < M) {
 #pragma unroll
-      for (int i = 0; i < SLOTS; ++i) {
-        if (i * NT < KC) {
-          const int kc = tid + i * NT;
-          if (kc < KC)
-            *reinterpret_cast<u32x4*>(lds + m * x_stride + kc * 16) = BITS == 4 ? perm_q4(cx[m][i]) : cx[m][i];
-        }
+      for (int j = 0; j < XSL; ++j) {
+        const int c = lane + 64 * j;
+        if (c < XCH)
+          *reinterpret_cast<u32x4*>(wl + m * XW + c * 16) = BITS == 4 ? perm_q4(cx[m][j]) : cx[m][j];
       }
     }
   }
-  if (stid < sb_chunks) {
-    // Chunk stid holds entries [8 stid, 8 stid + 8) of the workgroup's [16 rows][G] scales; the
-    // run may cross into the next row when G is not a multiple of 8.
-    int r = (stid * 8) / G;
-    int c = stid * 8 - r * G;
-    float* szw = reinterpret_cast<float*>(lds + sz_lds) + smat * 16 * P;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t sw = cs[j >> 1], zw = cz[j >> 1];
-      const float sv = __uint_as_float((j & 1) ? (sw & 0xffff0000u) : (sw << 16));
-      const float zv = __uint_as_float((j & 1) ? (zw & 0xffff0000u) : (zw << 16));
-      *reinterpret_cast<f32x2*>(szw + r * P + 2 * c) = f32x2{sv, BITS == 4 ? fmaf(-128.0f, sv, zv) : zv};
-      if (++c == G) {
-        c = 0;
-        ++r;
-      }
+  for (int j = 0; j < SBL; ++j) {
+    const int e = lane + 64 * j;
+    if (e < 16 * NGW) {
+      const int r = e / NGW, gl = e - r * NGW;
+      const float sv = __uint_as_float(cs[j] << 16), zv = __uint_as_float(cz[j] << 16);
+      *reinterpret_cast<f32x2*>(szw + r * PW + 2 * gl) = f32x2{sv, BITS == 4 ? fmaf(-128.0f, sv, zv) : zv};
     }
   }
-  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   // 4. Per load step: NM MFMAs x . codes and NM MFMAs x . ones (group sums), then the fold of
   //    each group, y += s*acc + zc*X.
-  const unsigned char* xa[NM];  // this lane's activation run for MFMA i at load step ls0
+  const unsigned char* xa[NM];  // this lane's activation run for MFMA i at the wave's first step
 #pragma unroll
   for (int i = 0; i < NM; ++i) {
     int k;
@@ -225,9 +240,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
     else if constexpr (!G64) k = 32 * q + 8 * i;
     else if (i < 2) k = (q < 2 ? 32 * q : 32 * (q - 2) + 16) + 8 * i;
     else k = (q < 2 ? 64 + 32 * q : 32 * q + 16) + 8 * (i - 2);
-    xa[i] = lds + (c16 < M ? c16 : 0) * x_stride + (ls0 * CPL + k) * 2;
+    xa[i] = wl + (c16 < M ? c16 : 0) * XW + k * 2;
   }
-  const float* sz = reinterpret_cast<const float*>(lds + sz_lds) + (mat * 16 + c16) * P;
+  const float* sz = szw + c16 * PW;
   bf16x8 ones;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
@@ -240,9 +255,20 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
     for (int e = 0; e < E; ++e) yacc[e] = fmaf(s, acc[e], fmaf(zc, xsum[e], yacc[e]));
   };
 
+  // Activation runs: only lanes of A rows c16 < M read them (at M = 1 that is 4 lanes of 64, a
+  // sixteenth of the LDS traffic).  The other lanes keep their previous (finite) contents: an A
+  // row m >= M only feeds result row m, which is never stored.
+  const bool row_lane = c16 < M;
+  bf16x8 a[NM];
+#pragma unroll
+  for (int i = 0; i < NM; ++i) a[i] = bf16x8{};
+
 #pragma unroll
   for (int d = 0; d < STEPS; ++d) {
-    const int ls = ls0 + d;
+    if (row_lane) {
+#pragma unroll
+      for (int i = 0; i < NM; ++i) a[i] = *reinterpret_cast<const bf16x8*>(xa[i] + d * (CPL * 2));
+    }
     uint32_t w[4] = {wv[d][0], wv[d][1], wv[d][2], wv[d][3]};
     if constexpr (BITS == 4 && G64) {
       swap_lane_halves(w[0], w[2]);
@@ -257,18 +283,18 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
       const int h = (BITS == 4 && G64) ? i >> 1 : 0;
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(xa[i] + d * (CPL * 2));
       const bf16x8 b = BITS == 4 ? unpack_q4(w[i]) : cvt_q8(w[2 * i], w[2 * i + 1]);
-      acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[h], 0, 0, 0);
-      xsum[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xsum[h], 0, 0, 0);
+      acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b, acc[h], 0, 0, 0);
+      xsum[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], ones, xsum[h], 0, 0, 0);
     }
     if constexpr (BITS == 4 && G64) {
-      const f32x4 p = *reinterpret_cast<const f32x4*>(sz + 4 * ls);  // groups 2ls, 2ls+1
+      const f32x4 p = *reinterpret_cast<const f32x4*>(sz + 4 * d);  // groups 2ls, 2ls+1
       fold(acc[0], xsum[0], p[0], p[1]);
       fold(acc[1], xsum[1], p[2], p[3]);
     } else {
-      const int g = (BITS == 4 || G64) ? ls : ls >> 1;  // Q4/128: one group per step; Q8: 64 codes
-      const f32x2 p = *reinterpret_cast<const f32x2*>(sz + 2 * g);
+      // Q4/128 and Q8/64: one group per step; Q8/128: a group every two steps
+      const int gl = (BITS == 4 || G64) ? d : ((ls0 + d) >> 1) - g0;
+      const f32x2 p = *reinterpret_cast<const f32x2*>(sz + 2 * gl);
       fold(acc[0], xsum[0], p[0], p[1]);
     }
   }
@@ -302,33 +328,42 @@ struct QmvPlan {
   int waves, steps, mr, lds;  // waves: all waves of the workgroup (per matrix x matrices)
 };
 
-constexpr int kStepChoices[] = {8, 6, 4, 3, 2, 1};
+constexpr int kStepChoices[] = {1, 2, 3, 4, 6, 8};
 
-// Picks the most load steps per wave (at most 8) that divide the row's load-step count, fit a
-// workgroup, and keep the activation copy within kCopySlots chunks per thread.  Long streams per
-// wave in small workgroups measured best: at 100 MB, 8 steps x 3 waves streams 5.4 TB/s against
-// 3.6 TB/s for 2 steps x 12 waves, and the decode shapes are no slower.
+// Picks the load steps per wave: among the counts that divide the row's load steps, fit a
+// workgroup of at most kMaxWaves waves and its LDS, the one whose workgroup comes closest to 8
+// waves (fewer steps on a tie).  Measured on the decode shapes (M = 1..8, K = 3072 and 8192, with
+// per-wave operand staging), about 8 waves of 3-8 steps finish first: a wave starts folding as
+// soon as its own operands arrive, and more, shorter waves spread the fold over the SIMDs, while
+// a 16-wave workgroup fills a CU on its own (128 registers per wave).  Eight steps with more than
+// one activation row exceed the 128 registers a 1024-thread workgroup allows (spills doubled the
+// time), so that combination is not used.
 bool qmv_plan(int64_t M, int64_t K, int gs, int bits, int nmat, QmvPlan& p) {
   if (M < 1 || M > 8 || (bits != 4 && bits != 8) || (gs != 64 && gs != 128)) return false;
   const int64_t cpl = 512 / bits;
   if (K <= 0 || K % cpl != 0 || K % gs != 0) return false;
-  const int64_t LS = K / cpl, KC = K / 8, G = K / gs;
+  const int64_t LS = K / cpl;
   const int mr = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
+  bool found = false;
+  int64_t best_cost = 0;
   for (int steps : kStepChoices) {
     if (LS % steps != 0) continue;
+    if (steps == 8 && mr > 1) continue;
     const int64_t waves = nmat * (LS / steps);
     if (waves > kMaxWaves) continue;
-    const int64_t nt = waves * 64;
-    if ((KC + nt - 1) / nt > kCopySlots / mr) continue;
-    if (nmat * 2 * G > nt) continue;  // one scale chunk per thread
-    const int64_t operands = M * (2 * K + 16) + nmat * 16 * sz_pitch((int)G) * 4;
+    // activation chunks a lane stages (registers): at most kCopySlots across the rows
+    if (mr * ((steps * cpl / 8 + 63) / 64) > kCopySlots) continue;
+    const int64_t operands = waves * (int64_t)qmv_wave_lds(bits, gs == 64, steps, (int)M);
     const int64_t red = waves * 16 * 17 * 4;
     const int64_t lds = operands > red ? operands : red;
     if (lds > kMaxLds) continue;
+    const int64_t cost = waves > 8 ? waves - 8 : 8 - waves;
+    if (found && cost >= best_cost) continue;
+    found = true;
+    best_cost = cost;
     p = {(int)waves, steps, mr, (int)lds};
-    return true;
   }
-  return false;
+  return found;
 }
 
 // Device operands of one launch (the second matrix is used by the SwiGLU form only).
@@ -362,11 +397,16 @@ static int launch_qmv_mfma(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
 
 template <int BITS, bool G64, int STEPS, int NMAT>
 static int qmv_rows(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
-  switch (p.mr) {
-    case 1: return launch_qmv_mfma<BITS, G64, STEPS, 1, NMAT>(a, p, st);
-    case 2: return launch_qmv_mfma<BITS, G64, STEPS, 2, NMAT>(a, p, st);
-    case 4: return launch_qmv_mfma<BITS, G64, STEPS, 4, NMAT>(a, p, st);
-    default: return launch_qmv_mfma<BITS, G64, STEPS, 8, NMAT>(a, p, st);
+  if constexpr (STEPS == 8) {  // qmv_plan uses 8 steps for one activation row only
+    if (p.mr != 1) return set_error(MLXQ_EINVAL, "qmv: 8 load steps per wave need M = 1");
+    return launch_qmv_mfma<BITS, G64, 8, 1, NMAT>(a, p, st);
+  } else {
+    switch (p.mr) {
+      case 1: return launch_qmv_mfma<BITS, G64, STEPS, 1, NMAT>(a, p, st);
+      case 2: return launch_qmv_mfma<BITS, G64, STEPS, 2, NMAT>(a, p, st);
+      case 4: return launch_qmv_mfma<BITS, G64, STEPS, 4, NMAT>(a, p, st);
+      default: return launch_qmv_mfma<BITS, G64, STEPS, 8, NMAT>(a, p, st);
+    }
   }
 }
 
