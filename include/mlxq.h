@@ -49,6 +49,9 @@ typedef enum {
 typedef enum {
   MLXQ_ACT_NONE = 0,
   MLXQ_ACT_GELU = 1, /* exact erf GELU, mlx-gen-flux/src/transformer.rs:975 */
+  /* tanh-approximate GELU as separate ops in the activation dtype, src/nn.rs:321-329 (FLUX
+   * single-stream FFN and GeluApprox, mlx-gen-flux/src/transformer.rs:506,708,979) */
+  MLXQ_ACT_GELU_TANH = 2,
 } mlxq_activation;
 
 /* Thread-local description of the last failure on this thread ("" if none). */

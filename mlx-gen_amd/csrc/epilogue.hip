@@ -129,6 +129,7 @@ __global__ void linear_epilogue_kernel(XT* __restrict__ y, int64_t M, int64_t N,
     o = Act<XT>::rnd(o + Act<XT>::rnd(Act<XT>::rnd(r) * scale));
   }
   if (act == MLXQ_ACT_GELU) o = gelu_erf(o);
+  else if (act == MLXQ_ACT_GELU_TANH) o = gelu_tanh<sizeof(XT) == 2>(o);
   Act<XT>::st(y, t, o);
 }
 

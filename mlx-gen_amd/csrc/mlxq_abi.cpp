@@ -274,7 +274,8 @@ int mlxq_linear(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
   hipStream_t st = (hipStream_t)stream;
   mlxq_epilogue none = {nullptr, nullptr, nullptr, 0, 1.0f, MLXQ_ACT_NONE};
   const mlxq_epilogue& e = ep ? *ep : none;
-  if (e.activation != MLXQ_ACT_NONE && e.activation != MLXQ_ACT_GELU)
+  if (e.activation != MLXQ_ACT_NONE && e.activation != MLXQ_ACT_GELU &&
+      e.activation != MLXQ_ACT_GELU_TANH)
     return set_error(MLXQ_EINVAL, "linear: unknown activation %d", e.activation);
   if (e.lora_rank < 0 || e.lora_rank > 256)
     return set_error(MLXQ_EINVAL, "linear: lora_rank %lld outside [0, 256]", (long long)e.lora_rank);

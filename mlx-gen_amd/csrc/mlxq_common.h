@@ -95,6 +95,21 @@ __device__ __forceinline__ float gelu_erf(float v) {
   return 0.5f * v * g;
 }
 
+// Tanh-approximate GELU, 0.5 x (1 + tanh(c (x + 0.044715 x^3))) with c = sqrt(2/pi), evaluated
+// as the separate ops of reference src/nn.rs:321-329: every op rounded to the activation dtype
+// (bf16 when BF16, else f32) and the constants cast to it first.  x^3 of a bf16 value is exact in
+// f32 (24 significant bits), so rounding the f32 cube once is the rounded power.
+template <bool BF16>
+__device__ __forceinline__ float gelu_tanh(float x) {
+  auto rnd = [](float v) { return BF16 ? round_bf16(v) : v; };
+  const float c = rnd(0.7978845608028654f);
+  const float k = rnd(0.044715f);
+  const float x3 = rnd(x * x * x);
+  const float inner = rnd(rnd(x + rnd(x3 * k)) * c);
+  const float gate = rnd(rnd(tanhf(inner)) + 1.0f);
+  return rnd(rnd(x * 0.5f) * gate);
+}
+
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
 }  // namespace mlxq

@@ -220,6 +220,7 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
           if (epi.bias) o = round_bf16(o + bn);
           if (lora) o = round_bf16(o + round_bf16(round_bf16(r[v]) * epi.lora_scale));
           if (epi.act == MLXQ_ACT_GELU) o = gelu_erf(o);
+          else if (epi.act == MLXQ_ACT_GELU_TANH) o = gelu_tanh<true>(o);
           if (n_ok && m < M) y[m * N + n] = f32_to_bf16_bits(o);
         }
         __builtin_amdgcn_sched_barrier(0);

@@ -353,6 +353,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
           if (epi.bias) o = round_bf16(o + bias_v[e]);
           if (lora) o = round_bf16(o + round_bf16(round_bf16(r[e]) * epi.lora_scale));
           if (epi.act == MLXQ_ACT_GELU) o = gelu_erf(o);
+          else if (epi.act == MLXQ_ACT_GELU_TANH) o = gelu_tanh<true>(o);
           v[e] = o;
         }
       }

@@ -21,6 +21,7 @@ MLXQ_EDEVICE = 3
 
 MLXQ_ACT_NONE = 0
 MLXQ_ACT_GELU = 1
+MLXQ_ACT_GELU_TANH = 2
 
 # Every symbol include/mlxq.h declares; tests check the library exports all of them.
 EXPORTS = (

@@ -23,6 +23,10 @@
  *                      src/adapters.rs:300-322,543-549 (bias add, then LoRA residual); its
  *                      rounding points follow MLX's per-op bf16 rounding (not pinned by a golden).
  *   oracle_gelu_erf / oracle_silu: textbook closed forms (special values tested).
+ *   oracle_gelu_tanh   pinned in f32 by the closed form (the reference test points of
+ *                      src/nn.rs:722-738 among them) and by its distance to the exact GELU; the
+ *                      per-op bf16 rounding points follow src/nn.rs:321-329 and are not pinned
+ *                      by a golden (parity unpinned for bf16).
  *
  * Data convention: every float tensor crosses this interface as f32.  A bf16 tensor is passed as
  * the f32 values it represents (exact), and the `*_bf16` flags say where results are rounded to
@@ -213,6 +217,23 @@ float oracle_gelu_erf(float v, int out_bf16) {
     return rnd((float)(0.5 * d * (1.0 + erf(d / sqrt(2.0)))), out_bf16);
 }
 
+/*
+ * Tanh-approximate GELU of reference src/nn.rs:321-329 (FLUX single-stream FFN,
+ * mlx-gen-flux/src/transformer.rs:506,708,979): the eager op sequence
+ *   x3 = x^3; inner = (x + x3 * 0.044715) * c; gate = tanh(inner) + 1; y = (x * 0.5) * gate
+ * with c = (float)sqrt(2/pi) taken in double, every constant cast to the activation dtype and every
+ * op's result rounded to it.  The cube and tanh are evaluated in double, then rounded.
+ */
+float oracle_gelu_tanh(float v, int out_bf16) {
+    const float c = rnd((float)sqrt(2.0 / 3.14159265358979323846), out_bf16);
+    const float k = rnd(0.044715f, out_bf16);
+    const double d = (double)v;
+    const float x3 = rnd((float)(d * d * d), out_bf16);
+    const float inner = rnd(rnd(v + rnd(x3 * k, out_bf16), out_bf16) * c, out_bf16);
+    const float gate = rnd(rnd((float)tanh((double)inner), out_bf16) + 1.0f, out_bf16);
+    return rnd(rnd(v * 0.5f, out_bf16) * gate, out_bf16);
+}
+
 /* SiLU v * sigmoid(v), as in the SwiGLU of reference mlx-gen-sensenova/src/qwen3.rs:179. */
 float oracle_silu(float v, int out_bf16) {
     double d = (double)v;
@@ -229,7 +250,8 @@ float oracle_silu(float v, int out_bf16) {
  *   r  = xa . B               B [r,N]             B = lora_up^T with alpha/rank folded in,
  *   r2 = r * scale            scale in act dtype  src/adapters/loader.rs:568-569,597)
  *   y  = y2 + r2              if lora
- *   y  = act(y)               act: 0 none, 1 exact-erf GELU (mlx-gen-flux/src/transformer.rs:975)
+ *   y  = act(y)               act: 0 none, 1 exact-erf GELU (mlx-gen-flux/src/transformer.rs:975),
+ *                              2 tanh GELU (src/nn.rs:321-329)
  * The activation is the caller's next op (FeedForward::forward, transformer.rs:970-977), listed
  * here so a fused epilogue has a checker.  w_bf16 as in oracle_qmm.
  */
@@ -262,6 +284,9 @@ int oracle_linear(const float* x, int64_t M, int64_t K, const uint32_t* wq, cons
     if (act == 1) {
 #pragma omp parallel for schedule(static)
         for (int64_t i = 0; i < M * N; ++i) y[i] = oracle_gelu_erf(y[i], act_bf16);
+    } else if (act == 2) {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < M * N; ++i) y[i] = oracle_gelu_tanh(y[i], act_bf16);
     }
     return ORACLE_OK;
 }

@@ -50,6 +50,8 @@ def lib():
                                         _f32p, _f32p]
         l.oracle_gelu_erf.argtypes = [ctypes.c_float, _int]
         l.oracle_gelu_erf.restype = ctypes.c_float
+        l.oracle_gelu_tanh.argtypes = [ctypes.c_float, _int]
+        l.oracle_gelu_tanh.restype = ctypes.c_float
         l.oracle_silu.argtypes = [ctypes.c_float, _int]
         l.oracle_silu.restype = ctypes.c_float
         l.oracle_num_threads.restype = _int
@@ -173,6 +175,10 @@ def swiglu_mlp(x, gate, up, down, group_size=64, bits=4, w_bf16=False, act_bf16=
 
 def gelu_erf(v, out_bf16=True):
     return lib().oracle_gelu_erf(float(v), int(out_bf16))
+
+
+def gelu_tanh(v, out_bf16=True):
+    return lib().oracle_gelu_tanh(float(v), int(out_bf16))
 
 
 def silu(v, out_bf16=True):

@@ -188,7 +188,7 @@ def test_qmm_wide_vs_oracle(mlxq, M, K, N, gs, bits):
     assert_close(y, ref, f"wide M={M} K={K} N={N} gs={gs} b={bits}")
 
 
-@pytest.mark.parametrize("act", [0, 1])
+@pytest.mark.parametrize("act", [0, 1, 2])
 def test_linear_wide_bias_lora_act(mlxq, act):
     banner("linear wide epilogue", act)
     rng = np.random.default_rng(77 + act)
@@ -350,8 +350,25 @@ def test_f32_activations_large_m(mlxq):
 
 # ---------------------------------------------------------------- fused linear epilogue
 
+@pytest.mark.parametrize("act", [1, 2])
+def test_linear_f32_activations_act(mlxq, act):
+    """f32 activations (the FLUX.1 f32 stream): bias and activation evaluated in f32, no bf16
+    rounding anywhere, against the oracle's f32 op sequence."""
+    banner("linear f32 act", act)
+    rng = np.random.default_rng(31 + act)
+    M, K, N = 24, 256, 72
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    wq, s, b = mlxq.quantize(to_gpu(w, torch.float32), 64, 8)
+    y = to_np(mlxq.linear(to_gpu(x, torch.float32), wq, s, b, 64, 8, bias=to_gpu(bias, torch.float32),
+                          activation=act))
+    rwq, rs, rb = oracle.quantize(w, 64, 8)
+    ref = oracle.linear(x, rwq, rs, rb, 64, 8, w_bf16=False, act_bf16=False, bias=bias, act=act)
+    assert errors(y, ref)[0] < 1e-5
+
 @pytest.mark.parametrize("M", [4, 300])
-@pytest.mark.parametrize("act", [0, 1])
+@pytest.mark.parametrize("act", [0, 1, 2])
 def test_linear_bias_lora_act(mlxq, M, act):
     banner("linear epilogue", M, act)
     rng = np.random.default_rng(21 + M + act)

@@ -158,6 +158,28 @@ def test_gelu_and_silu_closed_forms():
     assert oracle.gelu_erf(0.0) == 0.0 and oracle.gelu_erf(30.0) == 30.0
 
 
+def test_gelu_tanh_closed_form_and_exact_gelu():
+    """Tanh GELU (reference src/nn.rs:321-329).  In f32 it is the closed form, at the reference's
+    own test points (src/nn.rs:722-738) and on a sweep; with bf16 rounding per op it stays within
+    bf16 rounding of the closed form and within the approximation's known distance (< 1e-3
+    absolute) of the exact-erf GELU; tanh saturation gives x for large x and 0 for large -x."""
+    c = math.sqrt(2.0 / math.pi)
+
+    def closed(v):
+        return 0.5 * v * (1.0 + math.tanh(c * (v + 0.044715 * v ** 3)))
+
+    pts = [-2.0, -0.5, 0.0, 0.5, 1.0, 3.0] + [float(np.float32(t)) for t in np.linspace(-6, 6, 97)]
+    for v in pts:
+        assert oracle.gelu_tanh(v, out_bf16=False) == pytest.approx(closed(v), rel=2e-6, abs=1e-7)
+    for v in oracle.bf16_round(np.linspace(-6, 6, 241).astype(np.float32)):
+        g = oracle.gelu_tanh(float(v))
+        assert g == oracle.bf16_round(np.float32(g))
+        assert abs(g - closed(float(v))) <= 0.016 * abs(float(v)) + 1e-3
+        assert abs(g - oracle.gelu_erf(float(v))) <= 0.016 * abs(float(v)) + 2e-3
+    assert oracle.gelu_tanh(0.0) == 0.0
+    assert oracle.gelu_tanh(8.0) == 8.0 and oracle.gelu_tanh(-8.0) == 0.0
+
+
 def test_linear_sequence_rounds_like_separate_ops():
     """bias then LoRA residual, each rounded to bf16, equals composing the pieces by hand."""
     rng = np.random.default_rng(4)
