@@ -137,6 +137,21 @@ int mlxq_linear(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
                 size_t workspace_bytes, void* stream);
 
 /*
+ * Stacked-expert projection — Proj::forward of the quantized MoE experts
+ * (mlx-gen-lens/src/text_encoder/gpt_oss.rs:412-425, quantized_matmul(x, wq, s, b, true) + bias)
+ * run for every expert of a stacked pack split along axis 0 (mlx-gen-lens/src/quant.rs:93-137):
+ *   for e in [0, E):  y[e] = round(round(x[e] . dequant(wq[e])^T) + bias[e])   (round() to x_dtype)
+ * wq [E, N, K*bits/32], scales/biases [E, N, K/group_size] (sb_dtype), bias [E, N] in x_dtype or
+ * NULL, y [E, M, N].  x is [M, K] shared by every expert when x_per_expert == 0 (the gate_up
+ * projection of gpt_oss.rs:702), else [E, M, K] (the down projection of :714).  Each expert's
+ * result equals the single-matrix mlxq_linear with that bias; bf16 x with M > 8 runs every expert
+ * in one GEMM launch.
+ */
+int mlxq_qmm_experts(const void* x, int x_dtype, int x_per_expert, int64_t E, int64_t M, int64_t K,
+                     const uint32_t* wq, const void* scales, const void* biases, int sb_dtype,
+                     const void* bias, int64_t N, int group_size, int bits, void* y, void* stream);
+
+/*
  * Fused SwiGLU gate/up for decode — the first two ops of Mlp::forward
  * (mlx-gen-sensenova/src/qwen3.rs:178-181): h = multiply(silu(gate.forward(x)), up.forward(x))
  * with gate/up quantized linears [F,K] sharing x [M,K]; one launch streams both weight matrices:

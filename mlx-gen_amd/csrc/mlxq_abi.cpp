@@ -262,6 +262,48 @@ int mlxq_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t 
   return run_cast(src, src_dtype, dst, dst_dtype, n, (hipStream_t)stream);
 }
 
+int mlxq_qmm_experts(const void* x, int x_dtype, int x_per_expert, int64_t E, int64_t M, int64_t K,
+                     const uint32_t* wq, const void* scales, const void* biases, int sb_dtype,
+                     const void* bias, int64_t N, int group_size, int bits, void* y, void* stream) {
+  g_err[0] = 0;
+  int rc;
+  if (E < 0) return set_error(MLXQ_EINVAL, "qmm_experts: E=%lld < 0", (long long)E);
+  if ((rc = check_mm("qmm_experts", x, x_dtype, M, K, wq, scales, biases, sb_dtype, N, group_size,
+                     bits, y)))
+    return rc;
+  if (E == 0 || M == 0 || N == 0) return MLXQ_OK;
+  const int xb = x_dtype == MLXQ_BFLOAT16 ? 2 : 4;
+  const int sbb = sb_dtype == MLXQ_BFLOAT16 ? 2 : 4;
+  if (bias && (rc = check_aligned("qmm_experts", "bias", bias, xb))) return rc;
+  QmmBatch bat;
+  bat.count = E;
+  bat.x = x_per_expert ? M * K : 0;
+  bat.w = N * (K * bits / 32);
+  bat.sb = N * (K / group_size);
+  bat.y = M * N;
+  bat.bias = N;
+  hipStream_t st = (hipStream_t)stream;
+  // All experts in one launch of the wide GEMM (grid.y = expert) when it applies: per-expert
+  // problems of an encoder batch are a few dozen tiles each, too few to fill 256 CUs alone.
+  const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  if (x_dtype == MLXQ_BFLOAT16 && M > 8 && K % 64 == 0 && E * tiles >= 128 && E <= 65535 &&
+      qmm_wide_fits(M, K, N, group_size, bits, sbb)) {
+    const QmmEpilogue qe = {(const uint16_t*)bias, nullptr, nullptr, 0, 1.0f, MLXQ_ACT_NONE};
+    return run_qmm_wide(x, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y, qe, st, bat);
+  }
+  // Otherwise expert by expert through the single-matrix paths (same rounding points).
+  for (int64_t e = 0; e < E; ++e) {
+    const mlxq_epilogue ep = {bias ? (const char*)bias + e * bat.bias * xb : nullptr, nullptr, nullptr,
+                              0, 1.0f, MLXQ_ACT_NONE};
+    if ((rc = mlxq_linear((const char*)x + e * bat.x * xb, x_dtype, M, K, wq + e * bat.w,
+                          (const char*)scales + e * bat.sb * sbb, (const char*)biases + e * bat.sb * sbb,
+                          sb_dtype, N, group_size, bits, &ep, (char*)y + e * bat.y * xb, nullptr, 0,
+                          stream)))
+      return rc;
+  }
+  return MLXQ_OK;
+}
+
 int mlxq_linear(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
                 const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
                 int bits, const mlxq_epilogue* ep, void* y, void* workspace, size_t workspace_bytes,

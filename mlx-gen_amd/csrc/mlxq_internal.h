@@ -16,6 +16,14 @@ struct QmmEpilogue {
   int act;               // mlxq_activation
 };
 
+// A stacked launch over `count` matrices of the same shape (the experts of an [E, out, ...] pack):
+// matrix e uses each operand's base pointer advanced by e times its stride (in elements of that
+// operand; a zero stride shares the operand, e.g. one activation matrix for every expert).
+struct QmmBatch {
+  int64_t count = 1;
+  int64_t x = 0, w = 0, sb = 0, y = 0, bias = 0;
+};
+
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
@@ -31,7 +39,7 @@ int run_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void*
 bool qmm_wide_fits(int64_t M, int64_t K, int64_t N, int gs, int bits, int sb_bytes);
 int run_qmm_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
                  int sb_dtype, int64_t N, int gs, int bits, void* y, const QmmEpilogue& epi,
-                 hipStream_t st);
+                 hipStream_t st, const QmmBatch& batch = QmmBatch{});
 bool qmv_mfma_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int64_t N, int gs, int bits);
 int run_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
                  int64_t N, int gs, int bits, void* y, hipStream_t st);

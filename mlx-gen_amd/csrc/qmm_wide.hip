@@ -111,7 +111,7 @@ template <typename SB, int BITS, int GS, int WAVES, bool FUSED>
 __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, const uint32_t* __restrict__ wq,
     const SB* __restrict__ scales, const SB* __restrict__ biases, int64_t N,
-    uint16_t* __restrict__ y, QmmEpilogue epi) {
+    uint16_t* __restrict__ y, QmmEpilogue epi, QmmBatch bat) {
   constexpr int NT = WAVES * 64;
   constexpr int TMW = kBM / 32;          // m sub-tiles per wave (all 256 rows)
   constexpr int TNW = kBN / WAVES / 32;  // n sub-tiles per wave
@@ -121,6 +121,16 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   static_assert(TNW >= 1 && A_PER >= 1 && A_ROWS % 16 == 0, "tile/wave shape");
   __shared__ __attribute__((aligned(16))) unsigned char smem[3][kBM * 128];
 
+  // Stacked launch: grid.y selects the matrix (expert); one matrix has all strides zero.
+  if (gridDim.y > 1) {
+    const int64_t e = blockIdx.y;
+    x += e * bat.x;
+    wq += e * bat.w;
+    scales += e * bat.sb;
+    biases += e * bat.sb;
+    y += e * bat.y;
+    if (epi.bias) epi.bias += e * bat.bias;
+  }
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, r32 = lane & 31, half = lane >> 5;
   const int64_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
@@ -381,27 +391,29 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
 template <typename SB, int BITS, int GS, int WAVES>
 static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                          const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st,
-                         int64_t tiles) {
+                         int64_t tiles, const QmmBatch& bat) {
   const bool fused = epi.bias || epi.rank16 || epi.act != MLXQ_ACT_NONE;
+  const dim3 grid((unsigned)tiles, (unsigned)bat.count);
   if (fused)
-    hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, true>), dim3((unsigned)tiles),
-                       dim3(WAVES * 64), 0, st, (const uint16_t*)x, M, K, wq, (const SB*)s,
-                       (const SB*)b, N, (uint16_t*)y, epi);
+    hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, true>), grid, dim3(WAVES * 64), 0, st,
+                       (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi,
+                       bat);
   else
-    hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, false>), dim3((unsigned)tiles),
-                       dim3(WAVES * 64), 0, st, (const uint16_t*)x, M, K, wq, (const SB*)s,
-                       (const SB*)b, N, (uint16_t*)y, epi);
+    hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, false>), grid, dim3(WAVES * 64), 0, st,
+                       (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi,
+                       bat);
   return check_launch("qmm_wide");
 }
 
 template <typename SB, int BITS, int GS>
 static int launch_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
-                       const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st) {
+                       const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st,
+                       const QmmBatch& bat) {
   const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
-  if (tiles == 0) return MLXQ_OK;
-  if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm: problem too large");
+  if (tiles == 0 || bat.count == 0) return MLXQ_OK;
+  if (tiles > 0x7fffffff || bat.count > 65535) return set_error(MLXQ_EINVAL, "qmm: problem too large");
   // 8 waves (two per SIMD) measured faster than 4 waves with twice the columns per wave.
-  return launch_wide_w<SB, BITS, GS, 8>(x, M, K, wq, s, b, N, y, epi, st, tiles);
+  return launch_wide_w<SB, BITS, GS, 8>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
 }
 
 bool qmm_wide_fits(int64_t M, int64_t K, int64_t N, int gs, int bits, int sb_bytes) {
@@ -411,9 +423,9 @@ bool qmm_wide_fits(int64_t M, int64_t K, int64_t N, int gs, int bits, int sb_byt
 
 int run_qmm_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
                  int sb_dtype, int64_t N, int gs, int bits, void* y, const QmmEpilogue& epi,
-                 hipStream_t st) {
+                 hipStream_t st, const QmmBatch& batch) {
 #define MLXQ_W(SB, B, G) \
-  if (bits == B && gs == G) return launch_wide<SB, B, G>(x, M, K, wq, s, b, N, y, epi, st);
+  if (bits == B && gs == G) return launch_wide<SB, B, G>(x, M, K, wq, s, b, N, y, epi, st, batch);
   if (sb_dtype == MLXQ_BFLOAT16) {
     MLXQ_W(uint16_t, 4, 32) MLXQ_W(uint16_t, 4, 64) MLXQ_W(uint16_t, 4, 128)
     MLXQ_W(uint16_t, 8, 32) MLXQ_W(uint16_t, 8, 64) MLXQ_W(uint16_t, 8, 128)

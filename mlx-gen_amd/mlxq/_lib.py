@@ -39,6 +39,7 @@ EXPORTS = (
     "mlxq_lora_residual",
     "mlxq_cast",
     "mlxq_swiglu",
+    "mlxq_qmm_experts",
 )
 
 
@@ -95,13 +96,15 @@ def load():
     lib.mlxq_lora_residual.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _i64, _i64, ctypes.c_float,
                                        _vp, _vp, ctypes.c_size_t, _vp]
     lib.mlxq_cast.argtypes = [_vp, _int, _vp, _int, _i64, _vp]
+    lib.mlxq_qmm_experts.argtypes = [_vp, _int, _int, _i64, _i64, _i64, _vp, _vp, _vp, _int, _vp, _i64,
+                                     _int, _int, _vp, _vp]
     lib.mlxq_swiglu.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _int, _i64, _int,
                                 _int, _vp, _vp]
     lib.mlxq_embedding.argtypes = [_vp, _i64, _vp, _vp, _vp, _int, _i64, _i64, _int, _int, _vp, _int,
                                    _vp]
     for name in ("mlxq_quantize", "mlxq_dequantize", "mlxq_quantized_matmul", "mlxq_qmm",
                  "mlxq_qmv", "mlxq_linear", "mlxq_packed_bits", "mlxq_embedding",
-                 "mlxq_lora_residual", "mlxq_cast", "mlxq_swiglu"):
+                 "mlxq_lora_residual", "mlxq_cast", "mlxq_swiglu", "mlxq_qmm_experts"):
         getattr(lib, name).restype = _int
     _lib = lib
     return lib

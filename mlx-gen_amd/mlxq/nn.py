@@ -188,6 +188,52 @@ class TokenEmbedding:
         self.weight = None
 
 
+@dataclass
+class StackedExperts:
+    """One MoE expert projection across all E experts as the stacked packed triple plus dense bias
+    (mlx-gen-lens/src/text_encoder/gpt_oss.rs:478-487, StackedExpertPack): weight [E, out,
+    in*bits/32], scales/biases [E, out, in/group_size], bias [E, out]."""
+    weight: torch.Tensor
+    scales: torch.Tensor
+    biases: torch.Tensor
+    bias: torch.Tensor
+    group_size: int = ops.DEFAULT_GROUP_SIZE
+    bits: int = 4
+
+    @property
+    def num_experts(self) -> int:
+        return self.weight.shape[0]
+
+    def split(self) -> List[QuantizedLinear]:
+        """Per-expert packs, the axis-0 split of mlx-gen-lens/src/quant.rs:111-137 (views, no copy)."""
+        return [QuantizedLinear(self.weight[e], self.scales[e], self.biases[e], self.bias[e],
+                                self.group_size, self.bits) for e in range(self.num_experts)]
+
+    def forward(self, x: torch.Tensor, per_expert: bool = False) -> torch.Tensor:
+        """Proj::forward of every expert (gpt_oss.rs:412-425) in one call: x [..., in] shared by all
+        experts, or [E, ..., in] with per_expert=True; returns [E, ..., out]."""
+        return ops.qmm_experts(x, self.weight, self.scales, self.biases, self.group_size, self.bits,
+                               bias=self.bias, per_expert=per_expert)
+
+
+def has_packed_experts(w: Dict[str, torch.Tensor], prefix: str, name: str) -> bool:
+    """mlx-gen-lens/src/quant.rs:80-83: a pre-quantized snapshot stores `{prefix}.experts.{name}_proj.scales`."""
+    return f"{prefix}.experts.{name}_proj.scales" in w
+
+
+def load_packed_experts(w: Dict[str, torch.Tensor], prefix: str, name: str) -> StackedExperts:
+    """mlx-gen-lens/src/quant.rs:93-137: the stacked triple `{prefix}.experts.{name}_proj.{weight,
+    scales,biases}` [E, out, ...] plus the dense bias `{prefix}.experts.{name}_proj_bias` [E, out];
+    bits inferred from the packed shapes, group size 64.  `.split()` gives the per-expert packs."""
+    base = f"{prefix}.experts.{name}_proj"
+    wq = _require(w, f"{base}.weight")
+    scales = _require(w, f"{base}.scales")
+    biases = _require(w, f"{base}.biases")
+    bias = _require(w, f"{prefix}.experts.{name}_proj_bias")
+    bits = ops.packed_bits(wq[0], scales[0], ops.DEFAULT_GROUP_SIZE)
+    return StackedExperts(wq, scales, biases, bias, ops.DEFAULT_GROUP_SIZE, bits)
+
+
 def _require(w: Dict[str, torch.Tensor], key: str) -> torch.Tensor:
     if key not in w:
         raise KeyError(f"missing tensor {key!r}")  # Weights::require (reference src/weights.rs)

@@ -156,6 +156,36 @@ def swiglu(x, gate, up, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4, out
     return h.reshape(*lead, F)
 
 
+def qmm_experts(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4, bias=None,
+                per_expert: bool = False, out=None):
+    """Every expert of a stacked packed projection: y[e] = quantized_matmul(x[e], wq[e], scales[e],
+    biases[e], transpose=True) + bias[e] — Proj::forward of the quantized MoE experts
+    (mlx-gen-lens/src/text_encoder/gpt_oss.rs:412-425) over the axis-0 split of the stacked pack
+    (mlx-gen-lens/src/quant.rs:111-137).  wq [E, N, K*bits/32], scales/biases [E, N, K/gs], bias
+    [E, N] in the activation dtype or None.  x [..., K] is shared by every expert, or with
+    per_expert=True it is [E, ..., K] (one input per expert).  Returns [E, ..., N]."""
+    _need_gpu(x, wq, scales, biases, bias)
+    E, N = wq.shape[0], wq.shape[1]
+    K = x.shape[-1]
+    if per_expert:
+        if x.shape[0] != E:
+            raise ValueError(f"qmm_experts: x has {x.shape[0]} experts, the pack {E}")
+        lead = x.shape[1:-1]
+    else:
+        lead = x.shape[:-1]
+    M = 1
+    for d in lead:
+        M *= d
+    x2 = x.contiguous()
+    wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
+    b = bias.to(x.dtype).contiguous() if bias is not None else None
+    y = out if out is not None else torch.empty((E, M, N), dtype=x.dtype, device=x.device)
+    check(_lib.load().mlxq_qmm_experts(_ptr(x2), _dt(x2), int(per_expert), E, M, K, _ptr(wq),
+                                       _ptr(scales), _ptr(biases), _dt(scales), _ptr(b), N,
+                                       group_size, bits, _ptr(y), _stream(x.device)))
+    return y.reshape(E, *lead, N)
+
+
 def linear_workspace_size(M: int, N: int, rank: int) -> int:
     return int(_lib.load().mlxq_linear_workspace_size(M, N, rank))
 

@@ -36,6 +36,25 @@ def test_lin_and_embedding_choose_packed_or_dense():
         nn.lin(bad, "a", False, 64)  # 24 words cannot pack 128 inputs at 4 or 8 bits
 
 
+def test_load_packed_experts_host_logic():
+    """mlx-gen-lens/src/quant.rs:80-137: the stacked expert triple is detected by its scales key,
+    bits come from the packed shapes, and the axis-0 split yields per-expert packs with bias."""
+    from mlxq import nn
+    E, N, K = 3, 8, 128
+    w = {"m.experts.gate_up_proj.weight": torch.zeros((E, N, K // 8), dtype=torch.int32),
+         "m.experts.gate_up_proj.scales": torch.zeros((E, N, K // 64), dtype=torch.bfloat16),
+         "m.experts.gate_up_proj.biases": torch.zeros((E, N, K // 64), dtype=torch.bfloat16),
+         "m.experts.gate_up_proj_bias": torch.arange(E * N, dtype=torch.float32).reshape(E, N)}
+    assert nn.has_packed_experts(w, "m", "gate_up") and not nn.has_packed_experts(w, "m", "down")
+    st = nn.load_packed_experts(w, "m", "gate_up")
+    assert st.bits == 4 and st.group_size == 64 and st.num_experts == E
+    parts = st.split()
+    assert len(parts) == E and parts[1].weight.shape == (N, K // 8) and parts[1].in_features() == K
+    assert torch.equal(parts[2].bias, w["m.experts.gate_up_proj_bias"][2])
+    with pytest.raises(KeyError):
+        nn.load_packed_experts(w, "m", "down")
+
+
 def test_snapshot_io_keeps_u32_and_config(tmp_path):
     from mlxq import io
     from safetensors import safe_open

@@ -206,3 +206,18 @@ def test_invalid_shapes_rejected():
         oracle.quantize(np.zeros((2, 100), np.float32), 64, 4)
     with pytest.raises(ValueError):
         oracle.quantize(np.zeros((2, 128), np.float32), 64, 3)
+
+
+def test_stack_split_commutes_with_packing():
+    """Affine quantization is per row, so packing a stacked expert weight [E*out, in] equals
+    packing each expert and stacking (the property mlx-gen-lens/src/quant.rs:85-92 relies on to
+    split a stacked on-disk pack back into per-expert packs)."""
+    rng = np.random.default_rng(12)
+    E, N, K = 3, 20, 256
+    w = oracle.bf16_round((rng.standard_normal((E, N, K)) * 0.02).astype(np.float32))
+    for bits in (4, 8):
+        stacked = oracle.quantize(w.reshape(E * N, K), 64, bits, sb_bf16=True)
+        for e in range(E):
+            per = oracle.quantize(w[e], 64, bits, sb_bf16=True)
+            for a, b in zip(stacked, per):
+                assert np.array_equal(a[e * N:(e + 1) * N], b)
