@@ -12,6 +12,8 @@ Also reported (same JSON line):
   gemv         config 4 decode GEMV, M in {1,2,4,8}: HBM GB/s over gate/up/down with the weights
                rotated over 8 copies (> the 256 MB Infinity Cache);
   quantize     config 3 quantize pass (4 x [5120,5120] bf16 -> Q8 g64): GB/s;
+  config1/3/5  the other BASELINE configs (quantize/dequantize/qmm, the Q8 projection, the LoRA sweep);
+  experts      the stacked-expert MoE projections (one launch vs one linear per expert);
   cpu_baseline the CPU oracle (fp64-accumulating C restatement, OpenMP) on a bounded row sample of
                the same up-projection, scaled to TFLOP/s.
 """
@@ -39,7 +41,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extras", action="store_true", help="headline GEMM only")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
-    p.add_argument("--only", choices=("all", "mlp", "gemv", "quantize", "copy", "configs"),
+    p.add_argument("--only", choices=("all", "mlp", "gemv", "quantize", "copy", "configs", "experts"),
                    default="all",
                    help="run one leg only (for profiling); 'copy' is the plain-copy calibration "
                         "kernel for the HBM byte counters")
@@ -296,6 +298,41 @@ def bench_config5(mlxq, torch):
             "sweep_ms": round(total_ms, 3), "cells_TFLOPs": cells}
 
 
+def bench_experts(mlxq, torch, n=512):
+    """Stacked-expert MoE projections of the Lens gpt-oss text encoder (mlx-gen-lens/src/config.rs:
+    hidden 2880, intermediate 2880, 32 experts; Q4 g64 packs with dense bias) at n = 512 tokens:
+    gate_up [32, 5760, 2880] on the shared x, down [32, 2880, 2880] on per-expert inputs.  One
+    qmm_experts launch per projection against the reference's call pattern, one quantized linear
+    (qmm + bias) per expert (mlx-gen-lens/src/text_encoder/gpt_oss.rs:700-720)."""
+    dev = torch.device("cuda:0")
+    E, H, I = 32, 2880, 2880
+    gu = [t.reshape(E, 2 * I, -1) for t in mlxq.quantize(gen_bf16((E * 2 * I, H), 0.02, 800, dev), 64, 4)]
+    dn = [t.reshape(E, H, -1) for t in mlxq.quantize(gen_bf16((E * H, I), 0.02, 801, dev), 64, 4)]
+    gu_bias = gen_bf16((E, 2 * I), 0.5, 802, dev)
+    dn_bias = gen_bf16((E, H), 0.5, 803, dev)
+    x = gen_bf16((n, H), 1.0, 804, dev)
+    xe = gen_bf16((E, n, I), 1.0, 805, dev)
+    y1 = torch.empty((E, n, 2 * I), dtype=torch.bfloat16, device=dev)
+    y2 = torch.empty((E, n, H), dtype=torch.bfloat16, device=dev)
+
+    def stacked():
+        mlxq.qmm_experts(x, *gu, 64, 4, bias=gu_bias, out=y1)
+        mlxq.qmm_experts(xe, *dn, 64, 4, bias=dn_bias, per_expert=True, out=y2)
+
+    def per_expert():
+        for e in range(E):
+            mlxq.linear(x, gu[0][e], gu[1][e], gu[2][e], 64, 4, bias=gu_bias[e])
+            mlxq.linear(xe[e], dn[0][e], dn[1][e], dn[2][e], 64, 4, bias=dn_bias[e])
+
+    flop = 2.0 * n * H * 2 * I * E + 2.0 * n * I * H * E
+    ms_one = graph_ms(torch, stacked, inner=2, reps=3)
+    ms_loop = graph_ms(torch, per_expert, inner=1, reps=3)
+    return {"tokens": n, "experts": E, "gflop": round(flop / 1e9, 1),
+            "one_launch_ms": round(ms_one, 3), "one_launch_TFLOPs": round(flop / (ms_one * 1e-3) / 1e12, 1),
+            "per_expert_ms": round(ms_loop, 3),
+            "per_expert_TFLOPs": round(flop / (ms_loop * 1e-3) / 1e12, 1)}
+
+
 def cpu_baseline(budget_s):
     """The CPU oracle on a bounded row sample of the config-2 up projection."""
     import numpy as np
@@ -406,6 +443,9 @@ def main():
     if args.only == "quantize":
         print(json.dumps({"quantize": bench_quantize(mlxq, torch)}))
         return
+    if args.only == "experts":
+        print(json.dumps({"experts": bench_experts(mlxq, torch)}))
+        return
     if args.only == "configs":
         print(json.dumps({"config1": bench_config1(mlxq, torch), "config3": bench_config3(mlxq, torch),
                           "config5": bench_config5(mlxq, torch)}))
@@ -441,6 +481,7 @@ def main():
         res["config1"] = bench_config1(mlxq, torch)
         res["config3"] = bench_config3(mlxq, torch)
         res["config5"] = bench_config5(mlxq, torch)
+        res["experts"] = bench_experts(mlxq, torch)
     if not args.no_cpu and args.only == "all":
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(res))

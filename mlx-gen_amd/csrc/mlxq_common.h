@@ -95,6 +95,17 @@ __device__ __forceinline__ float gelu_erf(float v) {
   return 0.5f * v * g;
 }
 
+// tanh from the hardware exp2 and reciprocal: tanh|z| = 1 - 2 / (exp(2|z|) + 1), sign restored.
+// Absolute error a few 1e-7 (the GELU below adds it to 1, so relative accuracy near 0 is not
+// needed); exp2 overflows to +inf for |z| > 44 and the reciprocal then gives exactly 1.  Kept
+// small on purpose: the fused GEMM epilogue inlines it, and the library tanhf made that epilogue
+// large enough to push the accumulator tile out of registers.
+__device__ __forceinline__ float tanh_hw(float z) {
+  const float e = __builtin_amdgcn_exp2f(fabsf(z) * 2.88539008177792681f);  // 2 / ln 2
+  const float t = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
+  return copysignf(t, z);
+}
+
 // Tanh-approximate GELU, 0.5 x (1 + tanh(c (x + 0.044715 x^3))) with c = sqrt(2/pi), evaluated
 // as the separate ops of reference src/nn.rs:321-329: every op rounded to the activation dtype
 // (bf16 when BF16, else f32) and the constants cast to it first.  x^3 of a bf16 value is exact in
@@ -106,7 +117,7 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   const float k = rnd(0.044715f);
   const float x3 = rnd(x * x * x);
   const float inner = rnd(rnd(x + rnd(x3 * k)) * c);
-  const float gate = rnd(rnd(tanhf(inner)) + 1.0f);
+  const float gate = rnd(rnd(tanh_hw(inner)) + 1.0f);
   return rnd(rnd(x * 0.5f) * gate);
 }
 

@@ -25,8 +25,9 @@ constexpr int BK = 64;
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
 
-// FUSED = false: plain y = bf16(acc).  FUSED = true: bias / rank-16 LoRA / activation epilogue.
-template <typename SB, int BITS, int GS, int BM, int BN, bool FUSED>
+// EPI = 0: plain y = bf16(acc).  EPI = 1: bias / rank-16 LoRA epilogue; EPI = 2, 3: the same
+// followed by the exact-erf or the tanh GELU (EPI - 1 is the mlxq_activation).
+template <typename SB, int BITS, int GS, int BM, int BN, int EPI>
 __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict__ x, int64_t M,
                                                      int64_t K, const uint32_t* __restrict__ wq,
                                                      const SB* __restrict__ scales,
@@ -175,7 +176,7 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
   }
 
   // Epilogue: y1 = bf16(acc); optional bias, LoRA residual, activation, each rounded to bf16.
-  if constexpr (!FUSED) {
+  if constexpr (EPI == 0) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -219,8 +220,8 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
           float o = round_bf16(acc[i][j][v]);
           if (epi.bias) o = round_bf16(o + bn);
           if (lora) o = round_bf16(o + round_bf16(round_bf16(r[v]) * epi.lora_scale));
-          if (epi.act == MLXQ_ACT_GELU) o = gelu_erf(o);
-          else if (epi.act == MLXQ_ACT_GELU_TANH) o = gelu_tanh<true>(o);
+          if constexpr (EPI - 1 == MLXQ_ACT_GELU) o = gelu_erf(o);
+          else if constexpr (EPI - 1 == MLXQ_ACT_GELU_TANH) o = gelu_tanh<true>(o);
           if (n_ok && m < M) y[m * N + n] = f32_to_bf16_bits(o);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -238,12 +239,18 @@ static int launch_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, c
   if (epi.rank16 != 0 && epi.rank16 != 16)
     return set_error(MLXQ_EINVAL, "qmm: the fused epilogue takes LoRA rank <= 16");
   const bool fused = epi.bias || epi.rank16 || epi.act != MLXQ_ACT_NONE;
-  if (fused)
-    hipLaunchKernelGGL((qmm_kernel<SB, BITS, GS, BM, BN, true>), dim3((unsigned)tiles), dim3(256), 0, st,
-                       (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi);
-  else
-    hipLaunchKernelGGL((qmm_kernel<SB, BITS, GS, BM, BN, false>), dim3((unsigned)tiles), dim3(256), 0, st,
-                       (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi);
+  const int kind = fused ? 1 + epi.act : 0;
+#define MLXQ_QL(E)                                                                                \
+  hipLaunchKernelGGL((qmm_kernel<SB, BITS, GS, BM, BN, E>), dim3((unsigned)tiles), dim3(256), 0, st, \
+                     (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi)
+  switch (kind) {
+    case 0: MLXQ_QL(0); break;
+    case 1: MLXQ_QL(1); break;
+    case 2: MLXQ_QL(2); break;
+    case 3: MLXQ_QL(3); break;
+    default: return set_error(MLXQ_EINVAL, "qmm: unknown activation %d", epi.act);
+  }
+#undef MLXQ_QL
   return check_launch("qmm");
 }
 

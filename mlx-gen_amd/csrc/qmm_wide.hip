@@ -107,11 +107,16 @@ __device__ __forceinline__ float sb_to_f32(uint32_t bits) {
 
 }  // namespace
 
-template <typename SB, int BITS, int GS, int WAVES, bool FUSED>
+// EPI selects the epilogue at compile time: 0 plain y = bf16(acc); 1 bias / rank-16 LoRA; 2 and 3
+// the same followed by the exact-erf or the tanh GELU (EPI - 1 is the mlxq_activation).  One
+// epilogue per instantiation keeps it small enough that the accumulator tile stays in registers.
+template <typename SB, int BITS, int GS, int WAVES, int EPI>
 __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, const uint32_t* __restrict__ wq,
     const SB* __restrict__ scales, const SB* __restrict__ biases, int64_t N,
     uint16_t* __restrict__ y, QmmEpilogue epi, QmmBatch bat) {
+  constexpr bool FUSED = EPI != 0;
+  constexpr int ACT = FUSED ? EPI - 1 : MLXQ_ACT_NONE;
   constexpr int NT = WAVES * 64;
   constexpr int TMW = kBM / 32;          // m sub-tiles per wave (all 256 rows)
   constexpr int TNW = kBN / WAVES / 32;  // n sub-tiles per wave
@@ -141,6 +146,14 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   const int64_t groups = K / GS;
   const int KT = (int)(K / 64);
   const int64_t wn0 = bn0 + (int64_t)wave * (kBN / WAVES);
+  // Dense bias of the tile's kBN columns: one value per thread, loaded now and parked in LDS for
+  // the epilogue, so the epilogue issues no global loads (each would wait on the tile's pending
+  // output stores too, since vmcnt counts stores).
+  __shared__ float bias_lds[kBN];
+  float bias_t = 0.0f;
+  if constexpr (FUSED) {
+    if (epi.bias && tid < kBN && bn0 + tid < N) bias_t = bf16_bits_to_f32(epi.bias[bn0 + tid]);
+  }
 
   // Buffer resources: 32-bit offsets (the host checks every operand fits in 4 GiB).  Rows past
   // M / N are clamped so every offset stays inside its operand.
@@ -319,6 +332,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   step(kt, F_{}, F_{});
 
   // ---- epilogue: lane holds m = bm0 + 32 i + r32 and n = wn0 + 32 j + 8 a + 4 h + b.
+  if constexpr (FUSED) {
+    if (epi.bias) {
+      if (tid < kBN) bias_lds[tid] = bias_t;
+      __syncthreads();
+    }
+  }
   const bool vec_ok = (N % 4) == 0;
   bf16x8 xa[TMW], lb[TNW];
   const bool lora = FUSED && epi.rank16 > 0;
@@ -346,8 +365,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
       for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const int64_t n = nb + 8 * a + b;
-          bias_v[4 * a + b] = (epi.bias && n < N) ? bf16_bits_to_f32(epi.bias[n]) : 0.0f;
+          bias_v[4 * a + b] = epi.bias ? bias_lds[nb - bn0 + 8 * a + b] : 0.0f;
         }
     }
 #pragma unroll
@@ -362,8 +380,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
           float o = round_bf16(v[e]);
           if (epi.bias) o = round_bf16(o + bias_v[e]);
           if (lora) o = round_bf16(o + round_bf16(round_bf16(r[e]) * epi.lora_scale));
-          if (epi.act == MLXQ_ACT_GELU) o = gelu_erf(o);
-          else if (epi.act == MLXQ_ACT_GELU_TANH) o = gelu_tanh<true>(o);
+          if constexpr (ACT == MLXQ_ACT_GELU) o = gelu_erf(o);
+          else if constexpr (ACT == MLXQ_ACT_GELU_TANH) o = gelu_tanh<true>(o);
           v[e] = o;
         }
       }
@@ -393,15 +411,19 @@ static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq
                          const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st,
                          int64_t tiles, const QmmBatch& bat) {
   const bool fused = epi.bias || epi.rank16 || epi.act != MLXQ_ACT_NONE;
+  const int kind = fused ? 1 + epi.act : 0;
   const dim3 grid((unsigned)tiles, (unsigned)bat.count);
-  if (fused)
-    hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, true>), grid, dim3(WAVES * 64), 0, st,
-                       (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi,
-                       bat);
-  else
-    hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, false>), grid, dim3(WAVES * 64), 0, st,
-                       (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi,
-                       bat);
+#define MLXQ_WL(E)                                                                                    \
+  hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, E>), grid, dim3(WAVES * 64), 0, st,        \
+                     (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi, bat)
+  switch (kind) {
+    case 0: MLXQ_WL(0); break;
+    case 1: MLXQ_WL(1); break;
+    case 2: MLXQ_WL(2); break;
+    case 3: MLXQ_WL(3); break;
+    default: return set_error(MLXQ_EINVAL, "qmm: unknown activation %d", epi.act);
+  }
+#undef MLXQ_WL
   return check_launch("qmm_wide");
 }
 
