@@ -34,15 +34,19 @@ __device__ __forceinline__ void load8<float>(const float* p, float (&v)[8]) {
 }
 
 // Codes: clamp(round((w - bias) / s), 0, nb) with round half away from zero and an IEEE
-// quotient, as MLX computes them.  The fast form is t = (w - bias) * (1/s) and
-// clamp(floor(t + 0.5), 0, nb): away from half-integers the few-ulp difference between t and the
-// exact quotient, and the rounding of t + 0.5, cannot change the result.  A code whose t lies
-// within 2^-12 of a half-integer is recomputed with the exact division and roundf (about one
-// element in 2000, handled in a rarely taken second pass).
+// quotient, as MLX computes them.  The fast form is t = (w - bias) * rcp(s), clamped to [0, nb]
+// and rounded to the nearest integer by adding 1.5 * 2^23 (the integer lands in the low mantissa
+// bits).  t differs from the exact quotient by at most ~3 ulp of t <= 255 (under 2^-15), and the
+// hardware rounding (ties to even) differs from round-half-away only at exact .5 ties; so every
+// code is right unless t lies within 2^-12 of a half-integer.  Those codes (about one element in
+// 2000) are recomputed with the exact division and roundf in a rarely taken second pass.  w - bias
+// is formed before the product on purpose: folding it into fma(w, 1/s, -bias/s) would add an
+// error proportional to |bias / s|, unbounded for a narrow group far from zero.
 __device__ __forceinline__ uint32_t code_fast(float a, float rs, float nb, bool& near) {
   const float t = a * rs;
-  near = fabsf((t - floorf(t)) - 0.5f) < 0x1p-12f;
-  return (uint32_t)fminf(fmaxf(floorf(t + 0.5f), 0.0f), nb);
+  near = fabsf(__builtin_amdgcn_fractf(t) - 0.5f) < 0x1p-12f;
+  const float tc = __builtin_amdgcn_fmed3f(t, 0.0f, nb);
+  return __float_as_uint(tc + 12582912.0f) & 0xffu;
 }
 __device__ __forceinline__ uint32_t code_exact(float a, float s, float nb) {
   return (uint32_t)fminf(fmaxf(roundf(a / s), 0.0f), nb);
@@ -92,7 +96,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const T* __restrict__ w, 
   const bool at_zero = q0 == 0.0f;
   s = at_zero ? s : edge / q0;
   const float bias = at_zero ? 0.0f : edge;
-  const float rs = 1.0f / s;
+  const float rs = __builtin_amdgcn_rcpf(s);  // error covered by the near-tie window
 
   if ((threadIdx.x & (LANES - 1)) == 0) {
     const int64_t g = chunk / LANES;  // row-major group index == row*(K/GS) + group

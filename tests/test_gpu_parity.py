@@ -97,6 +97,29 @@ def test_quantize_special_groups(mlxq, bits):
 
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_quantize_narrow_groups_far_from_zero(mlxq, bits, dtype):
+    """Groups whose range is tiny next to their magnitude (|bias / scale| up to ~1e7): the code
+    of w is (w - bias) / scale, and any evaluation that loses w - bias to cancellation in large
+    terms would misround codes here."""
+    banner("quantize narrow far groups", bits, dtype)
+    rng = np.random.default_rng(12 + bits)
+    rows = []
+    for centre in (100.0, -3.0e3, 0.5, 7.25e4, -1.0):
+        for width in (1e-2, 3e-4, 1e-5):
+            rows.append(centre + width * rng.random(512))
+    w = np.stack(rows).astype(np.float32)
+    if dtype == "bf16":
+        w = oracle.bf16_round(w)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    wq, s, b = mlxq.quantize(to_gpu(w, tdt), 64, bits)
+    rwq, rs, rb = oracle.quantize(w, 64, bits, sb_bf16=(dtype == "bf16"))
+    assert np.array_equal(to_np(wq), rwq)
+    assert np.array_equal(to_np(s), rs)
+    assert np.array_equal(to_np(b), rb)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
 def test_quantize_half_integer_ties(mlxq, bits, dtype):
     """Groups whose quotients (w - bias)/s land exactly on half-integers, and one ulp either side.
 
