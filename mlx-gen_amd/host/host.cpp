@@ -126,6 +126,14 @@ Array Array::reshape(std::vector<int64_t> shape) const {
   return a;
 }
 
+Array Array::index0(int64_t i) const {
+  if (ndim() < 1 || i < 0 || i >= shape_[0]) throw Error(MLXQ_EINVAL, "index0: index out of range");
+  Array a = *this;
+  a.shape_.erase(a.shape_.begin());
+  a.ptr_ = a.size() > 0 ? (char*)ptr_ + (size_t)i * a.nbytes() : nullptr;
+  return a;
+}
+
 // ---- ops --------------------------------------------------------------------------------------
 
 Array as_dtype(const Array& a, Dtype dt, hipStream_t s) {
@@ -179,6 +187,57 @@ int packed_bits(const Array& wq, const Array& scales, int group_size) {
   const int b = mlxq_packed_bits(wq.dim(1), scales.dim(1), group_size);
   if (b < 0) throw Error(MLXQ_EINVAL, mlxq_last_error());
   return b;
+}
+
+Array swiglu(const Array& x, const QuantizedLinear& gate, const QuantizedLinear& up, hipStream_t s) {
+  need_packed(gate.weight, "swiglu");
+  need_packed(up.weight, "swiglu");
+  if (gate.bias || up.bias) throw Error(MLXQ_EUNSUPPORTED, "swiglu: projections with a dense bias");
+  if (gate.group_size != up.group_size || gate.bits != up.bits ||
+      gate.weight.shape() != up.weight.shape() || x.ndim() < 1 || x.dim(-1) != gate.in_features())
+    throw Error(MLXQ_EINVAL, "swiglu: gate and up must be packed alike and match x");
+  const int64_t K = x.dim(-1), F = gate.weight.dim(0), M = K > 0 ? x.size() / K : 0;
+  std::vector<int64_t> shape = x.shape();
+  shape.back() = F;
+  Array h = Array::empty(shape, x.dtype());
+  check(mlxq_swiglu(x.data(), abi_dtype(x.dtype(), "swiglu"), M, K,
+                    (const uint32_t*)gate.weight.data(), gate.scales.data(), gate.biases.data(),
+                    (const uint32_t*)up.weight.data(), up.scales.data(), up.biases.data(),
+                    abi_dtype(gate.scales.dtype(), "swiglu"), F, gate.group_size, gate.bits, h.data(), s));
+  return h;
+}
+
+std::vector<QuantizedLinear> StackedExperts::split() const {
+  std::vector<QuantizedLinear> out;
+  for (int64_t e = 0; e < num_experts(); ++e)
+    out.push_back(QuantizedLinear{weight.index0(e), scales.index0(e), biases.index0(e),
+                                  bias ? std::optional<Array>(bias->index0(e)) : std::nullopt,
+                                  group_size, bits});
+  return out;
+}
+
+Array StackedExperts::forward(const Array& x, bool per_expert, hipStream_t s) const {
+  if (weight.dtype() != Dtype::Uint32 && weight.dtype() != Dtype::Int32)
+    throw Error(MLXQ_EINVAL, "experts: weight must hold packed uint32 codes");
+  if (weight.ndim() != 3 || scales.ndim() != 3 || x.ndim() < 1)
+    throw Error(MLXQ_EINVAL, "experts: expected [E, out, ...] stacks");
+  const int64_t E = num_experts(), N = weight.dim(1), K = x.dim(-1);
+  std::vector<int64_t> lead(x.shape().begin() + (per_expert ? 1 : 0), x.shape().end() - 1);
+  if (per_expert && (x.ndim() < 2 || x.dim(0) != E))
+    throw Error(MLXQ_EINVAL, "experts: per-expert x must lead with E");
+  int64_t M = 1;
+  for (int64_t d : lead) M *= d;
+  std::vector<int64_t> shape = {E};
+  shape.insert(shape.end(), lead.begin(), lead.end());
+  shape.push_back(N);
+  Array y = Array::empty(shape, x.dtype());
+  std::optional<Array> b;
+  if (bias) b = as_dtype(*bias, x.dtype(), s);
+  check(mlxq_qmm_experts(x.data(), abi_dtype(x.dtype(), "experts"), per_expert ? 1 : 0, E, M, K,
+                         (const uint32_t*)weight.data(), scales.data(), biases.data(),
+                         abi_dtype(scales.dtype(), "experts"), b ? b->data() : nullptr, N, group_size,
+                         bits, y.data(), s));
+  return y;
 }
 
 // ---- layers -----------------------------------------------------------------------------------
@@ -340,6 +399,24 @@ TokenEmbedding embedding(const Weights& w, const std::string& base, int group_si
                                                 group_size, bits);
   }
   return TokenEmbedding::dense(require(w, base + ".weight"));
+}
+
+bool has_packed_experts(const Weights& w, const std::string& prefix, const std::string& name) {
+  return w.count(prefix + ".experts." + name + "_proj.scales") > 0;
+}
+
+StackedExperts load_packed_experts(const Weights& w, const std::string& prefix, const std::string& name) {
+  const std::string base = prefix + ".experts." + name + "_proj";
+  StackedExperts st;
+  st.weight = require(w, base + ".weight");
+  st.scales = require(w, base + ".scales");
+  st.biases = require(w, base + ".biases");
+  st.bias = require(w, prefix + ".experts." + name + "_proj_bias");
+  st.group_size = 64;
+  if (st.weight.ndim() != 3 || st.scales.ndim() != 3)
+    throw Error(MLXQ_EINVAL, "load_packed_experts: expected [E, out, ...] stacks under " + base);
+  st.bits = packed_bits(st.weight.index0(0), st.scales.index0(0), st.group_size);
+  return st;
 }
 
 Weights quantize_map(const Weights& map, int bits, int group_size,

@@ -55,6 +55,9 @@ class Array {
 
   void to_host(void* dst) const;  // synchronous device-to-host copy of nbytes()
   Array reshape(std::vector<int64_t> shape) const;  // same buffer, new shape (same size)
+  // Sub-array i along axis 0 (shape without that axis), sharing this buffer, as split + squeeze
+  // along axis 0 do for the stacked expert packs (mlx-gen-lens/src/quant.rs:111-137).
+  Array index0(int64_t i) const;
 
   bool valid() const { return ptr_ != nullptr || size() == 0; }
   void* data() const { return ptr_; }
@@ -149,11 +152,38 @@ class TokenEmbedding {
   int group_size_ = 64, bits_ = 4;
 };
 
+// Fused SwiGLU of a decode MLP (mlx-gen-sensenova/src/qwen3.rs:178-181): h = silu(gate(x)) * up(x)
+// with both projections streamed in one launch.  Decode form only (bf16 x and scales, M <= 8,
+// no dense bias); other inputs throw Error(MLXQ_EUNSUPPORTED) and the caller runs two forwards.
+Array swiglu(const Array& x, const QuantizedLinear& gate, const QuantizedLinear& up,
+             hipStream_t s = nullptr);
+
+// One MoE expert projection across all E experts as its stacked packed triple plus dense bias
+// (mlx-gen-lens/src/text_encoder/gpt_oss.rs:478-487): weight [E, out, in*bits/32], scales/biases
+// [E, out, in/group_size], bias [E, out].
+struct StackedExperts {
+  Array weight, scales, biases;
+  std::optional<Array> bias;
+  int group_size = 64;
+  int bits = 4;
+
+  int64_t num_experts() const { return weight.dim(0); }
+  // Per-expert layers sharing the stack's buffers (the axis-0 split of quant.rs:111-137).
+  std::vector<QuantizedLinear> split() const;
+  // Proj::forward of every expert (gpt_oss.rs:412-425) in one call: x [..., in] shared by all
+  // experts, or [E, ..., in] with per_expert; returns [E, ..., out].
+  Array forward(const Array& x, bool per_expert = false, hipStream_t s = nullptr) const;
+};
+
 // ---- quant.rs --------------------------------------------------------------------------------
 using Weights = std::map<std::string, Array>;
 const Array& require(const Weights& w, const std::string& key);  // throws on a missing key
 AdaptableLinear lin(const Weights& w, const std::string& base, bool bias, int group_size);
 TokenEmbedding embedding(const Weights& w, const std::string& base, int group_size);
+// mlx-gen-lens/src/quant.rs:80-137: `{prefix}.experts.{name}_proj.{weight,scales,biases}` stacks
+// plus `{prefix}.experts.{name}_proj_bias`; bits from the packed shapes, group size 64.
+bool has_packed_experts(const Weights& w, const std::string& prefix, const std::string& name);
+StackedExperts load_packed_experts(const Weights& w, const std::string& prefix, const std::string& name);
 Weights quantize_map(const Weights& map, int bits, int group_size,
                      const std::function<bool(const std::string&)>& is_target,
                      hipStream_t s = nullptr);

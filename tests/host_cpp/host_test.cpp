@@ -19,6 +19,7 @@
 
 #include <unistd.h>
 
+#include "../../include/mlxq.h"
 #include "../../mlx-gen_amd/host/mlxq.hpp"
 
 extern "C" {
@@ -29,6 +30,7 @@ int oracle_dequantize(const uint32_t* wq, const float* scales, const float* bias
                       int gs, int bits, int out_bf16, float* out);
 int oracle_qmm(const float* x, int64_t M, int64_t K, const uint32_t* wq, const float* scales,
                const float* biases, int64_t N, int gs, int bits, int w_bf16, int out_bf16, float* y);
+float oracle_silu(float v, int out_bf16);
 int oracle_linear(const float* x, int64_t M, int64_t K, const uint32_t* wq, const float* scales,
                   const float* biases, int64_t N, int gs, int bits, int w_bf16, int act_bf16,
                   const float* bias, const float* lora_a, const float* lora_b, int64_t rank,
@@ -111,6 +113,27 @@ static fs::path repo_root(const char* argv0) {
 static void cpu_cases(const fs::path& root) {
   const fs::path tmp = fs::temp_directory_path() / ("mlxq_host_test_" + std::to_string(::getpid()));
   fs::create_directories(tmp);
+
+  banner("stacked expert packs: detection, bits, axis-0 split (host only)");
+  {
+    Weights w;
+    char* base = reinterpret_cast<char*>(0x100000);  // never dereferenced: shape logic only
+    w["m.experts.gate_up_proj.weight"] = Array::borrow(base, {3, 8, 16}, Dtype::Uint32);  // K=128 Q4
+    w["m.experts.gate_up_proj.scales"] = Array::borrow(base, {3, 8, 2}, Dtype::Bfloat16);
+    w["m.experts.gate_up_proj.biases"] = Array::borrow(base, {3, 8, 2}, Dtype::Bfloat16);
+    w["m.experts.gate_up_proj_bias"] = Array::borrow(base, {3, 8}, Dtype::Bfloat16);
+    EXPECT(has_packed_experts(w, "m", "gate_up") && !has_packed_experts(w, "m", "down"), "detection");
+    StackedExperts st = load_packed_experts(w, "m", "gate_up");
+    EXPECT(st.bits == 4 && st.group_size == 64 && st.num_experts() == 3, "bits/group/E");
+    std::vector<QuantizedLinear> parts = st.split();
+    EXPECT(parts.size() == 3 && parts[2].weight.shape() == std::vector<int64_t>({8, 16}) &&
+               parts[2].in_features() == 128, "split shapes");
+    EXPECT((char*)parts[2].weight.data() - base == 2 * 8 * 16 * 4 &&
+               (char*)parts[1].bias->data() - base == 8 * 2, "split offsets");
+    bool threw = false;
+    try { load_packed_experts(w, "m", "down"); } catch (const Error&) { threw = true; }
+    EXPECT(threw, "missing stack throws");
+  }
 
   banner("safetensors round trip, every dtype");
   {
@@ -282,6 +305,50 @@ static void gpu_cases(const fs::path& root) {
       }
     const double e = rel_fro(host_f32(y), ref);
     EXPECT(e < 2e-3, "relFro %.3e", e);
+  }
+
+  banner("fused SwiGLU decode and the stacked expert projection");
+  {
+    std::mt19937 rng(21);
+    const int64_t K = 512, F = 192, M = 3;
+    std::vector<float> wg = bf16_normal(rng, F * K, 0.02f), wu = bf16_normal(rng, F * K, 0.02f);
+    std::vector<float> xv = bf16_normal(rng, M * K, 1.0f);
+    QuantizedLinear gate = QuantizedLinear::try_from_linear(bf16_array(wg, {F, K}), std::nullopt, 64, 4);
+    QuantizedLinear up = QuantizedLinear::try_from_linear(bf16_array(wu, {F, K}), std::nullopt, 64, 4);
+    Array h = swiglu(bf16_array(xv, {M, K}), gate, up);
+    EXPECT(h.shape() == std::vector<int64_t>({M, F}) && h.dtype() == Dtype::Bfloat16, "swiglu shape");
+    std::vector<uint32_t> qg(F * K / 8), qu(F * K / 8);
+    std::vector<float> sg(F * K / 64), zg(F * K / 64), su(F * K / 64), zu(F * K / 64), g(M * F), u(M * F);
+    oracle_quantize(wg.data(), F, K, 64, 4, 1, qg.data(), sg.data(), zg.data());
+    oracle_quantize(wu.data(), F, K, 64, 4, 1, qu.data(), su.data(), zu.data());
+    oracle_qmm(xv.data(), M, K, qg.data(), sg.data(), zg.data(), F, 64, 4, 0, 1, g.data());
+    oracle_qmm(xv.data(), M, K, qu.data(), su.data(), zu.data(), F, 64, 4, 0, 1, u.data());
+    std::vector<float> ref(M * F);
+    for (int64_t i = 0; i < M * F; ++i) ref[i] = oracle_bf16_round(oracle_silu(g[i], 1) * u[i]);
+    double e = rel_fro(host_f32(h), ref);
+    EXPECT(e < 2e-3, "swiglu relFro %.3e", e);
+    bool unsupported = false;
+    try { swiglu(bf16_array(bf16_normal(rng, 20 * K, 1.0f), {20, K}), gate, up); }
+    catch (const Error& err) { unsupported = err.status == MLXQ_EUNSUPPORTED; }
+    EXPECT(unsupported, "swiglu outside the decode form reports EUNSUPPORTED");
+
+    // Experts: pack the stack [E*N, K] in one call, run every expert, compare with the split layers.
+    const int64_t E = 4, N = 96, Ke = 256, Mt = 40;
+    std::vector<float> we = bf16_normal(rng, E * N * Ke, 0.02f), be = bf16_normal(rng, E * N, 0.5f);
+    Packed p = quantize(bf16_array(we, {E * N, Ke}), 64, 4);
+    StackedExperts st{p.wq.reshape({E, N, Ke / 8}), p.scales.reshape({E, N, Ke / 64}),
+                      p.biases.reshape({E, N, Ke / 64}), bf16_array(be, {E, N}), 64, 4};
+    std::vector<float> xs = bf16_normal(rng, Mt * Ke, 1.0f);
+    Array y = st.forward(bf16_array(xs, {Mt, Ke}));
+    EXPECT(y.shape() == std::vector<int64_t>({E, Mt, N}), "experts shape");
+    std::vector<float> yh = host_f32(y);
+    std::vector<QuantizedLinear> parts = st.split();
+    for (int64_t ex = 0; ex < E; ++ex) {
+      std::vector<float> one = host_f32(parts[ex].forward(bf16_array(xs, {Mt, Ke})));
+      std::vector<float> mine(yh.begin() + ex * Mt * N, yh.begin() + (ex + 1) * Mt * N);
+      e = rel_fro(mine, one);
+      EXPECT(e < 2e-3, "expert %lld relFro %.3e", (long long)ex, e);
+    }
   }
 
   banner("TokenEmbedding quantize + forward, and the snapshot round trip");
