@@ -4,8 +4,11 @@
 // v_mfma_f32_32x32x16_bf16 accumulating in f32.
 //
 // Workgroup: WAVES waves (8 by default: two per SIMD, so one wave's VALU/LDS work overlaps the
-// other's MFMAs), block tile 256 (M) x 256 (N), K advanced 64 per step.  The waves split the tile
-// along N only: wave w owns columns [w*256/WAVES, (w+1)*256/WAVES) of all 256 rows.
+// other's MFMAs), block tile BM (M, 256 or 224) x 256 (N), K advanced 64 per step.  The waves split
+// the tile along N only: wave w owns columns [w*256/WAVES, (w+1)*256/WAVES) of all BM rows.  The
+// host picks BM per problem so that the tile count fills the CUs in as few, full rounds as
+// possible (1 workgroup per CU): e.g. M = 4608, N = 3072 gives 216 tiles of 256 rows (one round
+// with 40 CUs idle) but 252 tiles of 224 rows (one round of 12.5% shorter tiles).
 //   * weights: every lane loads its own packed words straight into registers (one 16-byte
 //     buffer load per 32-column sub-tile per K step for Q4, two for Q8) and dequantizes them into
 //     the MFMA operand registers — no LDS round trip, and each weight is dequantized exactly once
@@ -34,9 +37,10 @@ namespace mlxq {
 
 namespace {
 
-constexpr int kBM = 256;
+constexpr int kBM = 256;  // LDS activation tile rows (a BM < 256 tile leaves the last rows unused)
 constexpr int kBN = 256;
 constexpr int kGroupM = 4;
+constexpr int kStages = 4;  // activation LDS ring depth (power of two)
 constexpr int kBufferFlags = 0x00020000;  // raw buffer resource word 3 for gfx9-family loads
 
 __device__ __forceinline__ void tile_coords(int64_t bid, int64_t tiles_m, int64_t tiles_n,
@@ -55,6 +59,43 @@ __device__ __forceinline__ void tile_coords(int64_t bid, int64_t tiles_m, int64_
 }
 
 __device__ __forceinline__ int swz_f(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+// Wait until at most N vector memory operations of this wave are outstanding, leaving the LDS and
+// export counters open (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void mlxq_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for the pipelined loop: this wave's LDS reads done (lgkmcnt(0)), then
+// s_barrier.  Unlike __syncthreads() it has no release fence, which on this target would also
+// wait for every outstanding direct-to-LDS load; the loop waits for exactly the loads it needs
+// with mlxq_vmcnt before calling this.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
+  __builtin_amdgcn_s_barrier();
+}
+
+// 16-byte-per-lane buffer load straight into LDS (lane L's data lands at lds_addr + 16 L), as
+// inline asm: the compiler then adds no conservative wait for it before later LDS reads (it
+// cannot tell they touch other buffers); callers prove completion from their own vmcnt waits.
+// rsrc is a raw buffer resource in SGPRs.
+__device__ __forceinline__ void lds_dma16(u32x4 rsrc, uint32_t lds_addr, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// Register copy the compiler cannot elide: the weight ring's take must not be coalesced with
+// the ring slot, or the slot's next (in-flight) load would need a copy of its own — and a wait
+// for that load — at the loop back-edge.
+__device__ __forceinline__ uint32_t opaque_copy(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
 
 template <int B>
 __device__ __forceinline__ float ubyte(uint32_t v) {
@@ -110,7 +151,7 @@ __device__ __forceinline__ float sb_to_f32(uint32_t bits) {
 // EPI selects the epilogue at compile time: 0 plain y = bf16(acc); 1 bias / rank-16 LoRA; 2 and 3
 // the same followed by the exact-erf or the tanh GELU (EPI - 1 is the mlxq_activation).  One
 // epilogue per instantiation keeps it small enough that the accumulator tile stays in registers.
-template <typename SB, int BITS, int GS, int WAVES, int EPI>
+template <typename SB, int BITS, int GS, int WAVES, int EPI, int BM>
 __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, const uint32_t* __restrict__ wq,
     const SB* __restrict__ scales, const SB* __restrict__ biases, int64_t N,
@@ -118,13 +159,22 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   constexpr bool FUSED = EPI != 0;
   constexpr int ACT = FUSED ? EPI - 1 : MLXQ_ACT_NONE;
   constexpr int NT = WAVES * 64;
-  constexpr int TMW = kBM / 32;          // m sub-tiles per wave (all 256 rows)
+  constexpr int TMW = BM / 32;           // m sub-tiles per wave (all BM rows)
   constexpr int TNW = kBN / WAVES / 32;  // n sub-tiles per wave
   constexpr int WPL = BITS;              // packed words per lane per n sub-tile per K step (4 or 8)
   constexpr int A_PER = kBM * 8 / NT;    // 16-byte activation chunks per thread per K step
   constexpr int A_ROWS = NT / 8;         // row stride between a thread's chunks
-  static_assert(TNW >= 1 && A_PER >= 1 && A_ROWS % 16 == 0, "tile/wave shape");
-  __shared__ __attribute__((aligned(16))) unsigned char smem[3][kBM * 128];
+  static_assert(TNW >= 1 && A_PER >= 1 && A_ROWS % 16 == 0 && BM % 32 == 0 && BM <= kBM,
+                "tile/wave shape");
+  // bf16 scales/biases are staged through LDS in blocks of 8 groups (SPB K steps): per wave and
+  // 32-column sub-tile, two 1 KB buffers of [32 rows x 8 scales][32 rows x 8 biases], plus one
+  // 1 KB sink per wave for the placeholder loads (see load_b).
+  constexpr bool SZ_LDS = sizeof(SB) == 2;
+  constexpr int SPB = 8 * GS / 64;
+  constexpr int kSzBytes = SZ_LDS ? WAVES * TNW * 2048 + WAVES * 1024 : 0;
+  __shared__ __attribute__((aligned(16))) unsigned char lds_all[kStages * kBM * 128 + kSzBytes];
+  auto smem = reinterpret_cast<unsigned char (*)[kBM * 128]>(lds_all);
+  unsigned char* const sz_lds = lds_all + kStages * kBM * 128;
 
   // Stacked launch: grid.y selects the matrix (expert); one matrix has all strides zero.
   if (gridDim.y > 1) {
@@ -138,18 +188,20 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   }
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, r32 = lane & 31, half = lane >> 5;
-  const int64_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + kBN - 1) / kBN;
   int64_t tm, tn;
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int64_t bm0 = tm * kBM, bn0 = tn * kBN;
+  const int64_t bm0 = tm * BM, bn0 = tn * kBN;
   const int64_t kwords = K * BITS / 32;
   const int64_t groups = K / GS;
   const int KT = (int)(K / 64);
   const int64_t wn0 = bn0 + (int64_t)wave * (kBN / WAVES);
   // Dense bias of the tile's kBN columns: one value per thread, loaded now and parked in LDS for
   // the epilogue, so the epilogue issues no global loads (each would wait on the tile's pending
-  // output stores too, since vmcnt counts stores).
-  __shared__ float bias_lds[kBN];
+  // output stores too, since vmcnt counts stores).  It is parked in activation stage KT % 4,
+  // which no step reads or refills after step KT-4: the kernel keeps a single LDS object, and
+  // the compiler then adds no conservative wait for the direct-to-LDS loads before the ring's
+  // LDS reads (it did with a second LDS array).
   float bias_t = 0.0f;
   if constexpr (FUSED) {
     if (epi.bias && tid < kBN && bn0 + tid < N) bias_t = bf16_bits_to_f32(epi.bias[bn0 + tid]);
@@ -166,28 +218,37 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<SB*>(biases), (short)0, (int)(uint32_t)(N * groups * sizeof(SB)), kBufferFlags);
 
-  // ---- activation staging: thread owns chunk (tid & 7) of rows (tid >> 3) + A_ROWS * i.
-  const int a_row0 = tid >> 3, a_c = tid & 7;
+  // ---- activation staging: global -> LDS directly (buffer_load ... lds), 4-stage ring.  One such
+  // load moves 1 KB per wave: lane L's 16 bytes land at block + 16 L.  Wave wv's round i fills
+  // the block of rows A_ROWS i + 8 wv .. +7, so lane L loads the chunk of row
+  // A_ROWS i + 8 wv + (L >> 3) that belongs at position L & 7 under the swizzle, i.e. global
+  // chunk (L & 7) ^ f(row).  All kBM LDS rows are filled (uniform code); rows at or past BM
+  // repeat the tile's last row and are never read.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
   uint32_t a_goff[A_PER];
 #pragma unroll
   for (int i = 0; i < A_PER; ++i) {
-    const int64_t r = bm0 + a_row0 + A_ROWS * i < M ? bm0 + a_row0 + A_ROWS * i : M - 1;
-    a_goff[i] = (uint32_t)((r * K + a_c * 8) * 2);
+    const int rl = A_ROWS * i + 8 * wv + (lane >> 3);
+    const int c = (lane & 7) ^ swz_f(rl);
+    const int rt = rl < BM ? rl : BM - 1;
+    const int64_t r = bm0 + rt < M ? bm0 + rt : M - 1;
+    a_goff[i] = (uint32_t)((r * K + c * 8) * 2);
   }
-  const int a_lds = a_row0 * 128 + ((a_c ^ swz_f(a_row0)) << 4);
-  u32x4 areg[A_PER];
-  auto load_a = [&](int kt) {
+  auto dma_a = [&](int kt) {
+    unsigned char* base = smem[kt & (kStages - 1)];
+#if defined(__HIP_DEVICE_COMPILE__)
 #pragma unroll
     for (int i = 0; i < A_PER; ++i)
-      areg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, a_goff[i] + (uint32_t)kt * 128u, 0, 0));
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < A_PER; ++i)
-      *reinterpret_cast<u32x4*>(smem[buf] + a_lds + i * A_ROWS * 128) = areg[i];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, (__attribute__((address_space(3))) void*)(base + (A_ROWS * i + 8 * wv) * 128), 16,
+          a_goff[i] + (uint32_t)kt * 128u, 0, 0, 0);
+#else
+    (void)base;
+#endif
   };
 
-  // ---- weight rows of this lane: n = wn0 + 32 j + r32 (clamped to N-1 like A rows)
+  // ---- weight rows of this lane: n = wn0 + 32 j + r32 (clamped to N-1 like A rows).  Packed
+  // words and raw scale/bias bits go through a 2-slot register ring (slot = step parity).
   uint32_t w_goff[TNW], g_base[TNW];
   bool n_ok[TNW];
 #pragma unroll
@@ -198,9 +259,40 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     w_goff[j] = (uint32_t)((nn * kwords + half * WPL) * 4);
     g_base[j] = (uint32_t)(nn * groups);
   }
-  uint32_t braw[TNW][WPL];
-  uint32_t bs[TNW], bz[TNW];  // raw scale/bias bits
-  auto load_b = [&](int kt) {
+  uint32_t braw[2][TNW][WPL];
+  uint32_t bs[2][TNW], bz[2][TNW];  // raw scale/bias bits (f32 scales: loaded with the words)
+  // bf16 scales and biases: one resource over both arrays (the host checks that they lie within
+  // 4 GiB of each other), so that one load can fetch scales in half 0 and biases in half 1.
+  // Lane (h, r32) of a block load fetches 8 groups of row r32 of its sub-tile; lane L lands at
+  // buffer + 16 L, i.e. [32 rows x 16 B scales][32 rows x 16 B biases].
+  const uint16_t* sb_lo = (const uint16_t*)scales < (const uint16_t*)biases ? (const uint16_t*)scales
+                                                                          : (const uint16_t*)biases;
+  const uint32_t s_rel = (uint32_t)((const uint16_t*)scales - sb_lo) * 2u;
+  const uint32_t z_rel = (uint32_t)((const uint16_t*)biases - sb_lo) * 2u;
+  const uint64_t sb_addr = (uint64_t)(uintptr_t)sb_lo;
+  const u32x4 rsz = {(uint32_t)sb_addr, (uint32_t)(sb_addr >> 32) & 0xffffu,
+                     (uint32_t)((s_rel > z_rel ? s_rel : z_rel) + (uint64_t)N * groups * 2),
+                     (uint32_t)kBufferFlags};
+  const uint32_t sz_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)sz_lds;
+  const uint32_t sz_sink = sz_base + WAVES * TNW * 2048 + wv * 1024;
+  // The scale/bias load that goes with load_b(kt), issued as if by step kt-3: it fetches block
+  // b+1 when step kt-3's take starts reading block b (kt-2 = b*SPB) and block b+1 exists;
+  // otherwise all lanes read the first 16 bytes of the scales into this wave's sink.  Issuing
+  // one op with every load_b keeps the loop body free of branches (a branch here made the
+  // compiler's own waits conservative) and the vmcnt counts fixed.
+  auto dma_sz = [&](int kt) {
+    const int ks = kt - 2;  // first step of the block the issuing take starts
+    const bool fetch = (ks & (SPB - 1)) == 0 && ks + SPB < KT;
+    const int blk = ks / SPB + 1;
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) {
+      const uint32_t dst = fetch ? sz_base + (uint32_t)((wv * TNW + j) * 2048 + (blk & 1) * 1024) : sz_sink;
+      const uint32_t off = fetch ? (half ? z_rel : s_rel) + (g_base[j] + (uint32_t)blk * 8u) * 2u : s_rel;
+      lds_dma16(rsz, dst, off);
+    }
+  };
+  auto load_b = [&](int kt, auto SLOT) {
+    constexpr int sl = decltype(SLOT)::value;
     const uint32_t g = (uint32_t)((kt * 64 + half * 32) / GS);
 #pragma unroll
     for (int j = 0; j < TNW; ++j) {
@@ -209,12 +301,21 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
         const u32x4 v = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, w_goff[j] + (uint32_t)kt * (8u * WPL) + 16u * q, 0, 0));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) braw[j][4 * q + e] = v[e];
+        for (int e = 0; e < 4; ++e) braw[sl][j][4 * q + e] = v[e];
       }
-      bs[j] = load_sb_bits<SB>(rs, g_base[j] + g);
-      bz[j] = load_sb_bits<SB>(rz, g_base[j] + g);
+      if constexpr (!SZ_LDS) {
+        bs[sl][j] = load_sb_bits<SB>(rs, g_base[j] + g);
+        bz[sl][j] = load_sb_bits<SB>(rz, g_base[j] + g);
+      }
     }
+    if constexpr (SZ_LDS) dma_sz(kt);
+    (void)g;
   };
+  constexpr int B_OPS = TNW * (WPL / 4 + (SZ_LDS ? 1 : 2));  // vector memory ops of one load_b
+  // Ops of one load_b issued after the last op the take needs (the bf16 path's scale/bias load
+  // goes to LDS and is waited for separately).
+  constexpr int B_TAIL = SZ_LDS ? TNW : 0;
+
 
   // ---- fragment read offsets (LDS): row i*32 + r32, chunk 4h + kk
   int a_off[4];
@@ -229,22 +330,33 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  // ---- software pipeline.  A tiles rotate through 3 LDS buffers: step kt reads buffer kt%3
-  // while A(kt+1) is written to (kt+1)%3 at the top of the step and A(kt+2) is in flight in
-  // registers.  One barrier per step, between the tile write and the first read of it (the
-  // prefetch of step kt+1's first fragments during MFMA group kk=3).  Within a step, the next
-  // group's activation fragments (LDS) and weight fragments (dequantized in registers) are
-  // prepared while the current group's MFMAs run.
+  // ---- software pipeline.  Step kt reads LDS stage kt%4; the activation tiles of steps kt+1
+  // (landed), kt+2 and kt+3 (in flight) occupy the other stages, and the weights of steps kt+1
+  // and kt+2 sit in the register ring, so every global load is issued two steps before its
+  // use.  One barrier per step, mid-step: before it each wave waits for its own loads of
+  // A(kt+1), after it the tile is complete for all waves and stage (kt+3)%4 — last read in step
+  // kt-1 — is refilled.  The waits are explicit vmcnt counts over the fixed issue order
+  // A(0) W(0) A(1) W(1) ...; a scheduling fence keeps the weight take (VALU on loaded
+  // registers) from being hoisted across the barrier, where it would force an early wait.
   uint32_t bcur[TNW][WPL];
   float scur[TNW], s16cur[TNW], zcur[TNW];
-  auto take_b = [&]() {
+  auto take_b = [&](auto SLOT, int ktn) {  // ktn: the step these weights belong to
+    constexpr int sl = decltype(SLOT)::value;
 #pragma unroll
     for (int j = 0; j < TNW; ++j) {
 #pragma unroll
-      for (int e = 0; e < WPL; ++e) bcur[j][e] = braw[j][e];
-      scur[j] = sb_to_f32<SB>(bs[j]);
+      for (int e = 0; e < WPL; ++e) bcur[j][e] = opaque_copy(braw[sl][j][e]);
+      if constexpr (SZ_LDS) {
+        const int g = (ktn * 64 + half * 32) / GS;
+        const unsigned char* p =
+            sz_lds + (wave * TNW + j) * 2048 + ((g >> 3) & 1) * 1024 + r32 * 16 + (g & 7) * 2;
+        scur[j] = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
+        zcur[j] = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p + 512));
+      } else {
+        scur[j] = sb_to_f32<SB>(bs[sl][j]);
+        zcur[j] = sb_to_f32<SB>(bz[sl][j]);
+      }
       s16cur[j] = scur[j] * 0.0625f;
-      zcur[j] = sb_to_f32<SB>(bz[j]);
     }
   };
   bf16x8 af[2][TMW], bfr[2][TNW];
@@ -264,49 +376,75 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[slot][j], af[slot][i], acc[i][j], 0, 0, 0);
   };
   constexpr int MF = TMW * TNW;  // MFMAs per group
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
 
-  load_a(0);
-  load_b(0);
-  store_a(0);
-  if (KT > 1) load_a(1);
-  take_b();
-  if (KT > 1) load_b(1);
-  __syncthreads();
+  // Prologue: issue A(0) W(0) A(1) W(1) A(2) W(2), wait for A(0) and W(0).  W(j) goes to ring
+  // slot (KT - j) & 1, counted from the end so that the last three steps always use the same
+  // slots whatever KT is.
+  auto prologue = [&](auto SA, auto SB_) __attribute__((always_inline)) {  // SA = slot of W(0)
+    if constexpr (SZ_LDS) {  // block 0, before A(0): complete once A(0) is
+#pragma unroll
+      for (int j = 0; j < TNW; ++j)
+        lds_dma16(rsz, sz_base + (uint32_t)((wv * TNW + j) * 2048), (half ? z_rel : s_rel) + g_base[j] * 2u);
+    }
+    dma_a(0);
+    load_b(0, SA);
+    if (KT > 1) {
+      dma_a(1);
+      load_b(1, SB_);
+    }
+    if (KT > 2) {
+      dma_a(2);
+      mlxq_vmcnt<B_TAIL + A_PER + B_OPS + A_PER>();
+    } else if (KT > 1) {
+      mlxq_vmcnt<B_TAIL + A_PER + B_OPS>();
+    } else {
+      mlxq_vmcnt<B_TAIL>();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    take_b(SA, 0);
+    if (KT > 2) load_b(2, SA);
+  };
+  if (KT & 1) prologue(S1{}, S0{});
+  else prologue(S0{}, S1{});
+  lds_barrier();
   read_a(0, smem[0], 0);
   deq_b(0, 0);
 
-  // One K step.  NEXT: a step kt+1 exists; NEXT2: a step kt+2 exists.  Compile-time so the body
-  // is branch-free and the two scheduling regions (split by the barrier) can be interleaved:
-  // each MFMA is followed by a share of the next group's LDS reads, dequant VALU and loads.
-  auto step = [&](int kt, auto NEXT, auto NEXT2) {
-    constexpr bool next = decltype(NEXT)::value, next2 = decltype(NEXT2)::value;
-    const unsigned char* As = smem[kt % 3];
-    const unsigned char* An = smem[(kt + 1) % 3];
-    if constexpr (next) {
-      store_a((kt + 1) % 3);
-      if constexpr (next2) load_a(kt + 2);
-    }
+  // One K step.  N1/N2/N3: steps kt+1/kt+2/kt+3 exist; SLOT = (KT-kt-1)&1 holds W(kt+1) and
+  // then receives W(kt+3).  All compile-time so the body is branch-free and the two scheduling regions
+  // (split by the barrier) interleave each MFMA with a share of LDS reads, dequant VALU and loads.
+  auto step = [&](int kt, auto SLOT, auto N1_, auto N2_, auto N3_) __attribute__((always_inline)) {
+    constexpr bool N1 = decltype(N1_)::value, N2 = decltype(N2_)::value, N3 = decltype(N3_)::value;
+    const unsigned char* As = smem[kt & (kStages - 1)];
+    const unsigned char* An = smem[(kt + 1) & (kStages - 1)];
     read_a(1, As, 1);
     deq_b(1, 1);
     mfma_group(0);
     read_a(0, As, 2);
     deq_b(0, 2);
     mfma_group(1);
-    if constexpr (next) __builtin_amdgcn_sched_group_barrier(0x200, A_PER, 0);  // tile writes first
 #pragma unroll
     for (int q = 0; q < 2 * MF; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                          // MFMA
-      if (q % MF < TMW) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // LDS read
-      if (next2 && q < A_PER) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // global load
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);                          // VALU
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                     // MFMA
+      if (q % MF < TMW) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);                     // VALU
     }
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    // A(kt+1) issued before W(kt+1) [, A(kt+2), W(kt+2)].
+    if constexpr (N1) mlxq_vmcnt<B_OPS + (N2 ? A_PER + B_OPS : 0)>();
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (N3) dma_a(kt + 3);
     read_a(1, As, 3);
     deq_b(1, 3);
     mfma_group(0);
-    if constexpr (next) {
-      take_b();
-      if constexpr (next2) load_b(kt + 2);
+    if constexpr (N1) {
+      // W(kt+1) issued before [A(kt+2), W(kt+2),] [A(kt+3)].
+      mlxq_vmcnt<B_TAIL + (N2 ? A_PER + B_OPS : 0) + (N3 ? A_PER : 0)>();
+      take_b(SLOT, kt + 1);
+      if constexpr (N3) load_b(kt + 3, SLOT);
       read_a(0, An, 0);
       deq_b(0, 0);
     }
@@ -314,24 +452,39 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
 #pragma unroll
     for (int q = 0; q < 2 * MF; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (q < MF || next) {
+      if (q < MF || N1) {
         if (q % MF < TMW) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
-      if (next2 && q >= MF && q < MF + 2 + TNW * WPL / 4) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (N3 && q < A_PER) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (N3 && q >= MF && q < MF + B_OPS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
-  int kt = 0;
-  for (; kt + 2 < KT; ++kt) step(kt, T_{}, T_{});
-  if (kt + 1 < KT) {
-    step(kt, T_{}, F_{});
-    ++kt;
+  // Scale/bias block b+1 is fetched with load_b(kt+3) by the step kt = b*SPB - 1 whose take starts
+  // reading block b, into the buffer block b-1 used.  Completion: the load is issued before
+  // A(kt+4), and step kt+3 waits for A(kt+4) before its barrier; block b+1 is first read by the
+  // take of step kt+SPB, SPB >= 4.
+  // Steps 0 .. KT-4 in pairs (one peeled when their count is odd), then the last three steps.
+  if (KT >= 4) {
+    int kt = 0;
+    if ((KT - 3) & 1) {
+      step(0, S1{}, T_{}, T_{}, T_{});
+      kt = 1;
+    }
+    for (; kt < KT - 3; kt += 2) {
+      step(kt, S0{}, T_{}, T_{}, T_{});
+      step(kt + 1, S1{}, T_{}, T_{}, T_{});
+    }
   }
-  step(kt, F_{}, F_{});
+  if (KT >= 3) step(KT - 3, S0{}, T_{}, T_{}, F_{});
+  if (KT >= 2) step(KT - 2, S1{}, T_{}, F_{}, F_{});
+  step(KT - 1, S0{}, F_{}, F_{}, F_{});
 
   // ---- epilogue: lane holds m = bm0 + 32 i + r32 and n = wn0 + 32 j + 8 a + 4 h + b.
+  float* bias_lds = reinterpret_cast<float*>(smem[KT & (kStages - 1)]);
   if constexpr (FUSED) {
     if (epi.bias) {
       if (tid < kBN) bias_lds[tid] = bias_t;
@@ -406,7 +559,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   if constexpr (TNW > 1) epilogue_cols(std::integral_constant<int, 1>{});
 }
 
-template <typename SB, int BITS, int GS, int WAVES>
+template <typename SB, int BITS, int GS, int WAVES, int BM>
 static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                          const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st,
                          int64_t tiles, const QmmBatch& bat) {
@@ -414,7 +567,7 @@ static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq
   const int kind = fused ? 1 + epi.act : 0;
   const dim3 grid((unsigned)tiles, (unsigned)bat.count);
 #define MLXQ_WL(E)                                                                                    \
-  hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, E>), grid, dim3(WAVES * 64), 0, st,        \
+  hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, E, BM>), grid, dim3(WAVES * 64), 0, st,    \
                      (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi, bat)
   switch (kind) {
     case 0: MLXQ_WL(0); break;
@@ -427,19 +580,64 @@ static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq
   return check_launch("qmm_wide");
 }
 
+// Workgroups that run at once: one per CU (the kernel's LDS and registers allow no second).
+static int64_t resident_workgroups() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] <= 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Tile height for a problem: the launch takes ceil(tiles / CUs) rounds of tiles whose time is
+// roughly proportional to BM plus a fixed per-tile share (weight loads and dequant, pipeline fill);
+// pick the BM with the smallest rounds * (BM + 32).
+static int qmm_wide_tile_rows(int64_t M, int64_t N, int64_t count) {
+  const int64_t cus = resident_workgroups();
+  const int64_t tn = (N + kBN - 1) / kBN;
+  int best = kBM;
+  int64_t best_cost = -1;
+  for (int bm : {256, 224}) {
+    const int64_t tiles = (M + bm - 1) / bm * tn * count;
+    const int64_t cost = (tiles + cus - 1) / cus * (bm + 32);
+    if (best_cost < 0 || cost < best_cost) best = bm, best_cost = cost;
+  }
+  return best;
+}
+
 template <typename SB, int BITS, int GS>
 static int launch_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                        const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st,
                        const QmmBatch& bat) {
-  const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
-  if (tiles == 0 || bat.count == 0) return MLXQ_OK;
-  if (tiles > 0x7fffffff || bat.count > 65535) return set_error(MLXQ_EINVAL, "qmm: problem too large");
+  if (M == 0 || N == 0 || bat.count == 0) return MLXQ_OK;
+  if (bat.count > 65535) return set_error(MLXQ_EINVAL, "qmm: problem too large");
   // 8 waves (two per SIMD) measured faster than 4 waves with twice the columns per wave.
-  return launch_wide_w<SB, BITS, GS, 8>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+  // bf16 scales (the reference's layout) also get the 224-row tile; f32 scales keep 256.
+  const int bm = std::is_same<SB, uint16_t>::value ? qmm_wide_tile_rows(M, N, bat.count) : kBM;
+  const int64_t tiles = ((M + bm - 1) / bm) * ((N + kBN - 1) / kBN);
+  if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm: problem too large");
+  if constexpr (std::is_same<SB, uint16_t>::value) {
+    if (bm == 224) return launch_wide_w<SB, BITS, GS, 8, 224>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+  }
+  return launch_wide_w<SB, BITS, GS, 8, kBM>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+}
+
+bool qmm_wide_sb_reach(const void* scales, const void* biases, int64_t bytes, int sb_bytes) {
+  if (sb_bytes != 2) return true;
+  const uint64_t s = (uint64_t)(uintptr_t)scales, b = (uint64_t)(uintptr_t)biases;
+  const uint64_t lo = s < b ? s : b, hi = s < b ? b : s;
+  return hi - lo + (uint64_t)bytes < ((uint64_t)1 << 32);
 }
 
 bool qmm_wide_fits(int64_t M, int64_t K, int64_t N, int gs, int bits, int sb_bytes) {
   const int64_t lim = (int64_t)1 << 32;
+  // bf16 scales and biases are staged in blocks of 8 groups: K / gs must be a multiple of 8.
+  if (sb_bytes == 2 && (K / gs) % 8 != 0) return false;
   return M * K * 2 < lim && N * (K * bits / 32) * 4 < lim && N * (K / gs) * sb_bytes < lim;
 }
 

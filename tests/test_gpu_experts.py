@@ -41,10 +41,10 @@ def _check(mlxq, y, x, packs, bias, gs, bits, per_expert, w_bf16, rows=None, wha
 
 @pytest.mark.parametrize("per_expert", [False, True])
 def test_experts_one_launch(mlxq, per_expert):
-    """E = 8 experts of [2048, 256] Q4 g64 at M = 512: 128 GEMM tiles, one launch over grid.y."""
+    """E = 8 experts of [2048, 512] Q4 g64 at M = 512: 128 GEMM tiles, one launch over grid.y."""
     banner("experts one launch", per_expert)
     rng = np.random.default_rng(5 + per_expert)
-    E, M, N, K, gs, bits = 8, 512, 2048, 256, 64, 4
+    E, M, N, K, gs, bits = 8, 512, 2048, 512, 64, 4
     packs, wq, s, b = _stack(rng, E, N, K, gs, bits)
     bias = bf16_normal(rng, (E, N), 0.5)
     x = bf16_normal(rng, (E, M, K) if per_expert else (M, K))

@@ -191,13 +191,19 @@ def test_qmm_gemm_vs_oracle(mlxq, M, K, N, gs, bits):
 
 
 WIDE_CASES = [
-    # Shapes with >= 128 256x256 tiles take the wide kernel (weights dequantized in registers).
-    (2304, 256, 4096, 64, 4),
-    (2000, 192, 4136, 32, 8),   # ragged M and N
-    (2048, 384, 4096, 128, 4),
-    (2304, 128, 4096, 64, 8),
+    # Shapes with >= 128 256x256 tiles and K / group_size a multiple of 8 take the wide kernel
+    # (bf16 scales/biases staged in LDS in blocks of 8 groups).  Cases cover 1..3 scale blocks,
+    # ragged M and N, and both tile heights: on 256 CUs the N = 4096-ish cases run 224-row tiles
+    # (one round either way), the N = 32768 cases need 256-row tiles to stay in one round.
+    (2304, 512, 4096, 64, 4),    # one block
+    (2000, 256, 4136, 32, 8),    # ragged M and N, one block of 4 steps
+    (2048, 2048, 4096, 128, 4),  # two blocks of 16 steps
+    (2304, 1024, 4096, 64, 8),   # two blocks
+    (2048, 768, 4096, 32, 4),    # three blocks of 4 steps
+    (512, 1024, 32768, 64, 4),
+    (500, 512, 32768, 32, 8),
+    (2304, 256, 4096, 64, 4),    # K / gs = 4: falls back to the tiled kernel
 ]
-
 
 @pytest.mark.parametrize("M,K,N,gs,bits", WIDE_CASES)
 def test_qmm_wide_vs_oracle(mlxq, M, K, N, gs, bits):
@@ -211,11 +217,28 @@ def test_qmm_wide_vs_oracle(mlxq, M, K, N, gs, bits):
     assert_close(y, ref, f"wide M={M} K={K} N={N} gs={gs} b={bits}")
 
 
+@pytest.mark.parametrize("M,K,N,gs,bits", [(2048, 192, 4096, 64, 4), (2048, 64, 4096, 32, 4),
+                                           (2100, 320, 4352, 64, 8), (2048, 512, 4096, 128, 8)])
+def test_qmm_wide_f32_scales(mlxq, M, K, N, gs, bits):
+    """bf16 activations with f32 scales/biases: the wide kernel's register-loaded scale path,
+    any K % 64 == 0 (K/64 = 3, 1, 5 and 8 steps cover both prologue parities)."""
+    banner("qmm wide f32 scales", M, K, N, gs, bits)
+    rng = np.random.default_rng(M + K + N + 7 * bits)
+    x = bf16_normal(rng, (M, K))
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    rwq, rs, rb = oracle.quantize(w, gs, bits)
+    assert rs.dtype == np.float32
+    y = to_np(mlxq.qmm(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs, torch.float32), to_gpu(rb, torch.float32),
+                       gs, bits))
+    ref = oracle.quantized_matmul(x, rwq, rs, rb, gs, bits, w_bf16=True, out_bf16=True)
+    assert_close(y, ref, f"wide f32 scales M={M} K={K} N={N} gs={gs} b={bits}")
+
+
 @pytest.mark.parametrize("act", [0, 1, 2])
 def test_linear_wide_bias_lora_act(mlxq, act):
     banner("linear wide epilogue", act)
     rng = np.random.default_rng(77 + act)
-    M, K, N, r = 2100, 256, 4200, 16
+    M, K, N, r = 2100, 512, 4200, 16
     x = bf16_normal(rng, (M, K))
     w = bf16_normal(rng, (N, K), 0.02)
     bias = bf16_normal(rng, (N,), 0.5)
