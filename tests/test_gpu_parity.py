@@ -193,18 +193,17 @@ def test_qmm_gemm_vs_oracle(mlxq, M, K, N, gs, bits):
 WIDE_CASES = [
     # Shapes with >= 128 256x256 tiles and K / group_size a multiple of 8 take the wide kernel
     # (bf16 scales/biases staged in LDS in blocks of 8 groups).  Cases cover 1..3 scale blocks,
-    # ragged M and N, and both tile heights: on 256 CUs the N = 4096-ish cases run 224-row tiles
-    # (one round either way), the N = 32768 cases need 256-row tiles to stay in one round.
+    # ragged M and N, and both tile heights: on 256 CUs the one-round cases run 256-row tiles,
+    # the two-round cases marked 224 run 224-row tiles.
     (2304, 512, 4096, 64, 4),    # one block
     (2000, 256, 4136, 32, 8),    # ragged M and N, one block of 4 steps
     (2048, 2048, 4096, 128, 4),  # two blocks of 16 steps
-    (2304, 1024, 4096, 64, 8),   # two blocks
-    (2048, 768, 4096, 32, 4),    # three blocks of 4 steps
+    (2304, 512, 8192, 64, 8),    # 224
+    (2000, 768, 8400, 32, 4),    # 224, ragged, three blocks of 4 steps
     (512, 1024, 32768, 64, 4),
     (500, 512, 32768, 32, 8),
     (2304, 256, 4096, 64, 4),    # K / gs = 4: falls back to the tiled kernel
 ]
-
 @pytest.mark.parametrize("M,K,N,gs,bits", WIDE_CASES)
 def test_qmm_wide_vs_oracle(mlxq, M, K, N, gs, bits):
     banner("qmm wide", M, K, N, gs, bits)
