@@ -233,6 +233,40 @@ def test_qmm_wide_f32_scales(mlxq, M, K, N, gs, bits):
     assert_close(y, ref, f"wide f32 scales M={M} K={K} N={N} gs={gs} b={bits}")
 
 
+# Stream-K launches: on 256 CUs these shapes fill under 70% of their data-parallel rounds, so
+# 256 workgroups split the tiles' K ranges (units of 8 scale groups) evenly; tiles cut between
+# two or three workgroups are finished by the last to arrive from f32 partial sums.
+STREAMK_CASES = [
+    # M, K, N, gs, bits, act, bias: (units per tile, tiles) -> contributors per tile
+    (2304, 4096, 4096, 64, 4, 0, False),   # 8 units x 144 tiles over 256: up to 3 per tile
+    (2304, 1024, 4096, 64, 8, 1, True),    # 2 units x 144 tiles: 2 per tile, bias + GELU
+    (1000, 2048, 6000, 32, 4, 2, True),    # ragged M and N, 16 units x 96 tiles, tanh GELU
+    (4608, 3072, 4352, 64, 4, 0, False),   # 306 tiles: 2 rounds at 60%
+]
+
+
+@pytest.mark.parametrize("M,K,N,gs,bits,act,bias", STREAMK_CASES)
+def test_qmm_wide_stream_k(mlxq, M, K, N, gs, bits, act, bias):
+    """Stream-K launches against the oracle on sampled rows (each output row depends only on its
+    input row; the samples include every 256-row tile boundary), and bit-identical on a rerun."""
+    banner("stream-K", M, K, N, gs, bits, act, bias)
+    rng = np.random.default_rng(M + K + N + act)
+    x = bf16_normal(rng, (M, K))
+    w = bf16_normal(rng, (N, K), 0.02)
+    bv = bf16_normal(rng, (N,), 0.5) if bias else None
+    rwq, rs, rb = oracle.quantize(w, gs, bits, sb_bf16=True)
+    args = (to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), gs, bits)
+    kw = dict(bias=to_gpu(bv) if bias else None, activation=act)
+    y1 = mlxq.linear(*args, **kw)
+    y2 = mlxq.linear(*args, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2), "stream-K result differs between runs"
+    edges = [r for t in range(0, M, 256) for r in (t, t + 255) if r < M]
+    rows = np.unique(np.concatenate([edges, rng.choice(M, 24, replace=False), [M - 1]]))
+    ref = oracle.linear(x[rows], rwq, rs, rb, gs, bits, w_bf16=True, act_bf16=True, bias=bv, act=act)
+    assert_close(to_np(y1)[rows], ref, f"stream-K M={M} K={K} N={N}")
+
+
 @pytest.mark.parametrize("act", [0, 1, 2])
 def test_linear_wide_bias_lora_act(mlxq, act):
     banner("linear wide epilogue", act)
