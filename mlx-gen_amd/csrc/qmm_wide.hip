@@ -29,6 +29,7 @@
 // Tile order is XCD-aware: workgroups are dispatched round-robin over the 8 XCDs, so consecutive
 // ids are remapped to give each XCD a contiguous slice of a grouped (4 M-tiles x all N-tiles)
 // tile order, keeping the activation and weight tiles a slice shares resident in that XCD's L2.
+#include <atomic>
 #include <cstdlib>
 #include <map>
 #include <mutex>
@@ -46,6 +47,17 @@ constexpr int kBN = 256;
 constexpr int kGroupM = 4;
 constexpr int kStages = 4;  // activation LDS ring depth (power of two)
 constexpr int kBufferFlags = 0x00020000;  // raw buffer resource word 3 for gfx9-family loads
+
+// GELU tables: entry h is the bf16 result of the epilogue's exact-erf ([0]) and tanh ([1])
+// GELU for the bf16 input with bits h.  Filled once per device by act_table_kernel.
+__device__ uint16_t g_act_table[2][65536];
+
+__global__ __launch_bounds__(256) void act_table_kernel() {
+  const int h = blockIdx.x * 256 + threadIdx.x;
+  const float v = bf16_bits_to_f32((uint32_t)h);
+  g_act_table[0][h] = f32_to_bf16_bits(gelu_erf(v));
+  g_act_table[1][h] = f32_to_bf16_bits(gelu_tanh<true>(v));
+}
 
 }  // namespace
 
@@ -212,7 +224,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   constexpr bool SZ_LDS = sizeof(SB) == 2;
   constexpr int SPB = 8 * GS / 64;
   constexpr int kSzBytes = SZ_LDS ? WAVES * TNW * 2048 + WAVES * 1024 : 0;
-  __shared__ __attribute__((aligned(16))) unsigned char lds_all[kStages * kBM * 128 + kSzBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds_all[kStages * kBM * 128 + kSzBytes + kBN * 4];
   auto smem = reinterpret_cast<unsigned char (*)[kBM * 128]>(lds_all);
   unsigned char* const sz_lds = lds_all + kStages * kBM * 128;
 
@@ -472,7 +484,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     take_b(SA, 0);
     if (KT > 2) load_b(2, SA);
   };
-  if (KT & 1) prologue(S1{}, S0{});
+  // bf16 scales: KT is a whole number of scale blocks (SPB >= 4 steps), so even.
+  if (!SZ_LDS && (KT & 1)) prologue(S1{}, S0{});
   else prologue(S0{}, S1{});
   lds_barrier();
   read_a(0, smem[0], 0);
@@ -536,7 +549,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   // Steps 0 .. KT-4 in pairs (one peeled when their count is odd), then the last three steps.
   if (KT >= 4) {
     int kt = 0;
-    if ((KT - 3) & 1) {
+    if (SZ_LDS || ((KT - 3) & 1)) {
       step(0, S1{}, T_{}, T_{}, T_{});
       kt = 1;
     }
@@ -614,11 +627,27 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   }
 
   // ---- epilogue: lane holds m = bm0 + 32 i + r32 and n = wn0 + 32 j + 8 a + 4 h + b.
-  float* bias_lds = reinterpret_cast<float*>(smem[KT & (kStages - 1)]);
+  // With an activation, the input of the GELU is a bf16 value (the rounded sum of the product,
+  // bias and LoRA terms), so the activation is a lookup in a 65536-entry bf16 table of the same
+  // device function (g_act_table, bit-identical to evaluating it): the table is copied into the
+  // now idle activation ring while the first pass rounds and adds into the accumulators, and a
+  // second pass looks up and stores.  Evaluating the exact-erf GELU cost ~20 VALU ops per output
+  // with the MFMA idle (~15 k cycles per 224x256 tile).
+  constexpr bool TABLE = ACT != MLXQ_ACT_NONE;
+  float* bias_lds = reinterpret_cast<float*>(lds_all + kStages * kBM * 128 + kSzBytes);
   if constexpr (FUSED) {
-    if (epi.bias) {
-      if (tid < kBN) bias_lds[tid] = bias_t;
-      __syncthreads();
+    if (epi.bias && tid < kBN) bias_lds[tid] = bias_t;
+    if (epi.bias || TABLE) __syncthreads();  // bias visible; every wave past its last ring read
+  }
+  if constexpr (TABLE) {
+    const uint64_t ta = (uint64_t)(uintptr_t)&g_act_table[ACT - 1][0];
+    const u32x4 rt = {(uint32_t)ta, (uint32_t)(ta >> 32) & 0xffffu, 65536u * 2u, (uint32_t)kBufferFlags};
+    const uint32_t lbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds_all;
+    constexpr int kPer = 65536 * 2 / 1024 / WAVES;  // 1 KB loads per wave
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+      const uint32_t blk = (uint32_t)(wv * kPer + r) * 1024u;
+      lds_dma16(rt, lbase + blk, blk + (uint32_t)lane * 16u);
     }
   }
   const bool vec_ok = (N % 4) == 0;
@@ -638,6 +667,24 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
         lb[j] = *reinterpret_cast<const bf16x8*>(epi.lbt + (wn0 + j * 32 + r32) * 16 + half * 8);
     }
   }
+  // Store 16 outputs of accumulator (i, j), given as bf16 bits (two per word).
+  auto store_tile = [&](int i, int64_t nb, const uint32_t (&pk)[8]) {
+    const int64_t m = bm0 + i * 32 + r32;
+    if (m < M) {
+      uint16_t* yrow = y + m * N;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int64_t n = nb + 8 * a;
+        if (vec_ok && n + 3 < N) {
+          *reinterpret_cast<u32x2*>(yrow + n) = u32x2{pk[2 * a], pk[2 * a + 1]};
+        } else {
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            if (n + b < N) yrow[n + b] = (uint16_t)(pk[2 * a + b / 2] >> (16 * (b & 1)));
+        }
+      }
+    }
+  };
   // One 32-column sub-tile per call; J is a compile-time index so acc stays in registers.
   auto epilogue_cols = [&](auto J) {
     constexpr int j = decltype(J)::value;
@@ -653,8 +700,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     }
 #pragma unroll
     for (int i = 0; i < TMW; ++i) {
-      const int64_t m = bm0 + i * 32 + r32;
-      f32x16 v = acc[i][j];
+      f32x16& v = acc[i][j];
       if constexpr (FUSED) {
         f32x16 r = {};
         if (lora) r = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lb[j], xa[i], r, 0, 0, 0);
@@ -663,30 +709,41 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
           float o = round_bf16(v[e]);
           if (epi.bias) o = round_bf16(o + bias_v[e]);
           if (lora) o = round_bf16(o + round_bf16(round_bf16(r[e]) * epi.lora_scale));
-          if constexpr (ACT == MLXQ_ACT_GELU) o = gelu_erf(o);
-          else if constexpr (ACT == MLXQ_ACT_GELU_TANH) o = gelu_tanh<true>(o);
           v[e] = o;
         }
       }
-      if (m < M) {
-        uint16_t* yrow = y + m * N;
+      if constexpr (!TABLE) {
+        uint32_t pk[8];
 #pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const int64_t n = nb + 8 * a;
-          if (vec_ok && n + 3 < N) {
-            u32x2 p = {pack_bf16x2(v[4 * a], v[4 * a + 1]), pack_bf16x2(v[4 * a + 2], v[4 * a + 3])};
-            *reinterpret_cast<u32x2*>(yrow + n) = p;
-          } else {
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-              if (n + b < N) yrow[n + b] = f32_to_bf16_bits(v[4 * a + b]);
-          }
-        }
+        for (int q = 0; q < 8; ++q) pk[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
+        store_tile(i, nb, pk);
       }
     }
   };
   epilogue_cols(std::integral_constant<int, 0>{});
   if constexpr (TNW > 1) epilogue_cols(std::integral_constant<int, 1>{});
+  if constexpr (TABLE) {
+    mlxq_vmcnt<0>();  // this wave's table loads
+    __syncthreads();  // and every other wave's
+    const uint16_t* tab = reinterpret_cast<const uint16_t*>(lds_all);
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) {
+      const int64_t nb = wn0 + j * 32 + 4 * half;
+#pragma unroll
+      for (int i = 0; i < TMW; ++i) {
+        uint32_t pk[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          // v holds bf16-rounded values: the high half of the f32 is the bf16 code.
+          const uint32_t lo = tab[__float_as_uint(acc[i][j][2 * q]) >> 16];
+          const uint32_t hi = tab[__float_as_uint(acc[i][j][2 * q + 1]) >> 16];
+          pk[q] = lo | (hi << 16);
+        }
+        store_tile(i, nb, pk);
+      }
+    }
+    if constexpr (SKM) __syncthreads();  // table reads done before the next segment's loads
+  }
   if constexpr (SKM) {
     __syncthreads();  // the next segment's prologue refills the LDS
     u_cur = (tile + 1) * upt;
@@ -694,12 +751,18 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   } while (SKM && u_cur < u_end);  // segments
 }
 
+static int ensure_act_table(hipStream_t st);
+
 template <typename SB, int BITS, int GS, int WAVES, int BM, bool SKM = false>
 static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                          const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st,
                          int64_t workgroups, const QmmBatch& bat, const QmmStreamK& sk = QmmStreamK{}) {
   const bool fused = epi.bias || epi.rank16 || epi.act != MLXQ_ACT_NONE;
   const int kind = fused ? 1 + epi.act : 0;
+  if (kind >= 2) {
+    const int rc = ensure_act_table(st);
+    if (rc != MLXQ_OK) return rc;
+  }
   const dim3 grid((unsigned)workgroups, (unsigned)bat.count);
 #define MLXQ_WL(E)                                                                                    \
   hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, E, BM, SKM>), grid, dim3(WAVES * 64), 0, st, \
@@ -713,6 +776,27 @@ static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq
   }
 #undef MLXQ_WL
   return check_launch("qmm_wide");
+}
+
+// The GELU tables are filled on a device's first GELU launch and the host waits for that fill
+// once, so later launches on any stream find them complete.  Under graph capture (no waiting
+// possible) the fill is captured ahead of the GEMM instead and the device stays unmarked.
+static std::atomic<int> g_act_table_ready[64];
+
+static int ensure_act_table(hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(MLXQ_EDEVICE, "qmm: no current device");
+  const bool slot = dev >= 0 && dev < 64;
+  if (slot && g_act_table_ready[dev].load(std::memory_order_acquire)) return MLXQ_OK;
+  hipLaunchKernelGGL(act_table_kernel, dim3(256), dim3(256), 0, st);
+  int rc = check_launch("act_table");
+  if (rc != MLXQ_OK) return rc;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (slot && hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
+    if (hipStreamSynchronize(st) != hipSuccess) return set_error(MLXQ_EDEVICE, "qmm: act table fill failed");
+    g_act_table_ready[dev].store(1, std::memory_order_release);
+  }
+  return MLXQ_OK;
 }
 
 // Workgroups that run at once: one per CU (the kernel's LDS and registers allow no second).
