@@ -30,11 +30,7 @@
 // ids are remapped to give each XCD a contiguous slice of a grouped (4 M-tiles x all N-tiles)
 // tile order, keeping the activation and weight tiles a slice shares resident in that XCD's L2.
 #include <atomic>
-#include <cstdlib>
-#include <map>
-#include <mutex>
 #include <type_traits>
-#include <utility>
 
 #include "mlxq_common.h"
 
@@ -61,13 +57,6 @@ __global__ __launch_bounds__(256) void act_table_kernel() {
 
 }  // namespace
 
-// Stream-K launch parameters (groups == 0: data-parallel launch, one tile per workgroup).
-struct QmmStreamK {
-  float* partials = nullptr;    // [groups][2][BM * 256] f32, uncached workspace
-  uint32_t* counters = nullptr; // [tiles], zero between launches
-  int64_t groups = 0;           // workgroups of the launch
-  int64_t upt = 0;              // K units (SPB steps) per tile
-};
 
 namespace {
 
@@ -83,7 +72,7 @@ __device__ __forceinline__ void grouped_coords(int64_t L, int64_t tiles_m, int64
   tn = idx / gsz;
 }
 
-// Workgroup bid of a data-parallel launch.  Workgroups are dispatched round-robin over the 8
+// Tile of workgroup bid.  Workgroups are dispatched round-robin over the 8
 // XCDs, so consecutive ids are remapped to give each XCD a contiguous slice of the grouped order.
 __device__ __forceinline__ void tile_coords(int64_t bid, int64_t tiles_m, int64_t tiles_n,
                                             int64_t& tm, int64_t& tn) {
@@ -94,11 +83,6 @@ __device__ __forceinline__ void tile_coords(int64_t bid, int64_t tiles_m, int64_
   grouped_coords(L, tiles_m, tiles_n, tm, tn);
 }
 
-// Stream-K position of workgroup bid among G: XCD-contiguous, so that the workgroups sharing a
-// stretch of tiles (and their partial sums) mostly sit on one XCD.
-__device__ __forceinline__ int64_t sk_position(int64_t bid, int64_t G) {
-  return G % 8 == 0 ? (bid % 8) * (G / 8) + bid / 8 : bid;
-}
 
 __device__ __forceinline__ int swz_f(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
@@ -203,11 +187,11 @@ __device__ __forceinline__ float sb_to_f32(uint32_t bits) {
 // EPI selects the epilogue at compile time: 0 plain y = bf16(acc); 1 bias / rank-16 LoRA; 2 and 3
 // the same followed by the exact-erf or the tanh GELU (EPI - 1 is the mlxq_activation).  One
 // epilogue per instantiation keeps it small enough that the accumulator tile stays in registers.
-template <typename SB, int BITS, int GS, int WAVES, int EPI, int BM, bool SKM>
+template <typename SB, int BITS, int GS, int WAVES, int EPI, int BM>
 __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, const uint32_t* __restrict__ wq,
     const SB* __restrict__ scales, const SB* __restrict__ biases, int64_t N,
-    uint16_t* __restrict__ y, QmmEpilogue epi, QmmBatch bat, QmmStreamK sk) {
+    uint16_t* __restrict__ y, QmmEpilogue epi, QmmBatch bat) {
   constexpr bool FUSED = EPI != 0;
   constexpr int ACT = FUSED ? EPI - 1 : MLXQ_ACT_NONE;
   constexpr int NT = WAVES * 64;
@@ -248,35 +232,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + kBN - 1) / kBN;
   const int64_t kwords = K * BITS / 32;
   const int64_t groups = K / GS;
-  // Work list.  Data-parallel launch: one whole tile, workgroup blockIdx.x.  Stream-K launch
-  // (sk.groups workgroups): the tiles' K ranges, in units of SPB steps, laid end to end in the
-  // grouped tile order and cut into sk.groups equal contiguous ranges; a range covers the tail
-  // of one tile, whole tiles, and the head of another, and each piece is a segment below.
-  static_assert(!SKM || SZ_LDS, "stream-K launches need bf16 scales (K units of 8 groups)");
-  const int64_t upt = SKM ? sk.upt : 1;
-  int64_t u_cur = 0, u_end = 1, u_first = 0;
-  if constexpr (SKM) {
-    const int64_t G = sk.groups, U = tiles_m * tiles_n * upt;
-    const int64_t v = sk_position(blockIdx.x, G);
-    u_cur = v * U / G;
-    u_end = (v + 1) * U / G;
-    u_first = u_cur;
-    if (u_cur >= u_end) return;
-  }
-  do {
-  int64_t tile, tm, tn, ku0 = 0, ku1 = 1;
-  if constexpr (!SKM) {
-    tile = blockIdx.x;
-    tile_coords(tile, tiles_m, tiles_n, tm, tn);
-  } else {
-    tile = u_cur / upt;
-    grouped_coords(tile, tiles_m, tiles_n, tm, tn);
-    ku0 = u_cur - tile * upt;
-    ku1 = u_end - tile * upt < upt ? u_end - tile * upt : upt;
-  }
-  const bool whole = !SKM || (ku0 == 0 && ku1 == upt);
-  const int64_t k0 = SKM ? ku0 * SPB : 0;  // first K step of this segment
-  const int KT = SKM ? (int)((ku1 - ku0) * SPB) : (int)(K / 64);
+  int64_t tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int KT = (int)(K / 64);
   const int64_t bm0 = tm * BM, bn0 = tn * kBN;
   const int64_t wn0 = bn0 + (int64_t)wave * (kBN / WAVES);
   // Dense bias of the tile's kBN columns: one value per thread, loaded now and parked in LDS for
@@ -315,7 +273,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     const int c = (lane & 7) ^ swz_f(rl);
     const int rt = rl < BM ? rl : BM - 1;
     const int64_t r = bm0 + rt < M ? bm0 + rt : M - 1;
-    a_goff[i] = (uint32_t)((r * K + c * 8 + k0 * 64) * 2);
+    a_goff[i] = (uint32_t)((r * K + c * 8) * 2);
   }
   auto dma_a = [&](int kt) {
     unsigned char* base = smem[kt & (kStages - 1)];
@@ -339,8 +297,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     const int64_t n = wn0 + j * 32 + r32;
     n_ok[j] = n < N;
     const int64_t nn = n_ok[j] ? n : N - 1;
-    w_goff[j] = (uint32_t)((nn * kwords + half * WPL + k0 * 2 * WPL) * 4);
-    g_base[j] = (uint32_t)(nn * groups + k0 * 64 / GS);
+    w_goff[j] = (uint32_t)((nn * kwords + half * WPL) * 4);
+    g_base[j] = (uint32_t)(nn * groups);
   }
   uint32_t braw[2][TNW][WPL];
   uint32_t bs[2][TNW], bz[2][TNW];  // raw scale/bias bits (f32 scales: loaded with the words)
@@ -567,70 +525,6 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   if (KT >= 2) step(KT - 2, S1{}, T_{}, F_{}, F_{});
   step(KT - 1, S0{}, F_{}, F_{}, F_{});
 
-  // ---- stream-K fixup of a partial tile.  Every contributor stores its f32 partial (in
-  // register order: float4 chunk c of thread t at c * NT + t) to its slot in the uncached
-  // workspace, waits for the stores, and bumps the tile's counter; the last to arrive adds the
-  // other partials in K order (deterministic: a left fold over the contributors, bit-identical
-  // to it for two contributors by commutativity), resets the counter for the next launch and
-  // runs the epilogue.  No workgroup ever waits for another.
-  if (SKM && !whole) {
-    constexpr int CH = TMW * TNW * 4;  // float4 chunks per thread
-    const int64_t G = sk.groups, U = tiles_m * tiles_n * upt;
-    const int64_t slot_elems = (int64_t)NT * CH * 4;
-    auto slot_ptr = [&](int64_t v, int slot) {
-      return reinterpret_cast<f32x4*>(sk.partials + (v * 2 + slot) * slot_elems);
-    };
-    auto chunk = [&](f32x4* p, int c) -> f32x4& { return p[c * NT + tid]; };
-    // Position v's range starts at u_begin(v) = v*U/G; the first position whose range holds unit
-    // u is ((u+1)*G - 1) / U.  A contributor whose range starts inside the tile holds it in
-    // slot 0 (its first segment), the one that started before it in slot 1 (its last).
-    auto owner = [&](int64_t u) { return ((u + 1) * G - 1) / U; };
-    auto slot_of = [&](int64_t v) { return v * U / G >= tile * upt ? 0 : 1; };
-    const int64_t v_me = sk_position(blockIdx.x, G);
-    const int64_t v_first = owner(tile * upt), v_last = owner((tile + 1) * upt - 1);
-    f32x4* mine = slot_ptr(v_me, u_cur == u_first ? 0 : 1);
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      const f32x16& a = acc[c / (4 * TNW)][(c / 4) % TNW];
-      const int q = c % 4;
-      chunk(mine, c) = f32x4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
-    }
-    mlxq_vmcnt<0>();
-    __syncthreads();
-    volatile uint32_t* flag = reinterpret_cast<volatile uint32_t*>(smem[KT & (kStages - 1)]) + 512;
-    if (tid == 0)
-      *flag = __hip_atomic_fetch_add(sk.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    const bool last = *flag == (uint32_t)(v_last - v_first);
-    __syncthreads();
-    if (!last) {
-      u_cur = (tile + 1) * upt;
-      continue;
-    }
-    auto add_from = [&](f32x4* p, bool assign) {
-#pragma unroll
-      for (int c0 = 0; c0 < CH; c0 += 4) {
-        f32x4 t[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) t[c] = chunk(p, c0 + c);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          f32x16& a = acc[(c0 + c) / (4 * TNW)][((c0 + c) / 4) % TNW];
-          const int q = (c0 + c) % 4;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) a[4 * q + e] = assign ? t[c][e] : a[4 * q + e] + t[c][e];
-        }
-      }
-    };
-    if (v_last - v_first == 1) {
-      const int64_t vo = v_me == v_first ? v_last : v_first;
-      add_from(slot_ptr(vo, slot_of(vo)), false);
-    } else {
-      for (int64_t v = v_first; v <= v_last; ++v) add_from(slot_ptr(v, slot_of(v)), v == v_first);
-    }
-    if (tid == 0) __hip_atomic_store(sk.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-
   // ---- epilogue: lane holds m = bm0 + 32 i + r32 and n = wn0 + 32 j + 8 a + 4 h + b.
   // With an activation, the input of the GELU is a bf16 value (the rounded sum of the product,
   // bias and LoRA terms), so the activation is a lookup in a 65536-entry bf16 table of the same
@@ -780,29 +674,24 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
       if (m < M && n < N) *reinterpret_cast<u32x4*>(y + m * N + n) = v;
     }
   }
-  if constexpr (SKM) {
-    __syncthreads();  // the next segment's prologue refills the LDS
-    u_cur = (tile + 1) * upt;
-  }
-  } while (SKM && u_cur < u_end);  // segments
 }
 
 static int ensure_act_table(hipStream_t st);
 
-template <typename SB, int BITS, int GS, int WAVES, int BM, bool SKM = false>
+template <typename SB, int BITS, int GS, int WAVES, int BM>
 static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                          const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st,
-                         int64_t workgroups, const QmmBatch& bat, const QmmStreamK& sk = QmmStreamK{}) {
+                         int64_t tiles, const QmmBatch& bat) {
   const bool fused = epi.bias || epi.rank16 || epi.act != MLXQ_ACT_NONE;
   const int kind = fused ? 1 + epi.act : 0;
   if (kind >= 2) {
     const int rc = ensure_act_table(st);
     if (rc != MLXQ_OK) return rc;
   }
-  const dim3 grid((unsigned)workgroups, (unsigned)bat.count);
+  const dim3 grid((unsigned)tiles, (unsigned)bat.count);
 #define MLXQ_WL(E)                                                                                    \
-  hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, E, BM, SKM>), grid, dim3(WAVES * 64), 0, st, \
-                     (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi, bat, sk)
+  hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, E, BM>), grid, dim3(WAVES * 64), 0, st,    \
+                     (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi, bat)
   switch (kind) {
     case 0: MLXQ_WL(0); break;
     case 1: MLXQ_WL(1); break;
@@ -864,58 +753,6 @@ static int qmm_wide_tile_rows(int64_t M, int64_t N, int64_t count) {
   return 256;
 }
 
-// ---- stream-K workspace.  Per (device, stream): partial-sum slots for every workgroup of a
-// launch and the tile counters, in uncached device memory so that partial sums written by one
-// XCD are read by another without cache maintenance.  Made on first use outside graph capture
-// (counters cleared on the stream) and kept for the life of the process: uncached memory that
-// a kernel has read is never freed.  Launches on one stream are ordered, so they share it
-// safely; other streams get their own.
-constexpr int64_t kSkMaxTiles = int64_t(1) << 20;
-struct SkWorkspace {
-  float* partials = nullptr;
-  uint32_t* counters = nullptr;
-};
-static std::mutex g_sk_mu;
-static std::map<std::pair<int, hipStream_t>, SkWorkspace> g_sk_ws;
-
-static const SkWorkspace* sk_workspace(hipStream_t st, int64_t groups) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  std::lock_guard<std::mutex> lock(g_sk_mu);
-  const auto key = std::make_pair(dev, st);
-  const auto it = g_sk_ws.find(key);
-  if (it != g_sk_ws.end()) return &it->second;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-  if (g_sk_ws.size() >= 16) return nullptr;
-  SkWorkspace w;
-  const size_t pbytes = (size_t)groups * 2 * kBM * kBN * sizeof(float);
-  const size_t cbytes = (size_t)kSkMaxTiles * sizeof(uint32_t);
-  if (hipExtMallocWithFlags(reinterpret_cast<void**>(&w.partials), pbytes, hipDeviceMallocUncached) != hipSuccess ||
-      hipExtMallocWithFlags(reinterpret_cast<void**>(&w.counters), cbytes, hipDeviceMallocUncached) != hipSuccess ||
-      hipMemsetAsync(w.counters, 0, cbytes, st) != hipSuccess) {
-    (void)hipGetLastError();  // the data-parallel launch still works; nothing is freed
-    return nullptr;
-  }
-  return &(g_sk_ws[key] = w);
-}
-
-// Stream-K spreads a launch's work evenly over all CUs, for the price of one f32 partial-sum
-// exchange per cut tile.  The CUs of a launch share one power budget, though: with all 256 busy
-// the clock falls (M = 4608, N = 3072, K = 12288: 1.88 GHz with the 216 CUs of the data-parallel
-// launch, 1.69 GHz with 256 under stream-K, for no net gain), so idle CUs in a last round cost
-// less than their count suggests.  Stream-K is used only when the data-parallel launch fills
-// under 70% of its rounds.  MLXQ_STREAMK=0 disables it.
-static bool streamk_wanted(int64_t tiles, int64_t cus) {
-  static const int env = [] {
-    const char* e = std::getenv("MLXQ_STREAMK");
-    return e ? std::atoi(e) : -1;
-  }();
-  if (env == 0) return false;
-  const int64_t rounds = (tiles + cus - 1) / cus;
-  return tiles * 100 < rounds * cus * 70 && tiles <= kSkMaxTiles;
-}
-
 template <typename SB, int BITS, int GS>
 static int launch_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                        const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st,
@@ -928,20 +765,6 @@ static int launch_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, 
   const int64_t tiles = ((M + bm - 1) / bm) * ((N + kBN - 1) / kBN);
   if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm: problem too large");
   if constexpr (std::is_same<SB, uint16_t>::value) {
-    // Stream-K (bf16 scales: K units of 8 groups; one matrix), 256-row tiles.
-    const int64_t cus = resident_workgroups();
-    if (bat.count == 1 && streamk_wanted(tiles, cus)) {
-      const int64_t t256 = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
-      if (const SkWorkspace* ws = sk_workspace(st, cus)) {
-        QmmStreamK sk;
-        sk.partials = ws->partials;
-        sk.counters = ws->counters;
-        sk.groups = cus;
-        sk.upt = (K / 64) / (8 * GS / 64);
-        if (t256 <= kSkMaxTiles)
-          return launch_wide_w<SB, BITS, GS, 8, kBM, true>(x, M, K, wq, s, b, N, y, epi, st, cus, bat, sk);
-      }
-    }
     if (bm == 224) return launch_wide_w<SB, BITS, GS, 8, 224>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
   }
   return launch_wide_w<SB, BITS, GS, 8, kBM>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
