@@ -123,4 +123,55 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
+// ---- MFMA GEMM weight dequantization (shared by the GEMM kernels)
+// v_cvt_f32_ubyteN: byte N of v as an exact f32.
+template <int B>
+__device__ __forceinline__ float ubyte(uint32_t v) {
+  float r;
+  if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+  if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+  if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+  if constexpr (B == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
+// Dequantize 8 codes into a bf16x8 MFMA operand: word kk of w (Q4, codes 0..7) or words 2kk,
+// 2kk+1 (Q8), each value bf16(fma(code, s, z)).  s16 = s/16 (exact) pairs with the odd Q4
+// codes, which are extracted still shifted left by 4: fma(16c, s/16, z) == fma(c, s, z).
+template <int BITS>
+__device__ __forceinline__ bf16x8 dequant8(const uint32_t* w, int kk, float s, float s16, float z) {
+  u32x4 o;
+  if constexpr (BITS == 4) {
+    const uint32_t v = w[kk];
+    const uint32_t lo = v & 0x0f0f0f0fu, hi = v & 0xf0f0f0f0u;
+    o[0] = pack_bf16x2(fmaf(ubyte<0>(lo), s, z), fmaf(ubyte<0>(hi), s16, z));
+    o[1] = pack_bf16x2(fmaf(ubyte<1>(lo), s, z), fmaf(ubyte<1>(hi), s16, z));
+    o[2] = pack_bf16x2(fmaf(ubyte<2>(lo), s, z), fmaf(ubyte<2>(hi), s16, z));
+    o[3] = pack_bf16x2(fmaf(ubyte<3>(lo), s, z), fmaf(ubyte<3>(hi), s16, z));
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t v = w[2 * kk + h];
+      o[2 * h] = pack_bf16x2(fmaf(ubyte<0>(v), s, z), fmaf(ubyte<1>(v), s, z));
+      o[2 * h + 1] = pack_bf16x2(fmaf(ubyte<2>(v), s, z), fmaf(ubyte<3>(v), s, z));
+    }
+  }
+  return __builtin_bit_cast(bf16x8, o);
+}
+
+// Scale/bias element as raw bits, converted with sb_to_f32 when used: a conversion right after
+// the load would make the caller wait for it there.
+template <typename SB>
+__device__ __forceinline__ uint32_t load_sb_bits(__amdgpu_buffer_rsrc_t r, uint32_t idx) {
+  if constexpr (sizeof(SB) == 2)
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, idx * 2u, 0, 0);
+  else
+    return __builtin_amdgcn_raw_buffer_load_b32(r, idx * 4u, 0, 0);
+}
+template <typename SB>
+__device__ __forceinline__ float sb_to_f32(uint32_t bits) {
+  if constexpr (sizeof(SB) == 2) return bf16_bits_to_f32(bits & 0xffffu);
+  else return __uint_as_float(bits);
+}
+
 }  // namespace mlxq

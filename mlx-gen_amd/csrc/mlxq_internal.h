@@ -40,6 +40,10 @@ bool qmm_wide_fits(int64_t M, int64_t K, int64_t N, int gs, int bits, int sb_byt
 // bf16 scales and biases are read through one 32-bit-offset buffer resource: both arrays
 // (bytes each) must lie within 4 GiB of the lower one.  Always true for f32 scales.
 bool qmm_wide_sb_reach(const void* scales, const void* biases, int64_t bytes, int sb_bytes);
+bool qmm_small_fits(int64_t M, int64_t K, int64_t N, int gs, int bits, int sb_bytes);
+int run_qmm_small(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+                  const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y,
+                  const QmmEpilogue& epi, hipStream_t st);
 int run_qmm_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
                  int sb_dtype, int64_t N, int gs, int bits, void* y, const QmmEpilogue& epi,
                  hipStream_t st, const QmmBatch& batch = QmmBatch{});

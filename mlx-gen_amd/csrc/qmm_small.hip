@@ -1,0 +1,246 @@
+// qmm_small.hip — quantized GEMM for small grids (text-encoder prefill: M up to a few hundred).
+//
+// y[M,N] = x[M,K] . W^T with the semantics of the other GEMM kernels: every weight dequantized
+// to bf16 as round_bf16(fma(code, scale, bias)), v_mfma_f32_32x32x16_bf16 accumulating in f32,
+// the epilogue's ops rounded to bf16 where the reference's separate ops round.
+//
+// When M x N gives few tiles, a tile kernel leaves most CUs idle and each workgroup walks all of
+// K one latency-bound step after another.  Here a workgroup of 8 waves owns a 64x64 output tile
+// and the waves split K: wave w takes K steps [w*KT/8, (w+1)*KT/8), loading its activation and
+// weight fragments straight into MFMA registers (no LDS in the loop) two steps ahead, so a tile
+// has eight independent load chains of KT/8 steps instead of one of KT.  The eight partial tiles
+// meet in LDS and are added in wave order (deterministic); waves 0-3 then finish one 32x32
+// sub-tile each.
+// MFMA roles (as in qmm_wide.hip): weights are the A operand (rows n), activations the B operand
+// (columns m); lane (h = lane >> 5, r = lane & 31) holds m = r and n = 8a + 4h + b in element
+// 4a + b of its f32x16, and covers k in [8(4h+kk), +8) of a 64-wide K step for MFMA kk.
+#include "mlxq_common.h"
+
+namespace mlxq {
+
+namespace {
+
+constexpr int kTile = 64;   // output tile rows and columns
+constexpr int kWaves = 8;   // waves per workgroup, splitting K
+constexpr int kBufferFlags = 0x00020000;
+
+template <typename SB, int BITS>
+struct SmallOps {           // one K step of one lane's operands
+  u32x4 a[2][4];            // activations: row sub-tile i, MFMA kk
+  uint32_t w[2][BITS];      // packed words: column sub-tile j
+  uint32_t s[2], z[2];      // raw scale / bias bits of sub-tile j
+};
+
+template <typename SB, int BITS, int GS, int EPI>
+__global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
+    const uint16_t* __restrict__ x, int64_t M, int64_t K, const uint32_t* __restrict__ wq,
+    const SB* __restrict__ scales, const SB* __restrict__ biases, int64_t N,
+    uint16_t* __restrict__ y, QmmEpilogue epi) {
+  constexpr bool FUSED = EPI != 0;
+  constexpr int ACT = FUSED ? EPI - 1 : MLXQ_ACT_NONE;
+  constexpr int WPL = BITS;  // packed words per lane per sub-tile per K step
+  // Partial tiles: [wave][sub-tile][quad of elements][lane] x 4 floats (128 KB).
+  __shared__ __attribute__((aligned(16))) f32x4 part[kWaves][4][4][64];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6, r32 = lane & 31, half = lane >> 5;
+  const int64_t tiles_m = (M + kTile - 1) / kTile;
+  const int64_t bm0 = (blockIdx.x % tiles_m) * kTile, bn0 = (blockIdx.x / tiles_m) * kTile;
+  const int64_t kwords = K * BITS / 32, groups = K / GS;
+  const int KT = (int)(K / 64);
+  const int k_begin = wave * KT / kWaves, nst = (wave + 1) * KT / kWaves - k_begin;
+
+  // Buffer resources (32-bit offsets: the host checks the operands fit in 4 GiB); rows past M
+  // and N are clamped to the last row, so every offset stays inside its operand.
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(x), (short)0, (int)(uint32_t)(M * K * 2), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(wq), (short)0, (int)(uint32_t)(N * kwords * 4), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<SB*>(scales), (short)0, (int)(uint32_t)(N * groups * sizeof(SB)), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<SB*>(biases), (short)0, (int)(uint32_t)(N * groups * sizeof(SB)), kBufferFlags);
+  uint32_t a_off[2], w_off[2], g_base[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t m = bm0 + 32 * i + r32 < M ? bm0 + 32 * i + r32 : M - 1;
+    a_off[i] = (uint32_t)((m * K + 32 * half) * 2);
+    const int64_t n = bn0 + 32 * i + r32 < N ? bn0 + 32 * i + r32 : N - 1;
+    w_off[i] = (uint32_t)((n * kwords + half * WPL) * 4);
+    g_base[i] = (uint32_t)(n * groups);
+  }
+
+  auto load = [&](int kt, SmallOps<SB, BITS>& d) {
+    const uint32_t g = (uint32_t)((kt * 64 + half * 32) / GS);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        d.a[i][kk] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, a_off[i] + (uint32_t)kt * 128u + 16u * kk, 0, 0));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int q = 0; q < WPL / 4; ++q) {
+        const u32x4 v = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[j] + (uint32_t)kt * (8u * WPL) + 16u * q, 0, 0));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d.w[j][4 * q + e] = v[e];
+      }
+      d.s[j] = load_sb_bits<SB>(rs, g_base[j] + g);
+      d.z[j] = load_sb_bits<SB>(rz, g_base[j] + g);
+    }
+  };
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  auto compute = [&](const SmallOps<SB, BITS>& c) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float s = sb_to_f32<SB>(c.s[j]), z = sb_to_f32<SB>(c.z[j]);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const bf16x8 b = dequant8<BITS>(c.w[j], kk, s, s * 0.0625f, z);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              b, __builtin_bit_cast(bf16x8, c.a[i][kk]), acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+
+  // Two register slots, loads two steps ahead.  Loads past the wave's last step repeat that
+  // step (never computed), so every iteration issues the same loads and the compiler's waits
+  // count exactly; the scheduling fences keep each slot's refill after its last read.
+  if (nst > 0) {
+    auto kt_of = [&](int t) { return k_begin + (t < nst ? t : nst - 1); };
+    SmallOps<SB, BITS> o0, o1;
+    load(kt_of(0), o0);
+    load(kt_of(1), o1);
+    for (int t = 0; t < nst; t += 2) {
+      compute(o0);
+      __builtin_amdgcn_sched_barrier(0);
+      load(kt_of(t + 2), o0);
+      if (t + 1 < nst) compute(o1);
+      __builtin_amdgcn_sched_barrier(0);
+      load(kt_of(t + 3), o1);
+    }
+  }
+
+  // ---- reduction over the eight K slices, in wave order.
+#pragma unroll
+  for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x16& a = acc[sub >> 1][sub & 1];
+      part[wave][sub][q][lane] = f32x4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+    }
+  __syncthreads();
+  if (wave >= 4) return;
+  const int i = wave >> 1, j = wave & 1;  // this wave's sub-tile
+  f32x16 v;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    f32x4 t = part[0][wave][q][lane];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) t += part[w][wave][q][lane];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * q + e] = t[e];
+  }
+
+  // ---- epilogue (lane: m = bm0 + 32 i + r32, n = bn0 + 32 j + 8 a + 4 h + b).
+  const int64_t m = bm0 + 32 * i + r32;
+  const int64_t nb = bn0 + 32 * j + 4 * half;
+  if constexpr (FUSED) {
+    const bool lora = epi.rank16 > 0;
+    f32x16 r = {};
+    if (lora) {
+      const int64_t nr = bn0 + 32 * j + r32;
+      bf16x8 xa = {}, lb = {};
+      if (m < M) xa = *reinterpret_cast<const bf16x8*>(epi.xa + m * 16 + half * 8);
+      if (nr < N) lb = *reinterpret_cast<const bf16x8*>(epi.lbt + nr * 16 + half * 8);
+      r = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lb, xa, r, 0, 0, 0);
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int e = 4 * a + b;
+        const int64_t n = nb + 8 * a + b;
+        float o = round_bf16(v[e]);
+        if (epi.bias) o = round_bf16(o + (n < N ? bf16_bits_to_f32(epi.bias[n]) : 0.0f));
+        if (lora) o = round_bf16(o + round_bf16(round_bf16(r[e]) * epi.lora_scale));
+        if constexpr (ACT == MLXQ_ACT_GELU) o = gelu_erf(o);
+        else if constexpr (ACT == MLXQ_ACT_GELU_TANH) o = gelu_tanh<true>(o);
+        v[e] = o;
+      }
+  }
+  if (m < M) {
+    uint16_t* yrow = y + m * N;
+    const bool vec_ok = (N % 4) == 0;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int64_t n = nb + 8 * a;
+      if (vec_ok && n + 3 < N) {
+        *reinterpret_cast<u32x2*>(yrow + n) =
+            u32x2{pack_bf16x2(v[4 * a], v[4 * a + 1]), pack_bf16x2(v[4 * a + 2], v[4 * a + 3])};
+      } else {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          if (n + b < N) yrow[n + b] = f32_to_bf16_bits(v[4 * a + b]);
+      }
+    }
+  }
+}
+
+template <typename SB, int BITS, int GS>
+static int launch_small(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+                        const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st) {
+  const int64_t tiles = ((M + kTile - 1) / kTile) * ((N + kTile - 1) / kTile);
+  const bool fused = epi.bias || epi.rank16 || epi.act != MLXQ_ACT_NONE;
+  const int kind = fused ? 1 + epi.act : 0;
+#define MLXQ_SL(E)                                                                                 \
+  hipLaunchKernelGGL((qmm_small_kernel<SB, BITS, GS, E>), dim3((unsigned)tiles), dim3(kWaves * 64), \
+                     0, st, (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N,            \
+                     (uint16_t*)y, epi)
+  switch (kind) {
+    case 0: MLXQ_SL(0); break;
+    case 1: MLXQ_SL(1); break;
+    case 2: MLXQ_SL(2); break;
+    case 3: MLXQ_SL(3); break;
+    default: return set_error(MLXQ_EINVAL, "qmm: unknown activation %d", epi.act);
+  }
+#undef MLXQ_SL
+  return check_launch("qmm_small");
+}
+
+}  // namespace
+
+bool qmm_small_fits(int64_t M, int64_t K, int64_t N, int gs, int bits, int sb_bytes) {
+  const int64_t lim = (int64_t)1 << 32;
+  return K % 64 == 0 && M * K * 2 < lim && N * (K * bits / 32) * 4 < lim &&
+         N * (K / gs) * sb_bytes < lim && (M + kTile - 1) / kTile * ((N + kTile - 1) / kTile) < 0x7fffffff;
+}
+
+int run_qmm_small(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+                  const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y,
+                  const QmmEpilogue& epi, hipStream_t st) {
+  if (M == 0 || N == 0) return MLXQ_OK;
+#define MLXQ_SM(SB, B, G) \
+  if (bits == B && gs == G) return launch_small<SB, B, G>(x, M, K, wq, s, b, N, y, epi, st);
+  if (sb_dtype == MLXQ_BFLOAT16) {
+    MLXQ_SM(uint16_t, 4, 32) MLXQ_SM(uint16_t, 4, 64) MLXQ_SM(uint16_t, 4, 128)
+    MLXQ_SM(uint16_t, 8, 32) MLXQ_SM(uint16_t, 8, 64) MLXQ_SM(uint16_t, 8, 128)
+  } else {
+    MLXQ_SM(float, 4, 32) MLXQ_SM(float, 4, 64) MLXQ_SM(float, 4, 128)
+    MLXQ_SM(float, 8, 32) MLXQ_SM(float, 8, 64) MLXQ_SM(float, 8, 128)
+  }
+#undef MLXQ_SM
+  return set_error(MLXQ_EINVAL, "qmm: unsupported bits=%d group_size=%d", bits, gs);
+}
+
+}  // namespace mlxq

@@ -166,7 +166,9 @@ def test_quantize_config1_full_size(mlxq):
 # ---------------------------------------------------------------- GEMM (MFMA, bf16 tiles)
 
 GEMM_CASES = [
-    # (M, K, N, gs, bits)
+    # (M, K, N, gs, bits).  With K >= 512 and at most 400 64x64 tiles the K-split kernel
+    # (qmm_small) runs: config 1 and the four cases below the big-tile one; the rest take the
+    # tile kernel.
     (256, 3072, 3072, 64, 4),   # config 1 shape
     (64, 256, 128, 64, 4),
     (200, 320, 136, 32, 4),     # ragged M, N; K % 64 == 0
