@@ -287,8 +287,7 @@ int mlxq_qmm_experts(const void* x, int x_dtype, int x_per_expert, int64_t E, in
   // problems of an encoder batch are a few dozen tiles each, too few to fill 256 CUs alone.
   const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
   if (x_dtype == MLXQ_BFLOAT16 && M > 8 && K % 64 == 0 && E * tiles >= 128 && E <= 65535 &&
-      qmm_wide_fits(M, K, N, group_size, bits, sbb) &&
-      qmm_wide_sb_reach(scales, biases, E * N * (K / group_size) * sbb, sbb)) {
+      qmm_wide_fits(M, K, N, group_size, bits, sbb)) {
     const QmmEpilogue qe = {(const uint16_t*)bias, nullptr, nullptr, 0, 1.0f, MLXQ_ACT_NONE};
     return run_qmm_wide(x, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y, qe, st, bat);
   }

@@ -37,8 +37,8 @@ int run_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void*
             int sb_dtype, int64_t N, int gs, int bits, void* y, const QmmEpilogue& epi,
             hipStream_t st);
 bool qmm_wide_fits(int64_t M, int64_t K, int64_t N, int gs, int bits, int sb_bytes);
-// bf16 scales and biases are read through one 32-bit-offset buffer resource: both arrays
-// (bytes each) must lie within 4 GiB of the lower one.  Always true for f32 scales.
+// Whether bf16 scales and biases (bytes each) lie within 4 GiB of the lower of the two, so the
+// wide GEMM can read both through one 32-bit-offset buffer resource.  Always true for f32.
 bool qmm_wide_sb_reach(const void* scales, const void* biases, int64_t bytes, int sb_bytes);
 bool qmm_small_fits(int64_t M, int64_t K, int64_t N, int gs, int bits, int sb_bytes);
 int run_qmm_small(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,

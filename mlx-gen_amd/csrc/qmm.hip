@@ -270,8 +270,7 @@ int run_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void*
   // ragged-K problems take the 128/256-tile kernel below.
   const int64_t wide_tiles = ((M + 255) / 256) * ((N + 255) / 256);
   if (K % 64 == 0 && wide_tiles >= 128 &&
-      qmm_wide_fits(M, K, N, gs, bits, sb_dtype == MLXQ_BFLOAT16 ? 2 : 4) &&
-      qmm_wide_sb_reach(s, b, N * (K / gs) * 2, sb_dtype == MLXQ_BFLOAT16 ? 2 : 4))
+      qmm_wide_fits(M, K, N, gs, bits, sb_dtype == MLXQ_BFLOAT16 ? 2 : 4))
     return run_qmm_wide(x, M, K, wq, s, b, sb_dtype, N, gs, bits, y, epi, st);
   // Small grids with a long K: the K-split kernel (64x64 tiles, 8 waves each taking a slice of
   // K).  Measured against the tile kernel on N = K = 3072: 21 vs 57 us at M = 16, 30 vs 59 us at

@@ -138,7 +138,9 @@ __device__ __forceinline__ uint32_t opaque_copy(uint32_t v) {
 // EPI selects the epilogue at compile time: 0 plain y = bf16(acc); 1 bias / rank-16 LoRA; 2 and 3
 // the same followed by the exact-erf or the tanh GELU (EPI - 1 is the mlxq_activation).  One
 // epilogue per instantiation keeps it small enough that the accumulator tile stays in registers.
-template <typename SB, int BITS, int GS, int WAVES, int EPI, int BM>
+// SZL: bf16 scales/biases staged through LDS in 8-group blocks (needs K / GS % 8 == 0 and both
+// arrays within 4 GiB of each other); otherwise every K step loads them into registers.
+template <typename SB, int BITS, int GS, int WAVES, int EPI, int BM, bool SZL>
 __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, const uint32_t* __restrict__ wq,
     const SB* __restrict__ scales, const SB* __restrict__ biases, int64_t N,
@@ -156,7 +158,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   // bf16 scales/biases are staged through LDS in blocks of 8 groups (SPB K steps): per wave and
   // 32-column sub-tile, two 1 KB buffers of [32 rows x 8 scales][32 rows x 8 biases], plus one
   // 1 KB sink per wave for the placeholder loads (see load_b).
-  constexpr bool SZ_LDS = sizeof(SB) == 2;
+  constexpr bool SZ_LDS = SZL;
+  static_assert(!SZL || sizeof(SB) == 2, "LDS-staged scales are bf16");
   constexpr int SPB = 8 * GS / 64;
   constexpr int kSzBytes = SZ_LDS ? WAVES * TNW * 2048 + WAVES * 1024 : 0;
   // The epilogue reuses the ring (and scale region) for the output tile, BM rows of kBN bf16 at
@@ -629,7 +632,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
 
 static int ensure_act_table(hipStream_t st);
 
-template <typename SB, int BITS, int GS, int WAVES, int BM>
+template <typename SB, int BITS, int GS, int WAVES, int BM, bool SZL>
 static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                          const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st,
                          int64_t tiles, const QmmBatch& bat) {
@@ -641,7 +644,7 @@ static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq
   }
   const dim3 grid((unsigned)tiles, (unsigned)bat.count);
 #define MLXQ_WL(E)                                                                                    \
-  hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, E, BM>), grid, dim3(WAVES * 64), 0, st,    \
+  hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, E, BM, SZL>), grid, dim3(WAVES * 64), 0, st, \
                      (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi, bat)
   switch (kind) {
     case 0: MLXQ_WL(0); break;
@@ -711,14 +714,18 @@ static int launch_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, 
   if (M == 0 || N == 0 || bat.count == 0) return MLXQ_OK;
   if (bat.count > 65535) return set_error(MLXQ_EINVAL, "qmm: problem too large");
   // 8 waves (two per SIMD) measured faster than 4 waves with twice the columns per wave.
-  // bf16 scales (the reference's layout) also get the 224-row tile; f32 scales keep 256.
-  const int bm = std::is_same<SB, uint16_t>::value ? qmm_wide_tile_rows(M, N, bat.count) : kBM;
+  // bf16 scales (the reference's layout) with LDS-staged scale blocks also get the 224-row
+  // tile; other layouts keep 256 rows.
+  constexpr bool kBf16 = std::is_same<SB, uint16_t>::value;
+  const bool szl = kBf16 && (K / GS) % 8 == 0 && qmm_wide_sb_reach(s, b, N * (K / GS) * 2, 2);
+  const int bm = szl ? qmm_wide_tile_rows(M, N, bat.count) : kBM;
   const int64_t tiles = ((M + bm - 1) / bm) * ((N + kBN - 1) / kBN);
   if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm: problem too large");
-  if constexpr (std::is_same<SB, uint16_t>::value) {
-    if (bm == 224) return launch_wide_w<SB, BITS, GS, 8, 224>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+  if constexpr (kBf16) {
+    if (szl && bm == 224) return launch_wide_w<SB, BITS, GS, 8, 224, true>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+    if (szl) return launch_wide_w<SB, BITS, GS, 8, kBM, true>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
   }
-  return launch_wide_w<SB, BITS, GS, 8, kBM>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+  return launch_wide_w<SB, BITS, GS, 8, kBM, false>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
 }
 
 bool qmm_wide_sb_reach(const void* scales, const void* biases, int64_t bytes, int sb_bytes) {
@@ -730,8 +737,6 @@ bool qmm_wide_sb_reach(const void* scales, const void* biases, int64_t bytes, in
 
 bool qmm_wide_fits(int64_t M, int64_t K, int64_t N, int gs, int bits, int sb_bytes) {
   const int64_t lim = (int64_t)1 << 32;
-  // bf16 scales and biases are staged in blocks of 8 groups: K / gs must be a multiple of 8.
-  if (sb_bytes == 2 && (K / gs) % 8 != 0) return false;
   return M * K * 2 < lim && N * (K * bits / 32) * 4 < lim && N * (K / gs) * sb_bytes < lim;
 }
 

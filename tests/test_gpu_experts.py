@@ -39,12 +39,14 @@ def _check(mlxq, y, x, packs, bias, gs, bits, per_expert, w_bf16, rows=None, wha
         assert_close(y[e][sel], ref, f"{what} expert {e}")
 
 
-@pytest.mark.parametrize("per_expert", [False, True])
-def test_experts_one_launch(mlxq, per_expert):
-    """E = 8 experts of [2048, 512] Q4 g64 at M = 512: 128 GEMM tiles, one launch over grid.y."""
-    banner("experts one launch", per_expert)
-    rng = np.random.default_rng(5 + per_expert)
-    E, M, N, K, gs, bits = 8, 512, 2048, 512, 64, 4
+@pytest.mark.parametrize("per_expert,K", [(False, 512), (True, 512), (True, 2880)])
+def test_experts_one_launch(mlxq, per_expert, K):
+    """E = 8 experts of [2048, K] Q4 g64 at M = 512: 128 GEMM tiles, one launch over grid.y.
+    K = 512 stages the scales in LDS blocks of 8 groups; K = 2880 (45 groups, the gpt-oss
+    expert width) loads them per K step."""
+    banner("experts one launch", per_expert, K)
+    rng = np.random.default_rng(5 + per_expert + K)
+    E, M, N, gs, bits = 8, 512, 2048, 64, 4
     packs, wq, s, b = _stack(rng, E, N, K, gs, bits)
     bias = bf16_normal(rng, (E, N), 0.5)
     x = bf16_normal(rng, (E, M, K) if per_expert else (M, K))

@@ -196,10 +196,11 @@ def test_qmm_gemm_vs_oracle(mlxq, M, K, N, gs, bits):
 
 
 WIDE_CASES = [
-    # Shapes with >= 128 256x256 tiles and K / group_size a multiple of 8 take the wide kernel
-    # (bf16 scales/biases staged in LDS in blocks of 8 groups).  Cases cover 1..3 scale blocks,
-    # ragged M and N, and both tile heights: on 256 CUs the one-round cases run 256-row tiles,
-    # the two-round cases marked 224 run 224-row tiles.
+    # Shapes with >= 128 256x256 tiles take the wide kernel.  With K / group_size a multiple of
+    # 8, bf16 scales/biases are staged in LDS in blocks of 8 groups: cases cover 1..3 scale
+    # blocks, ragged M and N, and both tile heights (on 256 CUs the one-round cases run 256-row
+    # tiles, the two-round cases marked 224 run 224-row tiles).  Otherwise (marked "regs") each
+    # K step loads its scales into registers, 256-row tiles, odd and even step counts.
     (2304, 512, 4096, 64, 4),    # one block
     (2000, 256, 4136, 32, 8),    # ragged M and N, one block of 4 steps
     (2048, 2048, 4096, 128, 4),  # two blocks of 16 steps
@@ -207,7 +208,9 @@ WIDE_CASES = [
     (2000, 768, 8400, 32, 4),    # 224, ragged, three blocks of 4 steps
     (512, 1024, 32768, 64, 4),
     (500, 512, 32768, 32, 8),
-    (2304, 256, 4096, 64, 4),    # K / gs = 4: falls back to the tiled kernel
+    (2304, 256, 4096, 64, 4),    # regs, K / gs = 4, 4 steps
+    (512, 2880, 8192, 64, 4),    # regs, K / gs = 45 (the gpt-oss expert width), 45 steps
+    (1000, 192, 8200, 32, 8),    # regs, ragged, K / gs = 6, 3 steps
 ]
 @pytest.mark.parametrize("M,K,N,gs,bits", WIDE_CASES)
 def test_qmm_wide_vs_oracle(mlxq, M, K, N, gs, bits):
