@@ -1,9 +1,9 @@
 // quantize.hip — affine group quantize / dequantize for gfx950.
 //
-// Both kernels are HBM-bound streaming passes over a flat 1-D grid.  quantize: one thread owns 16
-// consecutive elements of a row (two 16-byte bf16 loads; two or four packed words out), a group
-// of gs elements is gs/16 adjacent lanes, and the group's min/max is a butterfly over those
-// lanes.  dequantize: one thread owns 8 elements (one or two packed words in, one 16-byte bf16
+// Both kernels are HBM-bound streaming passes over a flat 1-D grid.  quantize: one thread owns 32
+// consecutive elements of a row (four 16-byte bf16 loads; four or eight packed words out), a
+// group of gs elements is gs/32 adjacent lanes, and the group's min/max is a DPP exchange over
+// those lanes.  dequantize: one thread owns 8 elements (one or two packed words in, one 16-byte bf16
 // store out).
 #include "mlxq_common.h"
 
@@ -34,59 +34,65 @@ __device__ __forceinline__ void load8<float>(const float* p, float (&v)[8]) {
 }
 
 // Codes: clamp(round((w - bias) / s), 0, nb) with round half away from zero and an IEEE
-// quotient, as MLX computes them.  The fast form is t = (w - bias) * rcp(s), clamped to [0, nb]
-// and rounded to the nearest integer by adding 1.5 * 2^23 (the integer lands in the low mantissa
-// bits).  t differs from the exact quotient by at most ~3 ulp of t <= 255 (under 2^-15), and the
-// hardware rounding (ties to even) differs from round-half-away only at exact .5 ties; so every
-// code is right unless t lies within 2^-12 of a half-integer.  Those codes (about one element in
-// 2000) are recomputed with the exact division and roundf in a rarely taken second pass.  w - bias
-// is formed before the product on purpose: folding it into fma(w, 1/s, -bias/s) would add an
-// error proportional to |bias / s|, unbounded for a narrow group far from zero.
-__device__ __forceinline__ uint32_t code_fast(float a, float rs, float nb, bool& near) {
-  const float t = a * rs;
-  near = fabsf(__builtin_amdgcn_fractf(t) - 0.5f) < 0x1p-12f;
-  const float tc = __builtin_amdgcn_fmed3f(t, 0.0f, nb);
-  return __float_as_uint(tc + 12582912.0f) & 0xffu;
-}
+// quotient, as MLX computes them.  The fast form evaluates y = (w - bias) * rcp(s) + 0.5 + 2^-12
+// in one FMA; for t >= 0, round half away is floor(t + 0.5), so the code is floor(y) clamped to
+// [0, nb] (a truncating convert of med3(y, 0, nb)).  The product differs from the exact quotient
+// by at most ~3 ulp of t <= 255 (under 2^-14 with y's own rounding), so floor(y) is right unless
+// t lies within 2^-12 of a half-integer, i.e. unless fract(y) < 2^-11.  Those codes (about one
+// element in 2000) are recomputed with the exact division and roundf in a rarely taken second
+// pass.  w - bias is formed before the product on purpose: folding it into
+// fma(w, 1/s, -bias/s) would add an error proportional to |bias / s|, unbounded for a narrow
+// group far from zero.
 __device__ __forceinline__ uint32_t code_exact(float a, float s, float nb) {
   return (uint32_t)fminf(fmaxf(roundf(a / s), 0.0f), nb);
+}
+
+// max / min over the LANES (1, 2 or 4) adjacent lanes of a group: DPP quad permutes (xor 1,
+// xor 2), no LDS traffic.
+template <int LANES>
+__device__ __forceinline__ void group_minmax(float& mx, float& mn) {
+  if constexpr (LANES >= 2) {
+    mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0xB1, 0xF, 0xF, false)));
+    mn = fminf(mn, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mn), 0xB1, 0xF, 0xF, false)));
+  }
+  if constexpr (LANES >= 4) {
+    mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0x4E, 0xF, 0xF, false)));
+    mn = fminf(mn, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mn), 0x4E, 0xF, 0xF, false)));
+  }
+  static_assert(LANES == 1 || LANES == 2 || LANES == 4, "group lanes");
 }
 
 // w [N,K] (bf16 bits or f32) -> wq [N, K*BITS/32], scales/biases [N, K/GS] in T.
 // Group parameters follow MLX's edge-exact affine scheme: the larger-magnitude end of the group
 // range is reproduced exactly (it becomes the bias) and the scale carries the sign.
-// A thread owns EPT = 16 consecutive elements (two 16-byte bf16 loads), so a group is GS/16
-// lanes (2, 4 or 8) and its min/max is a butterfly over those lanes.
+// A thread owns EPT = 32 consecutive elements (four 16-byte bf16 loads), so a group is GS/32
+// lanes (1, 2 or 4): the per-group work (three IEEE divisions, the lane exchange) is shared by
+// 32 elements, and each element costs about seven VALU operations.
 template <typename T, int BITS, int GS>
 __global__ __launch_bounds__(256) void quantize_kernel(const T* __restrict__ w, int64_t n_chunks,
                                                        uint32_t* __restrict__ wq,
                                                        T* __restrict__ scales, T* __restrict__ biases) {
-  constexpr int EPT = 16;
+  constexpr int EPT = 32;
   constexpr int LANES = GS / EPT;  // lanes per group
-  constexpr int WPT = EPT * BITS / 32;  // packed words per thread: 2 (Q4) or 4 (Q8)
+  constexpr int WPT = EPT * BITS / 32;  // packed words per thread: 4 (Q4) or 8 (Q8)
   constexpr float nb = (float)((1 << BITS) - 1);
+  constexpr float kTieWin = 0x1p-12f;
   const int64_t chunk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  // n_chunks is a multiple of LANES, so whole groups are either fully in or fully out.
+  // n_chunks is a multiple of LANES, so whole groups are either fully in or fully out.  Threads
+  // past the end read chunk 0 (in bounds; n_chunks > 0) and return before storing anything.
   const bool live = chunk < n_chunks;
+  const int64_t src = live ? chunk : 0;
   float v[EPT];
-  if (live) {
-    load8<T>(w + chunk * EPT, *reinterpret_cast<float(*)[8]>(&v[0]));
-    load8<T>(w + chunk * EPT + 8, *reinterpret_cast<float(*)[8]>(&v[8]));
-  } else {
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) v[i] = 0.0f;
-  }
+  for (int q = 0; q < EPT / 8; ++q)
+    load8<T>(w + src * EPT + 8 * q, *reinterpret_cast<float(*)[8]>(&v[8 * q]));
   float mx = v[0], mn = v[0];
 #pragma unroll
   for (int i = 1; i < EPT; ++i) {
     mx = fmaxf(mx, v[i]);
     mn = fminf(mn, v[i]);
   }
-#pragma unroll
-  for (int off = 1; off < LANES; off <<= 1) {
-    mx = fmaxf(mx, __shfl_xor(mx, off));
-    mn = fminf(mn, __shfl_xor(mn, off));
-  }
+  group_minmax<LANES>(mx, mn);
   if (!live) return;
   float s = fmaxf((mx - mn) / nb, 1e-7f);
   const bool side = fabsf(mn) > fabsf(mx);
@@ -104,30 +110,31 @@ __global__ __launch_bounds__(256) void quantize_kernel(const T* __restrict__ w, 
     SBLoad<T>::st(biases, g, bias);
   }
   uint32_t words[WPT];
-  uint32_t near_mask = 0;
-#pragma unroll
-  for (int j = 0; j < WPT; ++j) words[j] = 0u;
+  bool near[EPT];
+  bool any_near = false;
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
-    bool near;
-    const uint32_t c = code_fast(v[i] - bias, rs, nb, near);
-    near_mask |= (uint32_t)near << i;
-    words[i * BITS / 32] |= c << ((i * BITS) % 32);
+    const float y = fmaf(v[i] - bias, rs, 0.5f + kTieWin);
+    near[i] = __builtin_amdgcn_fractf(y) < 2.0f * kTieWin;
+    any_near |= near[i];
+    const uint32_t c = (uint32_t)__builtin_amdgcn_fmed3f(y, 0.0f, nb);
+    constexpr int per = 32 / BITS;
+    if (i % per == 0) words[i / per] = c;
+    else words[i / per] |= c << ((i % per) * BITS);
   }
-  if (__builtin_expect(near_mask != 0u, 0)) {
+  if (__builtin_expect(any_near, 0)) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
-      if (near_mask & (1u << i)) {
+      if (near[i]) {
         const uint32_t sh = (i * BITS) % 32, m = ((1u << BITS) - 1u) << sh;
         words[i * BITS / 32] = (words[i * BITS / 32] & ~m) | (code_exact(v[i] - bias, s, nb) << sh);
       }
     }
   }
-  if constexpr (WPT == 2) {
-    *reinterpret_cast<u32x2*>(wq + chunk * 2) = u32x2{words[0], words[1]};
-  } else {
-    *reinterpret_cast<u32x4*>(wq + chunk * 4) = u32x4{words[0], words[1], words[2], words[3]};
-  }
+#pragma unroll
+  for (int q = 0; q < WPT / 4; ++q)
+    *reinterpret_cast<u32x4*>(wq + chunk * WPT + 4 * q) =
+        u32x4{words[4 * q], words[4 * q + 1], words[4 * q + 2], words[4 * q + 3]};
 }
 
 // wq/scales/biases -> out [N,K] in the scales dtype: out = round(fma(code, scale, bias)).
@@ -170,7 +177,7 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const uint32_t* __restr
 template <typename T, int BITS, int GS>
 static int launch_quantize(const void* w, int64_t N, int64_t K, uint32_t* wq, void* s, void* b,
                            hipStream_t st) {
-  const int64_t n_chunks = N * K / 16;  // K % GS == 0 and GS >= 32, so K % 16 == 0
+  const int64_t n_chunks = N * K / 32;  // K % GS == 0 and GS >= 32, so K % 32 == 0
   if (n_chunks == 0) return MLXQ_OK;
   const int64_t blocks = (n_chunks + 255) / 256;
   hipLaunchKernelGGL((quantize_kernel<T, BITS, GS>), dim3((unsigned)blocks), dim3(256), 0, st,
