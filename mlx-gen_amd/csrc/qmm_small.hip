@@ -14,6 +14,13 @@
 // MFMA roles (as in qmm_wide.hip): weights are the A operand (rows n), activations the B operand
 // (columns m); lane (h = lane >> 5, r = lane & 31) holds m = r and n = 8a + 4h + b in element
 // 4a + b of its f32x16, and covers k in [8(4h+kk), +8) of a 64-wide K step for MFMA kk.
+//
+// bf16 scales and biases with K / GS a multiple of 8 (SZS) are staged per wave in LDS, in blocks
+// of 8 groups for the tile's 64 weight rows: lane L loads row L's 8 scales and 8 biases with two
+// 16-byte loads one block ahead, writes them to the wave's 2 KB region at the block boundary, and
+// every K step reads its row's pair from there.  Per-step 2-byte loads would touch 32 cache
+// lines per load instruction for 64 useful bytes; the block load touches one line per row per 8
+// groups.
 #include "mlxq_common.h"
 
 namespace mlxq {
@@ -31,7 +38,7 @@ struct SmallOps {           // one K step of one lane's operands
   uint32_t s[2], z[2];      // raw scale / bias bits of sub-tile j
 };
 
-template <typename SB, int BITS, int GS, int EPI>
+template <typename SB, int BITS, int GS, int EPI, bool SZS>
 __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, const uint32_t* __restrict__ wq,
     const SB* __restrict__ scales, const SB* __restrict__ biases, int64_t N,
@@ -41,6 +48,9 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
   constexpr int WPL = BITS;  // packed words per lane per sub-tile per K step
   // Partial tiles: [wave][sub-tile][quad of elements][lane] x 4 floats (128 KB).
   __shared__ __attribute__((aligned(16))) f32x4 part[kWaves][4][4][64];
+  // Staged scale/bias blocks: [wave][scales, biases][64 rows][8 groups] bf16.
+  __shared__ __attribute__((aligned(16))) uint16_t sz_lds[SZS ? kWaves * 1024 : 8];
+  static_assert(!SZS || sizeof(SB) == 2, "staged scales are bf16");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, r32 = lane & 31, half = lane >> 5;
@@ -87,8 +97,32 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) d.w[j][4 * q + e] = v[e];
       }
-      d.s[j] = load_sb_bits<SB>(rs, g_base[j] + g);
-      d.z[j] = load_sb_bits<SB>(rz, g_base[j] + g);
+      if constexpr (!SZS) {
+        d.s[j] = load_sb_bits<SB>(rs, g_base[j] + g);
+        d.z[j] = load_sb_bits<SB>(rz, g_base[j] + g);
+      }
+    }
+    (void)g;
+  };
+  // Scale/bias block staging (SZS): pending block in registers, lane L = tile row L.
+  constexpr int SPB = 8 * GS / 64;  // K steps per block of 8 groups
+  u32x4 ps = {}, pz = {};
+  const int64_t srow = bn0 + lane < N ? bn0 + lane : N - 1;
+  const uint32_t sz_row = (uint32_t)(srow * groups * 2);
+  const int last_blk = (int)(groups / 8) - 1;
+  uint16_t* const sz_w = sz_lds + (SZS ? wave * 1024 : 0);
+  auto load_blk = [&](int b) {
+    if constexpr (SZS) {
+      const uint32_t off = sz_row + (uint32_t)(b < last_blk ? b : last_blk) * 16u;
+      ps = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+      pz = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rz, off, 0, 0));
+    }
+    (void)b;
+  };
+  auto write_blk = [&]() {
+    if constexpr (SZS) {
+      *reinterpret_cast<u32x4*>(sz_w + lane * 8) = ps;
+      *reinterpret_cast<u32x4*>(sz_w + 512 + lane * 8) = pz;
     }
   };
   f32x16 acc[2][2];
@@ -98,10 +132,19 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-  auto compute = [&](const SmallOps<SB, BITS>& c) {
+  auto compute = [&](const SmallOps<SB, BITS>& c, int kt) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const float s = sb_to_f32<SB>(c.s[j]), z = sb_to_f32<SB>(c.z[j]);
+      float s, z;
+      if constexpr (SZS) {
+        const int gi = ((kt * 64 + half * 32) / GS) & 7;
+        s = bf16_bits_to_f32(sz_w[(32 * j + r32) * 8 + gi]);
+        z = bf16_bits_to_f32(sz_w[512 + (32 * j + r32) * 8 + gi]);
+      } else {
+        s = sb_to_f32<SB>(c.s[j]);
+        z = sb_to_f32<SB>(c.z[j]);
+      }
+      (void)kt;
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const bf16x8 b = dequant8<BITS>(c.w[j], kk, s, s * 0.0625f, z);
@@ -116,16 +159,34 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
   // Two register slots, loads two steps ahead.  Loads past the wave's last step repeat that
   // step (never computed), so every iteration issues the same loads and the compiler's waits
   // count exactly; the scheduling fences keep each slot's refill after its last read.
+  // Scale blocks: the block of the wave's first step is written before the loop and the next
+  // one loaded; a step that starts a block writes the pending block (loaded a block earlier) and
+  // loads the one after it.
   if (nst > 0) {
     auto kt_of = [&](int t) { return k_begin + (t < nst ? t : nst - 1); };
+    auto block_edge = [&](int kt) {
+      if constexpr (SZS) {
+        if (kt != k_begin && kt % SPB == 0) {
+          write_blk();
+          load_blk(kt / SPB + 1);
+        }
+      }
+    };
     SmallOps<SB, BITS> o0, o1;
+    load_blk(k_begin / SPB);
     load(kt_of(0), o0);
     load(kt_of(1), o1);
+    write_blk();
+    load_blk(k_begin / SPB + 1);
     for (int t = 0; t < nst; t += 2) {
-      compute(o0);
+      block_edge(k_begin + t);
+      compute(o0, k_begin + t);
       __builtin_amdgcn_sched_barrier(0);
       load(kt_of(t + 2), o0);
-      if (t + 1 < nst) compute(o1);
+      if (t + 1 < nst) {
+        block_edge(k_begin + t + 1);
+        compute(o1, k_begin + t + 1);
+      }
       __builtin_amdgcn_sched_barrier(0);
       load(kt_of(t + 3), o1);
     }
@@ -203,16 +264,29 @@ static int launch_small(const void* x, int64_t M, int64_t K, const uint32_t* wq,
   const int64_t tiles = ((M + kTile - 1) / kTile) * ((N + kTile - 1) / kTile);
   const bool fused = epi.bias || epi.rank16 || epi.act != MLXQ_ACT_NONE;
   const int kind = fused ? 1 + epi.act : 0;
-#define MLXQ_SL(E)                                                                                 \
-  hipLaunchKernelGGL((qmm_small_kernel<SB, BITS, GS, E>), dim3((unsigned)tiles), dim3(kWaves * 64), \
-                     0, st, (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N,            \
+  if (kind > 3) return set_error(MLXQ_EINVAL, "qmm: unknown activation %d", epi.act);
+  // bf16 scales with whole blocks of 8 groups are staged in LDS (16-byte aligned row blocks).
+  const bool szs = std::is_same<SB, uint16_t>::value && (K / GS) % 8 == 0;
+#define MLXQ_SL(E, Z)                                                                                 \
+  hipLaunchKernelGGL((qmm_small_kernel<SB, BITS, GS, E, Z>), dim3((unsigned)tiles), dim3(kWaves * 64), \
+                     0, st, (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N,               \
                      (uint16_t*)y, epi)
+  if constexpr (std::is_same<SB, uint16_t>::value) {
+    if (szs) {
+      switch (kind) {
+        case 0: MLXQ_SL(0, true); break;
+        case 1: MLXQ_SL(1, true); break;
+        case 2: MLXQ_SL(2, true); break;
+        default: MLXQ_SL(3, true); break;
+      }
+      return check_launch("qmm_small");
+    }
+  }
   switch (kind) {
-    case 0: MLXQ_SL(0); break;
-    case 1: MLXQ_SL(1); break;
-    case 2: MLXQ_SL(2); break;
-    case 3: MLXQ_SL(3); break;
-    default: return set_error(MLXQ_EINVAL, "qmm: unknown activation %d", epi.act);
+    case 0: MLXQ_SL(0, false); break;
+    case 1: MLXQ_SL(1, false); break;
+    case 2: MLXQ_SL(2, false); break;
+    default: MLXQ_SL(3, false); break;
   }
 #undef MLXQ_SL
   return check_launch("qmm_small");

@@ -167,8 +167,10 @@ def test_quantize_config1_full_size(mlxq):
 
 GEMM_CASES = [
     # (M, K, N, gs, bits).  With K >= 512 and at most 400 64x64 tiles the K-split kernel
-    # (qmm_small) runs: config 1 and the four cases below the big-tile one; the rest take the
-    # tile kernel.
+    # (qmm_small) runs: config 1 and the cases below the big-tile one; the rest take the tile
+    # kernel.  qmm_small stages bf16 scales in LDS blocks of 8 groups when K / gs % 8 == 0
+    # (waves whose K range starts mid-block, 4/8/16 steps per block) and loads them per step
+    # otherwise (K / gs = 45 and 12 below).
     (256, 3072, 3072, 64, 4),   # config 1 shape
     (64, 256, 128, 64, 4),
     (200, 320, 136, 32, 4),     # ragged M, N; K % 64 == 0
@@ -180,6 +182,10 @@ GEMM_CASES = [
     (16, 3072, 3072, 64, 4),
     (512, 2048, 1000, 32, 8),   # ragged N
     (130, 4096, 2056, 128, 4),  # ragged M and N
+    (96, 1024, 704, 32, 4),     # 4 steps per block, 2 steps per wave
+    (64, 6144, 1024, 128, 8),   # 16 steps per block, 12 per wave
+    (100, 2880, 1088, 64, 4),   # K / gs = 45: per-step scale loads
+    (40, 1536, 520, 128, 4),    # K / gs = 12: per-step scale loads
 ]
 
 
