@@ -38,6 +38,19 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
 
+// LDS row swizzle of 16-byte chunks for 128-byte activation rows: chunk c of row r is stored at
+// position c ^ swz_f(r), which keeps the MFMA fragment reads (32 rows, one chunk each) spread
+// over all banks.
+__device__ __forceinline__ int swz_f(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+// Wait until at most N vector memory operations of this wave are outstanding, leaving the LDS and
+// export counters open (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void mlxq_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 // Scale/bias element loaders for the two supported storage dtypes.
 template <typename SB>
 struct SBLoad;

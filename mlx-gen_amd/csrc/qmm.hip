@@ -273,10 +273,11 @@ int run_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void*
       qmm_wide_fits(M, K, N, gs, bits, sb_dtype == MLXQ_BFLOAT16 ? 2 : 4))
     return run_qmm_wide(x, M, K, wq, s, b, sb_dtype, N, gs, bits, y, epi, st);
   // Small grids with a long K: the K-split kernel (64x64 tiles, 8 waves each taking a slice of
-  // K).  Measured against the tile kernel on N = K = 3072: 21 vs 57 us at M = 16, 30 vs 59 us at
-  // M = 256, 57 vs 62 us at M = 512 (384 small tiles), but 82 vs 74 us at M = 1024 (768).
+  // K).  Measured against the tile kernel on N = K = 3072 (Q4 g64): 13 vs 59 us at M = 256,
+  // 42 vs 72 us at M = 1024 (768 small tiles), 65 vs 73 us at M = 1536 (1152), 77 vs 75 us at
+  // M = 2048 (1536); M = 512, N = 9216 with bias and GELU (1152) 86 vs 87 us.
   const int64_t small_tiles = ((M + 63) / 64) * ((N + 63) / 64);
-  if (K >= 512 && small_tiles <= 400 && qmm_small_fits(M, K, N, gs, bits, sb_dtype == MLXQ_BFLOAT16 ? 2 : 4))
+  if (K >= 512 && small_tiles <= 1152 && qmm_small_fits(M, K, N, gs, bits, sb_dtype == MLXQ_BFLOAT16 ? 2 : 4))
     return run_qmm_small(x, M, K, wq, s, b, sb_dtype, N, gs, bits, y, epi, st);
 #define MLXQ_M(SB, B, G) \
   if (bits == B && gs == G) return qmm_tile<SB, B, G>(x, M, K, wq, s, b, N, y, epi, st);

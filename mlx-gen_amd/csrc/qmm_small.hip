@@ -6,11 +6,13 @@
 //
 // When M x N gives few tiles, a tile kernel leaves most CUs idle and each workgroup walks all of
 // K one latency-bound step after another.  Here a workgroup of 8 waves owns a 64x64 output tile
-// and the waves split K: wave w takes K steps [w*KT/8, (w+1)*KT/8), loading its activation and
-// weight fragments straight into MFMA registers (no LDS in the loop) two steps ahead, so a tile
-// has eight independent load chains of KT/8 steps instead of one of KT.  The eight partial tiles
-// meet in LDS and are added in wave order (deterministic); waves 0-3 then finish one 32x32
-// sub-tile each.
+// and the waves split K: wave w takes K steps [w*KT/8, (w+1)*KT/8), so a tile has eight
+// independent load chains of KT/8 steps instead of one of KT.  Each wave moves its activation
+// rows global -> LDS with direct-to-LDS loads one step ahead (a private 2-stage ring, 8 rows x
+// 128 bytes per load, i.e. whole cache lines) and reads MFMA fragments back with ds_read_b128;
+// its weight fragments go straight into registers two steps ahead.  The eight partial tiles meet
+// in LDS (over the rings) and are added in wave order (deterministic); waves 0-3 then finish one
+// 32x32 sub-tile each.
 // MFMA roles (as in qmm_wide.hip): weights are the A operand (rows n), activations the B operand
 // (columns m); lane (h = lane >> 5, r = lane & 31) holds m = r and n = 8a + 4h + b in element
 // 4a + b of its f32x16, and covers k in [8(4h+kk), +8) of a 64-wide K step for MFMA kk.
@@ -32,8 +34,7 @@ constexpr int kWaves = 8;   // waves per workgroup, splitting K
 constexpr int kBufferFlags = 0x00020000;
 
 template <typename SB, int BITS>
-struct SmallOps {           // one K step of one lane's operands
-  u32x4 a[2][4];            // activations: row sub-tile i, MFMA kk
+struct SmallOps {           // one K step of one lane's register operands
   uint32_t w[2][BITS];      // packed words: column sub-tile j
   uint32_t s[2], z[2];      // raw scale / bias bits of sub-tile j
 };
@@ -46,10 +47,14 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
   constexpr bool FUSED = EPI != 0;
   constexpr int ACT = FUSED ? EPI - 1 : MLXQ_ACT_NONE;
   constexpr int WPL = BITS;  // packed words per lane per sub-tile per K step
-  // Partial tiles: [wave][sub-tile][quad of elements][lane] x 4 floats (128 KB).
-  __shared__ __attribute__((aligned(16))) f32x4 part[kWaves][4][4][64];
-  // Staged scale/bias blocks: [wave][scales, biases][64 rows][8 groups] bf16.
-  __shared__ __attribute__((aligned(16))) uint16_t sz_lds[SZS ? kWaves * 1024 : 8];
+  // One LDS object (a second one makes the compiler wait for every direct-to-LDS load before
+  // any LDS read): per wave 16 KB — its 2-stage activation ring [stage][64 rows][128 B] during
+  // the loop, its partial tile [sub-tile][quad][lane] x 4 floats after it — then, with SZS, the
+  // staged scale/bias blocks [wave][scales, biases][64 rows][8 groups] bf16.
+  constexpr int kWaveBytes = 16384;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kWaves * kWaveBytes + (SZS ? kWaves * 2048 : 0)];
+  auto part = reinterpret_cast<f32x4 (*)[4][4][64]>(lds);
+  uint16_t* const sz_lds = reinterpret_cast<uint16_t*>(lds + kWaves * kWaveBytes);
   static_assert(!SZS || sizeof(SB) == 2, "staged scales are bf16");
 
   const int tid = threadIdx.x;
@@ -70,24 +75,41 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
       const_cast<SB*>(scales), (short)0, (int)(uint32_t)(N * groups * sizeof(SB)), kBufferFlags);
   const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<SB*>(biases), (short)0, (int)(uint32_t)(N * groups * sizeof(SB)), kBufferFlags);
-  uint32_t a_off[2], w_off[2], g_base[2];
+  uint32_t w_off[2], g_base[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int64_t m = bm0 + 32 * i + r32 < M ? bm0 + 32 * i + r32 : M - 1;
-    a_off[i] = (uint32_t)((m * K + 32 * half) * 2);
-    const int64_t n = bn0 + 32 * i + r32 < N ? bn0 + 32 * i + r32 : N - 1;
-    w_off[i] = (uint32_t)((n * kwords + half * WPL) * 4);
-    g_base[i] = (uint32_t)(n * groups);
+  for (int j = 0; j < 2; ++j) {
+    const int64_t n = bn0 + 32 * j + r32 < N ? bn0 + 32 * j + r32 : N - 1;
+    w_off[j] = (uint32_t)((n * kwords + half * WPL) * 4);
+    g_base[j] = (uint32_t)(n * groups);
   }
+  // Activation ring: load u of a step fills rows 8u .. 8u+7 of the stage, lane L the chunk at
+  // position L & 7 of row 8u + (L >> 3), i.e. global chunk (L & 7) ^ swz_f(row) (rows past M
+  // repeat row M-1).  Fragment (i, kk) of lane (h, r) is chunk 4h + kk of row 32i + r.
+  unsigned char* const ring = lds + wave * kWaveBytes;
+  uint32_t a_goff[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int rl = 8 * u + (lane >> 3);
+    const int64_t m = bm0 + rl < M ? bm0 + rl : M - 1;
+    a_goff[u] = (uint32_t)((m * K + ((lane & 7) ^ swz_f(rl)) * 8) * 2);
+  }
+  int a_rd[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) a_rd[kk] = r32 * 128 + (((4 * half + kk) ^ swz_f(r32)) << 4);
+  auto dma_a = [&](int kt, int stage) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    unsigned char* base = ring + stage * 8192;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, (__attribute__((address_space(3))) void*)(base + u * 1024), 16, a_goff[u] + (uint32_t)kt * 128u, 0, 0, 0);
+#else
+    (void)kt; (void)stage;
+#endif
+  };
 
   auto load = [&](int kt, SmallOps<SB, BITS>& d) {
     const uint32_t g = (uint32_t)((kt * 64 + half * 32) / GS);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        d.a[i][kk] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, a_off[i] + (uint32_t)kt * 128u + 16u * kk, 0, 0));
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -132,7 +154,13 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-  auto compute = [&](const SmallOps<SB, BITS>& c, int kt) {
+  auto compute = [&](const SmallOps<SB, BITS>& c, int kt, int stage) {
+    const unsigned char* As = ring + stage * 8192;
+    u32x4 af[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) af[i][kk] = *reinterpret_cast<const u32x4*>(As + i * 4096 + a_rd[kk]);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       float s, z;
@@ -151,7 +179,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
 #pragma unroll
         for (int i = 0; i < 2; ++i)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              b, __builtin_bit_cast(bf16x8, c.a[i][kk]), acc[i][j], 0, 0, 0);
+              b, __builtin_bit_cast(bf16x8, af[i][kk]), acc[i][j], 0, 0, 0);
       }
     }
   };
@@ -162,6 +190,11 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
   // Scale blocks: the block of the wave's first step is written before the loop and the next
   // one loaded; a step that starts a block writes the pending block (loaded a block earlier) and
   // loads the one after it.
+  // Per step t: [scale block edge], A(t+1) into stage (t+1)&1, wait for A(t), compute, W(t+2).
+  // A(t) was followed by W(t+1) (NW ops), possibly a block load (2) and A(t+1) (8): waiting for
+  // at most NW + 8 outstanding completes it (a block load only makes the wait longer).  Loads past
+  // the wave's last step repeat that step (never computed), so every step issues the same ops.
+  constexpr int NW = 2 * (WPL / 4) + (SZS ? 0 : 4);
   if (nst > 0) {
     auto kt_of = [&](int t) { return k_begin + (t < nst ? t : nst - 1); };
     auto block_edge = [&](int kt) {
@@ -174,23 +207,33 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
     };
     SmallOps<SB, BITS> o0, o1;
     load_blk(k_begin / SPB);
+    dma_a(k_begin, 0);
     load(kt_of(0), o0);
     load(kt_of(1), o1);
     write_blk();
     load_blk(k_begin / SPB + 1);
     for (int t = 0; t < nst; t += 2) {
       block_edge(k_begin + t);
-      compute(o0, k_begin + t);
+      dma_a(kt_of(t + 1), 1);
+      mlxq_vmcnt<NW + 8>();
+      __builtin_amdgcn_sched_barrier(0);
+      compute(o0, k_begin + t, 0);
       __builtin_amdgcn_sched_barrier(0);
       load(kt_of(t + 2), o0);
       if (t + 1 < nst) {
         block_edge(k_begin + t + 1);
-        compute(o1, k_begin + t + 1);
+        dma_a(kt_of(t + 2), 0);
+        mlxq_vmcnt<NW + 8>();
+        __builtin_amdgcn_sched_barrier(0);
+        compute(o1, k_begin + t + 1, 1);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
       load(kt_of(t + 3), o1);
     }
   }
+  // Every direct-to-LDS load has landed before the ring is overwritten by the partial tile.
+  mlxq_vmcnt<0>();
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- reduction over the eight K slices, in wave order.
 #pragma unroll

@@ -84,15 +84,6 @@ __device__ __forceinline__ void tile_coords(int64_t bid, int64_t tiles_m, int64_
 }
 
 
-__device__ __forceinline__ int swz_f(int row) { return (row & 7) ^ ((row >> 3) & 1); }
-
-// Wait until at most N vector memory operations of this wave are outstanding, leaving the LDS and
-// export counters open (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14).
-template <int N>
-__device__ __forceinline__ void mlxq_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
 
 // Workgroup barrier for the pipelined loop: this wave's LDS reads done (lgkmcnt(0)), then
 // s_barrier.  Unlike __syncthreads() it has no release fence, which on this target would also

@@ -166,11 +166,11 @@ def test_quantize_config1_full_size(mlxq):
 # ---------------------------------------------------------------- GEMM (MFMA, bf16 tiles)
 
 GEMM_CASES = [
-    # (M, K, N, gs, bits).  With K >= 512 and at most 400 64x64 tiles the K-split kernel
-    # (qmm_small) runs: config 1 and the cases below the big-tile one; the rest take the tile
-    # kernel.  qmm_small stages bf16 scales in LDS blocks of 8 groups when K / gs % 8 == 0
-    # (waves whose K range starts mid-block, 4/8/16 steps per block) and loads them per step
-    # otherwise (K / gs = 45 and 12 below).
+    # (M, K, N, gs, bits).  With K >= 512 and at most 1152 64x64 tiles the K-split kernel
+    # (qmm_small) runs; shorter K and larger grids (short of the wide kernel's 128 256x256
+    # tiles) take the tile kernel.  qmm_small stages bf16 scales in LDS blocks of 8 groups when
+    # K / gs % 8 == 0 (waves whose K range starts mid-block, 4/8/16 steps per block) and loads
+    # them per step otherwise (K / gs = 45 and 12 below).
     (256, 3072, 3072, 64, 4),   # config 1 shape
     (64, 256, 128, 64, 4),
     (200, 320, 136, 32, 4),     # ragged M, N; K % 64 == 0
@@ -178,7 +178,7 @@ GEMM_CASES = [
     (300, 512, 520, 128, 8),
     (129, 384, 264, 64, 8),
     (9, 256, 256, 32, 4),       # smallest GEMM M
-    (600, 1024, 1280, 64, 4),   # big-tile path
+    (600, 1024, 1280, 64, 4),
     (16, 3072, 3072, 64, 4),
     (512, 2048, 1000, 32, 8),   # ragged N
     (130, 4096, 2056, 128, 4),  # ragged M and N
@@ -186,6 +186,8 @@ GEMM_CASES = [
     (64, 6144, 1024, 128, 8),   # 16 steps per block, 12 per wave
     (100, 2880, 1088, 64, 4),   # K / gs = 45: per-step scale loads
     (40, 1536, 520, 128, 4),    # K / gs = 12: per-step scale loads
+    (1000, 1024, 2000, 64, 8),  # 512 small tiles
+    (2048, 1024, 3072, 64, 4),  # 1536 small tiles: tile kernel
 ]
 
 
