@@ -266,10 +266,14 @@ static int qmm_tile(const void* x, int64_t M, int64_t K, const uint32_t* wq, con
 int run_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
             int sb_dtype, int64_t N, int gs, int bits, void* y, const QmmEpilogue& epi,
             hipStream_t st) {
-  // The 256x256 wide kernel needs K % 64 == 0 and enough tiles to occupy the CUs; small or
-  // ragged-K problems take the 128/256-tile kernel below.
+  // The wide kernel needs K % 64 == 0 and enough tiles to occupy the CUs: 256x256 tiles, or
+  // below 128 of those 256x128 tiles with 4 waves (which beat the K-split kernel from 128 such
+  // tiles on: M = 512, N = 12288, K = 3072 52 vs 84 us; M = 2048, N = 3072, K = 8192 120 vs
+  // 204 us; below it lost: M = 1024, N = 3072 46 vs 43 us at 96 tiles).  Small or ragged-K
+  // problems take the K-split or the 128/256-tile kernel below.
   const int64_t wide_tiles = ((M + 255) / 256) * ((N + 255) / 256);
-  if (K % 64 == 0 && wide_tiles >= 128 &&
+  const int64_t narrow_tiles = ((M + 255) / 256) * ((N + 127) / 128);
+  if (K % 64 == 0 && (wide_tiles >= 128 || narrow_tiles >= 128) &&
       qmm_wide_fits(M, K, N, gs, bits, sb_dtype == MLXQ_BFLOAT16 ? 2 : 4))
     return run_qmm_wide(x, M, K, wq, s, b, sb_dtype, N, gs, bits, y, epi, st);
   // Small grids with a long K: the K-split kernel (64x64 tiles, 8 waves each taking a slice of

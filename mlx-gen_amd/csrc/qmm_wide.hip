@@ -131,7 +131,7 @@ __device__ __forceinline__ uint32_t opaque_copy(uint32_t v) {
 // epilogue per instantiation keeps it small enough that the accumulator tile stays in registers.
 // SZL: bf16 scales/biases staged through LDS in 8-group blocks (needs K / GS % 8 == 0 and both
 // arrays within 4 GiB of each other); otherwise every K step loads them into registers.
-template <typename SB, int BITS, int GS, int WAVES, int EPI, int BM, bool SZL>
+template <typename SB, int BITS, int GS, int WAVES, int EPI, int BM, bool SZL, int BN>
 __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, const uint32_t* __restrict__ wq,
     const SB* __restrict__ scales, const SB* __restrict__ biases, int64_t N,
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   constexpr int ACT = FUSED ? EPI - 1 : MLXQ_ACT_NONE;
   constexpr int NT = WAVES * 64;
   constexpr int TMW = BM / 32;           // m sub-tiles per wave (all BM rows)
-  constexpr int TNW = kBN / WAVES / 32;  // n sub-tiles per wave
+  constexpr int TNW = BN / WAVES / 32;  // n sub-tiles per wave
   constexpr int WPL = BITS;              // packed words per lane per n sub-tile per K step (4 or 8)
   constexpr int A_PER = kBM * 8 / NT;    // 16-byte activation chunks per thread per K step
   constexpr int A_ROWS = NT / 8;         // row stride between a thread's chunks
@@ -153,12 +153,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   static_assert(!SZL || sizeof(SB) == 2, "LDS-staged scales are bf16");
   constexpr int SPB = 8 * GS / 64;
   constexpr int kSzBytes = SZ_LDS ? WAVES * TNW * 2048 + WAVES * 1024 : 0;
-  // The epilogue reuses the ring (and scale region) for the output tile, BM rows of kBN bf16 at
+  // The epilogue reuses the ring (and scale region) for the output tile, BM rows of BN bf16 at
   // a 528-byte pitch; the dense bias sits after both.
   constexpr int kRing = kStages * kBM * 128 + kSzBytes;
-  constexpr int kOut = BM * (kBN * 2 + 16);
+  constexpr int kOut = BM * (BN * 2 + 16);
   constexpr int kMain = kRing > kOut ? kRing : kOut;
-  __shared__ __attribute__((aligned(16))) unsigned char lds_all[kMain + kBN * 4];
+  __shared__ __attribute__((aligned(16))) unsigned char lds_all[kMain + BN * 4];
   auto smem = reinterpret_cast<unsigned char (*)[kBM * 128]>(lds_all);
   unsigned char* const sz_lds = lds_all + kStages * kBM * 128;
 
@@ -174,15 +174,15 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   }
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, r32 = lane & 31, half = lane >> 5;
-  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + kBN - 1) / kBN;
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   const int64_t kwords = K * BITS / 32;
   const int64_t groups = K / GS;
   int64_t tm, tn;
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int KT = (int)(K / 64);
-  const int64_t bm0 = tm * BM, bn0 = tn * kBN;
-  const int64_t wn0 = bn0 + (int64_t)wave * (kBN / WAVES);
-  // Dense bias of the tile's kBN columns: one value per thread, loaded now and parked in LDS for
+  const int64_t bm0 = tm * BM, bn0 = tn * BN;
+  const int64_t wn0 = bn0 + (int64_t)wave * (BN / WAVES);
+  // Dense bias of the tile's BN columns: one value per thread, loaded now and parked in LDS for
   // the epilogue, so the epilogue issues no global loads (each would wait on the tile's pending
   // output stores too, since vmcnt counts stores).  It is parked in activation stage KT % 4,
   // which no step reads or refills after step KT-4: the kernel keeps a single LDS object, and
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   // LDS reads (it did with a second LDS array).
   float bias_t = 0.0f;
   if constexpr (FUSED) {
-    if (epi.bias && tid < kBN && bn0 + tid < N) bias_t = bf16_bits_to_f32(epi.bias[bn0 + tid]);
+    if (epi.bias && tid < BN && bn0 + tid < N) bias_t = bf16_bits_to_f32(epi.bias[bn0 + tid]);
   }
 
   // Buffer resources: 32-bit offsets (the host checks every operand fits in 4 GiB).  Rows past
@@ -482,11 +482,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   // 528 bytes, so the 32 rows of a lane group fall on different banks) and stored with 16 bytes
   // per lane, two whole 512-byte rows per instruction, instead of 8-byte pieces of 32 rows —
   // ~900 instead of ~7000 cache-line writes per 224x256 tile.
-  constexpr int PITCH = kBN * 2 + 16;
+  constexpr int PITCH = BN * 2 + 16;
   const bool via_lds = (N % 8) == 0;
   float* bias_lds = reinterpret_cast<float*>(lds_all + kMain);
   if constexpr (FUSED) {
-    if (epi.bias && tid < kBN) bias_lds[tid] = bias_t;
+    if (epi.bias && tid < BN) bias_lds[tid] = bias_t;
   }
   __syncthreads();  // bias visible; every wave past its last ring read
   if constexpr (TABLE) {
@@ -520,7 +520,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   // 16 outputs of accumulator (i, j) as bf16 bits, two per word: to the LDS tile, or straight
   // to y (N % 8 != 0).
   auto put_tile = [&](int i, int j, const uint32_t (&pk)[8]) {
-    const int cl = wave * (kBN / WAVES) + j * 32 + 4 * half;  // tile column of element 0
+    const int cl = wave * (BN / WAVES) + j * 32 + 4 * half;  // tile column of element 0
     if (via_lds) {
       unsigned char* row = lds_all + (i * 32 + r32) * PITCH + cl * 2;
 #pragma unroll
@@ -547,7 +547,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   // bias, LoRA and their roundings in place; without an activation, pack and put.
   auto epilogue_cols = [&](auto J) {
     constexpr int j = decltype(J)::value;
-    const int cb = wave * (kBN / WAVES) + j * 32 + 4 * half;
+    const int cb = wave * (BN / WAVES) + j * 32 + 4 * half;
     float bias_v[16];
     if constexpr (FUSED) {
 #pragma unroll
@@ -609,11 +609,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   }
   if (via_lds) {
     __syncthreads();
-    // Row-major copy out: 32 lanes per 512-byte row, 16 rows per pass of the workgroup.
-    const int c16 = tid & 31;
+    // Row-major copy out: LPR lanes per BN * 2-byte row, NT / LPR rows per pass of the workgroup.
+    constexpr int LPR = BN * 2 / 16;
+    const int c16 = tid % LPR;
     const int64_t n = bn0 + c16 * 8;
 #pragma unroll 4
-    for (int r = tid >> 5; r < BM; r += NT / 32) {
+    for (int r = tid / LPR; r < BM; r += NT / LPR) {
       const int64_t m = bm0 + r;
       const u32x4 v = *reinterpret_cast<const u32x4*>(lds_all + r * PITCH + c16 * 16);
       if (m < M && n < N) *reinterpret_cast<u32x4*>(y + m * N + n) = v;
@@ -623,7 +624,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
 
 static int ensure_act_table(hipStream_t st);
 
-template <typename SB, int BITS, int GS, int WAVES, int BM, bool SZL>
+template <typename SB, int BITS, int GS, int WAVES, int BM, bool SZL, int BN>
 static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                          const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st,
                          int64_t tiles, const QmmBatch& bat) {
@@ -635,7 +636,7 @@ static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq
   }
   const dim3 grid((unsigned)tiles, (unsigned)bat.count);
 #define MLXQ_WL(E)                                                                                    \
-  hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, E, BM, SZL>), grid, dim3(WAVES * 64), 0, st, \
+  hipLaunchKernelGGL((qmm_wide_kernel<SB, BITS, GS, WAVES, E, BM, SZL, BN>), grid, dim3(WAVES * 64), 0, st, \
                      (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi, bat)
   switch (kind) {
     case 0: MLXQ_WL(0); break;
@@ -709,14 +710,25 @@ static int launch_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, 
   // tile; other layouts keep 256 rows.
   constexpr bool kBf16 = std::is_same<SB, uint16_t>::value;
   const bool szl = kBf16 && (K / GS) % 8 == 0 && qmm_wide_sb_reach(s, b, N * (K / GS) * 2, 2);
+  // Grids under 128 tiles of 256 x 256 (mid-size prefill) take 256 x 128 tiles with 4 waves:
+  // the same 256 x 32 strip per wave, twice the tiles.
+  const bool narrow = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN) * bat.count < 128;
+  if (narrow) {
+    const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + 127) / 128);
+    if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm: problem too large");
+    if constexpr (kBf16) {
+      if (szl) return launch_wide_w<SB, BITS, GS, 4, kBM, true, 128>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+    }
+    return launch_wide_w<SB, BITS, GS, 4, kBM, false, 128>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+  }
   const int bm = szl ? qmm_wide_tile_rows(M, N, bat.count) : kBM;
   const int64_t tiles = ((M + bm - 1) / bm) * ((N + kBN - 1) / kBN);
   if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm: problem too large");
   if constexpr (kBf16) {
-    if (szl && bm == 224) return launch_wide_w<SB, BITS, GS, 8, 224, true>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
-    if (szl) return launch_wide_w<SB, BITS, GS, 8, kBM, true>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+    if (szl && bm == 224) return launch_wide_w<SB, BITS, GS, 8, 224, true, kBN>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+    if (szl) return launch_wide_w<SB, BITS, GS, 8, kBM, true, kBN>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
   }
-  return launch_wide_w<SB, BITS, GS, 8, kBM, false>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+  return launch_wide_w<SB, BITS, GS, 8, kBM, false, kBN>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
 }
 
 bool qmm_wide_sb_reach(const void* scales, const void* biases, int64_t bytes, int sb_bytes) {

@@ -187,7 +187,7 @@ GEMM_CASES = [
     (100, 2880, 1088, 64, 4),   # K / gs = 45: per-step scale loads
     (40, 1536, 520, 128, 4),    # K / gs = 12: per-step scale loads
     (1000, 1024, 2000, 64, 8),  # 512 small tiles
-    (2048, 1024, 3072, 64, 4),  # 1536 small tiles: tile kernel
+    (2048, 1024, 3072, 64, 4),  # 1536 small tiles: wide kernel, 256x128 tiles
 ]
 
 
@@ -219,6 +219,11 @@ WIDE_CASES = [
     (2304, 256, 4096, 64, 4),    # regs, K / gs = 4, 4 steps
     (512, 2880, 8192, 64, 4),    # regs, K / gs = 45 (the gpt-oss expert width), 45 steps
     (1000, 192, 8200, 32, 8),    # regs, ragged, K / gs = 6, 3 steps
+    # Under 128 256x256 tiles but at least 128 of 256x128 (4 waves, "narrow"):
+    (1536, 3072, 3072, 64, 4),   # narrow, 144 tiles
+    (600, 1024, 6000, 32, 8),    # narrow, ragged M and N
+    (1030, 512, 4100, 64, 4),    # narrow, N % 8 != 0: direct stores
+    (1030, 576, 4097, 64, 4),    # narrow, N % 4 != 0: element stores, K / gs = 9: regs
 ]
 @pytest.mark.parametrize("M,K,N,gs,bits", WIDE_CASES)
 def test_qmm_wide_vs_oracle(mlxq, M, K, N, gs, bits):
@@ -233,7 +238,8 @@ def test_qmm_wide_vs_oracle(mlxq, M, K, N, gs, bits):
 
 
 @pytest.mark.parametrize("M,K,N,gs,bits", [(2048, 192, 4096, 64, 4), (2048, 64, 4096, 32, 4),
-                                           (2100, 320, 4352, 64, 8), (2048, 512, 4096, 128, 8)])
+                                           (2100, 320, 4352, 64, 8), (2048, 512, 4096, 128, 8),
+                                           (1024, 256, 4096, 64, 4)])
 def test_qmm_wide_f32_scales(mlxq, M, K, N, gs, bits):
     """bf16 activations with f32 scales/biases: the wide kernel's register-loaded scale path,
     any K % 64 == 0 (K/64 = 3, 1, 5 and 8 steps cover both prologue parities)."""
@@ -281,11 +287,14 @@ def test_qmm_odd_grids(mlxq, M, K, N, gs, bits, act, bias):
     assert_close(to_np(y1)[rows], ref, f"odd grid M={M} K={K} N={N}")
 
 
+@pytest.mark.parametrize("M", [2100, 1100])
 @pytest.mark.parametrize("act", [0, 1, 2])
-def test_linear_wide_bias_lora_act(mlxq, act):
-    banner("linear wide epilogue", act)
-    rng = np.random.default_rng(77 + act)
-    M, K, N, r = 2100, 512, 4200, 16
+def test_linear_wide_bias_lora_act(mlxq, act, M):
+    """Fused bias + LoRA + activation epilogue on 256x256 tiles (M = 2100) and on 256x128
+    tiles with 4 waves (M = 1100: 85 wide tiles, 165 narrow ones)."""
+    banner("linear wide epilogue", act, M)
+    rng = np.random.default_rng(77 + act + M)
+    K, N, r = 512, 4200, 16
     x = bf16_normal(rng, (M, K))
     w = bf16_normal(rng, (N, K), 0.02)
     bias = bf16_normal(rng, (N,), 0.5)
