@@ -34,16 +34,34 @@ __global__ void lora_prep_kernel(const XT* __restrict__ x, int64_t M, int64_t K,
 }
 
 // bf16 x.A on the matrix cores: xa[M,R] = round_bf16(x[M,K] . A[K,rank]), columns >= rank zero.
-// A workgroup owns 16 rows of x and 16 columns of xa; its 4 waves split K (32 per MFMA step,
+// A workgroup owns 16 rows of x and 16 columns of xa; its 8 waves split K (32 per MFMA step,
 // K % 32 == 0 because K is a multiple of the group size) and reduce through LDS.  The MFMA's B
 // operand needs 8 consecutive k of one column of the k-major A: 8 two-byte loads per lane and
-// step, all L1 hits (A is at most K x 256 x 2 bytes and every workgroup reads it).
-constexpr int kXaWaves = 4;
+// step, L1/L2 hits (A is at most K x 256 x 2 bytes and every workgroup reads it).  Each wave
+// walks its K range in chunks of kXaChunk steps, double-buffered: a chunk's loads are issued
+// before the previous chunk's MFMAs, so a wave waits for memory about once instead of once per
+// step (the x rows come from HBM).
+constexpr int kXaWaves = 8;
+constexpr int kXaChunk = 4;
+// Workgroups past the x.A grid (blockIdx.x >= xa_blocks) write lbt[N,R] = B[rank,N]^T instead
+// (zero padded, the GEMM epilogue's operand), so the LoRA preparation is one launch.
 __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* __restrict__ x, int M,
                                                                 int K, const uint16_t* __restrict__ A,
-                                                                int rank, int R, uint16_t* __restrict__ xa) {
+                                                                int rank, int R, uint16_t* __restrict__ xa,
+                                                                int xa_blocks, const uint16_t* __restrict__ B,
+                                                                int64_t N, uint16_t* __restrict__ lbt) {
   __shared__ float red[kXaWaves][16 * 16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if ((int)blockIdx.x >= xa_blocks) {
+    if (blockIdx.y != 0) return;
+    const int64_t u = ((int64_t)blockIdx.x - xa_blocks) * (kXaWaves * 64) + tid;
+    if (u < N * R) {
+      const int64_t n = u / R;
+      const int rr = (int)(u % R);
+      lbt[u] = rr < rank ? B[(int64_t)rr * N + n] : (uint16_t)0;
+    }
+    return;
+  }
   const int c16 = lane & 15, q = lane >> 4;
   const int m0 = blockIdx.x * 16, r0 = blockIdx.y * 16;
   const int xrow = m0 + c16 < M ? m0 + c16 : M - 1;
@@ -53,36 +71,57 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
   const int ks0 = wave * per, ks1 = ks0 + per < KS ? ks0 + per : KS;
   const uint16_t* xp = x + (int64_t)xrow * K + 8 * q;
   const uint16_t* ap = A + (int64_t)(8 * q) * rank + (rvalid ? r : 0);
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int ks = ks0; ks < ks1; ++ks) {
-    const bf16x8 a = *reinterpret_cast<const bf16x8*>(xp + ks * 32);
-    u32x4 bw;
+  struct Chunk {
+    bf16x8 a[kXaChunk];
+    uint16_t w[kXaChunk][8];
+  };
+  // Steps past the wave's range repeat its last step (in bounds) and are not accumulated.  Every
+  // load is unconditional (lanes of columns >= rank read column 0 and zero it afterwards): a
+  // conditional load made the compiler wait for each one before the next.
+  auto load = [&](int ks, Chunk& c) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t lo = rvalid ? ap[(int64_t)(ks * 32 + 2 * j) * rank] : 0u;
-      const uint32_t hi = rvalid ? ap[(int64_t)(ks * 32 + 2 * j + 1) * rank] : 0u;
-      bw[j] = lo | (hi << 16);
+    for (int u = 0; u < kXaChunk; ++u) {
+      const int k = ks + u < ks1 ? ks + u : ks1 - 1;
+      c.a[u] = *reinterpret_cast<const bf16x8*>(xp + k * 32);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c.w[u][j] = ap[(int64_t)(k * 32 + j) * rank];  // column 0 if !rvalid
     }
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, bw), acc, 0, 0, 0);
+  };
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int ks, const Chunk& c) {
+#pragma unroll
+    for (int u = 0; u < kXaChunk; ++u) {
+      if (ks + u < ks1) {
+        u32x4 bw;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          bw[j] = rvalid ? (uint32_t)c.w[u][2 * j] | ((uint32_t)c.w[u][2 * j + 1] << 16) : 0u;
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c.a[u], __builtin_bit_cast(bf16x8, bw), acc, 0, 0, 0);
+      }
+    }
+  };
+  if (ks0 < ks1) {
+    Chunk c0, c1;
+    load(ks0, c0);
+    for (int ks = ks0; ks < ks1; ks += 2 * kXaChunk) {
+      load(ks + kXaChunk, c1);
+      compute(ks, c0);
+      if (ks + kXaChunk < ks1) {
+        load(ks + 2 * kXaChunk, c0);
+        compute(ks + kXaChunk, c1);
+      }
+    }
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) red[wave][(4 * q + e) * 16 + c16] = acc[e];
   __syncthreads();
-  const int m = tid >> 4, n = tid & 15;
-  float v = 0.0f;
+  if (tid < 256) {
+    const int m = tid >> 4, n = tid & 15;
+    float v = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kXaWaves; ++w) v += red[w][m * 16 + n];
-  if (m0 + m < M) xa[(int64_t)(m0 + m) * R + r0 + n] = f32_to_bf16_bits(v);
-}
-
-// lbt[N,R] = B[rank,N]^T, zero padded (the epilogue's MFMA operand).
-template <typename XT>
-__global__ void lora_bt_kernel(const XT* __restrict__ B, int64_t N, int rank, int R, XT* __restrict__ lbt) {
-  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (u >= N * R) return;
-  const int64_t n = u / R;
-  const int r = (int)(u % R);
-  lbt[u] = r < rank ? B[(int64_t)r * N + n] : (XT)0;
+    for (int w = 0; w < kXaWaves; ++w) v += red[w][m * 16 + n];
+    if (m0 + m < M) xa[(int64_t)(m0 + m) * R + r0 + n] = f32_to_bf16_bits(v);
+  }
 }
 
 int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* A, const void* B,
@@ -90,17 +129,15 @@ int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* 
   const int64_t total = M * R + N * R;
   if (total == 0) return MLXQ_OK;
   const int64_t blocks = (total + 255) / 256;
-  if (x_dtype == MLXQ_BFLOAT16 && K % 32 == 0 && M < (1LL << 31) / 16 && K < (1LL << 31)) {
-    if (M > 0) {
-      hipLaunchKernelGGL(lora_xa_kernel, dim3((unsigned)((M + 15) / 16), (unsigned)(R / 16)),
-                         dim3(kXaWaves * 64), 0, st, (const uint16_t*)x, (int)M, (int)K,
-                         (const uint16_t*)A, rank, R, (uint16_t*)xa);
-      int rc = check_launch("lora_xa");
-      if (rc) return rc;
-    }
-    if (N > 0)
-      hipLaunchKernelGGL(lora_bt_kernel<uint16_t>, dim3((unsigned)((N * R + 255) / 256)), dim3(256), 0,
-                         st, (const uint16_t*)B, N, rank, R, (uint16_t*)lbt);
+  const int64_t bt_blocks = (N * R + kXaWaves * 64 - 1) / (kXaWaves * 64);
+  if (x_dtype == MLXQ_BFLOAT16 && K % 32 == 0 && M < (1LL << 31) / 16 && K < (1LL << 31) &&
+      bt_blocks < (1LL << 30)) {
+    // x.A workgroups (16 rows x 16 columns each), then the B^T workgroups.
+    const int xa_blocks = (int)((M + 15) / 16);
+    hipLaunchKernelGGL(lora_xa_kernel, dim3((unsigned)(xa_blocks + bt_blocks), (unsigned)(R / 16)),
+                       dim3(kXaWaves * 64), 0, st, (const uint16_t*)x, (int)M, (int)K,
+                       (const uint16_t*)A, rank, R, (uint16_t*)xa, xa_blocks, (const uint16_t*)B, N,
+                       (uint16_t*)lbt);
   } else if (x_dtype == MLXQ_BFLOAT16) {
     hipLaunchKernelGGL(lora_prep_kernel<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
                        (const uint16_t*)x, M, K, (const uint16_t*)A, (const uint16_t*)B, N, rank, R,

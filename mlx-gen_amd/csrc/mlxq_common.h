@@ -38,6 +38,38 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
 
+// Rounds a and b to bf16 (RNE) in place with one conversion for both.
+__device__ __forceinline__ void round_bf16x2(float& a, float& b) {
+  const uint32_t w = pack_bf16x2(a, b);
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+}
+
+// The fused bias / LoRA epilogue on two outputs, rounded to bf16 after each op as the
+// reference's separate ops round: o = rnd(rnd(rnd(acc) + bias) + rnd(rnd(r) * scale)).  With
+// scale == 1 the product's rounding is the identity and is skipped.
+__device__ __forceinline__ void epilogue_bias_lora2(float& o0, float& o1, bool has_bias, float b0,
+                                                    float b1, bool lora, float r0, float r1,
+                                                    float scale) {
+  round_bf16x2(o0, o1);
+  if (has_bias) {
+    o0 += b0;
+    o1 += b1;
+    round_bf16x2(o0, o1);
+  }
+  if (lora) {
+    round_bf16x2(r0, r1);
+    if (scale != 1.0f) {
+      r0 *= scale;
+      r1 *= scale;
+      round_bf16x2(r0, r1);
+    }
+    o0 += r0;
+    o1 += r1;
+    round_bf16x2(o0, o1);
+  }
+}
+
 // LDS row swizzle of 16-byte chunks for 128-byte activation rows: chunk c of row r is stored at
 // position c ^ swz_f(r), which keeps the MFMA fragment reads (32 rows, one chunk each) spread
 // over all banks.

@@ -272,15 +272,22 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
+      for (int b = 0; b < 4; b += 2) {
         const int e = 4 * a + b;
         const int64_t n = nb + 8 * a + b;
-        float o = round_bf16(v[e]);
-        if (epi.bias) o = round_bf16(o + (n < N ? bf16_bits_to_f32(epi.bias[n]) : 0.0f));
-        if (lora) o = round_bf16(o + round_bf16(round_bf16(r[e]) * epi.lora_scale));
-        if constexpr (ACT == MLXQ_ACT_GELU) o = gelu_erf(o);
-        else if constexpr (ACT == MLXQ_ACT_GELU_TANH) o = gelu_tanh<true>(o);
-        v[e] = o;
+        const float b0 = epi.bias && n < N ? bf16_bits_to_f32(epi.bias[n]) : 0.0f;
+        const float b1 = epi.bias && n + 1 < N ? bf16_bits_to_f32(epi.bias[n + 1]) : 0.0f;
+        float o0 = v[e], o1 = v[e + 1];
+        epilogue_bias_lora2(o0, o1, epi.bias != nullptr, b0, b1, lora, r[e], r[e + 1], epi.lora_scale);
+        v[e] = o0;
+        v[e + 1] = o1;
+        if constexpr (ACT == MLXQ_ACT_GELU) {
+          v[e] = gelu_erf(v[e]);
+          v[e + 1] = gelu_erf(v[e + 1]);
+        } else if constexpr (ACT == MLXQ_ACT_GELU_TANH) {
+          v[e] = gelu_tanh<true>(v[e]);
+          v[e + 1] = gelu_tanh<true>(v[e + 1]);
+        }
       }
   }
   if (m < M) {

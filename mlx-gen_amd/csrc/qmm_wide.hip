@@ -562,11 +562,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
         f32x16 r = {};
         if (lora) r = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lb[j], xa[i], r, 0, 0, 0);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          float o = round_bf16(v[e]);
-          if (epi.bias) o = round_bf16(o + bias_v[e]);
-          if (lora) o = round_bf16(o + round_bf16(round_bf16(r[e]) * epi.lora_scale));
-          v[e] = o;
+        for (int e = 0; e < 16; e += 2) {
+          float o0 = v[e], o1 = v[e + 1];
+          epilogue_bias_lora2(o0, o1, epi.bias != nullptr, bias_v[e], bias_v[e + 1], lora, r[e],
+                              r[e + 1], epi.lora_scale);
+          v[e] = o0;
+          v[e + 1] = o1;
         }
       }
       if constexpr (!TABLE) {
