@@ -197,13 +197,25 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
     for (int i = 0; i < TM; ++i) {
       const int64_t mrow = bm0 + wm * WM + i * 32 + r32;
       xa[i] = bf16x8{};
-      if (lora && mrow < M) xa[i] = *reinterpret_cast<const bf16x8*>(epi.xa + mrow * 16 + half * 8);
+      if (lora) xa[i] = *reinterpret_cast<const bf16x8*>(epi.xa + (mrow < M ? mrow : M - 1) * 16 + half * 8);
     }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int64_t n = bn0 + wn * WN + j * 32 + r32;
       lb[j] = bf16x8{};
-      if (lora && n < N) lb[j] = *reinterpret_cast<const bf16x8*>(epi.lbt + n * 16 + half * 8);
+      if (lora) lb[j] = *reinterpret_cast<const bf16x8*>(epi.lbt + (n < N ? n : N - 1) * 16 + half * 8);
+    }
+    // Bias of this lane's columns, loaded together up front (clamped: columns past N are never
+    // stored) so the loads are not waited for one at a time.
+    float bcol[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bcol[j] = 0.0f;
+    if (epi.bias) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t n = bn0 + wn * WN + j * 32 + r32;
+        bcol[j] = bf16_bits_to_f32(epi.bias[n < N ? n : N - 1]);
+      }
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -213,7 +225,7 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
         const bool n_ok = n < N;
         f32x16 r = {};
         if (lora) r = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[i], lb[j], r, 0, 0, 0);
-        const float bn = (epi.bias && n_ok) ? bf16_bits_to_f32(epi.bias[n]) : 0.0f;
+        const float bn = bcol[j];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int64_t m = bm0 + wm * WM + i * 32 + (v >> 2) * 8 + half * 4 + (v & 3);

@@ -262,21 +262,31 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
   if constexpr (FUSED) {
     const bool lora = epi.rank16 > 0;
     f32x16 r = {};
+    // Rows past M and columns past N read clamped operands (never stored): per-lane conditional
+    // loads made the compiler wait for each one in turn.
     if (lora) {
-      const int64_t nr = bn0 + 32 * j + r32;
-      bf16x8 xa = {}, lb = {};
-      if (m < M) xa = *reinterpret_cast<const bf16x8*>(epi.xa + m * 16 + half * 8);
-      if (nr < N) lb = *reinterpret_cast<const bf16x8*>(epi.lbt + nr * 16 + half * 8);
+      const int64_t nr = bn0 + 32 * j + r32 < N ? bn0 + 32 * j + r32 : N - 1;
+      const int64_t mr = m < M ? m : M - 1;
+      const bf16x8 xa = *reinterpret_cast<const bf16x8*>(epi.xa + mr * 16 + half * 8);
+      const bf16x8 lb = *reinterpret_cast<const bf16x8*>(epi.lbt + nr * 16 + half * 8);
       r = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lb, xa, r, 0, 0, 0);
+    }
+    float bv[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bv[e] = 0.0f;
+    if (epi.bias) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t n = nb + 8 * (e >> 2) + (e & 3);
+        bv[e] = bf16_bits_to_f32(epi.bias[n < N ? n : N - 1]);
+      }
     }
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
       for (int b = 0; b < 4; b += 2) {
         const int e = 4 * a + b;
-        const int64_t n = nb + 8 * a + b;
-        const float b0 = epi.bias && n < N ? bf16_bits_to_f32(epi.bias[n]) : 0.0f;
-        const float b1 = epi.bias && n + 1 < N ? bf16_bits_to_f32(epi.bias[n + 1]) : 0.0f;
+        const float b0 = bv[e], b1 = bv[e + 1];
         float o0 = v[e], o1 = v[e + 1];
         epilogue_bias_lora2(o0, o1, epi.bias != nullptr, b0, b1, lora, r[e], r[e + 1], epi.lora_scale);
         v[e] = o0;

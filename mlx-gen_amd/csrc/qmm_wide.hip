@@ -190,7 +190,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   // LDS reads (it did with a second LDS array).
   float bias_t = 0.0f;
   if constexpr (FUSED) {
-    if (epi.bias && tid < BN && bn0 + tid < N) bias_t = bf16_bits_to_f32(epi.bias[bn0 + tid]);
+    // Unconditional load of a clamped column (columns past N are never stored): a per-lane
+    // conditional load made the compiler wait for it before the first operand loads.
+    if (epi.bias) {
+      const int64_t nn = bn0 + (tid < BN ? tid : 0);
+      bias_t = bf16_bits_to_f32(epi.bias[nn < N ? nn : N - 1]);
+    }
   }
 
   // Buffer resources: 32-bit offsets (the host checks every operand fits in 4 GiB).  Rows past
@@ -505,16 +510,20 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   const bool lora = FUSED && epi.rank16 > 0;
   if constexpr (FUSED) {
 #pragma unroll
-    for (int i = 0; i < TMW; ++i) {
-      const int64_t m = bm0 + i * 32 + r32;
-      xa[i] = bf16x8{};
-      if (lora && m < M) xa[i] = *reinterpret_cast<const bf16x8*>(epi.xa + m * 16 + half * 8);
-    }
+    for (int i = 0; i < TMW; ++i) xa[i] = bf16x8{};
 #pragma unroll
-    for (int j = 0; j < TNW; ++j) {
-      lb[j] = bf16x8{};
-      if (lora && n_ok[j])
-        lb[j] = *reinterpret_cast<const bf16x8*>(epi.lbt + (wn0 + j * 32 + r32) * 16 + half * 8);
+    for (int j = 0; j < TNW; ++j) lb[j] = bf16x8{};
+    if (lora) {  // rows past M / columns past N read clamped ones: never stored
+#pragma unroll
+      for (int i = 0; i < TMW; ++i) {
+        const int64_t m = bm0 + i * 32 + r32 < M ? bm0 + i * 32 + r32 : M - 1;
+        xa[i] = *reinterpret_cast<const bf16x8*>(epi.xa + m * 16 + half * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < TNW; ++j) {
+        const int64_t n = wn0 + j * 32 + r32 < N ? wn0 + j * 32 + r32 : N - 1;
+        lb[j] = *reinterpret_cast<const bf16x8*>(epi.lbt + n * 16 + half * 8);
+      }
     }
   }
   // 16 outputs of accumulator (i, j) as bf16 bits, two per word: to the LDS tile, or straight
