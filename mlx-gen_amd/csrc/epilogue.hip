@@ -51,7 +51,8 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
                                                                 int xa_blocks, const uint16_t* __restrict__ B,
                                                                 int64_t N, uint16_t* __restrict__ lbt) {
   __shared__ float red[kXaWaves][16 * 16];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave is made scalar so the K-range branches below are uniform scalar branches.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   if ((int)blockIdx.x >= xa_blocks) {
     if (blockIdx.y != 0) return;
     const int64_t u = ((int64_t)blockIdx.x - xa_blocks) * (kXaWaves * 64) + tid;
@@ -68,7 +69,8 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
   const int r = r0 + c16;
   const bool rvalid = r < rank;
   const int KS = K / 32, per = (KS + kXaWaves - 1) / kXaWaves;
-  const int ks0 = wave * per, ks1 = ks0 + per < KS ? ks0 + per : KS;
+  const int ks0 = __builtin_amdgcn_readfirstlane(wave * per);
+  const int ks1 = __builtin_amdgcn_readfirstlane(ks0 + per < KS ? ks0 + per : KS);
   const uint16_t* xp = x + (int64_t)xrow * K + 8 * q;
   const uint16_t* ap = A + (int64_t)(8 * q) * rank + (rvalid ? r : 0);
   struct Chunk {
@@ -88,16 +90,20 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
     }
   };
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  // Every MFMA of a chunk is issued; steps past the wave's range and padding columns get a zero B
+  // operand through a mask the compiler cannot see through.  MFMA does not honour the EXEC mask:
+  // given a visible "operand is zero" condition the compiler predicated the MFMA on EXEC without
+  // a branch, and with one step per wave it then added the repeated step a second time.
   auto compute = [&](int ks, const Chunk& c) {
 #pragma unroll
     for (int u = 0; u < kXaChunk; ++u) {
-      if (ks + u < ks1) {
-        u32x4 bw;
+      uint32_t keep = rvalid && ks + u < ks1 ? 0xffffffffu : 0u;
+      asm volatile("" : "+v"(keep));
+      u32x4 bw;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          bw[j] = rvalid ? (uint32_t)c.w[u][2 * j] | ((uint32_t)c.w[u][2 * j + 1] << 16) : 0u;
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c.a[u], __builtin_bit_cast(bf16x8, bw), acc, 0, 0, 0);
-      }
+      for (int j = 0; j < 4; ++j)
+        bw[j] = ((uint32_t)c.w[u][2 * j] | ((uint32_t)c.w[u][2 * j + 1] << 16)) & keep;
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c.a[u], __builtin_bit_cast(bf16x8, bw), acc, 0, 0, 0);
     }
   };
   if (ks0 < ks1) {

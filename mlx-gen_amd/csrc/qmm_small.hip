@@ -63,7 +63,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
   const int64_t bm0 = (blockIdx.x % tiles_m) * kTile, bn0 = (blockIdx.x / tiles_m) * kTile;
   const int64_t kwords = K * BITS / 32, groups = K / GS;
   const int KT = (int)(K / 64);
-  const int k_begin = wave * KT / kWaves, nst = (wave + 1) * KT / kWaves - k_begin;
+  // Scalar (wave-uniform) K range: the step branches below stay scalar branches, never EXEC
+  // predication (which MFMA does not honour).
+  const int k_begin = __builtin_amdgcn_readfirstlane(wave * KT / kWaves);
+  const int nst = __builtin_amdgcn_readfirstlane((wave + 1) * KT / kWaves) - k_begin;
 
   // Buffer resources (32-bit offsets: the host checks the operands fit in 4 GiB); rows past M
   // and N are clamped to the last row, so every offset stays inside its operand.

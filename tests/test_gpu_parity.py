@@ -489,6 +489,28 @@ def test_linear_bias_lora_act(mlxq, M, act):
     assert_close(y, ref, f"linear M={M} act={act}")
 
 
+@pytest.mark.parametrize("K", [64, 256, 320])
+@pytest.mark.parametrize("rank,scale", [(8, 1.0), (16, 0.75), (24, 1.5)])
+def test_linear_lora_short_k_ranks(mlxq, K, rank, scale):
+    """LoRA with K < 512 (the 128/256-tile GEMM, whose epilogue fuses rank <= 16) and rank 24
+    (plain GEMM + elementwise epilogue): the x.A preparation with one or two K steps per wave
+    and padding columns (rank 8 and 24 pad to 16 and 32)."""
+    banner("linear lora short K", K, rank, scale)
+    rng = np.random.default_rng(K + rank)
+    M, N = 37, 192
+    x = bf16_normal(rng, (M, K))
+    w = bf16_normal(rng, (N, K), 0.02)
+    bias = bf16_normal(rng, (N,), 0.1)
+    A = bf16_normal(rng, (K, rank), 0.05)
+    B = bf16_normal(rng, (rank, N), 0.05)
+    rwq, rs, rb = oracle.quantize(w, 64, 4, sb_bf16=True)
+    y = to_np(mlxq.linear(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), 64, 4,
+                          bias=to_gpu(bias), lora_a=to_gpu(A), lora_b=to_gpu(B), lora_scale=scale))
+    ref = oracle.linear(x, rwq, rs, rb, 64, 4, w_bf16=True, act_bf16=True, bias=bias,
+                        lora_a=A, lora_b=B, lora_scale=scale)
+    assert_close(y, ref, f"lora K={K} rank={rank}")
+
+
 # ---------------------------------------------------------------- errors never crash
 
 def test_invalid_arguments_return_errors(mlxq):
