@@ -45,12 +45,17 @@ constexpr int kXaWaves = 8;
 constexpr int kXaChunk = 4;
 // Workgroups past the x.A grid (blockIdx.x >= xa_blocks) write lbt[N,R] = B[rank,N]^T instead
 // (zero padded, the GEMM epilogue's operand), so the LoRA preparation is one launch.
+// A16 (rank 16, one 16-column block): a chunk of A (4 steps x 32 rows x 16 columns) is 4 KB of
+// contiguous memory, fetched with four 16-byte loads per lane and transposed through the wave's
+// 4 KB LDS buffer, instead of 32 two-byte gathers per lane.
+template <bool A16>
 __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* __restrict__ x, int M,
                                                                 int K, const uint16_t* __restrict__ A,
                                                                 int rank, int R, uint16_t* __restrict__ xa,
                                                                 int xa_blocks, const uint16_t* __restrict__ B,
                                                                 int64_t N, uint16_t* __restrict__ lbt) {
   __shared__ float red[kXaWaves][16 * 16];
+  __shared__ __attribute__((aligned(16))) uint16_t abuf[A16 ? kXaWaves * 2048 : 8];
   // wave is made scalar so the K-range branches below are uniform scalar branches.
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   if ((int)blockIdx.x >= xa_blocks) {
@@ -75,8 +80,10 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
   const uint16_t* ap = A + (int64_t)(8 * q) * rank + (rvalid ? r : 0);
   struct Chunk {
     bf16x8 a[kXaChunk];
-    uint16_t w[kXaChunk][8];
+    uint16_t w[A16 ? 1 : kXaChunk][8];
+    u32x4 araw[A16 ? kXaChunk : 1];  // A16: lane l's 64 bytes of the chunk (rows 2l, 2l+1)
   };
+  uint16_t* const wbuf = abuf + (A16 ? wave * 2048 : 0);
   // Steps past the wave's range repeat its last step (in bounds) and are not accumulated.  Every
   // load is unconditional (lanes of columns >= rank read column 0 and zero it afterwards): a
   // conditional load made the compiler wait for each one before the next.
@@ -85,8 +92,25 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
     for (int u = 0; u < kXaChunk; ++u) {
       const int k = ks + u < ks1 ? ks + u : ks1 - 1;
       c.a[u] = *reinterpret_cast<const bf16x8*>(xp + k * 32);
+      if constexpr (!A16) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) c.w[u][j] = ap[(int64_t)(k * 32 + j) * rank];  // column 0 if !rvalid
+        for (int j = 0; j < 8; ++j) c.w[u][j] = ap[(int64_t)(k * 32 + j) * rank];  // column 0 if !rvalid
+      }
+    }
+    if constexpr (A16) {
+#pragma unroll
+      for (int p = 0; p < kXaChunk; ++p) {  // row ks*32 + 2 lane + p/2, columns 8 (p&1) .. +8
+        const int row = ks * 32 + 2 * lane + (p >> 1);
+        c.araw[p] = *reinterpret_cast<const u32x4*>(A + (int64_t)(row < K ? row : K - 1) * 16 + 8 * (p & 1));
+      }
+    }
+  };
+  // A16: the chunk's rows into the wave's buffer, [128 rows][16 columns] bf16 (after this wave's
+  // reads of the previous chunk, LDS being in order within a wave).
+  auto stage = [&](const Chunk& c) {
+    if constexpr (A16) {
+#pragma unroll
+      for (int p = 0; p < kXaChunk; ++p) *reinterpret_cast<u32x4*>(wbuf + lane * 32 + p * 8) = c.araw[p];
     }
   };
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -101,8 +125,17 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
       asm volatile("" : "+v"(keep));
       u32x4 bw;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bw[j] = ((uint32_t)c.w[u][2 * j] | ((uint32_t)c.w[u][2 * j + 1] << 16)) & keep;
+      for (int j = 0; j < 4; ++j) {
+        uint32_t lo, hi;
+        if constexpr (A16) {
+          lo = wbuf[(u * 32 + 8 * q + 2 * j) * 16 + c16];
+          hi = wbuf[(u * 32 + 8 * q + 2 * j + 1) * 16 + c16];
+        } else {
+          lo = c.w[u][2 * j];
+          hi = c.w[u][2 * j + 1];
+        }
+        bw[j] = (lo | (hi << 16)) & keep;
+      }
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c.a[u], __builtin_bit_cast(bf16x8, bw), acc, 0, 0, 0);
     }
   };
@@ -111,9 +144,11 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
     load(ks0, c0);
     for (int ks = ks0; ks < ks1; ks += 2 * kXaChunk) {
       load(ks + kXaChunk, c1);
+      stage(c0);
       compute(ks, c0);
       if (ks + kXaChunk < ks1) {
         load(ks + 2 * kXaChunk, c0);
+        stage(c1);
         compute(ks + kXaChunk, c1);
       }
     }
@@ -140,10 +175,15 @@ int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* 
       bt_blocks < (1LL << 30)) {
     // x.A workgroups (16 rows x 16 columns each), then the B^T workgroups.
     const int xa_blocks = (int)((M + 15) / 16);
-    hipLaunchKernelGGL(lora_xa_kernel, dim3((unsigned)(xa_blocks + bt_blocks), (unsigned)(R / 16)),
-                       dim3(kXaWaves * 64), 0, st, (const uint16_t*)x, (int)M, (int)K,
-                       (const uint16_t*)A, rank, R, (uint16_t*)xa, xa_blocks, (const uint16_t*)B, N,
-                       (uint16_t*)lbt);
+    const dim3 grid((unsigned)(xa_blocks + bt_blocks), (unsigned)(R / 16));
+    if (rank == 16 && R == 16)
+      hipLaunchKernelGGL(lora_xa_kernel<true>, grid, dim3(kXaWaves * 64), 0, st, (const uint16_t*)x,
+                         (int)M, (int)K, (const uint16_t*)A, rank, R, (uint16_t*)xa, xa_blocks,
+                         (const uint16_t*)B, N, (uint16_t*)lbt);
+    else
+      hipLaunchKernelGGL(lora_xa_kernel<false>, grid, dim3(kXaWaves * 64), 0, st, (const uint16_t*)x,
+                         (int)M, (int)K, (const uint16_t*)A, rank, R, (uint16_t*)xa, xa_blocks,
+                         (const uint16_t*)B, N, (uint16_t*)lbt);
   } else if (x_dtype == MLXQ_BFLOAT16) {
     hipLaunchKernelGGL(lora_prep_kernel<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
                        (const uint16_t*)x, M, K, (const uint16_t*)A, (const uint16_t*)B, N, rank, R,
