@@ -167,8 +167,8 @@ def test_quantize_config1_full_size(mlxq):
 
 GEMM_CASES = [
     # (M, K, N, gs, bits).  With K >= 512 and at most 1152 64x64 tiles the K-split kernel
-    # (qmm_small) runs; shorter K and larger grids (short of the wide kernel's 128 256x256
-    # tiles) take the tile kernel.  qmm_small stages bf16 scales in LDS blocks of 8 groups when
+    # (qmm_small) runs unless the wide kernel has 128 tiles of 256x256 or 256x128; shorter K
+    # takes the tile kernel.  qmm_small stages bf16 scales in LDS blocks of 8 groups when
     # K / gs % 8 == 0 (waves whose K range starts mid-block, 4/8/16 steps per block) and loads
     # them per step otherwise (K / gs = 45 and 12 below).
     (256, 3072, 3072, 64, 4),   # config 1 shape
@@ -239,10 +239,12 @@ def test_qmm_wide_vs_oracle(mlxq, M, K, N, gs, bits):
 
 @pytest.mark.parametrize("M,K,N,gs,bits", [(2048, 192, 4096, 64, 4), (2048, 64, 4096, 32, 4),
                                            (2100, 320, 4352, 64, 8), (2048, 512, 4096, 128, 8),
-                                           (1024, 256, 4096, 64, 4)])
+                                           (1024, 256, 4096, 64, 4), (128, 1024, 512, 64, 4),
+                                           (200, 768, 300, 32, 8)])
 def test_qmm_wide_f32_scales(mlxq, M, K, N, gs, bits):
     """bf16 activations with f32 scales/biases: the wide kernel's register-loaded scale path,
-    any K % 64 == 0 (K/64 = 3, 1, 5 and 8 steps cover both prologue parities)."""
+    any K % 64 == 0 (K/64 = 3, 1, 5 and 8 steps cover both prologue parities), its 256x128
+    form (M = 1024), and the K-split kernel's per-step scale loads (M = 128, 200)."""
     banner("qmm wide f32 scales", M, K, N, gs, bits)
     rng = np.random.default_rng(M + K + N + 7 * bits)
     x = bf16_normal(rng, (M, K))
