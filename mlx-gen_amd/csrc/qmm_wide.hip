@@ -182,22 +182,19 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   const int KT = (int)(K / 64);
   const int64_t bm0 = tm * BM, bn0 = tn * BN;
   const int64_t wn0 = bn0 + (int64_t)wave * (BN / WAVES);
-  // Dense bias of the tile's BN columns: one value per thread, loaded now and parked in LDS for
-  // the epilogue, so the epilogue issues no global loads (each would wait on the tile's pending
-  // output stores too, since vmcnt counts stores).  It is parked in activation stage KT % 4,
-  // which no step reads or refills after step KT-4: the kernel keeps a single LDS object, and
-  // the compiler then adds no conservative wait for the direct-to-LDS loads before the ring's
-  // LDS reads (it did with a second LDS array).
-  float bias_t = 0.0f;
+  // Dense bias of the tile's BN columns: one value per thread, loaded now and written to its LDS
+  // slot (after the ring and scale blocks, in the kernel's single LDS object) in the epilogue,
+  // so the epilogue issues no global loads (each would wait on the tile's pending output stores
+  // too, since vmcnt counts stores).  The load is unconditional on a clamped column (columns past
+  // N are never stored) and kept as raw bits until the epilogue: a per-lane conditional load, or
+  // converting the value right away, made the compiler wait for it before the first operand loads.
+  uint32_t bias_bits = 0;
   if constexpr (FUSED) {
-    // Unconditional load of a clamped column (columns past N are never stored): a per-lane
-    // conditional load made the compiler wait for it before the first operand loads.
     if (epi.bias) {
       const int64_t nn = bn0 + (tid < BN ? tid : 0);
-      bias_t = bf16_bits_to_f32(epi.bias[nn < N ? nn : N - 1]);
+      bias_bits = epi.bias[nn < N ? nn : N - 1];
     }
   }
-
   // Buffer resources: 32-bit offsets (the host checks every operand fits in 4 GiB).  Rows past
   // M / N are clamped so every offset stays inside its operand.
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
@@ -491,7 +488,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   const bool via_lds = (N % 8) == 0;
   float* bias_lds = reinterpret_cast<float*>(lds_all + kMain);
   if constexpr (FUSED) {
-    if (epi.bias && tid < BN) bias_lds[tid] = bias_t;
+    if (epi.bias && tid < BN) {
+      asm volatile("" : "+v"(bias_bits));  // first use here, so the load is waited for here
+      bias_lds[tid] = bf16_bits_to_f32(bias_bits);
+    }
   }
   __syncthreads();  // bias visible; every wave past its last ring read
   if constexpr (TABLE) {
