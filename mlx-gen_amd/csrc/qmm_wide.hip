@@ -310,6 +310,31 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) a_off[kk] = r32 * 128 + (((4 * half + kk) ^ swz_f(r32)) << 4);
 
+  // LoRA operands of the epilogue (x.A rows per m sub-tile, B^T rows per n sub-tile), loaded in
+  // the last K step so their latency hides behind its MFMAs (rows past M / N are clamped: never
+  // stored).
+  [[maybe_unused]] const bool lora_on = FUSED && epi.rank16 > 0;
+  [[maybe_unused]] bf16x8 xa_pf[TMW], lb_pf[TNW];
+  auto prefetch_lora = [&]() {
+    if constexpr (FUSED) {
+#pragma unroll
+      for (int i = 0; i < TMW; ++i) xa_pf[i] = bf16x8{};
+#pragma unroll
+      for (int j = 0; j < TNW; ++j) lb_pf[j] = bf16x8{};
+      if (lora_on) {
+#pragma unroll
+        for (int i = 0; i < TMW; ++i) {
+          const int64_t m = bm0 + i * 32 + r32 < M ? bm0 + i * 32 + r32 : M - 1;
+          xa_pf[i] = *reinterpret_cast<const bf16x8*>(epi.xa + m * 16 + half * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < TNW; ++j) {
+          const int64_t n = wn0 + j * 32 + r32 < N ? wn0 + j * 32 + r32 : N - 1;
+          lb_pf[j] = *reinterpret_cast<const bf16x8*>(epi.lbt + n * 16 + half * 8);
+        }
+      }
+    }
+  };
   f32x16 acc[TMW][TNW];
 #pragma unroll
   for (int i = 0; i < TMW; ++i)
@@ -425,6 +450,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     if constexpr (N1) mlxq_vmcnt<B_OPS + (N2 ? A_PER + B_OPS : 0)>();
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!N1) prefetch_lora();  // last step: no explicit waits follow
     if constexpr (N3) dma_a(kt + 3);
     read_a(1, As, 3);
     deq_b(1, 3);
@@ -510,21 +536,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   const bool lora = FUSED && epi.rank16 > 0;
   if constexpr (FUSED) {
 #pragma unroll
-    for (int i = 0; i < TMW; ++i) xa[i] = bf16x8{};
+    for (int i = 0; i < TMW; ++i) xa[i] = xa_pf[i];
 #pragma unroll
-    for (int j = 0; j < TNW; ++j) lb[j] = bf16x8{};
-    if (lora) {  // rows past M / columns past N read clamped ones: never stored
-#pragma unroll
-      for (int i = 0; i < TMW; ++i) {
-        const int64_t m = bm0 + i * 32 + r32 < M ? bm0 + i * 32 + r32 : M - 1;
-        xa[i] = *reinterpret_cast<const bf16x8*>(epi.xa + m * 16 + half * 8);
-      }
-#pragma unroll
-      for (int j = 0; j < TNW; ++j) {
-        const int64_t n = wn0 + j * 32 + r32 < N ? wn0 + j * 32 + r32 : N - 1;
-        lb[j] = *reinterpret_cast<const bf16x8*>(epi.lbt + n * 16 + half * 8);
-      }
-    }
+    for (int j = 0; j < TNW; ++j) lb[j] = lb_pf[j];
   }
   // 16 outputs of accumulator (i, j) as bf16 bits, two per word: to the LDS tile, or straight
   // to y (N % 8 != 0).
