@@ -137,6 +137,26 @@ int mlxq_linear(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
                 size_t workspace_bytes, void* stream);
 
 /*
+ * mlxq_linear without a workspace argument: the LoRA staging buffers (the bytes
+ * mlxq_linear_workspace_size reports) live in a static device array of
+ * MLXQ_NOALLOC_SCRATCH_BYTES that each GPU holds from the first call on it until the process ends.
+ * No counterpart in the reference: this entry point exists for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It calls no allocator.  A problem that needs more scratch than the array holds is
+ * rejected with MLXQ_EINVAL before any device work.  The first call on each device resolves the
+ * array's device address (hipGetSymbolAddress), so make it outside graph capture.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (several streams or threads)
+ * race and must be serialised by the caller.  Same arguments, results and errors as mlxq_linear
+ * otherwise.
+ */
+#define MLXQ_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+int mlxq_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
+                        const void* scales, const void* biases, int sb_dtype, int64_t N,
+                        int group_size, int bits, const mlxq_epilogue* epilogue, void* y,
+                        void* stream);
+
+/*
  * Stacked-expert projection — Proj::forward of the quantized MoE experts
  * (mlx-gen-lens/src/text_encoder/gpt_oss.rs:412-425, quantized_matmul(x, wq, s, b, true) + bias)
  * run for every expert of a stacked pack split along axis 0 (mlx-gen-lens/src/quant.rs:93-137):

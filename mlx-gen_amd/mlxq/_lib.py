@@ -23,6 +23,9 @@ MLXQ_ACT_NONE = 0
 MLXQ_ACT_GELU = 1
 MLXQ_ACT_GELU_TANH = 2
 
+# Size of the static per-device scratch array behind mlxq_linear_noalloc.
+MLXQ_NOALLOC_SCRATCH_BYTES = 8 << 20
+
 # Every symbol include/mlxq.h declares; tests check the library exports all of them.
 EXPORTS = (
     "mlxq_last_error",
@@ -34,6 +37,7 @@ EXPORTS = (
     "mlxq_qmv",
     "mlxq_linear_workspace_size",
     "mlxq_linear",
+    "mlxq_linear_noalloc",
     "mlxq_packed_bits",
     "mlxq_embedding",
     "mlxq_lora_residual",
@@ -92,6 +96,8 @@ def load():
     lib.mlxq_linear_workspace_size.restype = ctypes.c_size_t
     lib.mlxq_linear.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _vp, _int, _i64, _int, _int,
                                 ctypes.POINTER(Epilogue), _vp, _vp, ctypes.c_size_t, _vp]
+    lib.mlxq_linear_noalloc.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _vp, _int, _i64, _int,
+                                        _int, ctypes.POINTER(Epilogue), _vp, _vp]
     lib.mlxq_packed_bits.argtypes = [_i64, _i64, _int]
     lib.mlxq_lora_residual.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _i64, _i64, ctypes.c_float,
                                        _vp, _vp, ctypes.c_size_t, _vp]
@@ -103,7 +109,7 @@ def load():
     lib.mlxq_embedding.argtypes = [_vp, _i64, _vp, _vp, _vp, _int, _i64, _i64, _int, _int, _vp, _int,
                                    _vp]
     for name in ("mlxq_quantize", "mlxq_dequantize", "mlxq_quantized_matmul", "mlxq_qmm",
-                 "mlxq_qmv", "mlxq_linear", "mlxq_packed_bits", "mlxq_embedding",
+                 "mlxq_qmv", "mlxq_linear", "mlxq_linear_noalloc", "mlxq_packed_bits", "mlxq_embedding",
                  "mlxq_lora_residual", "mlxq_cast", "mlxq_swiglu", "mlxq_qmm_experts"):
         getattr(lib, name).restype = _int
     _lib = lib
