@@ -76,7 +76,9 @@ def bench_flux_mlp(mlxq, torch, steps, warmup):
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
-    ep_gelu = _lib.Epilogue(None, None, None, 0, 1.0, _lib.MLXQ_ACT_GELU)
+    # bf16 stream: the dtype-preserving exact GELU (src/nn.rs:344-355), so h stays bf16.
+    ep_gelu = _lib.Epilogue(None, None, None, 0, 1.0, _lib.MLXQ_ACT_GELU_EXACT, _lib.MLXQ_BFLOAT16,
+                            _lib.MLXQ_BFLOAT16)
 
     def up():
         _lib.check(lib.mlxq_linear(x.data_ptr(), 1, M, K, qu[0].data_ptr(), qu[1].data_ptr(),
@@ -286,7 +288,8 @@ def bench_config5(mlxq, torch):
                 q = mlxq.quantize(gen_bf16((N, K), 0.02, 600 + N + K, dev), gs, bits)
                 a = gen_bf16((K, 16), 0.01, 700 + K, dev)
                 b = gen_bf16((16, N), 0.01, 701 + N, dev)
-                ws = torch.empty(mlxq.linear_workspace_size(M, N, 16), dtype=torch.uint8, device=dev)
+                ws = torch.empty(mlxq.linear_workspace_size(torch.bfloat16, torch.bfloat16, M, N, lora_a=a),
+                                 dtype=torch.uint8, device=dev)
                 ms = graph_ms(torch, lambda: mlxq.linear(xs[K], *q, gs, bits, lora_a=a, lora_b=b,
                                                          workspace=ws), inner=4, reps=3)
                 flop = 2.0 * M * K * N + 2.0 * M * 16 * (K + N)

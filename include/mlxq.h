@@ -20,9 +20,18 @@
  *   - Alignment: activations, packed weights, outputs and workspaces 16 bytes; scales and biases
  *     4 bytes.  Misaligned pointers are rejected with MLXQ_EINVAL.
  *   - Every call returns an mlxq_status; on failure mlxq_last_error() (thread-local) describes
- *     it.  Invalid shapes are rejected with MLXQ_EINVAL, never a crash (the reference's
- *     packed_bits panics on malformed triples, src/quant.rs:38-41).
- *   - Re-entrant per stream; no global mutable state besides the thread-local error string.
+ *     it.  Arguments that contradict each other here (dtype codes, group_size/bits, K % gs,
+ *     alignment, null pointers) are rejected with MLXQ_EINVAL.  This layer sees pointers, not
+ *     tensor shapes: the C++ and Python hosts check every operand's shape and dtype against x
+ *     before they call in (the reference's packed_bits panics on malformed triples,
+ *     src/quant.rs:38-41).
+ *   - Dtypes follow MLX's promotion: an op on a bf16 and an f32 operand computes and returns f32
+ *     (quantized_matmul returns promote(x, scales); a bias add and a LoRA residual promote the
+ *     output the same way).  mlxq_linear_out_dtype gives the dtype y must have.
+ *   - Re-entrant per stream.  Process-wide state, all of it per device and written once: the two
+ *     GELU tables (device memory in the code object, filled by the first GELU GEMM on a device),
+ *     the cached CU count, the device address of mlxq_linear_noalloc's static scratch (guarded
+ *     by a mutex), plus the thread-local error string.
  */
 #ifndef MLXQ_H
 #define MLXQ_H
@@ -48,10 +57,16 @@ typedef enum {
 
 typedef enum {
   MLXQ_ACT_NONE = 0,
-  MLXQ_ACT_GELU = 1, /* exact erf GELU, mlx-gen-flux/src/transformer.rs:975 */
-  /* tanh-approximate GELU as separate ops in the activation dtype, src/nn.rs:321-329 (FLUX
+  /* mlx_rs::nn::gelu, the exact-erf GELU of FLUX's FeedForward (mlx-gen-flux/src/transformer.rs:975;
+   * also mlx-gen-qwen-image/src/text_encoder/vision/merger.rs:49, mlx-gen-ltx/src/connector.rs:252):
+   * its constants are f32 arrays, so a bf16 input promotes and the result is f32 (src/nn.rs:335-338) */
+  MLXQ_ACT_GELU = 1,
+  /* tanh-approximate GELU as separate ops in the input dtype, src/nn.rs:321-329 (FLUX
    * single-stream FFN and GeluApprox, mlx-gen-flux/src/transformer.rs:506,708,979) */
   MLXQ_ACT_GELU_TANH = 2,
+  /* dtype-preserving exact GELU, src/nn.rs:344-355 gelu_exact (x * (1 + erf(x / sqrt2))) / 2 as
+   * separate ops in the input dtype; the GELU of most crates' FFNs (bernini, boogu, pid, svd, ...) */
+  MLXQ_ACT_GELU_EXACT = 3,
 } mlxq_activation;
 
 /* Thread-local description of the last failure on this thread ("" if none). */
@@ -77,11 +92,12 @@ int mlxq_dequantize(const uint32_t* wq, const void* scales, const void* biases, 
 /*
  * quantized_matmul — replaces mlx_rs::ops::quantized_matmul(x, wq, scales, biases, transpose,
  * group_size, bits) (src/adapters.rs:309-317).  x [M,K] in x_dtype (batch dims flattened into
- * M); y [M,N] in x_dtype; fp32 accumulation.  Only transpose=1 (y = x . W^T, the only form the
- * reference uses) is implemented; transpose=0 returns MLXQ_EUNSUPPORTED.
- * Dispatch: bf16 x with M > 8 runs the MFMA GEMM (weights dequantized to bf16 tiles); bf16 x with
- * M <= 8 runs the bandwidth-bound GEMV (weights dequantized exactly in f32, factored per group);
- * f32 x runs the f32 kernel (exact f32 dequant).
+ * M); y [M,N] in promote(x_dtype, sb_dtype) (bf16 only when both are bf16, as MLX casts x, scales
+ * and biases to their result type); fp32 accumulation.  Only transpose=1 (y = x . W^T, the only
+ * form the reference uses) is implemented; transpose=0 returns MLXQ_EUNSUPPORTED.
+ * Dispatch: bf16 x and scales with M > 8 run the MFMA GEMM (weights dequantized to bf16 tiles);
+ * bf16 with M <= 8 runs the bandwidth-bound GEMV (weights dequantized exactly in f32, factored per
+ * group); an f32 operand runs the f32 kernels (exact f32 dequant, f32 result).
  */
 int mlxq_quantized_matmul(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
                           const void* scales, const void* biases, int sb_dtype, int64_t N,
@@ -100,11 +116,12 @@ int mlxq_embedding(const int32_t* ids, int64_t T, const uint32_t* wq, const void
                    int bits, void* out, int out_dtype, void* stream);
 
 /* Forced-kernel variants of quantized_matmul (same arguments, transpose implied = 1). */
-/* MFMA GEMM; x must be bf16; any M >= 1. */
+/* MFMA bf16-tile GEMM; x must be bf16; any M >= 1; y is bf16 whatever sb_dtype is (the kernel's
+ * native output: with f32 scales this is not quantized_matmul's promoted f32 result). */
 int mlxq_qmm(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
              const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
              int bits, void* y, void* stream);
-/* GEMV; bf16 or f32 x; 1 <= M <= 8. */
+/* GEMV; bf16 or f32 x; 1 <= M <= 8; y in promote(x_dtype, sb_dtype). */
 int mlxq_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
              const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
              int bits, void* y, void* stream);
@@ -114,11 +131,16 @@ int mlxq_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* w
  * LinearBase::forward's quantized arm plus AdaptableLinear::forward (src/adapters.rs:300-322,
  * 543-549) for one LoRA adapter (Adapter::residual, src/adapters.rs:260-270), optionally followed
  * by the caller's activation (FeedForward::forward, mlx-gen-flux/src/transformer.rs:970-977):
- *   y = act( round(round(qmm(x) + bias) + round(round(round(x.A).B) * scale)) )
- * with every round() to the activation dtype exactly where the reference's separate MLX ops
- * round.  bias [N], lora_a [K,rank], lora_b [rank,N] are in x_dtype and nullable (rank 0 = no
- * LoRA).  workspace must hold mlxq_linear_workspace_size(M, N, rank) bytes (NULL when that is
- * 0); rank <= 256.
+ *   y0 = qmm(x)                 in D0 = promote(x_dtype, sb_dtype)          (:309-317)
+ *   y1 = y0 + bias              in D1 = promote(D0, bias_dtype)             (:318-320)
+ *   r  = ((x.A).B) * scale      in DR = promote(x_dtype, lora_dtype), each op rounded to DR and
+ *                               scale cast to DR first (the factors keep their file dtype, :243-252)
+ *   y2 = y1 + r                 in D2 = promote(D1, DR), not cast back     (:546)
+ *   y  = act(y2)                GELU_TANH / GELU_EXACT per op in D2; GELU in f32
+ * Each round() happens exactly where the reference's separate MLX ops round, and y has dtype
+ * mlxq_linear_out_dtype().  bias [N] (bias_dtype), lora_a [K,rank] and lora_b [rank,N]
+ * (lora_dtype) are nullable (rank 0 = no LoRA); rank <= 256.  workspace must hold
+ * mlxq_linear_workspace_size() bytes (NULL when that is 0).
  */
 typedef struct {
   const void* bias;
@@ -127,9 +149,19 @@ typedef struct {
   int64_t lora_rank;
   float lora_scale;
   int activation; /* mlxq_activation */
+  int bias_dtype; /* mlxq_dtype of bias (ignored when bias is NULL) */
+  int lora_dtype; /* mlxq_dtype of lora_a and lora_b (ignored when lora_rank is 0) */
 } mlxq_epilogue;
 
-size_t mlxq_linear_workspace_size(int64_t M, int64_t N, int64_t lora_rank);
+/* The dtype y of mlxq_linear has for these operands (an mlxq_dtype), or -1 (with
+ * mlxq_last_error set) when a dtype code or the activation is invalid.  epilogue may be NULL. */
+int mlxq_linear_out_dtype(int x_dtype, int sb_dtype, const mlxq_epilogue* epilogue);
+
+/* Bytes of device workspace mlxq_linear needs (0: pass NULL): the LoRA staging (x.A and B^T
+ * padded to rank 16, 4 bytes per element) and, when a bf16 product promotes to an f32 result,
+ * the bf16 product itself [M, N].  0 as well for invalid arguments (mlxq_linear reports them). */
+size_t mlxq_linear_workspace_size(int x_dtype, int sb_dtype, int64_t M, int64_t N,
+                                  const mlxq_epilogue* epilogue);
 
 int mlxq_linear(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
                 const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
@@ -137,8 +169,8 @@ int mlxq_linear(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
                 size_t workspace_bytes, void* stream);
 
 /*
- * mlxq_linear without a workspace argument: the LoRA staging buffers (the bytes
- * mlxq_linear_workspace_size reports) live in a static device array of
+ * mlxq_linear without a workspace argument: the workspace mlxq_linear_workspace_size reports
+ * (LoRA staging, and the bf16 product of a promoted result) lives in a static device array of
  * MLXQ_NOALLOC_SCRATCH_BYTES that each GPU holds from the first call on it until the process ends.
  * No counterpart in the reference: this entry point exists for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
@@ -160,16 +192,19 @@ int mlxq_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, const 
  * Stacked-expert projection — Proj::forward of the quantized MoE experts
  * (mlx-gen-lens/src/text_encoder/gpt_oss.rs:412-425, quantized_matmul(x, wq, s, b, true) + bias)
  * run for every expert of a stacked pack split along axis 0 (mlx-gen-lens/src/quant.rs:93-137):
- *   for e in [0, E):  y[e] = round(round(x[e] . dequant(wq[e])^T) + bias[e])   (round() to x_dtype)
- * wq [E, N, K*bits/32], scales/biases [E, N, K/group_size] (sb_dtype), bias [E, N] in x_dtype or
- * NULL, y [E, M, N].  x is [M, K] shared by every expert when x_per_expert == 0 (the gate_up
- * projection of gpt_oss.rs:702), else [E, M, K] (the down projection of :714).  Each expert's
- * result equals the single-matrix mlxq_linear with that bias; bf16 x with M > 8 runs every expert
- * in one GEMM launch.
+ *   for e in [0, E):  y[e] = round(round(x[e] . dequant(wq[e])^T) + bias[e])
+ * rounded to D0 = promote(x_dtype, sb_dtype) and then promote(D0, bias_dtype), as mlxq_linear.
+ * wq [E, N, K*bits/32], scales/biases [E, N, K/group_size] (sb_dtype), bias [E, N] in bias_dtype
+ * or NULL, y [E, M, N].  The reference's stacked packs carry a bf16 bias (gpt_oss.rs:478-487); an
+ * f32 bias over a bf16 product would need a promoted second pass and returns MLXQ_EUNSUPPORTED.
+ * x is [M, K] shared by every expert when x_per_expert == 0 (the gate_up projection of
+ * gpt_oss.rs:702), else [E, M, K] (the down projection of :714).  Each expert's result equals the
+ * single-matrix mlxq_linear with that bias; bf16 x with M > 8 runs every expert in one GEMM launch.
  */
 int mlxq_qmm_experts(const void* x, int x_dtype, int x_per_expert, int64_t E, int64_t M, int64_t K,
                      const uint32_t* wq, const void* scales, const void* biases, int sb_dtype,
-                     const void* bias, int64_t N, int group_size, int bits, void* y, void* stream);
+                     const void* bias, int bias_dtype, int64_t N, int group_size, int bits, void* y,
+                     void* stream);
 
 /*
  * Fused SwiGLU gate/up for decode — the first two ops of Mlp::forward
@@ -189,11 +224,16 @@ int mlxq_swiglu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
  * One more LoRA adapter on an already computed output — the `out + adapter.residual(x)` step of
  * AdaptableLinear::forward (src/adapters.rs:543-549, Adapter::residual :260-270) for adapter
  * stacks beyond the one mlxq_linear fuses:
- *   y = round(y + round(round(round(x.A).B) * scale))   (round() to x_dtype, y in x_dtype)
- * A [K,rank], B [rank,N] in x_dtype, 1 <= rank <= 256; workspace as for mlxq_linear.
+ *   y_out = y_in + r,  r = ((x.A).B) * scale in DR = promote(x_dtype, lora_dtype) (each op rounded
+ *   to DR, scale cast to DR), the sum in promote(y_dtype, DR) — the dtype y_out must have.
+ * A [K,rank], B [rank,N] in lora_dtype, 1 <= rank <= 256.  y_out may be y_in when the sum keeps
+ * y_dtype; otherwise the two must not overlap.  workspace: mlxq_lora_residual_workspace_size().
  */
+size_t mlxq_lora_residual_workspace_size(int x_dtype, int lora_dtype, int64_t M, int64_t N,
+                                         int64_t rank);
 int mlxq_lora_residual(const void* x, int x_dtype, int64_t M, int64_t K, const void* lora_a,
-                       const void* lora_b, int64_t N, int64_t rank, float lora_scale, void* y,
+                       const void* lora_b, int lora_dtype, int64_t N, int64_t rank,
+                       float lora_scale, const void* y_in, int y_dtype, void* y_out,
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /*

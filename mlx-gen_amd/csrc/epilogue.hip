@@ -4,7 +4,8 @@
 // scale multiply rounded to the activation dtype) needs x.A once per call.  lora_prep computes it
 // together with the transposed, zero-padded up-projection so the GEMM epilogue can run the
 // rank-R product as one more MFMA K-step.  linear_epilogue applies bias / LoRA / activation to an
-// already computed y for the paths that do not fuse them (GEMV and f32 activations).
+// already computed y for the paths that do not fuse them (GEMV, f32 activations, ranks above 16
+// and every result MLX's dtype promotion makes f32 from a bf16 product).
 #include "mlxq_common.h"
 
 namespace mlxq {
@@ -165,14 +166,51 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
   }
 }
 
+// DR = f32 (an f32 activation or f32 factors): xa[M,R] = x . A and lbt[N,R] = B^T in f32, x and
+// the factors widened exactly (MLX promotes the bf16 operand of a mixed matmul to f32).
+template <typename XT, typename FT>
+__global__ void lora_prep_f32_kernel(const XT* __restrict__ x, int64_t M, int64_t K,
+                                     const FT* __restrict__ A, const FT* __restrict__ B, int64_t N,
+                                     int rank, int R, float* __restrict__ xa, float* __restrict__ lbt) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nxa = M * R;
+  if (t < nxa) {
+    const int64_t m = t / R;
+    const int r = (int)(t % R);
+    float acc = 0.0f;
+    if (r < rank) {
+      for (int64_t k = 0; k < K; ++k) acc = fmaf(Act<XT>::ld(x, m * K + k), Act<FT>::ld(A, k * rank + r), acc);
+    }
+    xa[t] = acc;
+  } else if (t < nxa + N * R) {
+    const int64_t u = t - nxa;
+    const int64_t n = u / R;
+    const int r = (int)(u % R);
+    lbt[u] = r < rank ? Act<FT>::ld(B, (int64_t)r * N + n) : 0.0f;
+  }
+}
+
 int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* A, const void* B,
-                  int64_t N, int rank, int R, void* xa, void* lbt, hipStream_t st) {
+                  int lora_dtype, int64_t N, int rank, int R, void* xa, void* lbt, hipStream_t st) {
   const int64_t total = M * R + N * R;
   if (total == 0) return MLXQ_OK;
   const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7fffffff) return set_error(MLXQ_EINVAL, "lora: problem too large");
+  if (x_dtype != MLXQ_BFLOAT16 || lora_dtype != MLXQ_BFLOAT16) {
+    const dim3 g((unsigned)blocks), b(256);
+    if (x_dtype == MLXQ_BFLOAT16)
+      hipLaunchKernelGGL((lora_prep_f32_kernel<uint16_t, float>), g, b, 0, st, (const uint16_t*)x, M, K,
+                         (const float*)A, (const float*)B, N, rank, R, (float*)xa, (float*)lbt);
+    else if (lora_dtype == MLXQ_BFLOAT16)
+      hipLaunchKernelGGL((lora_prep_f32_kernel<float, uint16_t>), g, b, 0, st, (const float*)x, M, K,
+                         (const uint16_t*)A, (const uint16_t*)B, N, rank, R, (float*)xa, (float*)lbt);
+    else
+      hipLaunchKernelGGL((lora_prep_f32_kernel<float, float>), g, b, 0, st, (const float*)x, M, K,
+                         (const float*)A, (const float*)B, N, rank, R, (float*)xa, (float*)lbt);
+    return check_launch("lora_prep");
+  }
   const int64_t bt_blocks = (N * R + kXaWaves * 64 - 1) / (kXaWaves * 64);
-  if (x_dtype == MLXQ_BFLOAT16 && K % 32 == 0 && M < (1LL << 31) / 16 && K < (1LL << 31) &&
-      bt_blocks < (1LL << 30)) {
+  if (K % 32 == 0 && M < (1LL << 31) / 16 && K < (1LL << 31) && bt_blocks < (1LL << 30)) {
     // x.A workgroups (16 rows x 16 columns each), then the B^T workgroups.
     const int xa_blocks = (int)((M + 15) / 16);
     const dim3 grid((unsigned)(xa_blocks + bt_blocks), (unsigned)(R / 16));
@@ -184,52 +222,60 @@ int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* 
       hipLaunchKernelGGL(lora_xa_kernel<false>, grid, dim3(kXaWaves * 64), 0, st, (const uint16_t*)x,
                          (int)M, (int)K, (const uint16_t*)A, rank, R, (uint16_t*)xa, xa_blocks,
                          (const uint16_t*)B, N, (uint16_t*)lbt);
-  } else if (x_dtype == MLXQ_BFLOAT16) {
+  } else {
     hipLaunchKernelGGL(lora_prep_kernel<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
                        (const uint16_t*)x, M, K, (const uint16_t*)A, (const uint16_t*)B, N, rank, R,
                        (uint16_t*)xa, (uint16_t*)lbt);
-  } else {
-    hipLaunchKernelGGL(lora_prep_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (const float*)x, M, K, (const float*)A, (const float*)B, N, rank, R,
-                       (float*)xa, (float*)lbt);
   }
   return check_launch("lora_prep");
 }
 
-// In place on y[M,N]: y = act(rnd(rnd(y + bias) + rnd(rnd(xa . lbt^T) * scale))).
-template <typename XT>
-__global__ void linear_epilogue_kernel(XT* __restrict__ y, int64_t M, int64_t N,
-                                       const XT* __restrict__ bias, const XT* __restrict__ xa,
-                                       const XT* __restrict__ lbt, int R, float scale, int act) {
+__device__ __forceinline__ float ld_any(const void* p, bool bf16, int64_t i) {
+  return bf16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
+}
+__device__ __forceinline__ float rnd_if(bool bf16, float v) { return bf16 ? round_bf16(v) : v; }
+
+// out = act(y1 + r), y1 = y_in + bias: every stage rounded to its promoted dtype (flags), the
+// sequence of LinearBase::forward's bias add and AdaptableLinear::forward's residual sum
+// (reference src/adapters.rs:318-320,543-549, Adapter::residual :260-270).  A bf16 activation is
+// the bf16 table's entry of its input; in f32 it is evaluated (GELU and the exact GELU as the
+// f32 erf form, the tanh GELU op by op).
+template <typename YI, typename YO>
+__global__ void linear_epilogue_kernel(LinearEpilogueArgs a) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= M * N) return;
-  const int64_t m = t / N, n = t % N;
-  float o = Act<XT>::ld(y, t);
-  if (bias) o = Act<XT>::rnd(o + Act<XT>::ld(bias, n));
-  if (R > 0) {
+  if (t >= a.M * a.N) return;
+  const int64_t m = t / a.N, n = t % a.N;
+  float o = Act<YI>::ld(static_cast<const YI*>(a.y_in), t);
+  if (a.bias) o = rnd_if(a.d1_bf16, o + ld_any(a.bias, a.bias_bf16, n));
+  if (a.R > 0) {
     float r = 0.0f;
-    for (int k = 0; k < R; ++k) r = fmaf(Act<XT>::ld(xa, m * R + k), Act<XT>::ld(lbt, n * R + k), r);
-    o = Act<XT>::rnd(o + Act<XT>::rnd(Act<XT>::rnd(r) * scale));
+    for (int k = 0; k < a.R; ++k)
+      r = fmaf(ld_any(a.xa, a.dr_bf16, m * a.R + k), ld_any(a.lbt, a.dr_bf16, n * a.R + k), r);
+    o = rnd_if(a.d2_bf16, o + rnd_if(a.dr_bf16, rnd_if(a.dr_bf16, r) * a.lora_scale));
   }
-  if (act == MLXQ_ACT_GELU) o = gelu_erf(o);
-  else if (act == MLXQ_ACT_GELU_TANH) o = gelu_tanh<sizeof(XT) == 2>(o);
-  Act<XT>::st(y, t, o);
+  const bool act_bf16 = a.d2_bf16;  // the activation's input dtype
+  if (a.act == MLXQ_ACT_GELU) {
+    o = gelu_erf(o);
+  } else if (a.act == MLXQ_ACT_GELU_TANH || a.act == MLXQ_ACT_GELU_EXACT) {
+    if (act_bf16) o = bf16_bits_to_f32(a.act_table[f32_to_bf16_bits(o)]);
+    else o = a.act == MLXQ_ACT_GELU_TANH ? gelu_tanh<false>(o) : gelu_erf(o);
+  }
+  Act<YO>::st(static_cast<YO*>(a.y_out), t, o);
 }
 
-int run_linear_epilogue(void* y, int x_dtype, int64_t M, int64_t N, const void* bias, const void* xa,
-                        const void* lbt, int R, float scale, int act, hipStream_t st) {
-  const int64_t total = M * N;
+int run_linear_epilogue(const LinearEpilogueArgs& a, hipStream_t st) {
+  const int64_t total = a.M * a.N;
   if (total == 0) return MLXQ_OK;
   const int64_t blocks = (total + 255) / 256;
-  if (x_dtype == MLXQ_BFLOAT16) {
-    hipLaunchKernelGGL(linear_epilogue_kernel<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (uint16_t*)y, M, N, (const uint16_t*)bias, (const uint16_t*)xa,
-                       (const uint16_t*)lbt, R, scale, act);
-  } else {
-    hipLaunchKernelGGL(linear_epilogue_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (float*)y, M, N, (const float*)bias, (const float*)xa, (const float*)lbt, R,
-                       scale, act);
-  }
+  if (blocks > 0x7fffffff) return set_error(MLXQ_EINVAL, "linear epilogue: problem too large");
+  const bool table_act = a.act == MLXQ_ACT_GELU_TANH || a.act == MLXQ_ACT_GELU_EXACT;
+  if (table_act && a.d2_bf16 && a.act_table == nullptr)
+    return set_error(MLXQ_EINVAL, "linear epilogue: activation table missing");
+  const dim3 g((unsigned)blocks), b(256);
+  if (a.y_in_bf16 && a.y_out_bf16) hipLaunchKernelGGL((linear_epilogue_kernel<uint16_t, uint16_t>), g, b, 0, st, a);
+  else if (a.y_in_bf16) hipLaunchKernelGGL((linear_epilogue_kernel<uint16_t, float>), g, b, 0, st, a);
+  else if (a.y_out_bf16) hipLaunchKernelGGL((linear_epilogue_kernel<float, uint16_t>), g, b, 0, st, a);
+  else hipLaunchKernelGGL((linear_epilogue_kernel<float, float>), g, b, 0, st, a);
   return check_launch("linear_epilogue");
 }
 

@@ -67,9 +67,108 @@ static int check_mm(const char* op, const void* x, int x_dtype, int64_t M, int64
   return MLXQ_OK;
 }
 
-static const QmmEpilogue kNoEpilogue = {nullptr, nullptr, nullptr, 0, 1.0f, MLXQ_ACT_NONE};
+static const QmmEpilogue kNoEpilogue = {nullptr, nullptr, nullptr, 0, 1.0f, kFusedActNone, nullptr};
 
 static inline int64_t round16(int64_t r) { return (r + 15) / 16 * 16; }
+static inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+// A scalar cast to bf16 (round to nearest even), as scalar(v).as_dtype(Bfloat16) does.
+static float bf16_scalar(float v) {
+  uint32_t u;
+  memcpy(&u, &v, 4);
+  u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+  memcpy(&v, &u, 4);
+  return v;
+}
+
+// The dtype of every stage of mlxq_linear under MLX's promotion (bf16 iff every operand that
+// meets there is bf16), from the reference op sequence of src/adapters.rs:243-252,300-322,543-549.
+struct LinearPlan {
+  bool d0_bf16 = true;   // qmm(x): promote(x, scales)
+  bool bias = false, d1_bf16 = true;  // + bias: promote(D0, bias)
+  bool lora = false, dr_bf16 = true;  // residual: promote(x, factors)
+  bool d2_bf16 = true;   // + residual: promote(D1, DR)
+  int act = MLXQ_ACT_NONE;
+  bool out_bf16 = true;  // GELU (mlx_rs::nn::gelu) returns f32
+  int R = 0;             // padded LoRA rank
+  // Workspace layout (byte offsets), total bytes.
+  size_t xa = 0, lbt = 0, y0 = 0, total = 0;
+  bool promoted() const { return d0_bf16 && !out_bf16; }  // bf16 product, f32 result
+};
+
+static int plan_linear(const char* op, int x_dtype, int sb_dtype, const mlxq_epilogue* ep,
+                       int64_t M, int64_t N, LinearPlan& p) {
+  int rc;
+  if ((rc = check_dtype(op, "x", x_dtype)) || (rc = check_dtype(op, "scales", sb_dtype))) return rc;
+  p = LinearPlan{};
+  p.d0_bf16 = x_dtype == MLXQ_BFLOAT16 && sb_dtype == MLXQ_BFLOAT16;
+  if (ep) {
+    if (ep->activation < MLXQ_ACT_NONE || ep->activation > MLXQ_ACT_GELU_EXACT)
+      return set_error(MLXQ_EINVAL, "%s: unknown activation %d", op, ep->activation);
+    if (ep->lora_rank < 0 || ep->lora_rank > 256)
+      return set_error(MLXQ_EINVAL, "%s: lora_rank %lld outside [0, 256]", op, (long long)ep->lora_rank);
+    p.bias = ep->bias != nullptr;
+    if (p.bias && (rc = check_dtype(op, "bias", ep->bias_dtype))) return rc;
+    p.lora = ep->lora_rank > 0;
+    if (p.lora && (rc = check_dtype(op, "LoRA factors", ep->lora_dtype))) return rc;
+    p.act = ep->activation;
+  }
+  p.d1_bf16 = p.d0_bf16 && (!p.bias || ep->bias_dtype == MLXQ_BFLOAT16);
+  p.dr_bf16 = x_dtype == MLXQ_BFLOAT16 && (!p.lora || ep->lora_dtype == MLXQ_BFLOAT16);
+  p.d2_bf16 = p.d1_bf16 && (!p.lora || p.dr_bf16);
+  p.out_bf16 = p.d2_bf16 && p.act != MLXQ_ACT_GELU;
+  p.R = p.lora ? (int)round16(ep->lora_rank) : 0;
+  size_t off = 0;
+  if (p.lora && M > 0 && N > 0) {
+    p.xa = off;
+    off += align256((size_t)(M * p.R * 4));
+    p.lbt = off;
+    off += align256((size_t)(N * p.R * 4));
+  }
+  if (p.promoted() && M > 0 && N > 0) {
+    p.y0 = off;
+    off += align256((size_t)(M * N * 2));
+  }
+  p.total = off;
+  return MLXQ_OK;
+}
+
+static LinearEpilogueArgs epilogue_args(const LinearPlan& p, const void* y_in, bool y_in_bf16,
+                                        void* y_out, int64_t M, int64_t N, const mlxq_epilogue* ep,
+                                        const void* xa, const void* lbt, float scale_dr) {
+  LinearEpilogueArgs a;
+  a.y_in = y_in;
+  a.y_in_bf16 = y_in_bf16;
+  a.y_out = y_out;
+  a.y_out_bf16 = p.out_bf16;
+  a.M = M;
+  a.N = N;
+  a.bias = p.bias ? ep->bias : nullptr;
+  a.bias_bf16 = p.bias && ep->bias_dtype == MLXQ_BFLOAT16;
+  a.d1_bf16 = p.d1_bf16;
+  a.xa = xa;
+  a.lbt = lbt;
+  a.R = p.lora ? p.R : 0;
+  a.dr_bf16 = p.dr_bf16;
+  a.lora_scale = scale_dr;
+  a.d2_bf16 = p.d2_bf16;
+  a.act = p.act;
+  return a;
+}
+
+static int fused_act_of(int act) {
+  return act == MLXQ_ACT_GELU_EXACT ? kFusedActGeluExact
+         : act == MLXQ_ACT_GELU_TANH ? kFusedActGeluTanh : kFusedActNone;
+}
+
+// The bf16 table an elementwise epilogue reads for a bf16 activation (null when none is read).
+static int epilogue_table(LinearEpilogueArgs& a, hipStream_t st) {
+  if ((a.act == MLXQ_ACT_GELU_TANH || a.act == MLXQ_ACT_GELU_EXACT) && a.d2_bf16) {
+    a.act_table = act_table_ptr(fused_act_of(a.act), st);
+    if (!a.act_table) return MLXQ_EDEVICE;
+  }
+  return MLXQ_OK;
+}
 
 }  // namespace mlxq
 
@@ -183,19 +282,40 @@ int mlxq_quantized_matmul(const void* x, int x_dtype, int64_t M, int64_t K, cons
                      group_size, bits, y)))
     return rc;
   if (M == 0 || N == 0) return MLXQ_OK;
-  if (x_dtype == MLXQ_BFLOAT16 && M > 8)
+  // MLX casts x, scales and biases to their result type: bf16 tiles only when all are bf16.
+  if (x_dtype == MLXQ_BFLOAT16 && sb_dtype == MLXQ_BFLOAT16 && M > 8)
     return run_qmm(x, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y, kNoEpilogue,
                    (hipStream_t)stream);
   return run_qmv(x, x_dtype, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y,
                  (hipStream_t)stream);
 }
 
-size_t mlxq_linear_workspace_size(int64_t M, int64_t N, int64_t lora_rank) {
-  if (lora_rank <= 0 || M <= 0 || N <= 0) return 0;
-  const int64_t R = round16(lora_rank);
-  // xa [M,R] and lbt [N,R], 4 bytes per element (enough for f32 activations), 256-B aligned.
-  const int64_t xa = (M * R * 4 + 255) / 256 * 256;
-  return (size_t)(xa + N * R * 4);
+int mlxq_linear_out_dtype(int x_dtype, int sb_dtype, const mlxq_epilogue* epilogue) {
+  g_err[0] = 0;
+  LinearPlan p;
+  if (plan_linear("linear_out_dtype", x_dtype, sb_dtype, epilogue, 0, 0, p)) return -1;
+  return p.out_bf16 ? MLXQ_BFLOAT16 : MLXQ_FLOAT32;
+}
+
+size_t mlxq_linear_workspace_size(int x_dtype, int sb_dtype, int64_t M, int64_t N,
+                                  const mlxq_epilogue* epilogue) {
+  if (M <= 0 || N <= 0) return 0;
+  LinearPlan p;
+  char saved[sizeof(g_err)];
+  memcpy(saved, g_err, sizeof(g_err));  // a size query leaves the error string alone
+  const int rc = plan_linear("linear_workspace_size", x_dtype, sb_dtype, epilogue, M, N, p);
+  memcpy(g_err, saved, sizeof(g_err));
+  return rc ? 0 : p.total;
+}
+
+size_t mlxq_lora_residual_workspace_size(int x_dtype, int lora_dtype, int64_t M, int64_t N,
+                                         int64_t rank) {
+  if (M <= 0 || N <= 0 || rank <= 0 || rank > 256) return 0;
+  (void)x_dtype;
+  (void)lora_dtype;
+  const int64_t R = round16(rank);
+  // xa [M,R] and lbt [N,R], 4 bytes per element (enough for f32), 256-byte aligned.
+  return align256((size_t)(M * R * 4)) + align256((size_t)(N * R * 4));
 }
 
 int mlxq_swiglu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq_gate,
@@ -221,18 +341,27 @@ int mlxq_swiglu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
 }
 
 int mlxq_lora_residual(const void* x, int x_dtype, int64_t M, int64_t K, const void* lora_a,
-                       const void* lora_b, int64_t N, int64_t rank, float lora_scale, void* y,
+                       const void* lora_b, int lora_dtype, int64_t N, int64_t rank,
+                       float lora_scale, const void* y_in, int y_dtype, void* y_out,
                        void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   int rc;
-  if ((rc = check_dtype("lora_residual", "x", x_dtype))) return rc;
+  if ((rc = check_dtype("lora_residual", "x", x_dtype)) ||
+      (rc = check_dtype("lora_residual", "LoRA factors", lora_dtype)) ||
+      (rc = check_dtype("lora_residual", "y", y_dtype)))
+    return rc;
   if (M < 0 || K <= 0 || N < 0) return set_error(MLXQ_EINVAL, "lora_residual: bad shape M=%lld K=%lld N=%lld",
                                                   (long long)M, (long long)K, (long long)N);
   if (rank < 1 || rank > 256)
     return set_error(MLXQ_EINVAL, "lora_residual: rank %lld outside [1, 256]", (long long)rank);
   if (M == 0 || N == 0) return MLXQ_OK;
-  if (!x || !lora_a || !lora_b || !y) return set_error(MLXQ_EINVAL, "lora_residual: null operand");
-  const size_t need = mlxq_linear_workspace_size(M, N, rank);
+  if (!x || !lora_a || !lora_b || !y_in || !y_out) return set_error(MLXQ_EINVAL, "lora_residual: null operand");
+  const bool dr_bf16 = x_dtype == MLXQ_BFLOAT16 && lora_dtype == MLXQ_BFLOAT16;
+  const bool out_bf16 = y_dtype == MLXQ_BFLOAT16 && dr_bf16;
+  if (y_in == y_out && out_bf16 != (y_dtype == MLXQ_BFLOAT16))
+    return set_error(MLXQ_EINVAL, "lora_residual: the sum promotes to float32 and cannot overwrite the "
+                                  "bfloat16 y_in in place");
+  const size_t need = mlxq_lora_residual_workspace_size(x_dtype, lora_dtype, M, N, rank);
   if (workspace == nullptr || workspace_bytes < need)
     return set_error(MLXQ_EINVAL, "lora_residual: workspace of %zu bytes is smaller than the %zu required",
                      workspace_bytes, need);
@@ -240,16 +369,24 @@ int mlxq_lora_residual(const void* x, int x_dtype, int64_t M, int64_t K, const v
   hipStream_t st = (hipStream_t)stream;
   const int R = (int)round16(rank);
   void* xa = workspace;
-  void* lbt = (char*)workspace + (M * R * 4 + 255) / 256 * 256;
-  if ((rc = run_lora_prep(x, x_dtype, M, K, lora_a, lora_b, N, (int)rank, R, xa, lbt, st))) return rc;
-  float scale = lora_scale;
-  if (x_dtype == MLXQ_BFLOAT16) {
-    uint32_t u;
-    memcpy(&u, &scale, 4);
-    u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
-    memcpy(&scale, &u, 4);
-  }
-  return run_linear_epilogue(y, x_dtype, M, N, nullptr, xa, lbt, R, scale, MLXQ_ACT_NONE, st);
+  void* lbt = (char*)workspace + align256((size_t)(M * R * 4));
+  if ((rc = run_lora_prep(x, x_dtype, M, K, lora_a, lora_b, lora_dtype, N, (int)rank, R, xa, lbt, st)))
+    return rc;
+  LinearEpilogueArgs a;
+  a.y_in = y_in;
+  a.y_in_bf16 = y_dtype == MLXQ_BFLOAT16;
+  a.y_out = y_out;
+  a.y_out_bf16 = out_bf16;
+  a.M = M;
+  a.N = N;
+  a.d1_bf16 = a.y_in_bf16;
+  a.xa = xa;
+  a.lbt = lbt;
+  a.R = R;
+  a.dr_bf16 = dr_bf16;
+  a.lora_scale = dr_bf16 ? bf16_scalar(lora_scale) : lora_scale;
+  a.d2_bf16 = out_bf16;
+  return run_linear_epilogue(a, st);
 }
 
 int mlxq_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream) {
@@ -264,17 +401,27 @@ int mlxq_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t 
 
 int mlxq_qmm_experts(const void* x, int x_dtype, int x_per_expert, int64_t E, int64_t M, int64_t K,
                      const uint32_t* wq, const void* scales, const void* biases, int sb_dtype,
-                     const void* bias, int64_t N, int group_size, int bits, void* y, void* stream) {
+                     const void* bias, int bias_dtype, int64_t N, int group_size, int bits, void* y,
+                     void* stream) {
   g_err[0] = 0;
   int rc;
   if (E < 0) return set_error(MLXQ_EINVAL, "qmm_experts: E=%lld < 0", (long long)E);
   if ((rc = check_mm("qmm_experts", x, x_dtype, M, K, wq, scales, biases, sb_dtype, N, group_size,
                      bits, y)))
     return rc;
+  const bool d0_bf16 = x_dtype == MLXQ_BFLOAT16 && sb_dtype == MLXQ_BFLOAT16;
+  if (bias) {
+    if ((rc = check_dtype("qmm_experts", "bias", bias_dtype))) return rc;
+    if (d0_bf16 && bias_dtype != MLXQ_BFLOAT16)
+      return set_error(MLXQ_EUNSUPPORTED, "qmm_experts: a float32 bias over a bfloat16 product (the "
+                                          "stacked packs carry bfloat16 biases)");
+  }
   if (E == 0 || M == 0 || N == 0) return MLXQ_OK;
   const int xb = x_dtype == MLXQ_BFLOAT16 ? 2 : 4;
+  const int yb = d0_bf16 ? 2 : 4;
   const int sbb = sb_dtype == MLXQ_BFLOAT16 ? 2 : 4;
-  if (bias && (rc = check_aligned("qmm_experts", "bias", bias, xb))) return rc;
+  const int bb = bias_dtype == MLXQ_BFLOAT16 ? 2 : 4;
+  if (bias && (rc = check_aligned("qmm_experts", "bias", bias, bb))) return rc;
   QmmBatch bat;
   bat.count = E;
   bat.x = x_per_expert ? M * K : 0;
@@ -286,18 +433,23 @@ int mlxq_qmm_experts(const void* x, int x_dtype, int x_per_expert, int64_t E, in
   // All experts in one launch of the wide GEMM (grid.y = expert) when it applies: per-expert
   // problems of an encoder batch are a few dozen tiles each, too few to fill 256 CUs alone.
   const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
-  if (x_dtype == MLXQ_BFLOAT16 && M > 8 && K % 64 == 0 && E * tiles >= 128 && E <= 65535 &&
+  if (d0_bf16 && M > 8 && K % 64 == 0 && E * tiles >= 128 && E <= 65535 &&
       qmm_wide_fits(M, K, N, group_size, bits, sbb)) {
-    const QmmEpilogue qe = {(const uint16_t*)bias, nullptr, nullptr, 0, 1.0f, MLXQ_ACT_NONE};
+    const QmmEpilogue qe = {(const uint16_t*)bias, nullptr, nullptr, 0, 1.0f, kFusedActNone, nullptr};
     return run_qmm_wide(x, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y, qe, st, bat);
   }
-  // Otherwise expert by expert through the single-matrix paths (same rounding points).
+  // Otherwise expert by expert through the single-matrix paths (same rounding points; no
+  // workspace: without LoRA nothing is staged and the result never promotes past D0).
   for (int64_t e = 0; e < E; ++e) {
-    const mlxq_epilogue ep = {bias ? (const char*)bias + e * bat.bias * xb : nullptr, nullptr, nullptr,
-                              0, 1.0f, MLXQ_ACT_NONE};
+    mlxq_epilogue ep = {};
+    ep.bias = bias ? (const char*)bias + e * bat.bias * bb : nullptr;
+    ep.lora_scale = 1.0f;
+    ep.activation = MLXQ_ACT_NONE;
+    ep.bias_dtype = bias_dtype;
+    ep.lora_dtype = x_dtype;
     if ((rc = mlxq_linear((const char*)x + e * bat.x * xb, x_dtype, M, K, wq + e * bat.w,
                           (const char*)scales + e * bat.sb * sbb, (const char*)biases + e * bat.sb * sbb,
-                          sb_dtype, N, group_size, bits, &ep, (char*)y + e * bat.y * xb, nullptr, 0,
+                          sb_dtype, N, group_size, bits, &ep, (char*)y + e * bat.y * yb, nullptr, 0,
                           stream)))
       return rc;
   }
@@ -312,55 +464,54 @@ int mlxq_linear(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
   int rc;
   if ((rc = check_mm("linear", x, x_dtype, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y)))
     return rc;
+  LinearPlan p;
+  if ((rc = plan_linear("linear", x_dtype, sb_dtype, ep, M, N, p))) return rc;
   if (M == 0 || N == 0) return MLXQ_OK;
-  hipStream_t st = (hipStream_t)stream;
-  mlxq_epilogue none = {nullptr, nullptr, nullptr, 0, 1.0f, MLXQ_ACT_NONE};
-  const mlxq_epilogue& e = ep ? *ep : none;
-  if (e.activation != MLXQ_ACT_NONE && e.activation != MLXQ_ACT_GELU &&
-      e.activation != MLXQ_ACT_GELU_TANH)
-    return set_error(MLXQ_EINVAL, "linear: unknown activation %d", e.activation);
-  if (e.lora_rank < 0 || e.lora_rank > 256)
-    return set_error(MLXQ_EINVAL, "linear: lora_rank %lld outside [0, 256]", (long long)e.lora_rank);
-  const bool lora = e.lora_rank > 0;
-  const int R = lora ? (int)round16(e.lora_rank) : 0;
-  void* xa = nullptr;
-  void* lbt = nullptr;
-  if (lora) {
-    if (!e.lora_a || !e.lora_b) return set_error(MLXQ_EINVAL, "linear: lora_rank > 0 but A/B are null");
-    const size_t need = mlxq_linear_workspace_size(M, N, e.lora_rank);
-    if (workspace == nullptr || workspace_bytes < need)
+  if (p.lora && (!ep->lora_a || !ep->lora_b))
+    return set_error(MLXQ_EINVAL, "linear: lora_rank > 0 but A/B are null");
+  if (p.bias && (rc = check_aligned("linear", "bias", ep->bias, ep->bias_dtype == MLXQ_BFLOAT16 ? 2 : 4)))
+    return rc;
+  if (p.total > 0) {
+    if (workspace == nullptr || workspace_bytes < p.total)
       return set_error(MLXQ_EINVAL, "linear: workspace of %zu bytes is smaller than the %zu required",
-                       workspace_bytes, need);
+                       workspace_bytes, p.total);
     if ((rc = check_aligned("linear", "workspace", workspace))) return rc;
-    xa = workspace;
-    lbt = (char*)workspace + (M * R * 4 + 255) / 256 * 256;
-    if ((rc = run_lora_prep(x, x_dtype, M, K, e.lora_a, e.lora_b, N, (int)e.lora_rank, R, xa, lbt, st)))
-      return rc;
   }
-  // The lora scale is applied as a scalar of the activation dtype (src/adapters.rs:268-269).
-  float scale = e.lora_scale;
-  if (x_dtype == MLXQ_BFLOAT16) {
-    uint32_t u;
-    memcpy(&u, &scale, 4);
-    u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
-    memcpy(&scale, &u, 4);
-  }
-  if (x_dtype == MLXQ_BFLOAT16 && M > 8) {
-    // The GEMM fuses the whole epilogue for LoRA rank <= 16; a wider adapter runs the plain
-    // GEMM followed by the elementwise epilogue (same rounding points).
-    if (R <= 16) {
-      QmmEpilogue qe = {(const uint16_t*)e.bias, (const uint16_t*)xa, (const uint16_t*)lbt, R,
-                        scale, e.activation};
+  hipStream_t st = (hipStream_t)stream;
+  void* xa = p.lora ? (char*)workspace + p.xa : nullptr;
+  void* lbt = p.lora ? (char*)workspace + p.lbt : nullptr;
+  if (p.lora && (rc = run_lora_prep(x, x_dtype, M, K, ep->lora_a, ep->lora_b, ep->lora_dtype, N,
+                                    (int)ep->lora_rank, p.R, xa, lbt, st)))
+    return rc;
+  // The LoRA scale is a scalar cast to the residual's dtype (src/adapters.rs:268-269).
+  const float scale = p.lora ? (p.dr_bf16 ? bf16_scalar(ep->lora_scale) : ep->lora_scale) : 1.0f;
+  const bool epilogue = p.bias || p.lora || p.act != MLXQ_ACT_NONE;
+  if (p.d0_bf16 && M > 8 && p.out_bf16) {
+    // Everything in bf16: the GEMM fuses the whole epilogue for LoRA rank <= 16; a wider adapter
+    // runs the plain GEMM followed by the elementwise epilogue (same rounding points).
+    if (p.R <= 16) {
+      QmmEpilogue qe = {p.bias ? (const uint16_t*)ep->bias : nullptr, (const uint16_t*)xa,
+                        (const uint16_t*)lbt, p.R, scale, fused_act_of(p.act), nullptr};
+      if (qe.act != kFusedActNone && !(qe.act_table = act_table_ptr(qe.act, st))) return MLXQ_EDEVICE;
       return run_qmm(x, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y, qe, st);
     }
     if ((rc = run_qmm(x, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y, kNoEpilogue, st)))
       return rc;
-    return run_linear_epilogue(y, x_dtype, M, N, e.bias, xa, lbt, R, scale, e.activation, st);
+    LinearEpilogueArgs a = epilogue_args(p, y, true, y, M, N, ep, xa, lbt, scale);
+    if ((rc = epilogue_table(a, st))) return rc;
+    return run_linear_epilogue(a, st);
   }
-  if ((rc = run_qmv(x, x_dtype, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y, st)))
-    return rc;
-  if (!e.bias && !lora && e.activation == MLXQ_ACT_NONE) return MLXQ_OK;
-  return run_linear_epilogue(y, x_dtype, M, N, e.bias, xa, lbt, R, scale, e.activation, st);
+  // The product in D0, straight into y when y has that dtype; a bf16 product whose result
+  // promotes to f32 goes through the workspace (the elementwise epilogue widens it into y).
+  void* y0 = p.promoted() ? (char*)workspace + p.y0 : y;
+  if (p.d0_bf16 && M > 8) rc = run_qmm(x, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y0,
+                                       kNoEpilogue, st);
+  else rc = run_qmv(x, x_dtype, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y0, st);
+  if (rc) return rc;
+  if (!epilogue && !p.promoted()) return MLXQ_OK;
+  LinearEpilogueArgs a = epilogue_args(p, y0, p.d0_bf16, y, M, N, ep, xa, lbt, scale);
+  if ((rc = epilogue_table(a, st))) return rc;
+  return run_linear_epilogue(a, st);
 }
 
 }  // extern "C"

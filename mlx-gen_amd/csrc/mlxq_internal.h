@@ -6,6 +6,14 @@
 
 namespace mlxq {
 
+// Activation fused into a bf16 GEMM epilogue (QmmEpilogue::act).  Both are functions of the
+// bf16 pre-activation, evaluated as a lookup in a per-device table of the bf16 result.
+enum FusedAct : int {
+  kFusedActNone = 0,
+  kFusedActGeluExact = 1,  // MLXQ_ACT_GELU_EXACT in bf16 (table 0)
+  kFusedActGeluTanh = 2,   // MLXQ_ACT_GELU_TANH in bf16 (table 1)
+};
+
 // Fused GEMM epilogue operands (all bf16, device pointers, nullable).
 struct QmmEpilogue {
   const uint16_t* bias;  // [N]
@@ -13,7 +21,30 @@ struct QmmEpilogue {
   const uint16_t* lbt;   // [N, rank16] = B^T, zero padded
   int rank16;            // padded LoRA rank (multiple of 16), 0 = no LoRA
   float lora_scale;      // already rounded to the activation dtype
-  int act;               // mlxq_activation
+  int act;               // FusedAct
+  const uint16_t* act_table;  // [65536] bf16 table of act (act_table_ptr), null when act is none
+};
+
+// The elementwise epilogue of a linear on an already computed product y_in [M, N]: bias, LoRA
+// residual and activation with each stage rounded to its promoted dtype (the *_bf16 flags), the
+// result written to y_out (may alias y_in when both have the same dtype).
+struct LinearEpilogueArgs {
+  const void* y_in = nullptr;
+  bool y_in_bf16 = true;
+  void* y_out = nullptr;
+  bool y_out_bf16 = true;
+  int64_t M = 0, N = 0;
+  const void* bias = nullptr;  // [N]
+  bool bias_bf16 = true;
+  bool d1_bf16 = true;         // y + bias rounds to bf16
+  const void* xa = nullptr;    // [M, R] x . A, already rounded to DR
+  const void* lbt = nullptr;   // [N, R] B^T
+  int R = 0;                   // padded rank, 0 = no LoRA
+  bool dr_bf16 = true;         // xa / lbt stored as bf16, r rounded to bf16
+  float lora_scale = 1.0f;     // already cast to DR
+  bool d2_bf16 = true;         // y + r rounds to bf16
+  int act = 0;                 // mlxq_activation
+  const uint16_t* act_table = nullptr;  // bf16 table of act when the activation runs in bf16
 };
 
 // A stacked launch over `count` matrices of the same shape (the experts of an [E, out, ...] pack):
@@ -31,6 +62,7 @@ int run_quantize(const void* w, int dtype, int64_t N, int64_t K, int gs, int bit
                  void* s, void* b, hipStream_t st);
 int run_dequantize(const uint32_t* wq, const void* s, const void* b, int dtype, int64_t N, int64_t K,
                    int gs, int bits, void* out, hipStream_t st);
+// Exact-f32-dequant product; y in promote(x_dtype, sb_dtype).
 int run_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
             const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st);
 int run_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
@@ -57,10 +89,14 @@ int run_swiglu_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq_g, co
 int run_embedding(const int32_t* ids, int64_t T, const uint32_t* wq, const void* s, const void* b,
                   int sb_dtype, int64_t vocab, int64_t hidden, int gs, int bits, void* out,
                   int out_dtype, hipStream_t st);
+// x.A and B^T for a LoRA residual in DR = promote(x_dtype, lora_dtype): bf16 arrays when both
+// are bf16, else f32 arrays (x and the factors widened exactly).
 int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* A, const void* B,
-                  int64_t N, int rank, int R, void* xa, void* lbt, hipStream_t st);
+                  int lora_dtype, int64_t N, int rank, int R, void* xa, void* lbt, hipStream_t st);
 int run_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, hipStream_t st);
-int run_linear_epilogue(void* y, int x_dtype, int64_t M, int64_t N, const void* bias, const void* xa,
-                        const void* lbt, int R, float lora_scale, int act, hipStream_t st);
+int run_linear_epilogue(const LinearEpilogueArgs& a, hipStream_t st);
+// Device address of the bf16 table of a FusedAct (filled on the device's first request), or
+// null with the error set.
+const uint16_t* act_table_ptr(int fused_act, hipStream_t st);
 
 }  // namespace mlxq

@@ -1,6 +1,7 @@
 // noalloc.hip — mlxq_linear_noalloc: the fused linear forward with its LoRA staging buffers in a
 // static device array instead of a caller workspace, for callers that cannot allocate device
-// memory.
+// memory.  A promoted result (a bf16 product with an f32 bias, f32 LoRA factors or the f32 GELU)
+// also stages the bf16 product [M, N] there.
 //
 // The array is a file-scope __device__ object, so every GPU the library runs on holds its own
 // copy (MLXQ_NOALLOC_SCRATCH_BYTES) from the first call on that GPU until the process ends.  In
@@ -8,8 +9,8 @@
 // with hipGetSymbolAddress (with that device current) and only that address is ever handed to
 // kernels.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two
 // streams, two threads) race on it.  Nothing in the array needs to start at zero: the LoRA
-// preparation writes every byte the GEMM epilogue later reads (x.A and B^T zero-padded to the
-// padded rank) before it is read, on the call's own stream.
+// preparation writes every byte the epilogues later read (x.A and B^T zero-padded to the padded
+// rank), and the product is written in full before it is read, all on the call's own stream.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -55,14 +56,12 @@ extern "C" int mlxq_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_
                                    const uint32_t* wq, const void* scales, const void* biases,
                                    int sb_dtype, int64_t N, int group_size, int bits,
                                    const mlxq_epilogue* epilogue, void* y, void* stream) {
-  const int64_t rank = epilogue ? epilogue->lora_rank : 0;
-  const size_t need = (rank > 0 && rank <= 256) ? mlxq_linear_workspace_size(M, N, rank) : 0;
+  const size_t need = mlxq_linear_workspace_size(x_dtype, sb_dtype, M, N, epilogue);
   if (need > (size_t)MLXQ_NOALLOC_SCRATCH_BYTES)
     return set_error(MLXQ_EINVAL,
-                     "linear_noalloc: M=%lld N=%lld rank=%lld needs %zu bytes of scratch, more than "
-                     "the %zu-byte static buffer (use mlxq_linear with a workspace)",
-                     (long long)M, (long long)N, (long long)rank, need,
-                     (size_t)MLXQ_NOALLOC_SCRATCH_BYTES);
+                     "linear_noalloc: M=%lld N=%lld needs %zu bytes of scratch, more than the "
+                     "%zu-byte static buffer (use mlxq_linear with a workspace)",
+                     (long long)M, (long long)N, need, (size_t)MLXQ_NOALLOC_SCRATCH_BYTES);
   void* ws = nullptr;
   if (need > 0) {
     const int rc = scratch_address(&ws);

@@ -232,8 +232,8 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
           float o = round_bf16(acc[i][j][v]);
           if (epi.bias) o = round_bf16(o + bn);
           if (lora) o = round_bf16(o + round_bf16(round_bf16(r[v]) * epi.lora_scale));
-          if constexpr (EPI - 1 == MLXQ_ACT_GELU) o = gelu_erf(o);
-          else if constexpr (EPI - 1 == MLXQ_ACT_GELU_TANH) o = gelu_tanh<true>(o);
+          // o is bf16 here: the activation is the bf16 table's entry for it.
+          if constexpr (EPI >= 2) o = bf16_bits_to_f32(epi.act_table[f32_to_bf16_bits(o)]);
           if (n_ok && m < M) y[m * N + n] = f32_to_bf16_bits(o);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -250,8 +250,9 @@ static int launch_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, c
   if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm: problem too large");
   if (epi.rank16 != 0 && epi.rank16 != 16)
     return set_error(MLXQ_EINVAL, "qmm: the fused epilogue takes LoRA rank <= 16");
-  const bool fused = epi.bias || epi.rank16 || epi.act != MLXQ_ACT_NONE;
+  const bool fused = epi.bias || epi.rank16 || epi.act != kFusedActNone;
   const int kind = fused ? 1 + epi.act : 0;
+  if (kind >= 2 && epi.act_table == nullptr) return set_error(MLXQ_EINVAL, "qmm: activation table missing");
 #define MLXQ_QL(E)                                                                                \
   hipLaunchKernelGGL((qmm_kernel<SB, BITS, GS, BM, BN, E>), dim3((unsigned)tiles), dim3(256), 0, st, \
                      (const uint16_t*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (uint16_t*)y, epi)

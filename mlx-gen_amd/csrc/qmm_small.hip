@@ -45,7 +45,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
     const SB* __restrict__ scales, const SB* __restrict__ biases, int64_t N,
     uint16_t* __restrict__ y, QmmEpilogue epi) {
   constexpr bool FUSED = EPI != 0;
-  constexpr int ACT = FUSED ? EPI - 1 : MLXQ_ACT_NONE;
+  constexpr int ACT = FUSED ? EPI - 1 : kFusedActNone;
   constexpr int WPL = BITS;  // packed words per lane per sub-tile per K step
   // One LDS object (a second one makes the compiler wait for every direct-to-LDS load before
   // any LDS read): per wave 16 KB — its 2-stage activation ring [stage][64 rows][128 B] during
@@ -294,12 +294,9 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
         epilogue_bias_lora2(o0, o1, epi.bias != nullptr, b0, b1, lora, r[e], r[e + 1], epi.lora_scale);
         v[e] = o0;
         v[e + 1] = o1;
-        if constexpr (ACT == MLXQ_ACT_GELU) {
-          v[e] = gelu_erf(v[e]);
-          v[e + 1] = gelu_erf(v[e + 1]);
-        } else if constexpr (ACT == MLXQ_ACT_GELU_TANH) {
-          v[e] = gelu_tanh<true>(v[e]);
-          v[e + 1] = gelu_tanh<true>(v[e + 1]);
+        if constexpr (ACT != kFusedActNone) {  // bf16 values: the table's entries for them
+          v[e] = bf16_bits_to_f32(epi.act_table[f32_to_bf16_bits(v[e])]);
+          v[e + 1] = bf16_bits_to_f32(epi.act_table[f32_to_bf16_bits(v[e + 1])]);
         }
       }
   }
@@ -325,9 +322,10 @@ template <typename SB, int BITS, int GS>
 static int launch_small(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                         const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st) {
   const int64_t tiles = ((M + kTile - 1) / kTile) * ((N + kTile - 1) / kTile);
-  const bool fused = epi.bias || epi.rank16 || epi.act != MLXQ_ACT_NONE;
+  const bool fused = epi.bias || epi.rank16 || epi.act != kFusedActNone;
   const int kind = fused ? 1 + epi.act : 0;
   if (kind > 3) return set_error(MLXQ_EINVAL, "qmm: unknown activation %d", epi.act);
+  if (kind >= 2 && epi.act_table == nullptr) return set_error(MLXQ_EINVAL, "qmm: activation table missing");
   // bf16 scales with whole blocks of 8 groups are staged in LDS (16-byte aligned row blocks).
   const bool szs = std::is_same<SB, uint16_t>::value && (K / GS) % 8 == 0;
 #define MLXQ_SL(E, Z)                                                                                 \

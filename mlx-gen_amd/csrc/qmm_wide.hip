@@ -44,15 +44,41 @@ constexpr int kGroupM = 4;
 constexpr int kStages = 4;  // activation LDS ring depth (power of two)
 constexpr int kBufferFlags = 0x00020000;  // raw buffer resource word 3 for gfx9-family loads
 
-// GELU tables: entry h is the bf16 result of the epilogue's exact-erf ([0]) and tanh ([1])
-// GELU for the bf16 input with bits h.  Filled once per device by act_table_kernel.
+// GELU tables: entry h is the bf16 result of the dtype-preserving exact GELU ([0], reference
+// src/nn.rs:344-355) and tanh GELU ([1], src/nn.rs:321-329) for the bf16 input with bits h,
+// each evaluated as the reference's separate bf16 ops: every op computed in f32 and its result
+// rounded to bf16, the constants cast to bf16 first.  The f32 value of each op is taken as the
+// correctly rounded one: the op is evaluated in double (erf and tanh to within an ulp of double)
+// and rounded to float, which for + - * / of two floats is the correctly rounded float result.
+// Filled once per device by act_table_kernel.
 __device__ uint16_t g_act_table[2][65536];
+
+__device__ __forceinline__ float bf16_op(double v) { return round_bf16((float)v); }
 
 __global__ __launch_bounds__(256) void act_table_kernel() {
   const int h = blockIdx.x * 256 + threadIdx.x;
-  const float v = bf16_bits_to_f32((uint32_t)h);
-  g_act_table[0][h] = f32_to_bf16_bits(gelu_erf(v));
-  g_act_table[1][h] = f32_to_bf16_bits(gelu_tanh<true>(v));
+  const float x = bf16_bits_to_f32((uint32_t)h);
+  const double xd = (double)x;
+  {  // gelu_exact: inner = erf(x / sqrt2); gate = 1 + inner; (x * gate) / 2
+    const float sqrt2 = round_bf16(1.41421356237309515f);
+    const float t1 = bf16_op(xd / (double)sqrt2);
+    const float t2 = bf16_op(erf((double)t1));
+    const float t3 = bf16_op(1.0 + (double)t2);
+    const float t4 = bf16_op(xd * (double)t3);
+    g_act_table[0][h] = f32_to_bf16_bits(bf16_op((double)t4 / 2.0));
+  }
+  {  // gelu_tanh: x3 = x^3; inner = (x + x3 * k) * c; gate = tanh(inner) + 1; (x * 0.5) * gate
+    const float c = round_bf16(0.7978845608028654f);
+    const float k = round_bf16(0.044715f);
+    const float x3 = bf16_op(xd * xd * xd);  // exact in double: 3 x 8 significant bits
+    const float t1 = bf16_op((double)x3 * (double)k);
+    const float t2 = bf16_op(xd + (double)t1);
+    const float inner = bf16_op((double)t2 * (double)c);
+    const float th = bf16_op(tanh((double)inner));
+    const float gate = bf16_op((double)th + 1.0);
+    const float xh = bf16_op(xd * 0.5);
+    g_act_table[1][h] = f32_to_bf16_bits(bf16_op((double)xh * (double)gate));
+  }
 }
 
 }  // namespace
@@ -127,7 +153,7 @@ __device__ __forceinline__ uint32_t opaque_copy(uint32_t v) {
 }  // namespace
 
 // EPI selects the epilogue at compile time: 0 plain y = bf16(acc); 1 bias / rank-16 LoRA; 2 and 3
-// the same followed by the exact-erf or the tanh GELU (EPI - 1 is the mlxq_activation).  One
+// the same followed by the bf16 exact or tanh GELU (EPI - 1 is the FusedAct).  One
 // epilogue per instantiation keeps it small enough that the accumulator tile stays in registers.
 // SZL: bf16 scales/biases staged through LDS in 8-group blocks (needs K / GS % 8 == 0 and both
 // arrays within 4 GiB of each other); otherwise every K step loads them into registers.
@@ -137,7 +163,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     const SB* __restrict__ scales, const SB* __restrict__ biases, int64_t N,
     uint16_t* __restrict__ y, QmmEpilogue epi, QmmBatch bat) {
   constexpr bool FUSED = EPI != 0;
-  constexpr int ACT = FUSED ? EPI - 1 : MLXQ_ACT_NONE;
+  constexpr int ACT = FUSED ? EPI - 1 : kFusedActNone;
   constexpr int NT = WAVES * 64;
   constexpr int TMW = BM / 32;           // m sub-tiles per wave (all BM rows)
   constexpr int TNW = BN / WAVES / 32;  // n sub-tiles per wave
@@ -505,7 +531,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   // now idle activation ring while the first pass rounds and adds into the accumulators, and a
   // second pass looks up and stores.  Evaluating the exact-erf GELU cost ~20 VALU ops per output
   // with the MFMA idle (~15 k cycles per 224x256 tile).
-  constexpr bool TABLE = ACT != MLXQ_ACT_NONE;
+  constexpr bool TABLE = ACT != kFusedActNone;
   // Output rows go out through LDS when N % 8 == 0: the tile is written to LDS row-major (pitch
   // 528 bytes, so the 32 rows of a lane group fall on different banks) and stored with 16 bytes
   // per lane, two whole 512-byte rows per instruction, instead of 8-byte pieces of 32 rows —
@@ -652,7 +678,7 @@ template <typename SB, int BITS, int GS, int WAVES, int BM, bool SZL, int BN>
 static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                          const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st,
                          int64_t tiles, const QmmBatch& bat) {
-  const bool fused = epi.bias || epi.rank16 || epi.act != MLXQ_ACT_NONE;
+  const bool fused = epi.bias || epi.rank16 || epi.act != kFusedActNone;
   const int kind = fused ? 1 + epi.act : 0;
   if (kind >= 2) {
     const int rc = ensure_act_table(st);
@@ -675,8 +701,11 @@ static int launch_wide_w(const void* x, int64_t M, int64_t K, const uint32_t* wq
 
 // The GELU tables are filled on a device's first GELU launch and the host waits for that fill
 // once, so later launches on any stream find them complete.  Under graph capture (no waiting
-// possible) the fill is captured ahead of the GEMM instead and the device stays unmarked.
+// possible) the fill is captured ahead of the GEMM instead and the device stays unmarked.  Two
+// threads making a device's first GELU call at once may both fill the tables; both write the
+// same values, so either order leaves them correct.
 static std::atomic<int> g_act_table_ready[64];
+static std::atomic<uintptr_t> g_act_table_addr[64];
 
 static int ensure_act_table(hipStream_t st) {
   int dev = 0;
@@ -694,18 +723,42 @@ static int ensure_act_table(hipStream_t st) {
   return MLXQ_OK;
 }
 
+const uint16_t* act_table_ptr(int fused_act, hipStream_t st) {
+  if (fused_act != kFusedActGeluExact && fused_act != kFusedActGeluTanh) {
+    set_error(MLXQ_EINVAL, "act table: activation %d has no bf16 table", fused_act);
+    return nullptr;
+  }
+  if (ensure_act_table(st) != MLXQ_OK) return nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error(MLXQ_EDEVICE, "act table: no usable current device");
+    return nullptr;
+  }
+  uintptr_t a = g_act_table_addr[dev].load(std::memory_order_acquire);
+  if (a == 0) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_act_table)) != hipSuccess || p == nullptr) {
+      set_error(MLXQ_EDEVICE, "act table: hipGetSymbolAddress failed");
+      return nullptr;
+    }
+    a = (uintptr_t)p;
+    g_act_table_addr[dev].store(a, std::memory_order_release);
+  }
+  return reinterpret_cast<const uint16_t*>(a) + (fused_act == kFusedActGeluExact ? 0 : 65536);
+}
+
 // Workgroups that run at once: one per CU (the kernel's LDS and registers allow no second).
 static int64_t resident_workgroups() {
-  static int cached[64] = {};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] <= 0) {
-    int cus = 0;
+  int cus = cached[dev].load(std::memory_order_relaxed);
+  if (cus <= 0) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
       cus = 256;
-    cached[dev] = cus;
+    cached[dev].store(cus, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return cus;
 }
 
 // Tile height for a problem.  A launch takes ceil(tiles / CUs) rounds (one workgroup per CU).

@@ -10,6 +10,8 @@
 // over K in 32-element chunks (16 B of Q4 codes / 32 B of Q8 codes per row per chunk), each chunk
 // inside a single group (group_size >= 32).  Lane partial sums are reduced across the wave at
 // the end.  x (M rows) is re-read per chunk from L1/L2 and shared by the ROWS weight rows.
+#include <type_traits>
+
 #include "mlxq_common.h"
 
 namespace mlxq {
@@ -64,12 +66,16 @@ __device__ __forceinline__ float dot_chunk(const uint32_t (&w)[BITS], const floa
   return acc;
 }
 
+// The result dtype is MLX's promote(x, scales): bf16 only when both are bf16.
+template <typename XT, typename SB>
+using QmvOut = typename std::conditional<sizeof(XT) == 2 && sizeof(SB) == 2, uint16_t, float>::type;
+
 template <typename XT, typename SB, int BITS, int GS, int MR, int ROWS>
 __global__ __launch_bounds__(256) void qmv_kernel(const XT* __restrict__ x, int M, int64_t K,
                                                   const uint32_t* __restrict__ wq,
                                                   const SB* __restrict__ scales,
                                                   const SB* __restrict__ biases, int64_t N,
-                                                  XT* __restrict__ y) {
+                                                  QmvOut<XT, SB>* __restrict__ y) {
   constexpr int WPC = BITS;  // uint32 words per 32-element chunk: 4 (Q4) or 8 (Q8)
   const int lane = threadIdx.x & 63;
   const int64_t n0 = ((int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * ROWS;
@@ -135,7 +141,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const XT* __restrict__ x, int 
     for (int r = 0; r < ROWS; ++r)
 #pragma unroll
       for (int m = 0; m < MR; ++m)
-        if (n0 + r < N && m0 + m < M) Act<XT>::st(y, (int64_t)(m0 + m) * N + n0 + r, acc[r][m]);
+        if (n0 + r < N && m0 + m < M) Act<QmvOut<XT, SB>>::st(y, (int64_t)(m0 + m) * N + n0 + r, acc[r][m]);
   }
 }
 
@@ -150,7 +156,7 @@ static int launch_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq, c
   if (gy > 65535) return set_error(MLXQ_EINVAL, "qmv: M=%lld too large for the f32 kernel", (long long)M);
   hipLaunchKernelGGL((qmv_kernel<XT, SB, BITS, GS, MR, ROWS>), dim3((unsigned)gx, (unsigned)gy),
                      dim3(256), 0, st, (const XT*)x, (int)M, K, wq, (const SB*)s, (const SB*)b, N,
-                     (XT*)y);
+                     (QmvOut<XT, SB>*)y);
   return check_launch("qmv");
 }
 

@@ -31,10 +31,48 @@ void need_packed(const Array& wq, const char* op) {
   if (wq.ndim() != 2) throw Error(MLXQ_EINVAL, std::string(op) + ": packed weights must be 2-D");
 }
 
-// Workspace for mlxq_linear / mlxq_lora_residual (nullptr-free empty array when none is needed).
-Array workspace(int64_t M, int64_t N, int64_t rank) {
-  const size_t need = mlxq_linear_workspace_size(M, N, rank);
-  return Array::empty({(int64_t)((need + 3) / 4)}, Dtype::Uint32);
+Dtype from_abi(int dt) { return dt == MLXQ_BFLOAT16 ? Dtype::Bfloat16 : Dtype::Float32; }
+
+// MLX's result type over float operands: bf16 only when both are bf16.
+Dtype promote(Dtype a, Dtype b) {
+  return a == Dtype::Bfloat16 && b == Dtype::Bfloat16 ? Dtype::Bfloat16 : Dtype::Float32;
+}
+
+// The packed triple against x's width K, as MLX's quantized_matmul checks it
+// (extract_quantized_matmul_dims): wq [..., N, K*bits/32], scales/biases [..., N, K/gs] alike.
+// `lead` leading dimensions (the expert axis of a stack) must match too.  Returns N.
+int64_t check_pack(const char* op, const Array& wq, const Array& scales, const Array& biases,
+                   int64_t K, int group_size, int bits, int lead = 0) {
+  const std::string o(op);
+  if (bits != 4 && bits != 8) throw Error(MLXQ_EINVAL, o + ": bits must be 4 or 8");
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    throw Error(MLXQ_EINVAL, o + ": group_size must be 32, 64 or 128");
+  if (wq.dtype() != Dtype::Uint32 && wq.dtype() != Dtype::Int32)
+    throw Error(MLXQ_EINVAL, o + ": packed weights must be uint32");
+  const int nd = lead + 2;
+  if (wq.ndim() != nd || scales.ndim() != nd || biases.ndim() != nd)
+    throw Error(MLXQ_EINVAL, o + ": wq, scales and biases must be " + std::to_string(nd) + "-D");
+  for (int i = 0; i < lead; ++i)
+    if (scales.dim(i) != wq.dim(i) || biases.dim(i) != wq.dim(i))
+      throw Error(MLXQ_EINVAL, o + ": stacked operands disagree on their leading dimensions");
+  const int64_t N = wq.dim(lead);
+  if (K % group_size != 0) throw Error(MLXQ_EINVAL, o + ": K is not a multiple of group_size");
+  if (wq.dim(lead + 1) * 32 != K * bits)
+    throw Error(MLXQ_EINVAL, o + ": wq has " + std::to_string(wq.dim(lead + 1)) +
+                                 " words per row, which does not pack x's K=" + std::to_string(K));
+  if (scales.dim(lead) != N || scales.dim(lead + 1) != K / group_size || biases.shape() != scales.shape())
+    throw Error(MLXQ_EINVAL, o + ": scales/biases must be [N, K/group_size]");
+  abi_dtype(scales.dtype(), op);
+  if (biases.dtype() != scales.dtype()) throw Error(MLXQ_EINVAL, o + ": biases and scales dtypes differ");
+  return N;
+}
+
+// The layer's reusable workspace grown to `need` bytes (empty array when none is needed).  It
+// stays allocated with the layer, so forward calls after the first allocate nothing.
+Array& grow_workspace(std::shared_ptr<Array>& ws, size_t need) {
+  if (!ws) ws = std::make_shared<Array>();
+  if (ws->nbytes() < need) *ws = Array::empty({(int64_t)((need + 3) / 4)}, Dtype::Uint32);
+  return *ws;
 }
 
 }  // namespace
@@ -159,8 +197,9 @@ Packed quantize(const Array& w, int group_size, int bits, hipStream_t s) {
 Array dequantize(const Array& wq, const Array& scales, const Array& biases, int group_size, int bits,
                  hipStream_t s) {
   need_packed(wq, "dequantize");
-  if (bits <= 0) throw Error(MLXQ_EINVAL, "dequantize: bits must be 4 or 8");
-  const int64_t N = wq.dim(0), K = wq.dim(1) * 32 / bits;
+  if (bits != 4 && bits != 8) throw Error(MLXQ_EINVAL, "dequantize: bits must be 4 or 8");
+  const int64_t K = wq.dim(1) * 32 / bits;
+  const int64_t N = check_pack("dequantize", wq, scales, biases, K, group_size, bits);
   Array out = Array::empty({N, K}, scales.dtype());
   check(mlxq_dequantize((const uint32_t*)wq.data(), scales.data(), biases.data(),
                         abi_dtype(scales.dtype(), "dequantize"), N, K, group_size, bits, out.data(), s));
@@ -171,10 +210,12 @@ Array quantized_matmul(const Array& x, const Array& wq, const Array& scales, con
                        bool transpose, int group_size, int bits, hipStream_t s) {
   need_packed(wq, "quantized_matmul");
   if (x.ndim() < 1) throw Error(MLXQ_EINVAL, "quantized_matmul: x must have a last dimension");
-  const int64_t K = x.dim(-1), N = wq.dim(0), M = K > 0 ? x.size() / K : 0;
+  abi_dtype(x.dtype(), "quantized_matmul");
+  const int64_t K = x.dim(-1), M = K > 0 ? x.size() / K : 0;
+  const int64_t N = check_pack("quantized_matmul", wq, scales, biases, K, group_size, bits);
   std::vector<int64_t> shape = x.shape();
   shape.back() = N;
-  Array y = Array::empty(shape, x.dtype());
+  Array y = Array::empty(shape, promote(x.dtype(), scales.dtype()));
   check(mlxq_quantized_matmul(x.data(), abi_dtype(x.dtype(), "quantized_matmul"), M, K,
                               (const uint32_t*)wq.data(), scales.data(), biases.data(),
                               abi_dtype(scales.dtype(), "quantized_matmul"), N, transpose ? 1 : 0,
@@ -194,12 +235,15 @@ Array swiglu(const Array& x, const QuantizedLinear& gate, const QuantizedLinear&
   need_packed(up.weight, "swiglu");
   if (gate.bias || up.bias) throw Error(MLXQ_EUNSUPPORTED, "swiglu: projections with a dense bias");
   if (gate.group_size != up.group_size || gate.bits != up.bits ||
-      gate.weight.shape() != up.weight.shape() || x.ndim() < 1 || x.dim(-1) != gate.in_features())
+      gate.weight.shape() != up.weight.shape() || x.ndim() < 1 || x.dim(-1) != gate.in_features() ||
+      gate.scales.dtype() != up.scales.dtype())
     throw Error(MLXQ_EINVAL, "swiglu: gate and up must be packed alike and match x");
-  const int64_t K = x.dim(-1), F = gate.weight.dim(0), M = K > 0 ? x.size() / K : 0;
+  const int64_t K = x.dim(-1), M = K > 0 ? x.size() / K : 0;
+  const int64_t F = check_pack("swiglu", gate.weight, gate.scales, gate.biases, K, gate.group_size, gate.bits);
+  check_pack("swiglu", up.weight, up.scales, up.biases, K, up.group_size, up.bits);
   std::vector<int64_t> shape = x.shape();
   shape.back() = F;
-  Array h = Array::empty(shape, x.dtype());
+  Array h = Array::empty(shape, promote(x.dtype(), gate.scales.dtype()));
   check(mlxq_swiglu(x.data(), abi_dtype(x.dtype(), "swiglu"), M, K,
                     (const uint32_t*)gate.weight.data(), gate.scales.data(), gate.biases.data(),
                     (const uint32_t*)up.weight.data(), up.scales.data(), up.biases.data(),
@@ -221,7 +265,10 @@ Array StackedExperts::forward(const Array& x, bool per_expert, hipStream_t s) co
     throw Error(MLXQ_EINVAL, "experts: weight must hold packed uint32 codes");
   if (weight.ndim() != 3 || scales.ndim() != 3 || x.ndim() < 1)
     throw Error(MLXQ_EINVAL, "experts: expected [E, out, ...] stacks");
-  const int64_t E = num_experts(), N = weight.dim(1), K = x.dim(-1);
+  const int64_t E = num_experts(), K = x.dim(-1);
+  const int64_t N = check_pack("experts", weight, scales, biases, K, group_size, bits, 1);
+  if (bias && (bias->ndim() != 2 || bias->dim(0) != E || bias->dim(1) != N))
+    throw Error(MLXQ_EINVAL, "experts: bias must be [E, out]");
   std::vector<int64_t> lead(x.shape().begin() + (per_expert ? 1 : 0), x.shape().end() - 1);
   if (per_expert && (x.ndim() < 2 || x.dim(0) != E))
     throw Error(MLXQ_EINVAL, "experts: per-expert x must lead with E");
@@ -230,12 +277,13 @@ Array StackedExperts::forward(const Array& x, bool per_expert, hipStream_t s) co
   std::vector<int64_t> shape = {E};
   shape.insert(shape.end(), lead.begin(), lead.end());
   shape.push_back(N);
-  Array y = Array::empty(shape, x.dtype());
-  std::optional<Array> b;
-  if (bias) b = as_dtype(*bias, x.dtype(), s);
+  Dtype ydt = promote(x.dtype(), scales.dtype());
+  if (bias) ydt = promote(ydt, bias->dtype());
+  Array y = Array::empty(shape, ydt);
   check(mlxq_qmm_experts(x.data(), abi_dtype(x.dtype(), "experts"), per_expert ? 1 : 0, E, M, K,
                          (const uint32_t*)weight.data(), scales.data(), biases.data(),
-                         abi_dtype(scales.dtype(), "experts"), b ? b->data() : nullptr, N, group_size,
+                         abi_dtype(scales.dtype(), "experts"), bias ? bias->data() : nullptr,
+                         bias ? abi_dtype(bias->dtype(), "experts") : MLXQ_BFLOAT16, N, group_size,
                          bits, y.data(), s));
   return y;
 }
@@ -249,17 +297,57 @@ QuantizedLinear QuantizedLinear::try_from_linear(const Array& weight, std::optio
 }
 
 Array QuantizedLinear::forward(const Array& x, hipStream_t s) const {
-  if (!bias) return quantized_matmul(x, weight, scales, biases, true, group_size, bits, s);
-  // src/adapters.rs:309-320: quantized_matmul, then the dense bias as a separate, rounded add.
-  const Array b = as_dtype(*bias, x.dtype(), s);
-  const int64_t K = x.dim(-1), N = weight.dim(0), M = K > 0 ? x.size() / K : 0;
+  return forward_fused(x, nullptr, MLXQ_ACT_NONE, s);
+}
+
+namespace {
+// `out` when given (checked against the result's shape and dtype), else a new array.
+Array output_array(const Array* out, const std::vector<int64_t>& shape, Dtype dt, const char* op) {
+  if (!out) return Array::empty(shape, dt);
+  if (out->shape() != shape || out->dtype() != dt)
+    throw Error(MLXQ_EINVAL, std::string(op) + ": out has the wrong shape or dtype (want " +
+                                 dtype_name(dt) + ")");
+  return *out;
+}
+}  // namespace
+
+Array QuantizedLinear::forward_fused(const Array& x, const Adapter* lora, int activation,
+                                     hipStream_t s, const Array* out) const {
+  // src/adapters.rs:309-320,543-549: quantized_matmul, then the dense bias and the adapter's
+  // residual as separate adds, each in its promoted dtype (bias and factors keep theirs).
+  if (x.ndim() < 1) throw Error(MLXQ_EINVAL, "linear: x must have a last dimension");
+  const int xdt = abi_dtype(x.dtype(), "linear");
+  const int64_t K = x.dim(-1), M = K > 0 ? x.size() / K : 0;
+  const int64_t N = check_pack("linear", weight, scales, biases, K, group_size, bits);
+  mlxq_epilogue e = {};
+  e.lora_scale = 1.0f;
+  e.activation = activation;
+  e.bias_dtype = e.lora_dtype = xdt;
+  if (bias) {
+    if (bias->ndim() != 1 || bias->dim(0) != N) throw Error(MLXQ_EINVAL, "linear: bias must be [out]");
+    e.bias = bias->data();
+    e.bias_dtype = abi_dtype(bias->dtype(), "linear");
+  }
+  if (lora) {
+    if (lora->a.ndim() != 2 || lora->b.ndim() != 2 || lora->a.dim(0) != K || lora->b.dim(1) != N ||
+        lora->a.dim(1) != lora->b.dim(0) || lora->a.dtype() != lora->b.dtype())
+      throw Error(MLXQ_EINVAL, "linear: LoRA factors must be A [in, r] and B [r, out] of one dtype");
+    e.lora_a = lora->a.data();
+    e.lora_b = lora->b.data();
+    e.lora_rank = lora->a.dim(1);
+    e.lora_scale = lora->scale;
+    e.lora_dtype = abi_dtype(lora->a.dtype(), "linear");
+  }
+  const int sdt = abi_dtype(scales.dtype(), "linear");
+  const int ydt = mlxq_linear_out_dtype(xdt, sdt, &e);
+  if (ydt < 0) throw Error(MLXQ_EINVAL, mlxq_last_error());
   std::vector<int64_t> shape = x.shape();
   shape.back() = N;
-  Array y = Array::empty(shape, x.dtype());
-  mlxq_epilogue e = {b.data(), nullptr, nullptr, 0, 1.0f, MLXQ_ACT_NONE};
-  check(mlxq_linear(x.data(), abi_dtype(x.dtype(), "linear"), M, K, (const uint32_t*)weight.data(),
-                    scales.data(), biases.data(), abi_dtype(scales.dtype(), "linear"), N, group_size,
-                    bits, &e, y.data(), nullptr, 0, s));
+  Array y = output_array(out, shape, from_abi(ydt), "linear");
+  Array& ws = grow_workspace(workspace_, mlxq_linear_workspace_size(xdt, sdt, M, N, &e));
+  check(mlxq_linear(x.data(), xdt, M, K, (const uint32_t*)weight.data(), scales.data(), biases.data(),
+                    sdt, N, group_size, bits, &e, y.data(), ws.nbytes() ? ws.data() : nullptr,
+                    ws.nbytes(), s));
   return y;
 }
 
@@ -294,38 +382,65 @@ void AdaptableLinear::quantize(int bits, std::optional<int> group_size, hipStrea
   dense_bias_.reset();
 }
 
-Array AdaptableLinear::forward(const Array& x, hipStream_t s) const {
+Array AdaptableLinear::forward(const Array& x, hipStream_t s) const { return forward_impl(x, nullptr, s); }
+
+void AdaptableLinear::forward_into(const Array& x, const Array& out, hipStream_t s) const {
+  forward_impl(x, &out, s);
+}
+
+Dtype AdaptableLinear::out_dtype(Dtype x_dtype) const {
+  if (!quantized_) throw Error(MLXQ_EUNSUPPORTED, "AdaptableLinear: the dense base is not on the quantized path");
+  const QuantizedLinear& q = *quantized_;
+  Dtype d = promote(x_dtype, q.scales.dtype());
+  if (q.bias) d = promote(d, q.bias->dtype());
+  for (const Adapter& ad : adapters_) d = promote(d, promote(x_dtype, ad.a.dtype()));
+  return d;
+}
+
+Array AdaptableLinear::forward_impl(const Array& x, const Array* out_arg, hipStream_t s) const {
   if (!quantized_)
     throw Error(MLXQ_EUNSUPPORTED,
                 "AdaptableLinear: the dense base is not on the quantized path; call quantize() first");
   const QuantizedLinear& q = *quantized_;
-  if (adapters_.empty()) return q.forward(x, s);
+  for (const Adapter& ad : adapters_)
+    if (ad.a.ndim() != 2 || ad.a.dim(1) > 256)
+      throw Error(MLXQ_EUNSUPPORTED, "AdaptableLinear: LoRA rank above 256");
+  if (adapters_.empty()) return q.forward_fused(x, nullptr, MLXQ_ACT_NONE, s, out_arg);
+  // The first adapter rides in mlxq_linear's epilogue, later ones are added one at a time
+  // (out = out + residual, src/adapters.rs:545-547), each sum in MLX's promoted dtype.  Every
+  // workspace is the layer's own (kept between calls), so nothing here waits for the device, and
+  // with a caller's output nothing is allocated after the first call: a result that promotes
+  // from bf16 to f32 part-way down the stack keeps its bf16 part in a layer-owned buffer.
+  const Dtype final_dt = out_dtype(x.dtype());
+  const Array* first_out = out_arg;
+  Array mid;
+  if (out_arg && adapters_.size() > 1) {
+    const Dtype d1 = promote(promote(x.dtype(), q.scales.dtype()),
+                             promote(q.bias ? q.bias->dtype() : x.dtype(), promote(x.dtype(), adapters_[0].a.dtype())));
+    if (d1 != final_dt) {
+      if (!mid_ || mid_->shape() != out_arg->shape() || mid_->dtype() != d1)
+        mid_ = std::make_shared<Array>(Array::empty(out_arg->shape(), d1));
+      mid = *mid_;
+      first_out = &mid;
+    }
+  }
+  Array y = q.forward_fused(x, &adapters_[0], MLXQ_ACT_NONE, s, first_out);
   const int xdt = abi_dtype(x.dtype(), "AdaptableLinear::forward");
   const int64_t K = x.dim(-1), N = q.weight.dim(0), M = K > 0 ? x.size() / K : 0;
-  std::vector<int64_t> shape = x.shape();
-  shape.back() = N;
-  Array y = Array::empty(shape, x.dtype());
-  std::optional<Array> b;
-  if (q.bias) b = as_dtype(*q.bias, x.dtype(), s);
-  // The first adapter rides in mlxq_linear's epilogue, later ones are added one at a time with
-  // the same rounding points (out = out + residual, src/adapters.rs:545-547).
-  for (size_t i = 0; i < adapters_.size(); ++i) {
+  for (size_t i = 1; i < adapters_.size(); ++i) {
     const Adapter& ad = adapters_[i];
+    if (ad.a.ndim() != 2 || ad.b.ndim() != 2 || ad.a.dim(0) != K || ad.b.dim(1) != N ||
+        ad.a.dim(1) != ad.b.dim(0) || ad.a.dtype() != ad.b.dtype())
+      throw Error(MLXQ_EINVAL, "AdaptableLinear: LoRA factors must be A [in, r] and B [r, out] of one dtype");
     const int64_t rank = ad.a.dim(1);
-    if (rank > 256) throw Error(MLXQ_EUNSUPPORTED, "AdaptableLinear: LoRA rank above 256");
-    const Array A = as_dtype(ad.a, x.dtype(), s), B = as_dtype(ad.b, x.dtype(), s);
-    Array ws = workspace(M, N, rank);
-    if (i == 0) {
-      mlxq_epilogue e = {b ? b->data() : nullptr, A.data(), B.data(), rank, ad.scale, MLXQ_ACT_NONE};
-      check(mlxq_linear(x.data(), xdt, M, K, (const uint32_t*)q.weight.data(), q.scales.data(),
-                        q.biases.data(), abi_dtype(q.scales.dtype(), "linear"), N, q.group_size,
-                        q.bits, &e, y.data(), ws.data(), ws.nbytes(), s));
-    } else {
-      check(mlxq_lora_residual(x.data(), xdt, M, K, A.data(), B.data(), N, rank, ad.scale, y.data(),
-                               ws.data(), ws.nbytes(), s));
-    }
-    // The workspace must outlive the kernels that read it.
-    hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    const int ldt = abi_dtype(ad.a.dtype(), "AdaptableLinear::forward");
+    const Dtype odt = promote(y.dtype(), promote(x.dtype(), ad.a.dtype()));
+    Array out = odt == y.dtype() ? y : (out_arg ? *out_arg : Array::empty(y.shape(), odt));
+    Array& ws = grow_workspace(workspace_, mlxq_lora_residual_workspace_size(xdt, ldt, M, N, rank));
+    check(mlxq_lora_residual(x.data(), xdt, M, K, ad.a.data(), ad.b.data(), ldt, N, rank, ad.scale,
+                             y.data(), abi_dtype(y.dtype(), "AdaptableLinear::forward"), out.data(),
+                             ws.data(), ws.nbytes(), s));
+    y = out;
   }
   return y;
 }

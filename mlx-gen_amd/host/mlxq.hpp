@@ -99,14 +99,24 @@ struct Adapter {
 
 struct QuantizedLinear {
   Array weight, scales, biases;  // packed triple (weight in U32)
-  std::optional<Array> bias;     // dense bias
+  std::optional<Array> bias;     // dense bias (its own dtype: an f32 bias promotes, as in MLX)
   int group_size = 64;
   int bits = 4;
 
   static QuantizedLinear try_from_linear(const Array& weight, std::optional<Array> bias,
                                          int group_size, int bits, hipStream_t s = nullptr);
+  // y = x . W^T (+ bias), in MLX's promoted dtype.
   Array forward(const Array& x, hipStream_t s = nullptr) const;
+  // forward with one LoRA adapter and an mlxq_activation fused after it (mlxq_linear); the
+  // result goes to *out when given (shape and dtype checked), else to a new array.
+  Array forward_fused(const Array& x, const Adapter* lora, int activation, hipStream_t s = nullptr,
+                      const Array* out = nullptr) const;
   int64_t in_features() const { return scales.dim(1) * group_size; }
+
+  // Device workspace of mlxq_linear, kept with the layer and grown on demand, so that forward
+  // calls after the first allocate none (last member: aggregate initialisation leaves it empty).
+  // Calls on one layer must be ordered on one stream.
+  mutable std::shared_ptr<Array> workspace_;
 };
 
 class AdaptableLinear {
@@ -122,14 +132,24 @@ class AdaptableLinear {
   std::array<int64_t, 2> base_shape() const;
   // src/adapters.rs:508-541: cast weight and bias to bf16, then pack; no-op when packed.
   void quantize(int bits, std::optional<int> group_size, hipStream_t s = nullptr);
-  // src/adapters.rs:300-322,543-549: base(x) (+ bias) + sum of adapter residuals, every step
-  // rounded to the activation dtype.  The dense base is not on this library's path and throws.
+  // src/adapters.rs:300-322,543-549: base(x) (+ bias) + sum of adapter residuals, each step
+  // rounded to its promoted dtype (bias and factors keep their own dtypes, as in MLX).  The dense
+  // base is not on this library's path and throws.  Workspaces are the layer's own and kept
+  // between calls: calls on one layer must be ordered on one stream.
   Array forward(const Array& x, hipStream_t s = nullptr) const;
+  // forward into a caller's array of shape [..., out] and dtype out_dtype(x.dtype()): after a
+  // first call with the same shapes this allocates nothing and never waits for the device, so it
+  // can be captured into a HIP graph.
+  void forward_into(const Array& x, const Array& out, hipStream_t s = nullptr) const;
+  Dtype out_dtype(Dtype x_dtype) const;
 
  private:
+  Array forward_impl(const Array& x, const Array* out, hipStream_t s) const;
   std::optional<Array> dense_weight_, dense_bias_;
   std::optional<QuantizedLinear> quantized_;
   std::vector<Adapter> adapters_;
+  mutable std::shared_ptr<Array> workspace_;  // mlxq_lora_residual staging, grown on demand
+  mutable std::shared_ptr<Array> mid_;        // a bf16 partial sum before an f32 adapter
 };
 
 class TokenEmbedding {

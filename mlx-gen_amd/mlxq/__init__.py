@@ -5,18 +5,20 @@ Drop-in for mlx-gen's quantized-linear path: the op triple ``quantize`` / ``dequ
 src/adapters.rs) and the ``QuantizedLinear`` / ``AdaptableLinear`` layer surface built on it.
 All compute runs in libmlxq_hip.so (hand-written HIP for gfx950) through its C ABI.
 """
-from ._lib import (MLXQ_ACT_GELU, MLXQ_ACT_GELU_TANH, MLXQ_ACT_NONE, MLXQ_BFLOAT16, MLXQ_FLOAT32,
-                   MlxqError, LIB_PATH, load)
-from .ops import (DEFAULT_GROUP_SIZE, dequantize, embedding, linear, linear_workspace_size,
-                  packed_bits, qmm, qmm_experts, qmv, quantize, quantized_matmul, swiglu)
+from ._lib import (MLXQ_ACT_GELU, MLXQ_ACT_GELU_EXACT, MLXQ_ACT_GELU_TANH, MLXQ_ACT_NONE,
+                   MLXQ_BFLOAT16, MLXQ_FLOAT32, MlxqError, LIB_PATH, load)
+from .ops import (DEFAULT_GROUP_SIZE, dequantize, embedding, linear, linear_out_dtype,
+                  linear_workspace_size, lora_residual, packed_bits, promote, qmm, qmm_experts, qmv,
+                  quantize, quantized_matmul, swiglu)
 from .nn import (Adapter, AdaptableLinear, QuantizedLinear, StackedExperts, TokenEmbedding,
                  has_packed_experts, lin, load_packed_experts, quantize_map)
 from . import io
 
 __all__ = [
-    "MLXQ_ACT_GELU", "MLXQ_ACT_GELU_TANH", "MLXQ_ACT_NONE", "MLXQ_BFLOAT16", "MLXQ_FLOAT32",
-    "MlxqError", "LIB_PATH", "load", "DEFAULT_GROUP_SIZE", "dequantize", "embedding", "linear",
-    "linear_workspace_size", "packed_bits", "qmm", "qmm_experts", "qmv", "quantize",
+    "MLXQ_ACT_GELU", "MLXQ_ACT_GELU_EXACT", "MLXQ_ACT_GELU_TANH", "MLXQ_ACT_NONE", "MLXQ_BFLOAT16",
+    "MLXQ_FLOAT32", "MlxqError", "LIB_PATH", "load", "DEFAULT_GROUP_SIZE", "dequantize", "embedding",
+    "linear", "linear_out_dtype", "linear_workspace_size", "lora_residual", "packed_bits", "promote",
+    "qmm", "qmm_experts", "qmv", "quantize",
     "quantized_matmul", "swiglu", "Adapter", "AdaptableLinear", "QuantizedLinear", "StackedExperts",
     "TokenEmbedding", "has_packed_experts", "lin", "load_packed_experts", "quantize_map", "io",
 ]

@@ -22,6 +22,7 @@ MLXQ_EDEVICE = 3
 MLXQ_ACT_NONE = 0
 MLXQ_ACT_GELU = 1
 MLXQ_ACT_GELU_TANH = 2
+MLXQ_ACT_GELU_EXACT = 3
 
 # Size of the static per-device scratch array behind mlxq_linear_noalloc.
 MLXQ_NOALLOC_SCRATCH_BYTES = 8 << 20
@@ -36,11 +37,13 @@ EXPORTS = (
     "mlxq_qmm",
     "mlxq_qmv",
     "mlxq_linear_workspace_size",
+    "mlxq_linear_out_dtype",
     "mlxq_linear",
     "mlxq_linear_noalloc",
     "mlxq_packed_bits",
     "mlxq_embedding",
     "mlxq_lora_residual",
+    "mlxq_lora_residual_workspace_size",
     "mlxq_cast",
     "mlxq_swiglu",
     "mlxq_qmm_experts",
@@ -63,6 +66,8 @@ class Epilogue(ctypes.Structure):
         ("lora_rank", ctypes.c_int64),
         ("lora_scale", ctypes.c_float),
         ("activation", ctypes.c_int),
+        ("bias_dtype", ctypes.c_int),
+        ("lora_dtype", ctypes.c_int),
     ]
 
 
@@ -92,18 +97,22 @@ def load():
     for name in ("mlxq_qmm", "mlxq_qmv"):
         getattr(lib, name).argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _vp, _int, _i64, _int, _int,
                                        _vp, _vp]
-    lib.mlxq_linear_workspace_size.argtypes = [_i64, _i64, _i64]
+    lib.mlxq_linear_workspace_size.argtypes = [_int, _int, _i64, _i64, ctypes.POINTER(Epilogue)]
     lib.mlxq_linear_workspace_size.restype = ctypes.c_size_t
+    lib.mlxq_linear_out_dtype.argtypes = [_int, _int, ctypes.POINTER(Epilogue)]
+    lib.mlxq_linear_out_dtype.restype = _int
+    lib.mlxq_lora_residual_workspace_size.argtypes = [_int, _int, _i64, _i64, _i64]
+    lib.mlxq_lora_residual_workspace_size.restype = ctypes.c_size_t
     lib.mlxq_linear.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _vp, _int, _i64, _int, _int,
                                 ctypes.POINTER(Epilogue), _vp, _vp, ctypes.c_size_t, _vp]
     lib.mlxq_linear_noalloc.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _vp, _int, _i64, _int,
                                         _int, ctypes.POINTER(Epilogue), _vp, _vp]
     lib.mlxq_packed_bits.argtypes = [_i64, _i64, _int]
-    lib.mlxq_lora_residual.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _i64, _i64, ctypes.c_float,
-                                       _vp, _vp, ctypes.c_size_t, _vp]
+    lib.mlxq_lora_residual.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _int, _i64, _i64,
+                                       ctypes.c_float, _vp, _int, _vp, _vp, ctypes.c_size_t, _vp]
     lib.mlxq_cast.argtypes = [_vp, _int, _vp, _int, _i64, _vp]
-    lib.mlxq_qmm_experts.argtypes = [_vp, _int, _int, _i64, _i64, _i64, _vp, _vp, _vp, _int, _vp, _i64,
-                                     _int, _int, _vp, _vp]
+    lib.mlxq_qmm_experts.argtypes = [_vp, _int, _int, _i64, _i64, _i64, _vp, _vp, _vp, _int, _vp,
+                                     _int, _i64, _int, _int, _vp, _vp]
     lib.mlxq_swiglu.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _int, _i64, _int,
                                 _int, _vp, _vp]
     lib.mlxq_embedding.argtypes = [_vp, _i64, _vp, _vp, _vp, _int, _i64, _i64, _int, _int, _vp, _int,

@@ -19,7 +19,7 @@ from typing import Callable, Dict, List, Optional
 import torch
 
 from . import ops
-from ._lib import MLXQ_ACT_NONE
+from ._lib import MLXQ_ACT_NONE, MLXQ_EUNSUPPORTED, MlxqError
 
 
 @dataclass
@@ -39,12 +39,13 @@ class QuantizedLinear:
         return cls(wq, s, b, bias, group_size, bits)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        # src/adapters.rs:309-320: quantized_matmul, then the dense bias as a separate add.
+        # src/adapters.rs:309-320: quantized_matmul, then the dense bias as a separate add in its
+        # own dtype (an f32 bias promotes a bf16 product to f32, as MLX's add does).
         if self.bias is None:
             return ops.quantized_matmul(x, self.weight, self.scales, self.biases, True,
                                         self.group_size, self.bits)
         return ops.linear(x, self.weight, self.scales, self.biases, self.group_size, self.bits,
-                          bias=self.bias.to(x.dtype))
+                          bias=self.bias)
 
     def in_features(self) -> int:
         # AdaptableLinear::base_shape (src/adapters.rs:491-502): in = scales.cols * group_size.
@@ -53,15 +54,19 @@ class QuantizedLinear:
 
 @dataclass
 class Adapter:
-    """LoRA adapter: residual = scale * (x.A).B, A [in, r], B [r, out] (alpha/rank folded in B)."""
+    """LoRA adapter: residual = scale * (x.A).B, A [in, r], B [r, out] (alpha/rank folded in B),
+    the factors kept in their file dtype (src/adapters.rs:243-252)."""
     a: torch.Tensor
     b: torch.Tensor
     scale: float = 1.0
 
     def residual(self, x: torch.Tensor) -> torch.Tensor:
-        # src/adapters.rs:260-270 — each op in the activation dtype.
-        r = (x @ self.a.to(x.dtype)) @ self.b.to(x.dtype)
-        return r * torch.tensor(self.scale, dtype=r.dtype, device=r.device)
+        """The dense-base arm's residual (src/adapters.rs:260-270): each op in
+        promote(x, factors), the scale cast to that dtype.  Over a quantized base the library
+        applies adapters instead (ops.linear, ops.lora_residual)."""
+        dt = ops.promote(x.dtype, self.a.dtype)
+        r = (x.to(dt) @ self.a.to(dt)) @ self.b.to(dt)
+        return r * torch.tensor(self.scale, dtype=dt, device=r.device)
 
 
 @dataclass
@@ -108,15 +113,22 @@ class AdaptableLinear:
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.quantized is not None:
+            # src/adapters.rs:543-549 over the quantized base, all in the library: the first
+            # adapter rides in mlxq_linear's epilogue, each further one is one mlxq_lora_residual
+            # (out = out + residual, promoted as MLX promotes).  Factors keep their dtype.
             q = self.quantized
-            # Single-LoRA stacks fuse into the library's epilogue with the reference's roundings.
-            if len(self.adapters) == 1 and self.adapters[0].a.shape[1] <= 256:
-                ad = self.adapters[0]
-                return ops.linear(x, q.weight, q.scales, q.biases, q.group_size, q.bits,
-                                  bias=None if q.bias is None else q.bias.to(x.dtype),
-                                  lora_a=ad.a.to(x.dtype), lora_b=ad.b.to(x.dtype),
-                                  lora_scale=ad.scale, activation=MLXQ_ACT_NONE)
-            out = q.forward(x)
+            for ad in self.adapters:
+                if ad.a.shape[1] > 256:
+                    raise MlxqError(MLXQ_EUNSUPPORTED, "AdaptableLinear: LoRA rank above 256")
+            if not self.adapters:
+                return q.forward(x)
+            first = self.adapters[0]
+            out = ops.linear(x, q.weight, q.scales, q.biases, q.group_size, q.bits, bias=q.bias,
+                             lora_a=first.a, lora_b=first.b, lora_scale=first.scale,
+                             activation=MLXQ_ACT_NONE)
+            for ad in self.adapters[1:]:
+                out = ops.lora_residual(x, out, ad.a, ad.b, ad.scale)
+            return out
         else:
             w = self.dense_weight
             if self.dense_bias is not None:

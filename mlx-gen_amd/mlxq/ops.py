@@ -7,9 +7,11 @@ Reference call sites (mlx_rs::ops, MLX 0.31.2 via pmetal-mlx-rs 0.25.8):
                    group_size, bits)                     src/adapters.rs:309-317
 
 Tensors are torch tensors on the GPU (torch only supplies device memory and the current
-stream).  bf16 and f32 are supported; outputs follow MLX's dtype rules (scales/biases in the
-weight dtype, matmul output in the activation dtype).  Errors raise ``MlxqError`` carrying the
-library's status and message.
+stream).  bf16 and f32 are supported and dtypes follow MLX's promotion: scales/biases in the
+weight dtype; a matmul returns promote(x, scales) (bf16 only when both are bf16); a bias add or a
+LoRA residual in f32 promotes the result to f32.  Every operand's shape and dtype is checked
+against x before anything is launched, as MLX's quantized_matmul checks them; failures raise
+``MlxqError`` with status MLXQ_EINVAL, and library errors carry the library's status and message.
 """
 from __future__ import annotations
 
@@ -18,7 +20,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import MLXQ_BFLOAT16, MLXQ_FLOAT32, Epilogue, check
+from ._lib import MLXQ_BFLOAT16, MLXQ_EINVAL, MLXQ_FLOAT32, Epilogue, MlxqError, check
 
 DEFAULT_GROUP_SIZE = 64  # src/quant.rs:32
 
@@ -29,6 +31,15 @@ def _dt(t: torch.Tensor) -> int:
     if t.dtype == torch.float32:
         return MLXQ_FLOAT32
     raise TypeError(f"mlxq supports bfloat16 and float32 tensors, got {t.dtype}")
+
+
+def _torch_dtype(dt: int):
+    return torch.bfloat16 if dt == MLXQ_BFLOAT16 else torch.float32
+
+
+def promote(*dtypes) -> torch.dtype:
+    """MLX's result type over bf16/f32 operands: bf16 only when every operand is bf16."""
+    return torch.bfloat16 if all(d == torch.bfloat16 for d in dtypes) else torch.float32
 
 
 def _ptr(t):
@@ -47,6 +58,49 @@ def _need_gpu(*ts):
 
 def _contig(t):
     return None if t is None else t.contiguous()
+
+
+def _bad(op: str, msg: str):
+    raise MlxqError(MLXQ_EINVAL, f"{op}: {msg}")
+
+
+def _float_dtype(op: str, what: str, t: torch.Tensor):
+    if t.dtype not in (torch.bfloat16, torch.float32):
+        _bad(op, f"{what} must be bfloat16 or float32, got {t.dtype}")
+
+
+def _check_pack(op: str, wq, scales, biases, K: int, group_size: int, bits: int, lead=()):
+    """The packed triple against the activation width K (MLX's extract_quantized_matmul_dims):
+    wq [*lead, N, K*bits/32] of 32-bit words, scales/biases [*lead, N, K/group_size] alike."""
+    if bits not in (4, 8):
+        _bad(op, f"bits must be 4 or 8 (got {bits})")
+    if group_size not in (32, 64, 128):
+        _bad(op, f"group_size must be 32, 64 or 128 (got {group_size})")
+    nd = len(lead) + 2
+    if wq.dim() != nd or scales.dim() != nd or biases.dim() != nd:
+        _bad(op, f"wq, scales and biases must be {nd}-D")
+    if wq.dtype not in (torch.int32, torch.uint32):
+        _bad(op, f"packed weights must be 32-bit words, got {wq.dtype}")
+    if tuple(wq.shape[:-2]) != tuple(lead) or tuple(scales.shape[:-2]) != tuple(lead):
+        _bad(op, f"stacked operands must lead with {tuple(lead)}")
+    N = wq.shape[-2]
+    if K % group_size:
+        _bad(op, f"K={K} is not a multiple of group_size={group_size}")
+    if wq.shape[-1] * 32 != K * bits:
+        _bad(op, f"wq has {wq.shape[-1]} words per row, which packs {wq.shape[-1] * 32 // bits} "
+                 f"{bits}-bit codes, not x's K={K}")
+    want = tuple(lead) + (N, K // group_size)
+    if tuple(scales.shape) != want or tuple(biases.shape) != want:
+        _bad(op, f"scales/biases must be {want} (got {tuple(scales.shape)} / {tuple(biases.shape)})")
+    _float_dtype(op, "scales", scales)
+    if biases.dtype != scales.dtype:
+        _bad(op, f"biases dtype {biases.dtype} differs from scales dtype {scales.dtype}")
+    return N
+
+
+def _check_out(op: str, out, dtype, numel: int, device):
+    if out.dtype != dtype or out.device != device or out.numel() != numel or not out.is_contiguous():
+        _bad(op, f"out must be a contiguous {dtype} tensor of {numel} elements on {device}")
 
 
 def quantize(w: torch.Tensor, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4):
@@ -71,10 +125,12 @@ def _k_of(wq: torch.Tensor, bits: int) -> int:
 
 
 def dequantize(wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4):
-    _need_gpu(wq, scales, biases)
+    if bits not in (4, 8):
+        _bad("dequantize", f"bits must be 4 or 8 (got {bits})")
     wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
-    N = wq.shape[0]
     K = _k_of(wq, bits)
+    N = _check_pack("dequantize", wq, scales, biases, K, group_size, bits)
+    _need_gpu(wq, scales, biases)
     out = torch.empty((N, K), dtype=scales.dtype, device=wq.device)
     check(_lib.load().mlxq_dequantize(_ptr(wq), _ptr(scales), _ptr(biases), _dt(scales), N, K,
                                       group_size, bits, _ptr(out), _stream(wq.device)))
@@ -82,18 +138,23 @@ def dequantize(wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: i
 
 
 def _mm(entry, x, wq, scales, biases, group_size, bits, *extra, out=None):
-    _need_gpu(x, wq, scales, biases)
+    if x.dim() < 1:
+        _bad(entry, "x must have a last dimension")
+    _float_dtype(entry, "x", x)
     K = x.shape[-1]
     lead = x.shape[:-1]
     x2 = x.reshape(-1, K).contiguous()
     wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
-    M, N = x2.shape[0], wq.shape[0]
+    N = _check_pack(entry, wq, scales, biases, K, group_size, bits)
+    M = x2.shape[0]
+    # The forced bf16-tile GEMM returns bf16; the others MLX's promote(x, scales).
+    ydt = torch.bfloat16 if entry == "mlxq_qmm" else promote(x.dtype, scales.dtype)
     if out is None:
-        y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+        y = torch.empty((M, N), dtype=ydt, device=x.device)
     else:
-        if out.dtype != x.dtype or out.device != x.device or out.numel() != M * N or not out.is_contiguous():
-            raise ValueError(f"out must be a contiguous {x.dtype} tensor of {M * N} elements on {x.device}")
+        _check_out(entry, out, ydt, M * N, x.device)
         y = out
+    _need_gpu(x, wq, scales, biases)
     args = [_ptr(x2), _dt(x2), M, K, _ptr(wq), _ptr(scales), _ptr(biases), _dt(scales), N]
     if entry == "mlxq_quantized_matmul":
         args.append(int(extra[0]))
@@ -104,12 +165,13 @@ def _mm(entry, x, wq, scales, biases, group_size, bits, *extra, out=None):
 
 def quantized_matmul(x, wq, scales, biases, transpose: bool = True,
                      group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4, out=None):
-    """y = x . dequantize(W)^T (transpose=True, the only form the reference uses)."""
+    """y = x . dequantize(W)^T (transpose=True, the only form the reference uses), in
+    promote(x, scales)."""
     return _mm("mlxq_quantized_matmul", x, wq, scales, biases, group_size, bits, transpose, out=out)
 
 
 def qmm(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4, out=None):
-    """Force the MFMA GEMM kernel (bf16 activations)."""
+    """Force the MFMA bf16-tile GEMM kernel (bf16 activations, bf16 result)."""
     return _mm("mlxq_qmm", x, wq, scales, biases, group_size, bits, out=out)
 
 
@@ -123,15 +185,17 @@ def embedding(ids, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bit
     """TokenEmbedding::forward's quantized arm (src/nn.rs:42-58): gather the packed rows of ids
     (any shape, int32/int64), dequantize, cast to out_dtype (f32 like the reference).  Ids outside
     [0, vocab) give NaN rows."""
-    _need_gpu(ids, wq, scales, biases)
-    wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
-    flat = ids.reshape(-1).to(torch.int32).contiguous()
-    vocab = wq.shape[0]
-    hidden = _k_of(wq, bits)
-    out = torch.empty((flat.numel(), hidden), dtype=out_dtype, device=wq.device)
-    odt = MLXQ_BFLOAT16 if out_dtype == torch.bfloat16 else MLXQ_FLOAT32
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise TypeError(f"embedding: out_dtype must be bfloat16 or float32, got {out_dtype}")
+    if bits not in (4, 8):
+        _bad("embedding", f"bits must be 4 or 8 (got {bits})")
+    wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
+    hidden = _k_of(wq, bits)
+    vocab = _check_pack("embedding", wq, scales, biases, hidden, group_size, bits)
+    _need_gpu(ids, wq, scales, biases)
+    flat = ids.reshape(-1).to(torch.int32).contiguous()
+    out = torch.empty((flat.numel(), hidden), dtype=out_dtype, device=wq.device)
+    odt = MLXQ_BFLOAT16 if out_dtype == torch.bfloat16 else MLXQ_FLOAT32
     check(_lib.load().mlxq_embedding(_ptr(flat), flat.numel(), _ptr(wq), _ptr(scales), _ptr(biases),
                                      _dt(scales), vocab, hidden, group_size, bits, _ptr(out), odt,
                                      _stream(wq.device)))
@@ -142,14 +206,21 @@ def swiglu(x, gate, up, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4, out
     """Fused decode SwiGLU h = silu(gate(x)) * up(x) (mlx-gen-sensenova/src/qwen3.rs:178-181), gate
     and up given as packed (wq, scales, biases) triples of shape [F, K].  Decode form only (bf16,
     M <= 8); other shapes raise MlxqError with status MLXQ_EUNSUPPORTED."""
-    _need_gpu(x, *gate, *up)
+    _float_dtype("swiglu", "x", x)
     K = x.shape[-1]
     lead = x.shape[:-1]
     x2 = x.reshape(-1, K).contiguous()
     g = [t.contiguous() for t in gate]
     u = [t.contiguous() for t in up]
-    M, F = x2.shape[0], g[0].shape[0]
-    h = out if out is not None else torch.empty((M, F), dtype=x.dtype, device=x.device)
+    F = _check_pack("swiglu", *g, K, group_size, bits)
+    if _check_pack("swiglu", *u, K, group_size, bits) != F or u[1].dtype != g[1].dtype:
+        _bad("swiglu", "gate and up must be packed alike")
+    M = x2.shape[0]
+    hdt = promote(x.dtype, g[1].dtype)
+    if out is not None:
+        _check_out("swiglu", out, hdt, M * F, x.device)
+    _need_gpu(x, *gate, *up)
+    h = out if out is not None else torch.empty((M, F), dtype=hdt, device=x.device)
     check(_lib.load().mlxq_swiglu(_ptr(x2), _dt(x2), M, K, _ptr(g[0]), _ptr(g[1]), _ptr(g[2]), _ptr(u[0]),
                                   _ptr(u[1]), _ptr(u[2]), _dt(g[1]), F, group_size, bits, _ptr(h),
                                   _stream(x.device)))
@@ -162,14 +233,19 @@ def qmm_experts(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bit
     biases[e], transpose=True) + bias[e] — Proj::forward of the quantized MoE experts
     (mlx-gen-lens/src/text_encoder/gpt_oss.rs:412-425) over the axis-0 split of the stacked pack
     (mlx-gen-lens/src/quant.rs:111-137).  wq [E, N, K*bits/32], scales/biases [E, N, K/gs], bias
-    [E, N] in the activation dtype or None.  x [..., K] is shared by every expert, or with
-    per_expert=True it is [E, ..., K] (one input per expert).  Returns [E, ..., N]."""
-    _need_gpu(x, wq, scales, biases, bias)
-    E, N = wq.shape[0], wq.shape[1]
+    [E, N] (bf16 in the reference's packs) or None.  x [..., K] is shared by every expert, or with
+    per_expert=True it is [E, ..., K] (one input per expert).  Returns [E, ..., N] in
+    promote(x, scales, bias)."""
+    _float_dtype("qmm_experts", "x", x)
+    if wq.dim() != 3:
+        _bad("qmm_experts", "wq must be a stacked [E, N, K*bits/32] pack")
+    E = wq.shape[0]
     K = x.shape[-1]
+    wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
+    N = _check_pack("qmm_experts", wq, scales, biases, K, group_size, bits, lead=(E,))
     if per_expert:
-        if x.shape[0] != E:
-            raise ValueError(f"qmm_experts: x has {x.shape[0]} experts, the pack {E}")
+        if x.dim() < 2 or x.shape[0] != E:
+            _bad("qmm_experts", f"per-expert x must lead with E={E}, got shape {tuple(x.shape)}")
         lead = x.shape[1:-1]
     else:
         lead = x.shape[:-1]
@@ -177,44 +253,130 @@ def qmm_experts(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bit
     for d in lead:
         M *= d
     x2 = x.contiguous()
-    wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
-    b = bias.to(x.dtype).contiguous() if bias is not None else None
-    y = out if out is not None else torch.empty((E, M, N), dtype=x.dtype, device=x.device)
+    b = _contig(bias)
+    if b is not None:
+        _float_dtype("qmm_experts", "bias", b)
+        if tuple(b.shape) != (E, N):
+            _bad("qmm_experts", f"bias must be ({E}, {N}), got {tuple(b.shape)}")
+    ydt = promote(x.dtype, scales.dtype, *(() if b is None else (b.dtype,)))
+    if out is not None:
+        _check_out("qmm_experts", out, ydt, E * M * N, x.device)
+    _need_gpu(x, wq, scales, biases, bias)
+    y = out if out is not None else torch.empty((E, M, N), dtype=ydt, device=x.device)
     check(_lib.load().mlxq_qmm_experts(_ptr(x2), _dt(x2), int(per_expert), E, M, K, _ptr(wq),
-                                       _ptr(scales), _ptr(biases), _dt(scales), _ptr(b), N,
-                                       group_size, bits, _ptr(y), _stream(x.device)))
+                                       _ptr(scales), _ptr(biases), _dt(scales), _ptr(b),
+                                       MLXQ_BFLOAT16 if b is None else _dt(b), N, group_size, bits,
+                                       _ptr(y), _stream(x.device)))
     return y.reshape(E, *lead, N)
 
 
-def linear_workspace_size(M: int, N: int, rank: int) -> int:
-    return int(_lib.load().mlxq_linear_workspace_size(M, N, rank))
+def _epilogue(bias, lora_a, lora_b, lora_scale, activation, x_dtype):
+    rank = 0 if lora_a is None else int(lora_a.shape[1])
+    return Epilogue(bias=None if bias is None else bias.data_ptr(),
+                    lora_a=None if lora_a is None else lora_a.data_ptr(),
+                    lora_b=None if lora_b is None else lora_b.data_ptr(),
+                    lora_rank=rank, lora_scale=float(lora_scale), activation=int(activation),
+                    bias_dtype=_dt(bias) if bias is not None else _dt_of(x_dtype),
+                    lora_dtype=_dt(lora_a) if lora_a is not None else _dt_of(x_dtype))
+
+
+def _dt_of(dtype) -> int:
+    return MLXQ_BFLOAT16 if dtype == torch.bfloat16 else MLXQ_FLOAT32
+
+
+def linear_out_dtype(x_dtype, scales_dtype, bias_dtype=None, lora_dtype=None, activation: int = 0):
+    """The dtype mlxq_linear returns for these operand dtypes (MLX's promotion, the library's rule)."""
+    ep = Epilogue(bias=1 if bias_dtype is not None else None, lora_a=None, lora_b=None,
+                  lora_rank=16 if lora_dtype is not None else 0, lora_scale=1.0,
+                  activation=int(activation),
+                  bias_dtype=_dt_of(bias_dtype if bias_dtype is not None else x_dtype),
+                  lora_dtype=_dt_of(lora_dtype if lora_dtype is not None else x_dtype))
+    dt = _lib.load().mlxq_linear_out_dtype(_dt_of(x_dtype), _dt_of(scales_dtype), ctypes.byref(ep))
+    if dt < 0:
+        raise MlxqError(MLXQ_EINVAL, _lib.load().mlxq_last_error().decode())
+    return _torch_dtype(dt)
+
+
+def linear_workspace_size(x_dtype, scales_dtype, M: int, N: int, bias=None, lora_a=None,
+                          activation: int = 0) -> int:
+    ep = _epilogue(bias, lora_a, lora_a, 1.0, activation, x_dtype)
+    return int(_lib.load().mlxq_linear_workspace_size(_dt_of(x_dtype), _dt_of(scales_dtype), M, N,
+                                                      ctypes.byref(ep)))
 
 
 def linear(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4, bias=None,
            lora_a=None, lora_b=None, lora_scale: float = 1.0, activation: int = 0, workspace=None):
     """Quantized AdaptableLinear forward with optional bias, one LoRA adapter and an activation,
-    rounded at the same points as the reference's separate ops."""
-    _need_gpu(x, wq, scales, biases, bias, lora_a, lora_b)
+    rounded at the same points as the reference's separate ops.  bias and the LoRA factors keep
+    their own dtypes; the result is in MLX's promoted dtype (linear_out_dtype)."""
+    _float_dtype("linear", "x", x)
     K = x.shape[-1]
     lead = x.shape[:-1]
     x2 = x.reshape(-1, K).contiguous()
     wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
     bias, lora_a, lora_b = _contig(bias), _contig(lora_a), _contig(lora_b)
-    M, N = x2.shape[0], wq.shape[0]
-    rank = 0 if lora_a is None else int(lora_a.shape[1])
-    ep = Epilogue(bias=None if bias is None else bias.data_ptr(),
-                  lora_a=None if lora_a is None else lora_a.data_ptr(),
-                  lora_b=None if lora_b is None else lora_b.data_ptr(),
-                  lora_rank=rank, lora_scale=float(lora_scale), activation=int(activation))
-    need = linear_workspace_size(M, N, rank)
+    N = _check_pack("linear", wq, scales, biases, K, group_size, bits)
+    M = x2.shape[0]
+    if bias is not None:
+        _float_dtype("linear", "bias", bias)
+        if tuple(bias.shape) != (N,):
+            _bad("linear", f"bias must have shape ({N},), got {tuple(bias.shape)}")
+    if (lora_a is None) != (lora_b is None):
+        _bad("linear", "LoRA needs both factors")
+    if lora_a is not None:
+        _float_dtype("linear", "LoRA A", lora_a)
+        if lora_a.dim() != 2 or lora_b.dim() != 2 or lora_a.shape[0] != K or lora_b.shape[1] != N \
+                or lora_a.shape[1] != lora_b.shape[0]:
+            _bad("linear", f"LoRA factors must be A [{K}, r] and B [r, {N}], got "
+                           f"{tuple(lora_a.shape)} and {tuple(lora_b.shape)}")
+        if lora_b.dtype != lora_a.dtype:
+            _bad("linear", "LoRA A and B must share a dtype")
+    _need_gpu(x, wq, scales, biases, bias, lora_a, lora_b)
+    ep = _epilogue(bias, lora_a, lora_b, lora_scale, activation, x.dtype)
+    lib = _lib.load()
+    odt = lib.mlxq_linear_out_dtype(_dt(x2), _dt(scales), ctypes.byref(ep))
+    if odt < 0:
+        raise MlxqError(MLXQ_EINVAL, lib.mlxq_last_error().decode())
+    need = int(lib.mlxq_linear_workspace_size(_dt(x2), _dt(scales), M, N, ctypes.byref(ep)))
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
-    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
-    check(_lib.load().mlxq_linear(_ptr(x2), _dt(x2), M, K, _ptr(wq), _ptr(scales), _ptr(biases),
-                                  _dt(scales), N, group_size, bits, ctypes.byref(ep), _ptr(y),
-                                  _ptr(workspace), 0 if workspace is None else need,
-                                  _stream(x.device)))
+    y = torch.empty((M, N), dtype=_torch_dtype(odt), device=x.device)
+    check(lib.mlxq_linear(_ptr(x2), _dt(x2), M, K, _ptr(wq), _ptr(scales), _ptr(biases),
+                          _dt(scales), N, group_size, bits, ctypes.byref(ep), _ptr(y),
+                          _ptr(workspace) if need else None, need, _stream(x.device)))
     return y.reshape(*lead, N)
+
+
+def lora_residual(x, y, lora_a, lora_b, lora_scale: float = 1.0, workspace=None):
+    """out = y + scale * (x.A).B — one more adapter of AdaptableLinear::forward's stack
+    (src/adapters.rs:543-549, Adapter::residual :260-270) on an already computed y.  The residual
+    runs in promote(x, A); the sum in promote(y, residual) (in place when that is y's dtype)."""
+    _float_dtype("lora_residual", "x", x)
+    _float_dtype("lora_residual", "y", y)
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    N = y.shape[-1]
+    if y.numel() != M * N:
+        _bad("lora_residual", f"y has {y.numel()} elements, x implies {M} rows of {N}")
+    lora_a, lora_b = lora_a.contiguous(), lora_b.contiguous()
+    _float_dtype("lora_residual", "LoRA A", lora_a)
+    if lora_a.dim() != 2 or lora_b.dim() != 2 or lora_a.shape[0] != K or lora_b.shape[1] != N \
+            or lora_a.shape[1] != lora_b.shape[0] or lora_b.dtype != lora_a.dtype:
+        _bad("lora_residual", f"LoRA factors must be A [{K}, r] and B [r, {N}] of one dtype")
+    _need_gpu(x, y, lora_a, lora_b)
+    rank = int(lora_a.shape[1])
+    y_in = y.contiguous()
+    odt = promote(y.dtype, x.dtype, lora_a.dtype)
+    out = y_in if odt == y.dtype else torch.empty(y.shape, dtype=odt, device=y.device)
+    lib = _lib.load()
+    need = int(lib.mlxq_lora_residual_workspace_size(_dt(x2), _dt(lora_a), M, N, rank))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    check(lib.mlxq_lora_residual(_ptr(x2), _dt(x2), M, K, _ptr(lora_a), _ptr(lora_b), _dt(lora_a), N,
+                                 rank, float(lora_scale), _ptr(y_in), _dt(y_in), _ptr(out),
+                                 _ptr(workspace), need, _stream(x.device)))
+    return out
 
 
 def packed_bits(wq, scales, group_size: int) -> int:

@@ -20,9 +20,13 @@
  *   oracle_qmm         pinned: fixture q4/q8 .qmm (f32 activations, exact dequant); textbook
  *                      matmul over the dequantized matrix for the bf16-tile variant.
  *   oracle_linear      pinned by composition: qmm + the reference op sequence of
- *                      src/adapters.rs:300-322,543-549 (bias add, then LoRA residual); its
- *                      rounding points follow MLX's per-op bf16 rounding (not pinned by a golden).
+ *                      src/adapters.rs:300-322,543-549 (bias add, then LoRA residual) under MLX's
+ *                      bf16/f32 promotion (src/adapters.rs:243-252); its rounding points follow
+ *                      MLX's per-op rounding (not pinned by a golden: parity unpinned for the
+ *                      bf16 rounding points).
  *   oracle_gelu_erf / oracle_silu: textbook closed forms (special values tested).
+ *   oracle_gelu_exact  the op sequence of src/nn.rs:344-355 in the input dtype; in f32 pinned by
+ *                      its distance to the closed form, in bf16 parity unpinned (rounding points).
  *   oracle_gelu_tanh   pinned in f32 by the closed form (the reference test points of
  *                      src/nn.rs:722-738 among them) and by its distance to the exact GELU; the
  *                      per-op bf16 rounding points follow src/nn.rs:321-329 and are not pinned
@@ -218,6 +222,22 @@ float oracle_gelu_erf(float v, int out_bf16) {
 }
 
 /*
+ * Dtype-preserving exact GELU of reference src/nn.rs:344-355 (gelu_exact): the ops
+ *   inner = erf(x / s2); gate = 1 + inner; y = (x * gate) / 2
+ * with s2 = (float)sqrt(2) cast to the input dtype, every op's result rounded to it (bf16 when
+ * out_bf16): each op is computed in f32 (correctly rounded: evaluated in double, then rounded to
+ * float) and then rounded, as MLX's bf16 elementwise ops compute through float.
+ */
+float oracle_gelu_exact(float v, int out_bf16) {
+    const float s2 = rnd((float)sqrt(2.0), out_bf16);
+    const float t1 = rnd((float)((double)v / (double)s2), out_bf16);
+    const float t2 = rnd((float)erf((double)t1), out_bf16);
+    const float t3 = rnd((float)(1.0 + (double)t2), out_bf16);
+    const float t4 = rnd((float)((double)v * (double)t3), out_bf16);
+    return rnd((float)((double)t4 / 2.0), out_bf16);
+}
+
+/*
  * Tanh-approximate GELU of reference src/nn.rs:321-329 (FLUX single-stream FFN,
  * mlx-gen-flux/src/transformer.rs:506,708,979): the eager op sequence
  *   x3 = x^3; inner = (x + x3 * 0.044715) * c; gate = tanh(inner) + 1; y = (x * 0.5) * gate
@@ -242,30 +262,41 @@ float oracle_silu(float v, int out_bf16) {
 
 /*
  * AdaptableLinear::forward over a quantized base (reference src/adapters.rs:543-549 and the
- * quantized arm of LinearBase::forward, :300-322), with every intermediate rounded to the
- * activation dtype the way separate MLX ops round it (act_bf16 = 1 for bf16 activations):
- *   y1 = qmm(x)                                  (src/adapters.rs:309-317)
- *   y2 = y1 + bias            if bias            (:318-320)
- *   xa = x . A                A [K,r]            (Adapter::residual, :260-270; A = lora_down^T,
- *   r  = xa . B               B [r,N]             B = lora_up^T with alpha/rank folded in,
- *   r2 = r * scale            scale in act dtype  src/adapters/loader.rs:568-569,597)
- *   y  = y2 + r2              if lora
- *   y  = act(y)               act: 0 none, 1 exact-erf GELU (mlx-gen-flux/src/transformer.rs:975),
- *                              2 tanh GELU (src/nn.rs:321-329)
+ * quantized arm of LinearBase::forward, :300-322) under MLX's dtype promotion: each op computes
+ * in the result type of its operands (bf16 only when all are bf16) and rounds to it.
+ *   y0 = qmm(x)                    D0 = promote(x, scales)          (src/adapters.rs:309-317)
+ *   y1 = y0 + bias   if bias       D1 = promote(D0, bias)           (:318-320)
+ *   xa = x . A                     DR = promote(x, factors)         (Adapter::residual, :260-270;
+ *   r  = xa . B                                                      A = lora_down^T, B = lora_up^T
+ *   r2 = r * scale   scale cast to DR                                with alpha/rank folded in,
+ *                                                                    src/adapters/loader.rs:568-599)
+ *   y2 = y1 + r2     if lora       D2 = promote(D1, DR), not cast back (:243-252, :546)
+ *   y  = act(y2)     act: 0 none; 1 mlx_rs::nn::gelu (exact erf in f32: its f32 constants
+ *                    promote a bf16 input, mlx-gen-flux/src/transformer.rs:975, src/nn.rs:335-338);
+ *                    2 tanh GELU per op in D2 (src/nn.rs:321-329); 3 exact GELU per op in D2
+ *                    (src/nn.rs:344-355)
  * The activation is the caller's next op (FeedForward::forward, transformer.rs:970-977), listed
- * here so a fused epilogue has a checker.  w_bf16 as in oracle_qmm.
+ * here so a fused epilogue has a checker.  w_bf16 as in oracle_qmm.  *out_bf16 receives whether
+ * y's dtype is bf16.
  */
 int oracle_linear(const float* x, int64_t M, int64_t K, const uint32_t* wq, const float* scales,
-                  const float* biases, int64_t N, int gs, int bits, int w_bf16, int act_bf16,
-                  const float* bias, const float* lora_a, const float* lora_b, int64_t rank,
-                  float lora_scale, int act, float* y) {
-    int rc = oracle_qmm(x, M, K, wq, scales, biases, N, gs, bits, w_bf16, act_bf16, y);
+                  const float* biases, int64_t N, int gs, int bits, int w_bf16, int x_bf16,
+                  int sb_bf16, const float* bias, int bias_bf16, const float* lora_a,
+                  const float* lora_b, int64_t rank, int lora_bf16, float lora_scale, int act,
+                  float* y, int* out_bf16) {
+    const int lora = lora_a && lora_b && rank > 0;
+    const int d0 = x_bf16 && sb_bf16;
+    const int d1 = d0 && (!bias || bias_bf16);
+    const int dr = x_bf16 && (!lora || lora_bf16);
+    const int d2 = d1 && (!lora || dr);
+    if (act < 0 || act > 3) return ORACLE_EINVAL;
+    int rc = oracle_qmm(x, M, K, wq, scales, biases, N, gs, bits, w_bf16, d0, y);
     if (rc) return rc;
     if (bias) {
 #pragma omp parallel for schedule(static)
-        for (int64_t i = 0; i < M * N; ++i) y[i] = rnd(y[i] + bias[i % N], act_bf16);
+        for (int64_t i = 0; i < M * N; ++i) y[i] = rnd(y[i] + bias[i % N], d1);
     }
-    if (lora_a && lora_b && rank > 0) {
+    if (lora) {
         float* xa = (float*)malloc(sizeof(float) * (size_t)(M * rank));
         float* r = (float*)malloc(sizeof(float) * (size_t)(M * N));
         if (!xa || !r) {
@@ -273,21 +304,25 @@ int oracle_linear(const float* x, int64_t M, int64_t K, const uint32_t* wq, cons
             free(r);
             return ORACLE_EINVAL;
         }
-        dense_mm(x, M, K, lora_a, rank, act_bf16, xa);
-        dense_mm(xa, M, rank, lora_b, N, act_bf16, r);
-        float sc = rnd(lora_scale, act_bf16);
+        dense_mm(x, M, K, lora_a, rank, dr, xa);
+        dense_mm(xa, M, rank, lora_b, N, dr, r);
+        float sc = rnd(lora_scale, dr);
 #pragma omp parallel for schedule(static)
-        for (int64_t i = 0; i < M * N; ++i) y[i] = rnd(y[i] + rnd(r[i] * sc, act_bf16), act_bf16);
+        for (int64_t i = 0; i < M * N; ++i) y[i] = rnd(y[i] + rnd(r[i] * sc, dr), d2);
         free(xa);
         free(r);
     }
     if (act == 1) {
 #pragma omp parallel for schedule(static)
-        for (int64_t i = 0; i < M * N; ++i) y[i] = oracle_gelu_erf(y[i], act_bf16);
+        for (int64_t i = 0; i < M * N; ++i) y[i] = oracle_gelu_erf(y[i], 0);
     } else if (act == 2) {
 #pragma omp parallel for schedule(static)
-        for (int64_t i = 0; i < M * N; ++i) y[i] = oracle_gelu_tanh(y[i], act_bf16);
+        for (int64_t i = 0; i < M * N; ++i) y[i] = oracle_gelu_tanh(y[i], d2);
+    } else if (act == 3) {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < M * N; ++i) y[i] = oracle_gelu_exact(y[i], d2);
     }
+    if (out_bf16) *out_bf16 = d2 && act != 1;
     return ORACLE_OK;
 }
 

@@ -44,7 +44,8 @@ def lib():
         l.oracle_qmm.argtypes = [_f32p, _i64, _i64, _u32p, _f32p, _f32p, _i64, _int, _int, _int,
                                  _int, _f32p]
         l.oracle_linear.argtypes = [_f32p, _i64, _i64, _u32p, _f32p, _f32p, _i64, _int, _int, _int,
-                                    _int, _f32p, _f32p, _f32p, _i64, ctypes.c_float, _int, _f32p]
+                                    _int, _int, _f32p, _int, _f32p, _f32p, _i64, _int,
+                                    ctypes.c_float, _int, _f32p, ctypes.POINTER(_int)]
         l.oracle_swiglu_mlp.argtypes = [_f32p, _i64, _i64, _u32p, _f32p, _f32p, _u32p, _f32p, _f32p,
                                         _i64, _u32p, _f32p, _f32p, _i64, _int, _int, _int, _int,
                                         _f32p, _f32p]
@@ -52,6 +53,8 @@ def lib():
         l.oracle_gelu_erf.restype = ctypes.c_float
         l.oracle_gelu_tanh.argtypes = [ctypes.c_float, _int]
         l.oracle_gelu_tanh.restype = ctypes.c_float
+        l.oracle_gelu_exact.argtypes = [ctypes.c_float, _int]
+        l.oracle_gelu_exact.restype = ctypes.c_float
         l.oracle_silu.argtypes = [ctypes.c_float, _int]
         l.oracle_silu.restype = ctypes.c_float
         l.oracle_num_threads.restype = _int
@@ -136,8 +139,12 @@ def quantized_matmul(x, wq, scales, biases, group_size=64, bits=4, w_bf16=True, 
 
 
 def linear(x, wq, scales, biases, group_size=64, bits=4, w_bf16=True, act_bf16=True, bias=None,
-           lora_a=None, lora_b=None, lora_scale=1.0, act=0):
-    """AdaptableLinear forward over a quantized base with optional bias, LoRA and GELU."""
+           lora_a=None, lora_b=None, lora_scale=1.0, act=0, x_bf16=None, sb_bf16=None,
+           bias_bf16=None, lora_bf16=None, return_dtype=False):
+    """AdaptableLinear forward over a quantized base with optional bias, LoRA and activation,
+    under MLX's promotion.  Each *_bf16 flag says whether that operand is bf16 (values are passed
+    as the f32 numbers they hold); unset flags default to act_bf16.  act: 0 none, 1 GELU
+    (f32 result), 2 tanh GELU, 3 exact GELU.  With return_dtype, returns (y, out_is_bf16)."""
     x, xp = _f32(x)
     wq, wqp = _u32(wq)
     scales, sp = _f32(scales)
@@ -148,11 +155,14 @@ def linear(x, wq, scales, biases, group_size=64, bits=4, w_bf16=True, act_bf16=T
     lora_a, ap = _opt_f32(lora_a)
     lora_b, bbp = _opt_f32(lora_b)
     rank = 0 if lora_a is None else lora_a.shape[1]
+    flag = lambda f: int(act_bf16 if f is None else f)
     y = np.empty((M, N), np.float32)
+    ob = _int(0)
     _check(lib().oracle_linear(xp, M, K, wqp, sp, bp, N, group_size, bits, int(w_bf16),
-                               int(act_bf16), biasp, ap, bbp, rank, float(lora_scale), int(act),
-                               y.ctypes.data_as(_f32p)), "linear")
-    return y
+                               flag(x_bf16), flag(sb_bf16), biasp, flag(bias_bf16), ap, bbp, rank,
+                               flag(lora_bf16), float(lora_scale), int(act),
+                               y.ctypes.data_as(_f32p), ctypes.byref(ob)), "linear")
+    return (y, bool(ob.value)) if return_dtype else y
 
 
 def swiglu_mlp(x, gate, up, down, group_size=64, bits=4, w_bf16=False, act_bf16=True):
@@ -179,6 +189,10 @@ def gelu_erf(v, out_bf16=True):
 
 def gelu_tanh(v, out_bf16=True):
     return lib().oracle_gelu_tanh(float(v), int(out_bf16))
+
+
+def gelu_exact(v, out_bf16=True):
+    return lib().oracle_gelu_exact(float(v), int(out_bf16))
 
 
 def silu(v, out_bf16=True):

@@ -32,9 +32,10 @@ int oracle_qmm(const float* x, int64_t M, int64_t K, const uint32_t* wq, const f
                const float* biases, int64_t N, int gs, int bits, int w_bf16, int out_bf16, float* y);
 float oracle_silu(float v, int out_bf16);
 int oracle_linear(const float* x, int64_t M, int64_t K, const uint32_t* wq, const float* scales,
-                  const float* biases, int64_t N, int gs, int bits, int w_bf16, int act_bf16,
-                  const float* bias, const float* lora_a, const float* lora_b, int64_t rank,
-                  float lora_scale, int act, float* y);
+                  const float* biases, int64_t N, int gs, int bits, int w_bf16, int x_bf16,
+                  int sb_bf16, const float* bias, int bias_bf16, const float* lora_a,
+                  const float* lora_b, int64_t rank, int lora_bf16, float lora_scale, int act,
+                  float* y, int* out_bf16);
 }
 
 namespace fs = std::filesystem;
@@ -286,8 +287,8 @@ static void gpu_cases(const fs::path& root) {
     EXPECT(host<uint32_t>(l.quantized().weight) == wq, "packed words");
     std::vector<float> bias_b(N);
     for (int64_t n = 0; n < N; ++n) bias_b[n] = oracle_bf16_round(bias[n]);
-    oracle_linear(x.data(), M, K, wq.data(), s.data(), z.data(), N, 64, 4, M > 8, 1, bias_b.data(),
-                  a1.data(), b1.data(), R1, 0.75f, 0, ref.data());
+    oracle_linear(x.data(), M, K, wq.data(), s.data(), z.data(), N, 64, 4, M > 8, 1, 1, bias_b.data(), 1,
+                  a1.data(), b1.data(), R1, 1, 0.75f, 0, ref.data(), nullptr);
     std::vector<float> xa(M * R2);
     for (int64_t m = 0; m < M; ++m)
       for (int64_t r = 0; r < R2; ++r) {
@@ -305,6 +306,80 @@ static void gpu_cases(const fs::path& root) {
       }
     const double e = rel_fro(host_f32(y), ref);
     EXPECT(e < 2e-3, "relFro %.3e", e);
+  }
+
+  banner("AdaptableLinear promotion: f32 bias, bf16 then f32 LoRA factors; graph capture");
+  {
+    // A snapshot loaded as is keeps an f32 bias and f32 adapter factors (src/adapters.rs:243-252):
+    // y0 bf16 + f32 bias -> f32, + bf16 adapter (residual bf16, sum f32), + f32 adapter -> f32.
+    std::mt19937 rng(9);
+    const int64_t M = 300, K = 512, N = 320, R1 = 16, R2 = 8;
+    std::vector<float> w = bf16_normal(rng, N * K, 0.02f), x = bf16_normal(rng, M * K, 1.0f);
+    std::vector<float> bias(N);
+    std::normal_distribution<float> nd(0.0f, 0.3f);
+    for (auto& v : bias) v = nd(rng);  // f32 values, not bf16-exact
+    std::vector<float> a1 = bf16_normal(rng, K * R1, 0.02f), b1 = bf16_normal(rng, R1 * N, 0.02f);
+    std::vector<float> a2(K * R2), b2(R2 * N);
+    for (auto& v : a2) v = nd(rng) * 0.05f;
+    for (auto& v : b2) v = nd(rng) * 0.05f;
+    QuantizedLinear q = QuantizedLinear::try_from_linear(bf16_array(w, {N, K}),
+                                                         Array::from_host(bias.data(), {N}, Dtype::Float32), 64, 4);
+    AdaptableLinear l = AdaptableLinear::from_quantized_parts(q.weight, q.scales, q.biases, q.bias, 64, 4);
+    l.push(Adapter{bf16_array(a1, {K, R1}), bf16_array(b1, {R1, N}), 0.5f});
+    l.push(Adapter{Array::from_host(a2.data(), {K, R2}, Dtype::Float32),
+                   Array::from_host(b2.data(), {R2, N}, Dtype::Float32), 1.25f});
+    const Array xin = bf16_array(x, {M, K});
+    EXPECT(l.out_dtype(Dtype::Bfloat16) == Dtype::Float32, "promoted dtype");
+    Array y = l.forward(xin);
+    EXPECT(y.dtype() == Dtype::Float32 && y.shape() == std::vector<int64_t>({M, N}), "promoted output");
+    // reference: oracle linear with the f32 bias and adapter 1 (sum in f32), then adapter 2 in f32
+    std::vector<uint32_t> wq(N * K / 8);
+    std::vector<float> sc(N * K / 64), zz(N * K / 64), ref(M * N);
+    oracle_quantize(w.data(), N, K, 64, 4, 1, wq.data(), sc.data(), zz.data());
+    int ob = -1;
+    oracle_linear(x.data(), M, K, wq.data(), sc.data(), zz.data(), N, 64, 4, 1, 1, 1, bias.data(), 0,
+                  a1.data(), b1.data(), R1, 1, 0.5f, 0, ref.data(), &ob);
+    EXPECT(ob == 0, "oracle dtype");
+    for (int64_t m = 0; m < M; ++m) {
+      double xa[R2];
+      for (int64_t r = 0; r < R2; ++r) {
+        double acc = 0;
+        for (int64_t k = 0; k < K; ++k) acc += (double)x[m * K + k] * a2[k * R2 + r];
+        xa[r] = (float)acc;
+      }
+      for (int64_t n = 0; n < N; ++n) {
+        double acc = 0;
+        for (int64_t r = 0; r < R2; ++r) acc += xa[r] * b2[r * N + n];
+        ref[m * N + n] = (float)(ref[m * N + n] + (float)((float)acc * 1.25f));
+      }
+    }
+    const std::vector<float> yh = host_f32(y);
+    double e = rel_fro(yh, ref);
+    EXPECT(e < 2e-3, "promoted relFro %.3e", e);
+    // The same forward into a caller's array, captured in a HIP graph and replayed: the layer
+    // allocates nothing and waits for nothing after its first call.
+    hipStream_t st;
+    EXPECT(hipStreamCreate(&st) == hipSuccess, "stream");
+    Array out = Array::empty({M, N}, Dtype::Float32);
+    l.forward_into(xin, out, st);  // first call: workspaces
+    EXPECT(hipStreamSynchronize(st) == hipSuccess, "sync");
+    EXPECT(host_f32(out) == yh, "forward_into differs from forward");
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    EXPECT(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal) == hipSuccess, "begin capture");
+    l.forward_into(xin, out, st);
+    EXPECT(hipStreamEndCapture(st, &graph) == hipSuccess, "end capture");
+    EXPECT(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess, "instantiate");
+    for (int rep = 0; rep < 3; ++rep) {
+      EXPECT(hipMemsetAsync(out.data(), 0, out.nbytes(), st) == hipSuccess, "clear");
+      EXPECT(hipGraphLaunch(exec, st) == hipSuccess, "replay");
+      EXPECT(hipStreamSynchronize(st) == hipSuccess, "sync");
+      EXPECT(host_f32(out) == yh, "graph replay %d differs from the eager result", rep);
+      (void)l.forward(xin);  // eager work between replays
+    }
+    (void)hipGraphExecDestroy(exec);
+    (void)hipGraphDestroy(graph);
+    (void)hipStreamDestroy(st);
   }
 
   banner("fused SwiGLU decode and the stacked expert projection");

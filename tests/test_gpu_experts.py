@@ -118,6 +118,6 @@ def test_experts_empty_and_mismatch(mlxq):
     packs, wq, s, b = _stack(rng, 2, 16, 128, 64, 4)
     x = to_gpu(bf16_normal(rng, (0, 128)))
     assert mlxq.qmm_experts(x, wq_to_gpu(wq), to_gpu(s), to_gpu(b), 64, 4).shape == (2, 0, 16)
-    with pytest.raises(ValueError):
+    with pytest.raises(mlxq.MlxqError, match="lead with E"):
         mlxq.qmm_experts(to_gpu(bf16_normal(rng, (3, 4, 128))), wq_to_gpu(wq), to_gpu(s), to_gpu(b),
                          64, 4, per_expert=True)

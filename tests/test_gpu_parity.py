@@ -263,7 +263,7 @@ def test_qmm_wide_f32_scales(mlxq, M, K, N, gs, bits):
 ODD_GRID_CASES = [
     # M, K, N, gs, bits, act, bias
     (2304, 4096, 4096, 64, 4, 0, False),   # 144 tiles: one round at 56 %
-    (2304, 1024, 4096, 64, 8, 1, True),    # bias + exact-erf GELU
+    (2304, 1024, 4096, 64, 8, 3, True),    # bias + exact GELU
     (1000, 2048, 6000, 32, 4, 2, True),    # ragged M and N (tiled kernel), tanh GELU
     (4608, 3072, 4352, 64, 4, 0, False),   # 357 224-row tiles: two rounds at 70 %
 ]
@@ -289,14 +289,15 @@ def test_qmm_odd_grids(mlxq, M, K, N, gs, bits, act, bias):
     assert_close(to_np(y1)[rows], ref, f"odd grid M={M} K={K} N={N}")
 
 
-@pytest.mark.parametrize("M", [2100, 1100])
-@pytest.mark.parametrize("act", [0, 1, 2])
-def test_linear_wide_bias_lora_act(mlxq, act, M):
-    """Fused bias + LoRA + activation epilogue on 256x256 tiles (M = 2100) and on 256x128
-    tiles with 4 waves (M = 1100: 85 wide tiles, 165 narrow ones)."""
-    banner("linear wide epilogue", act, M)
-    rng = np.random.default_rng(77 + act + M)
-    K, N, r = 512, 4200, 16
+@pytest.mark.parametrize("M,N", [(2100, 4200), (1100, 4200), (2100, 4100)])
+@pytest.mark.parametrize("act,scale", [(0, 1.0), (3, 1.0), (2, 1.0), (0, 0.75), (3, 1.5)])
+def test_linear_wide_bias_lora_act(mlxq, act, scale, M, N):
+    """Fused bias + LoRA + activation epilogue on 256x256 tiles (M = 2100), on 256x128 tiles
+    with 4 waves (M = 1100: 85 wide tiles, 165 narrow ones) and with ragged N (4100), with LoRA
+    scales other than 1 (their product rounding runs only then)."""
+    banner("linear wide epilogue", act, scale, M, N)
+    rng = np.random.default_rng(77 + act + M + N)
+    K, r = 512, 16
     x = bf16_normal(rng, (M, K))
     w = bf16_normal(rng, (N, K), 0.02)
     bias = bf16_normal(rng, (N,), 0.5)
@@ -304,17 +305,29 @@ def test_linear_wide_bias_lora_act(mlxq, act, M):
     B = bf16_normal(rng, (r, N), 0.01)
     rwq, rs, rb = oracle.quantize(w, 64, 4, sb_bf16=True)
     y = to_np(mlxq.linear(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), 64, 4,
-                          bias=to_gpu(bias), lora_a=to_gpu(A), lora_b=to_gpu(B), lora_scale=1.0,
+                          bias=to_gpu(bias), lora_a=to_gpu(A), lora_b=to_gpu(B), lora_scale=scale,
                           activation=act))
     ref = oracle.linear(x, rwq, rs, rb, 64, 4, w_bf16=True, act_bf16=True, bias=bias,
-                        lora_a=A, lora_b=B, lora_scale=1.0, act=act)
-    assert_close(y, ref, f"linear wide act={act}")
+                        lora_a=A, lora_b=B, lora_scale=scale, act=act)
+    assert_close(y, ref, f"linear wide act={act} scale={scale}")
 
 
-def test_flux_mlp_full_size_sampled_rows(mlxq):
-    """Config 2 at full size: every output row depends only on its own input row, so a seeded
-    sample of rows checked against the oracle covers the full-size launch (all tiles ran)."""
-    banner("config2 full size: up+gelu, down")
+def _band_rows(rng, M, heights=(224, 256)):
+    """At least one row in every M-tile band of each tile height (a random row per band, plus the
+    band edges of the first and last bands)."""
+    rows = {0, M - 1}
+    for h in heights:
+        for t in range(0, M, h):
+            hi = min(t + h, M)
+            rows.add(int(rng.integers(t, hi)))
+        rows.update({min(h, M - 1), min(h - 1, M - 1)})
+    return np.array(sorted(rows))
+
+
+def test_flux_mlp_full_size_all_rows(mlxq):
+    """Config 2 at full size, every output element against the OpenMP oracle: the up projection
+    with the dtype-preserving exact GELU fused (a bf16 stream), then the down projection."""
+    banner("config2 full size: up+gelu, down, all rows")
     M, K, F = 4608, 3072, 12288
     rng = np.random.default_rng(0)
     x = bf16_normal(rng, (M, K))
@@ -324,17 +337,17 @@ def test_flux_mlp_full_size_sampled_rows(mlxq):
     qd = oracle.quantize(wd, 64, 4, sb_bf16=True)
     gu = [wq_to_gpu(qu[0]), to_gpu(qu[1]), to_gpu(qu[2])]
     gd = [wq_to_gpu(qd[0]), to_gpu(qd[1]), to_gpu(qd[2])]
-    h = mlxq.linear(to_gpu(x), *gu, 64, 4, activation=mlxq.MLXQ_ACT_GELU)
+    h = mlxq.linear(to_gpu(x), *gu, 64, 4, activation=mlxq.MLXQ_ACT_GELU_EXACT)
     y = mlxq.quantized_matmul(h, *gd, True, 64, 4)
     torch.cuda.synchronize()
-    rows = np.sort(rng.choice(M, 40, replace=False))
-    rows = np.concatenate([[0, 255, 256, M - 1], rows])
+    assert h.dtype == torch.bfloat16 and y.dtype == torch.bfloat16
     h_np = to_np(h)
-    ref_h = oracle.linear(x[rows], *qu, 64, 4, w_bf16=True, act_bf16=True, act=1)
-    assert_close(h_np[rows], ref_h, "config2 up+gelu rows")
-    ref_y = oracle.quantized_matmul(h_np[rows], *qd, 64, 4, w_bf16=True, out_bf16=True)
-    assert_close(to_np(y)[rows], ref_y, "config2 down rows")
     assert np.isfinite(h_np).all()
+    ref_h = oracle.linear(x, *qu, 64, 4, w_bf16=True, act_bf16=True, act=3)
+    assert_close(h_np, ref_h, "config2 up+gelu, all rows")
+    del ref_h
+    ref_y = oracle.quantized_matmul(h_np, *qd, 64, 4, w_bf16=True, out_bf16=True)
+    assert_close(to_np(y), ref_y, "config2 down, all rows")
 
 
 def test_qmm_dispatch_matches_forced_kernels(mlxq):
@@ -454,7 +467,7 @@ def test_f32_activations_large_m(mlxq):
 
 # ---------------------------------------------------------------- fused linear epilogue
 
-@pytest.mark.parametrize("act", [1, 2])
+@pytest.mark.parametrize("act", [1, 2, 3])
 def test_linear_f32_activations_act(mlxq, act):
     """f32 activations (the FLUX.1 f32 stream): bias and activation evaluated in f32, no bf16
     rounding anywhere, against the oracle's f32 op sequence."""
@@ -472,7 +485,7 @@ def test_linear_f32_activations_act(mlxq, act):
     assert errors(y, ref)[0] < 1e-5
 
 @pytest.mark.parametrize("M", [4, 300])
-@pytest.mark.parametrize("act", [0, 1, 2])
+@pytest.mark.parametrize("act", [0, 1, 2, 3])
 def test_linear_bias_lora_act(mlxq, M, act):
     banner("linear epilogue", M, act)
     rng = np.random.default_rng(21 + M + act)
@@ -483,12 +496,13 @@ def test_linear_bias_lora_act(mlxq, M, act):
     A = bf16_normal(rng, (K, r), 0.01)
     B = bf16_normal(rng, (r, N), 0.01)
     rwq, rs, rb = oracle.quantize(w, 64, 4, sb_bf16=True)
-    y = to_np(mlxq.linear(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), 64, 4,
-                          bias=to_gpu(bias), lora_a=to_gpu(A), lora_b=to_gpu(B), lora_scale=0.75,
-                          activation=act))
-    ref = oracle.linear(x, rwq, rs, rb, 64, 4, w_bf16=(M > 8), act_bf16=True, bias=bias,
-                        lora_a=A, lora_b=B, lora_scale=0.75, act=act)
-    assert_close(y, ref, f"linear M={M} act={act}")
+    yt = mlxq.linear(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), 64, 4,
+                     bias=to_gpu(bias), lora_a=to_gpu(A), lora_b=to_gpu(B), lora_scale=0.75,
+                     activation=act)
+    ref, out_bf16 = oracle.linear(x, rwq, rs, rb, 64, 4, w_bf16=(M > 8), act_bf16=True, bias=bias,
+                                  lora_a=A, lora_b=B, lora_scale=0.75, act=act, return_dtype=True)
+    assert yt.dtype == (torch.bfloat16 if out_bf16 else torch.float32)  # GELU (act 1) promotes
+    assert_close(to_np(yt), ref, f"linear M={M} act={act}")
 
 
 @pytest.mark.parametrize("K", [64, 256, 320])
@@ -547,9 +561,9 @@ def test_config3_wan_projection_full_size_sampled_rows(mlxq):
     rwq, rs, rb = oracle.quantize(w, 64, 8, sb_bf16=True)
     assert np.array_equal(to_np(wq), rwq)
     assert np.array_equal(to_np(s), rs) and np.array_equal(to_np(b), rb)
-    rows = np.concatenate([[0, 255, 256, 32511, 32512, M - 1], np.sort(rng.choice(M, 26, replace=False))])
+    rows = _band_rows(rng, M)  # a row in every 224- and 256-row M-tile band
     ref = oracle.quantized_matmul(x[rows], rwq, rs, rb, 64, 8, w_bf16=True, out_bf16=True)
-    assert_close(to_np(y)[rows], ref, "config3 rows")
+    assert_close(to_np(y)[rows], ref, f"config3 {rows.size} rows (every M-tile band)")
 
 
 CONFIG5_SHAPES = [(9216, 3072), (3072, 3072), (12288, 3072), (3072, 12288), (18432, 3072)]
@@ -585,7 +599,10 @@ def test_config5_block_sweep_with_lora_sampled_rows(mlxq, bits, gs, N, K):
     gwq, gs_, gb = to_np(wq), to_np(s), to_np(b)
     rwq, rs, rb = oracle.quantize(w[:64], gs, bits, sb_bf16=True)
     assert np.array_equal(gwq[:64], rwq) and np.array_equal(gs_[:64], rs) and np.array_equal(gb[:64], rb)
-    rows = np.concatenate([[0, 255, 256, M - 1], np.sort(rng.choice(M, 12, replace=False))])
+    rows = _band_rows(rng, M)  # a row in every 224- and 256-row M-tile band
+    scale = 0.75 if (bits, gs, N, K) == (4, 64, 3072, 3072) else 1.0
+    if scale != 1.0:
+        y = mlxq.linear(gx, wq, s, b, gs, bits, lora_a=to_gpu(a), lora_b=to_gpu(bb), lora_scale=scale)
     ref = oracle.linear(x[rows], gwq, gs_, gb, gs, bits, w_bf16=True, act_bf16=True, lora_a=a,
-                        lora_b=bb, lora_scale=1.0)
-    assert_close(to_np(y)[rows], ref, f"config5 Q{bits} g{gs} {N}x{K}")
+                        lora_b=bb, lora_scale=scale)
+    assert_close(to_np(y)[rows], ref, f"config5 Q{bits} g{gs} {N}x{K} ({rows.size} rows)")

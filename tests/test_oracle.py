@@ -180,25 +180,117 @@ def test_gelu_tanh_closed_form_and_exact_gelu():
     assert oracle.gelu_tanh(8.0) == 8.0 and oracle.gelu_tanh(-8.0) == 0.0
 
 
-def test_linear_sequence_rounds_like_separate_ops():
-    """bias then LoRA residual, each rounded to bf16, equals composing the pieces by hand."""
-    rng = np.random.default_rng(4)
+def _torch_gelu_exact(v):
+    """src/nn.rs:344-355 in torch ops (each op in v's dtype, constants cast to it)."""
+    import torch
+    s2 = torch.tensor(math.sqrt(2.0), dtype=torch.float32).to(v.dtype)
+    inner = torch.erf(v / s2)
+    gate = torch.tensor(1.0, dtype=v.dtype) + inner
+    return (v * gate) / torch.tensor(2.0, dtype=v.dtype)
+
+
+def _torch_gelu_tanh(v):
+    """src/nn.rs:321-329 in torch ops (each op in v's dtype, constants cast to it)."""
+    import torch
+    c = torch.tensor(math.sqrt(2.0 / math.pi), dtype=torch.float32).to(v.dtype)
+    k = torch.tensor(0.044715, dtype=torch.float32).to(v.dtype)
+    x3 = (v.float() ** 3).to(v.dtype)  # MLX's power: one float pow, rounded once (torch's bf16
+    #                                     pow multiplies and rounds step by step)
+    inner = (v + x3 * k) * c
+    gate = torch.tanh(inner) + torch.tensor(1.0, dtype=v.dtype)
+    return (v * torch.tensor(0.5, dtype=v.dtype)) * gate
+
+
+def _all_bf16_values():
+    bits = np.arange(65536, dtype=np.uint32) << 16
+    v = bits.view(np.float32)
+    return v[np.isfinite(v)]
+
+
+@pytest.mark.parametrize("which", ["exact", "tanh"])
+def test_bf16_gelu_every_input_against_torch_ops(which):
+    """The oracle's per-op bf16 GELUs on every finite bf16 input against the same op sequence run
+    as torch bf16 tensor ops (an independent implementation of per-op bf16 rounding and of erf/
+    tanh).  A dropped op, a wrong constant or a wrong rounding point moves thousands of entries;
+    torch's own f32 erf/tanh are within an ulp, which can move a rare entry by one bf16 ulp."""
+    import torch
+    v = _all_bf16_values()
+    f = oracle.gelu_exact if which == "exact" else oracle.gelu_tanh
+    got = np.array([f(float(t)) for t in v], dtype=np.float32)
+    tf = _torch_gelu_exact if which == "exact" else _torch_gelu_tanh
+    want = tf(torch.from_numpy(v).to(torch.bfloat16)).float().numpy()
+    same = (got == want) | (np.isnan(got) & np.isnan(want))
+    bad = np.flatnonzero(~same)
+    ulps = np.abs(got[bad].view(np.int32) - want[bad].view(np.int32)) >> 16
+    print(f"{which}: {bad.size} of {v.size} inputs differ from torch's ops, max {ulps.max() if bad.size else 0} ulp")
+    assert bad.size <= 16 and (bad.size == 0 or ulps.max() <= 1)
+
+
+def test_gelu_exact_f32_is_the_closed_form():
+    # Per op in f32, 1 + erf(v/sqrt2) is computed to within an f32 ulp of 1, so the result is within
+    # |v| * 2^-23 (plus the other ops' relative rounding) of the closed form.
+    for v in (-5.0, -1.0, -0.25, 0.0, 0.3, 2.0, 7.0):
+        want = 0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0)))
+        got = oracle.gelu_exact(v, out_bf16=False)
+        assert abs(got - want) <= abs(v) * 2.0 ** -23 + abs(want) * 4e-7
+    # per-op bf16: 1 + erf rounds to 0 for large negative inputs, so the result is -0
+    assert oracle.gelu_exact(-4.0) == 0.0 and oracle.gelu_exact(4.0) == 4.0
+
+
+@pytest.mark.parametrize("bias_dt,lora_dt,act", [
+    ("bf16", "bf16", 0), ("bf16", "bf16", 1), ("bf16", "bf16", 2), ("bf16", "bf16", 3),
+    ("f32", "bf16", 0), ("bf16", "f32", 0), ("f32", "f32", 2), ("bf16", "f32", 3), (None, "f32", 1),
+])
+def test_linear_sequence_matches_torch_promotion(bias_dt, lora_dt, act):
+    """oracle.linear against the reference's op sequence (src/adapters.rs:309-320, :260-270,
+    :543-549) written as torch tensor ops on operands of the stated dtypes: torch promotes bf16 and
+    f32 exactly as MLX does (bf16 only when both operands are bf16) and rounds per op, so this
+    checks the oracle's promotion and rounding points by an independent route.  Matmuls are done
+    in float64 and rounded to their result dtype on both sides."""
+    import torch
+    rng = np.random.default_rng(4 + act)
     M, K, N, r = 6, 128, 40, 16
+    bf, f32 = torch.bfloat16, torch.float32
+    tdt = {"bf16": bf, "f32": f32}
     x = oracle.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
     w = oracle.bf16_round((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
-    bias = oracle.bf16_round(rng.standard_normal(N).astype(np.float32))
-    A = oracle.bf16_round((rng.standard_normal((K, r)) * 0.01).astype(np.float32))
-    B = oracle.bf16_round((rng.standard_normal((r, N)) * 0.01).astype(np.float32))
+    bias = rng.standard_normal(N).astype(np.float32)
+    A = (rng.standard_normal((K, r)) * 0.05).astype(np.float32)
+    B = (rng.standard_normal((r, N)) * 0.05).astype(np.float32)
+    if bias_dt == "bf16":
+        bias = oracle.bf16_round(bias)
+    if lora_dt == "bf16":
+        A, B = oracle.bf16_round(A), oracle.bf16_round(B)
     wq, s, b = oracle.quantize(w, 64, 4, sb_bf16=True)
-    y = oracle.linear(x, wq, s, b, 64, 4, bias=bias, lora_a=A, lora_b=B, lora_scale=0.5, act=1)
-    rb = oracle.bf16_round
-    y1 = oracle.quantized_matmul(x, wq, s, b, 64, 4)
-    y2 = rb(y1 + bias)
-    xa = rb((x.astype(np.float64) @ A.astype(np.float64)).astype(np.float32))
-    rr = rb((xa.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
-    y3 = rb(y2 + rb(rr * np.float32(0.5)))
-    want = np.vectorize(lambda v: oracle.gelu_erf(v))(y3).astype(np.float32)
-    assert np.array_equal(y, want)
+    y, out_bf16 = oracle.linear(x, wq, s, b, 64, 4, bias=None if bias_dt is None else bias,
+                                lora_a=A, lora_b=B, lora_scale=0.75, act=act, x_bf16=True,
+                                sb_bf16=True, bias_bf16=bias_dt == "bf16", lora_bf16=lora_dt == "bf16",
+                                return_dtype=True)
+    # torch restatement
+    t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a)).to(dt)
+    y0 = t(oracle.quantized_matmul(x, wq, s, b, 64, 4, out_bf16=False), f32).to(bf)
+    out = y0 + t(bias, tdt[bias_dt]) if bias_dt else y0
+    dr = bf if lora_dt == "bf16" else f32
+    xa = t(x.astype(np.float64) @ A.astype(np.float64), f32).to(dr)
+    rr = t(xa.double().numpy() @ B.astype(np.float64), f32).to(dr)
+    out = out + rr * torch.tensor(0.75, dtype=f32).to(dr)
+    if act == 1:
+        out = t(0.5 * out.double().numpy() * (1.0 + np.vectorize(math.erf)(out.double().numpy() /
+                                                                          math.sqrt(2.0))), f32)
+    elif act == 2:
+        out = _torch_gelu_tanh(out)
+    elif act == 3:
+        out = _torch_gelu_exact(out)
+    assert out_bf16 == (out.dtype == bf)
+    want = out.float().numpy()
+    if act in (0, 1):
+        tol = 0.0 if act == 0 else 1e-6
+        np.testing.assert_allclose(y, want, rtol=tol, atol=0)
+    elif out_bf16:  # bf16: every input agrees with torch's ops (test above)
+        np.testing.assert_array_equal(y, want)
+    else:  # f32: torch's float erf / tanh are within a few ulps of the oracle's double ones
+        diff = np.abs(y.view(np.int32) - want.view(np.int32))
+        assert (diff <= 8).all()
 
 
 def test_invalid_shapes_rejected():

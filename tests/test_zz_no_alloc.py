@@ -42,7 +42,7 @@ def _run(mlxq, c, noalloc, scale, act):
     lib = _lib.load()
     y = torch.empty((c["M"], c["N"]), dtype=torch.bfloat16, device="cuda")
     ep = _lib.Epilogue(c["bias"].data_ptr(), c["A"].data_ptr(), c["B"].data_ptr(), c["rank"],
-                       float(scale), int(act))
+                       float(scale), int(act), _lib.MLXQ_BFLOAT16, _lib.MLXQ_BFLOAT16)
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     args = [c["x"].data_ptr(), _lib.MLXQ_BFLOAT16, c["M"], c["K"], c["wq"].data_ptr(),
             c["s"].data_ptr(), c["b"].data_ptr(), _lib.MLXQ_BFLOAT16, c["N"], 64, 4,
@@ -50,7 +50,8 @@ def _run(mlxq, c, noalloc, scale, act):
     if noalloc:
         _lib.check(lib.mlxq_linear_noalloc(*args, st))
     else:
-        need = int(lib.mlxq_linear_workspace_size(c["M"], c["N"], c["rank"]))
+        need = int(lib.mlxq_linear_workspace_size(_lib.MLXQ_BFLOAT16, _lib.MLXQ_BFLOAT16, c["M"], c["N"],
+                                                  ctypes.byref(ep)))
         ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
         _lib.check(lib.mlxq_linear(*args, ws.data_ptr(), need, st))
         torch.cuda.synchronize()
@@ -69,7 +70,7 @@ def test_noalloc_matches_workspace_entry_point(mlxq, first, second):
     for i, (M, K, N, rank) in enumerate((first, second)):
         banner("noalloc", i, M, K, N, rank)
         c = _case(rng, M, K, N, rank)
-        scale, act = (0.75, 1) if i == 0 else (1.5, 0)
+        scale, act = (0.75, 3) if i == 0 else (1.5, 0)
         want = _run(mlxq, c, False, scale, act)
         got = _run(mlxq, c, True, scale, act)
         assert torch.equal(got, want), f"call {i}: noalloc output differs (M={M} N={N} r={rank})"
@@ -80,9 +81,10 @@ def test_noalloc_rejects_oversized_scratch(mlxq):
     lib = _lib.load()
     banner("noalloc oversized")
     M, N, rank = 1 << 16, 1 << 14, 64
-    need = int(lib.mlxq_linear_workspace_size(M, N, rank))
+    ep = _lib.Epilogue(None, 16, 16, rank, 1.0, 0, _lib.MLXQ_BFLOAT16, _lib.MLXQ_BFLOAT16)
+    need = int(lib.mlxq_linear_workspace_size(_lib.MLXQ_BFLOAT16, _lib.MLXQ_BFLOAT16, M, N,
+                                              ctypes.byref(ep)))
     assert need > _lib.MLXQ_NOALLOC_SCRATCH_BYTES
-    ep = _lib.Epilogue(None, 16, 16, rank, 1.0, 0)
     p = ctypes.c_void_p(16)
     st = lib.mlxq_linear_noalloc(p, _lib.MLXQ_BFLOAT16, M, 512, p, p, p, _lib.MLXQ_BFLOAT16, N, 64, 4,
                                  ctypes.byref(ep), p, None)
