@@ -156,17 +156,28 @@ def bench_gemv(mlxq, torch, reps=20):
                 mlxq.swiglu(x, g, u, 64, 4, out=h)
                 mlxq.qmv(h, *d, 64, 4, out=yd)
 
+        def valu():
+            for (g, u, d) in copies:
+                mlxq.qmv_valu(x, *g, 64, 4, out=yg)
+                mlxq.qmv_valu(x, *u, 64, 4, out=yu)
+                mlxq.qmv_valu(hh, *d, 64, 4, out=yd)
+
         us3 = graph_ms(torch, mlps, inner=1, reps=reps) * 1e3 / len(copies)
         us2 = graph_ms(torch, fused, inner=1, reps=reps) * 1e3 / len(copies)
+        usv = graph_ms(torch, valu, inner=1, reps=reps) * 1e3 / len(copies)
         nbytes3 = 2 * wbytes_gu + wbytes_d + 2 * (2 * M * K) + 2 * (2 * M * F) + 2 * M * F + 2 * M * K
         nbytes2 = 2 * wbytes_gu + wbytes_d + 2 * M * K + 2 * M * F + 2 * M * F + 2 * M * K
         out[f"M{M}"] = {"us_per_mlp": round(us3, 3), "GBs": round(nbytes3 / (us3 * 1e-6) / 1e9, 1),
                         "bytes_per_mlp": nbytes3,
                         "fused_us_per_mlp": round(us2, 3),
-                        "fused_GBs": round(nbytes2 / (us2 * 1e-6) / 1e9, 1)}
+                        "fused_GBs": round(nbytes2 / (us2 * 1e-6) / 1e9, 1),
+                        "fused_frac_of_hbm_peak": round(nbytes2 / (us2 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                        "valu_us_per_mlp": round(usv, 3),
+                        "valu_GBs": round(nbytes3 / (usv * 1e-6) / 1e9, 1)}
     out["note"] = ("per decode MLP, replayed from a HIP graph (rates include inter-kernel gaps): "
-                   "3 GEMV launches (gate, up, down) and the fused form (SwiGLU gate/up launch + "
-                   "down launch); per-kernel durations are in profiles/")
+                   "3 matrix-core GEMV launches (gate, up, down); the fused form (SwiGLU gate/up "
+                   "launch + down launch); and, for the kernel-choice A/B, 3 VALU GEMV launches "
+                   "(mlxq_qmv_valu); per-kernel durations are in profiles/")
     return out
 
 

@@ -126,6 +126,13 @@ int mlxq_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* w
              const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
              int bits, void* y, void* stream);
 
+/* The VALU GEMV (no matrix cores; exact f32 dequant); any x / scales dtype; 1 <= M <= 8; y in
+ * promote(x_dtype, sb_dtype).  The kernel quantized_matmul uses for f32 operands and group size
+ * 32; forced here so it can be measured against the matrix-core GEMV on bf16 decode shapes. */
+int mlxq_qmv_valu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
+                  const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
+                  int bits, void* y, void* stream);
+
 /*
  * Fused AdaptableLinear forward over a quantized base — replaces the op sequence of
  * LinearBase::forward's quantized arm plus AdaptableLinear::forward (src/adapters.rs:300-322,

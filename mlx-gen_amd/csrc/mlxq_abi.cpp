@@ -271,6 +271,19 @@ int mlxq_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* w
                  (hipStream_t)stream);
 }
 
+int mlxq_qmv_valu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
+                  const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
+                  int bits, void* y, void* stream) {
+  g_err[0] = 0;
+  int rc;
+  if ((rc = check_mm("qmv_valu", x, x_dtype, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y)))
+    return rc;
+  if (M > 8) return set_error(MLXQ_EINVAL, "qmv_valu: M=%lld exceeds the GEMV limit of 8", (long long)M);
+  if (M == 0 || N == 0) return MLXQ_OK;
+  return run_qmv_valu(x, x_dtype, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y,
+                      (hipStream_t)stream);
+}
+
 int mlxq_quantized_matmul(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
                           const void* scales, const void* biases, int sb_dtype, int64_t N,
                           int transpose, int group_size, int bits, void* y, void* stream) {

@@ -86,6 +86,10 @@ bool swiglu_qmv_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int6
 int run_swiglu_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq_g, const void* s_g,
                    const void* b_g, const uint32_t* wq_u, const void* s_u, const void* b_u, int64_t F,
                    int gs, int bits, void* h, hipStream_t st);
+// The VALU GEMV with exact f32 dequant, whatever the operand dtypes (the forced-kernel entry
+// point for measuring it against the matrix-core GEMV).
+int run_qmv_valu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+                 const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st);
 int run_embedding(const int32_t* ids, int64_t T, const uint32_t* wq, const void* s, const void* b,
                   int sb_dtype, int64_t vocab, int64_t hidden, int gs, int bits, void* out,
                   int out_dtype, hipStream_t st);

@@ -223,7 +223,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   }
   // Buffer resources: 32-bit offsets (the host checks every operand fits in 4 GiB).  Rows past
   // M / N are clamped so every offset stays inside its operand.
-  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+  [[maybe_unused]] const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(x), (short)0, (int)(uint32_t)(M * K * 2), kBufferFlags);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(wq), (short)0, (int)(uint32_t)(N * kwords * 4), kBufferFlags);

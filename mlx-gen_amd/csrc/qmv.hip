@@ -179,19 +179,24 @@ static int qmv_bits_gs(const void* x, int64_t M, int64_t K, const uint32_t* wq, 
   return set_error(MLXQ_EINVAL, "qmv: unsupported bits=%d group_size=%d", bits, gs);
 }
 
-// Exact-f32-dequant matmul for any M (M <= 8 is the decode GEMV; larger M tiles the grid in y).
-int run_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
-            const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st) {
-  // bf16 activations with 64/128 groups take the matrix-core GEMV; f32 activations and
-  // group_size 32 take the VALU kernel below (same exact-f32 dequant semantics).
-  if (qmv_mfma_applicable(x_dtype, sb_dtype, M, K, N, gs, bits))
-    return run_qmv_mfma(x, M, K, wq, s, b, N, gs, bits, y, st);
+int run_qmv_valu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+                 const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st) {
   if (x_dtype == MLXQ_BFLOAT16) {
     if (sb_dtype == MLXQ_BFLOAT16) return qmv_bits_gs<uint16_t, uint16_t>(x, M, K, wq, s, b, N, gs, bits, y, st);
     return qmv_bits_gs<uint16_t, float>(x, M, K, wq, s, b, N, gs, bits, y, st);
   }
   if (sb_dtype == MLXQ_BFLOAT16) return qmv_bits_gs<float, uint16_t>(x, M, K, wq, s, b, N, gs, bits, y, st);
   return qmv_bits_gs<float, float>(x, M, K, wq, s, b, N, gs, bits, y, st);
+}
+
+// Exact-f32-dequant matmul for any M (M <= 8 is the decode GEMV; larger M tiles the grid in y).
+int run_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+            const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st) {
+  // bf16 activations with 64/128 groups take the matrix-core GEMV; f32 activations and
+  // group_size 32 take the VALU kernel above (same exact-f32 dequant semantics).
+  if (qmv_mfma_applicable(x_dtype, sb_dtype, M, K, N, gs, bits))
+    return run_qmv_mfma(x, M, K, wq, s, b, N, gs, bits, y, st);
+  return run_qmv_valu(x, x_dtype, M, K, wq, s, b, sb_dtype, N, gs, bits, y, st);
 }
 
 }  // namespace mlxq

@@ -78,6 +78,12 @@ __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+// Raw buffer resource over `bytes` bytes at p: loads at offsets past the end return zero.
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const T* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(p), (short)0, bytes, kBufferFlags);
+}
+
 // v_permlane32_swap_b32: lanes 32..63 of `lo_keep` trade places with lanes 0..31 of `hi_keep`.
 // Afterwards lanes 0..31 still hold their own `lo_keep` and lanes 32..63 their own `hi_keep`.
 __device__ __forceinline__ void swap_lane_halves(uint32_t& lo_keep, uint32_t& hi_keep) {
@@ -95,6 +101,14 @@ __host__ __device__ constexpr int sz_pitch(int G) {
   return (p & 4) ? p : p + 4;
 }
 
+// Whether a tile of `steps` load steps per wave and MR activation rows stays within the 128
+// registers per lane of a 1024-thread workgroup (the counts the compiler reports for these
+// kernels): 8 steps only with one row, and for Q4 with group 64 (two groups per step) 6 steps
+// with at most two rows.  Larger combinations spilled (and spills doubled a launch's time).
+constexpr bool qmv_steps_fit(int bits, bool g64, int steps, int mr) {
+  return !(steps == 8 && mr > 1) && !(bits == 4 && g64 && steps == 6 && mr > 2);
+}
+
 }  // namespace
 
 // Scale/bias group slots one wave keeps: the groups its load steps touch (a group 128 of Q8 spans
@@ -109,198 +123,203 @@ __host__ __device__ constexpr int qmv_wave_lds(int bits, bool g64, int steps, in
   return M * (steps * (512 / bits) * 2 + 16) + 16 * sz_pitch(qmv_wave_groups(bits, g64, steps)) * 4;
 }
 
-// Launch contract (checked on the host by qmv_plan): 1 <= M <= MR, K % (512/BITS) == 0,
-// K % group == 0, bf16 scales and biases, LS = K*BITS/512 load steps per row with
-// LS % STEPS == 0 and blockDim.x = 64 * NMAT * LS/STEPS <= 1024, dynamic LDS of at least
-// max(waves * qmv_wave_lds, waves * 16 * 17 * 4) bytes, every buffer < 2 GiB.
-// NMAT = 2 is the SwiGLU decode form: the second wave half streams the same 16 rows of a second
-// matrix (up) and the output is round(round(silu(round(x.Wg^T))) * round(x.Wu^T)).
-// Each wave stages only its own operands (its K range of the activations, the scales and biases
-// of its groups) into its own LDS region, so it starts on its weights as soon as its own operands
-// land; the only workgroup barrier is the final split-K reduction.
-template <int BITS, bool G64, int STEPS, int MR, int NMAT>
-__global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
-    const uint16_t* __restrict__ x, int M, int K, const uint32_t* __restrict__ wq,
-    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    const uint32_t* __restrict__ wq2, const uint16_t* __restrict__ scales2,
-    const uint16_t* __restrict__ biases2, int N, uint16_t* __restrict__ y) {
-  constexpr int CPL = 512 / BITS;          // codes per row in one 64-byte load step
-  constexpr int GS = G64 ? 64 : 128;       // group size
-  constexpr int NM = BITS == 4 ? 4 : 2;    // MFMAs per load step
-  constexpr int E = MR < 4 ? MR : 4;       // result registers per lane that can hold a row < M
-  constexpr int XCH = STEPS * CPL / 8;     // 16-byte activation chunks per row in the wave's range
-  constexpr int XSL = (XCH + 63) / 64;     // ... per lane
-  constexpr int NGW = qmv_wave_groups(BITS, G64, STEPS);
-  constexpr int PW = sz_pitch(NGW);        // (s, zc) table row pitch, floats
-  constexpr int SBL = (16 * NGW + 63) / 64;  // scale entries per lane
-  constexpr int XW = STEPS * CPL * 2 + 16;   // LDS pitch of the wave's activation rows
-  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+// One 16-row GEMV tile as seen by one wave: the wave's K range of load steps, the operand
+// registers between the issue of its loads and their use, and its private LDS region.
+// Contract of every kernel built from it (checked on the host by qmv_plan):
+// 1 <= M <= MR, K % (512/BITS) == 0, K % group == 0, bf16 scales and biases, the row's
+// K*BITS/512 load steps split evenly over the waves of one matrix (STEPS each), dynamic LDS of at
+// least max(waves * qmv_wave_lds, waves * 16 * 17 * 4) bytes, every buffer < 2 GiB.
+template <int BITS, bool G64, int STEPS, int MR>
+struct GemvTile {
+  static constexpr int CPL = 512 / BITS;          // codes per row in one 64-byte load step
+  static constexpr int GS = G64 ? 64 : 128;       // group size
+  static constexpr int NM = BITS == 4 ? 4 : 2;    // MFMAs per load step
+  static constexpr int E = MR < 4 ? MR : 4;       // result registers per lane that can hold a row < M
+  static constexpr int XCH = STEPS * CPL / 8;     // 16-byte activation chunks per row in the wave's range
+  static constexpr int XSL = (XCH + 63) / 64;     // ... per lane
+  static constexpr int NGW = qmv_wave_groups(BITS, G64, STEPS);
+  static constexpr int PW = sz_pitch(NGW);        // (s, zc) table row pitch, floats
+  static constexpr int SBL = (16 * NGW + 63) / 64;  // scale entries per lane
+  static constexpr int XW = STEPS * CPL * 2 + 16;   // LDS pitch of the wave's activation rows
 
-  const int NT = blockDim.x;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int W = (NT >> 6) / NMAT;  // waves per matrix
-  const int mat = NMAT == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave_all / W);
-  const int wave = wave_all - mat * W;  // index within this wave's matrix
-  const int c16 = lane & 15, q = lane >> 4;
-  const int n0 = blockIdx.x * 16;
-  const int n = n0 + c16;
-  const int nn = n < N ? n : N - 1;
-  const int rowbytes = K * BITS / 8;
-  const int G = K / GS;
-  const int ls0 = wave * STEPS;  // this wave's load steps: [ls0, ls0 + STEPS)
-  const int kb = ls0 * CPL;      // its first activation index
-  const int g0 = kb / GS;        // its first group
-  unsigned char* const wl = lds + wave_all * (M * XW + 16 * PW * 4);  // this wave's LDS region
-  float* const szw = reinterpret_cast<float*>(wl + M * XW);
-
-  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(x), (short)0, M * K * 2, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(mat ? wq2 : wq), (short)0, (int)((uint32_t)N * (uint32_t)rowbytes), kBufferFlags);
-  // Rounded up to whole dwords: buffer range checks are per dword, and the last scale may share
-  // its dword with 2 bytes past the end (same aligned dword, so never another page).
-  const int sb_total = (int)(((uint32_t)N * (uint32_t)G * 2u + 3u) & ~3u);
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(mat ? scales2 : scales), (short)0, sb_total, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(mat ? biases2 : biases), (short)0, sb_total, kBufferFlags);
-
-  // 1. The wave's own operands first (they return before its weight stream): its activation
-  //    range as 16-byte chunks, and the scale and bias of each (row, group) slot it folds.
-  //    Out-of-range loads read as zero.
+  int lane, c16, q, n0, M, K, N, G, ls0, kb, g0;
+  unsigned char* wl;  // this wave's LDS region: activation rows, then the (s, zc) table
+  float* szw;
   u32x4 cx[MR][XSL];
-#pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    if (m < M) {
-#pragma unroll
-      for (int j = 0; j < XSL; ++j) {
-        const int c = lane + 64 * j;
-        cx[m][j] = load16(rx, c < XCH ? (uint32_t)((m * K + kb + c * 8) * 2) : kOob);
-      }
-    }
-  }
   uint32_t cs[SBL], cz[SBL];
-#pragma unroll
-  for (int j = 0; j < SBL; ++j) {
-    const int e = lane + 64 * j;
-    const int r = e / NGW, gl = e - r * NGW;  // constant divisor
-    const bool ok = e < 16 * NGW && n0 + r < N && g0 + gl < G;
-    const uint32_t off = ok ? ((uint32_t)(n0 + r) * (uint32_t)G + (uint32_t)(g0 + gl)) * 2u : kOob;
-    cs[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
-    cz[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rz, off, 0, 0);
+  u32x4 wv[STEPS];
+
+  // wave_all: the wave's index in the workgroup (selects its LDS region); wave: its index among
+  // the waves of its matrix (selects its K range); rows [n0, n0 + 16) of an [N, K] matrix.
+  __device__ __forceinline__ GemvTile(int lane_, int wave_all, int wave, int n0_, int M_, int K_,
+                                      int N_, unsigned char* lds) {
+    lane = lane_;
+    c16 = lane & 15;
+    q = lane >> 4;
+    n0 = n0_;
+    M = M_;
+    K = K_;
+    N = N_;
+    G = K / GS;
+    ls0 = wave * STEPS;
+    kb = ls0 * CPL;
+    g0 = kb / GS;
+    wl = lds + wave_all * (M * XW + 16 * PW * 4);
+    szw = reinterpret_cast<float*>(wl + M * XW);
   }
 
-  // 2. The wave's whole weight stream, issued once every wave of the workgroup has issued its
-  //    operand loads: a CU's vector memory requests are served in order, and a wave whose small
-  //    operand loads queue behind its neighbours' weight streams waits microseconds for them.
-  //    (A bare s_barrier: nothing here waits for the loads themselves.)
-  __builtin_amdgcn_s_barrier();
-  const uint32_t w_base = (uint32_t)nn * (uint32_t)rowbytes + (uint32_t)(ls0 * 64 + q * 16);
-  u32x4 wv[STEPS];
+  // The wave's activation range as 16-byte chunks (out-of-range chunks read as zero).
+  __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t rx) {
 #pragma unroll
-  for (int d = 0; d < STEPS; ++d) wv[d] = load16(rw, w_base + (uint32_t)d * 64u);
-
-  // 3. Operands into the wave's LDS region.  Q4 activation runs are stored permuted to
-  //    [0,2,4,6,1,3,5,7] so they pair with the unpacked code layout; scales and biases become
-  //    f32 pairs (s, b - 128 s) for Q4 and (s, b) for Q8, ready for the fold.  Only this wave
-  //    reads them back, so a wave-level ordering point replaces a workgroup barrier.
+    for (int m = 0; m < MR; ++m) {
+      if (m < M) {
 #pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    if (m < M) {
-#pragma unroll
-      for (int j = 0; j < XSL; ++j) {
-        const int c = lane + 64 * j;
-        if (c < XCH)
-          *reinterpret_cast<u32x4*>(wl + m * XW + c * 16) = BITS == 4 ? perm_q4(cx[m][j]) : cx[m][j];
+        for (int j = 0; j < XSL; ++j) {
+          const int c = lane + 64 * j;
+          cx[m][j] = load16(rx, c < XCH ? (uint32_t)((m * K + kb + c * 8) * 2) : kOob);
+        }
       }
     }
   }
+
+  // The scale and bias of each (row, group) slot the wave folds.
+  __device__ __forceinline__ void issue_sb(__amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rz) {
 #pragma unroll
-  for (int j = 0; j < SBL; ++j) {
-    const int e = lane + 64 * j;
-    if (e < 16 * NGW) {
-      const int r = e / NGW, gl = e - r * NGW;
-      const float sv = __uint_as_float(cs[j] << 16), zv = __uint_as_float(cz[j] << 16);
-      *reinterpret_cast<f32x2*>(szw + r * PW + 2 * gl) = f32x2{sv, BITS == 4 ? fmaf(-128.0f, sv, zv) : zv};
+    for (int j = 0; j < SBL; ++j) {
+      const int e = lane + 64 * j;
+      const int r = e / NGW, gl = e - r * NGW;  // constant divisor
+      const bool ok = e < 16 * NGW && n0 + r < N && g0 + gl < G;
+      const uint32_t off = ok ? ((uint32_t)(n0 + r) * (uint32_t)G + (uint32_t)(g0 + gl)) * 2u : kOob;
+      cs[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+      cz[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rz, off, 0, 0);
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // 4. Per load step: NM MFMAs x . codes and NM MFMAs x . ones (group sums), then the fold of
-  //    each group, y += s*acc + zc*X.
-  const unsigned char* xa[NM];  // this lane's activation run for MFMA i at the wave's first step
+  // The wave's whole weight stream: 16 rows x 64 contiguous bytes per load, rows past N clamped
+  // (never stored).
+  __device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t rw) {
+    const int n = n0 + c16;
+    const int nn = n < N ? n : N - 1;
+    const uint32_t w_base = (uint32_t)nn * (uint32_t)(K * BITS / 8) + (uint32_t)(ls0 * 64 + q * 16);
 #pragma unroll
-  for (int i = 0; i < NM; ++i) {
-    int k;
-    if constexpr (BITS == 8) k = 16 * q + 8 * i;
-    else if constexpr (!G64) k = 32 * q + 8 * i;
-    else if (i < 2) k = (q < 2 ? 32 * q : 32 * (q - 2) + 16) + 8 * i;
-    else k = (q < 2 ? 64 + 32 * q : 32 * q + 16) + 8 * (i - 2);
-    xa[i] = wl + (c16 < M ? c16 : 0) * XW + k * 2;
+    for (int d = 0; d < STEPS; ++d) wv[d] = load16(rw, w_base + (uint32_t)d * 64u);
   }
-  const float* sz = szw + c16 * PW;
-  bf16x8 ones;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
-  float yacc[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) yacc[e] = 0.0f;
 
-  auto fold = [&](const f32x4& acc, const f32x4& xsum, float s, float zc) {
+  // Operands into the wave's LDS region.  Q4 activation runs are stored permuted to
+  // [0,2,4,6,1,3,5,7] so they pair with the unpacked code layout; scales and biases become
+  // f32 pairs (s, b - 128 s) for Q4 and (s, b) for Q8, ready for the fold.  Only this wave
+  // reads them back, so a wave-level ordering point replaces a workgroup barrier.
+  __device__ __forceinline__ void stage() {
 #pragma unroll
-    for (int e = 0; e < E; ++e) yacc[e] = fmaf(s, acc[e], fmaf(zc, xsum[e], yacc[e]));
-  };
+    for (int m = 0; m < MR; ++m) {
+      if (m < M) {
+#pragma unroll
+        for (int j = 0; j < XSL; ++j) {
+          const int c = lane + 64 * j;
+          if (c < XCH)
+            *reinterpret_cast<u32x4*>(wl + m * XW + c * 16) = BITS == 4 ? perm_q4(cx[m][j]) : cx[m][j];
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < SBL; ++j) {
+      const int e = lane + 64 * j;
+      if (e < 16 * NGW) {
+        const int r = e / NGW, gl = e - r * NGW;
+        const float sv = __uint_as_float(cs[j] << 16), zv = __uint_as_float(cz[j] << 16);
+        *reinterpret_cast<f32x2*>(szw + r * PW + 2 * gl) = f32x2{sv, BITS == 4 ? fmaf(-128.0f, sv, zv) : zv};
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
 
-  // Activation runs: only lanes of A rows c16 < M read them (at M = 1 that is 4 lanes of 64, a
-  // sixteenth of the LDS traffic).  The other lanes keep their previous (finite) contents: an A
-  // row m >= M only feeds result row m, which is never stored.
-  const bool row_lane = c16 < M;
-  bf16x8 a[NM];
-#pragma unroll
-  for (int i = 0; i < NM; ++i) a[i] = bf16x8{};
-
-#pragma unroll
-  for (int d = 0; d < STEPS; ++d) {
-    if (row_lane) {
-#pragma unroll
-      for (int i = 0; i < NM; ++i) a[i] = *reinterpret_cast<const bf16x8*>(xa[i] + d * (CPL * 2));
-    }
-    uint32_t w[4] = {wv[d][0], wv[d][1], wv[d][2], wv[d][3]};
-    if constexpr (BITS == 4 && G64) {
-      swap_lane_halves(w[0], w[2]);
-      swap_lane_halves(w[1], w[3]);
-    }
-    f32x4 acc[2], xsum[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      acc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      xsum[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
+  // Per load step: NM MFMAs x . codes and NM MFMAs x . ones (group sums), then the fold of
+  // each group, y += s*acc + zc*X.  yacc[e] is result row 4q + e of column c16.
+  __device__ __forceinline__ void fold(float (&yacc)[E]) const {
+    const unsigned char* xa[NM];  // this lane's activation run for MFMA i at the wave's first step
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
-      const int h = (BITS == 4 && G64) ? i >> 1 : 0;
-      const bf16x8 b = BITS == 4 ? unpack_q4(w[i]) : cvt_q8(w[2 * i], w[2 * i + 1]);
-      acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b, acc[h], 0, 0, 0);
-      xsum[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], ones, xsum[h], 0, 0, 0);
+      int k;
+      if constexpr (BITS == 8) k = 16 * q + 8 * i;
+      else if constexpr (!G64) k = 32 * q + 8 * i;
+      else if (i < 2) k = (q < 2 ? 32 * q : 32 * (q - 2) + 16) + 8 * i;
+      else k = (q < 2 ? 64 + 32 * q : 32 * q + 16) + 8 * (i - 2);
+      xa[i] = wl + (c16 < M ? c16 : 0) * XW + k * 2;
     }
-    if constexpr (BITS == 4 && G64) {
-      const f32x4 p = *reinterpret_cast<const f32x4*>(sz + 4 * d);  // groups 2ls, 2ls+1
-      fold(acc[0], xsum[0], p[0], p[1]);
-      fold(acc[1], xsum[1], p[2], p[3]);
-    } else {
-      // Q4/128 and Q8/64: one group per step; Q8/128: a group every two steps
-      const int gl = (BITS == 4 || G64) ? d : ((ls0 + d) >> 1) - g0;
-      const f32x2 p = *reinterpret_cast<const f32x2*>(sz + 2 * gl);
-      fold(acc[0], xsum[0], p[0], p[1]);
+    const float* sz = szw + c16 * PW;
+    bf16x8 ones;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) yacc[e] = 0.0f;
+
+    auto fold1 = [&](const f32x4& acc, const f32x4& xsum, float s, float zc) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) yacc[e] = fmaf(s, acc[e], fmaf(zc, xsum[e], yacc[e]));
+    };
+
+    // Activation runs: only lanes of A rows c16 < M read them (at M = 1 that is 4 lanes of 64, a
+    // sixteenth of the LDS traffic).  The other lanes keep their previous (finite) contents: an A
+    // row m >= M only feeds result row m, which is never stored.
+    const bool row_lane = c16 < M;
+    bf16x8 a[NM];
+#pragma unroll
+    for (int i = 0; i < NM; ++i) a[i] = bf16x8{};
+
+#pragma unroll
+    for (int d = 0; d < STEPS; ++d) {
+      // Scheduling fences around each step's MFMAs: without them the scheduler interleaves
+      // steps and keeps several steps' operands and partial sums live at once (the Q4 g64
+      // decode kernels then ran out of registers).
+      __builtin_amdgcn_sched_barrier(0);
+      if (row_lane) {
+#pragma unroll
+        for (int i = 0; i < NM; ++i) a[i] = *reinterpret_cast<const bf16x8*>(xa[i] + d * (CPL * 2));
+      }
+      uint32_t w[4] = {wv[d][0], wv[d][1], wv[d][2], wv[d][3]};
+      if constexpr (BITS == 4 && G64) {
+        swap_lane_halves(w[0], w[2]);
+        swap_lane_halves(w[1], w[3]);
+      }
+      f32x4 acc[2], xsum[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        acc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        xsum[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        const int h = (BITS == 4 && G64) ? i >> 1 : 0;
+        const bf16x8 b = BITS == 4 ? unpack_q4(w[i]) : cvt_q8(w[2 * i], w[2 * i + 1]);
+        acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b, acc[h], 0, 0, 0);
+        xsum[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], ones, xsum[h], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (BITS == 4 && G64) {
+        const f32x4 p = *reinterpret_cast<const f32x4*>(sz + 4 * d);  // groups 2ls, 2ls+1
+        fold1(acc[0], xsum[0], p[0], p[1]);
+        fold1(acc[1], xsum[1], p[2], p[3]);
+      } else {
+        // Q4/128 and Q8/64: one group per step; Q8/128: a group every two steps
+        const int gl = (BITS == 4 || G64) ? d : ((ls0 + d) >> 1) - g0;
+        const f32x2 p = *reinterpret_cast<const f32x2*>(sz + 2 * gl);
+        fold1(acc[0], xsum[0], p[0], p[1]);
+      }
     }
   }
+};
 
-  // 5. Split-K reduction through LDS (reuses the operand area): [wave][m 0..15][n 0..15].
-  //    Only rows 4q + e with e < E can be < M; the rest are never written or read.
+// Split-K reduction of a tile's partial sums through LDS (reusing the operand area):
+// [wave][m 0..15][n 0..15], waves [0, W) of matrix 0 and [W, 2W) of matrix 1.  Only rows
+// 4q + e with e < E can be < M; the rest are never written or read.  NMAT = 2 stores
+// round(round(silu(round(g))) * round(u)) (qwen3.rs:178-181), else round(y), into y [M, N].
+template <int NMAT, int E>
+__device__ __forceinline__ void gemv_reduce_store(unsigned char* lds, const float (&yacc)[E],
+                                                  int wave_all, int W, int lane, int tid, int NT,
+                                                  int M, int n0, int N, uint16_t* __restrict__ y) {
+  const int c16 = lane & 15, q = lane >> 4;
   __syncthreads();
   float* red = reinterpret_cast<float*>(lds);
 #pragma unroll
@@ -322,6 +341,41 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   }
 }
 
+// The GEMV launch: a workgroup owns 16 weight rows and its waves split K.  NMAT = 2 is the
+// SwiGLU decode form: the second wave half streams the same 16 rows of a second matrix (up).
+// Each wave stages only its own operands (its K range of the activations, the scales and biases
+// of its groups) into its own LDS region, so it starts on its weights as soon as its own operands
+// land; the only workgroup barrier is the final split-K reduction.
+template <int BITS, bool G64, int STEPS, int MR, int NMAT>
+__global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
+    const uint16_t* __restrict__ x, int M, int K, const uint32_t* __restrict__ wq,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const uint32_t* __restrict__ wq2, const uint16_t* __restrict__ scales2,
+    const uint16_t* __restrict__ biases2, int N, uint16_t* __restrict__ y) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int NT = blockDim.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int W = (NT >> 6) / NMAT;  // waves per matrix
+  const int mat = NMAT == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave_all / W);
+  const int n0 = blockIdx.x * 16;
+  GemvTile<BITS, G64, STEPS, MR> t(lane, wave_all, wave_all - mat * W, n0, M, K, N, lds);
+  const int sb_total = (int)(((uint32_t)N * (uint32_t)t.G * 2u + 3u) & ~3u);  // whole dwords
+  t.issue_x(make_rsrc(x, M * K * 2));
+  t.issue_sb(make_rsrc(mat ? scales2 : scales, sb_total), make_rsrc(mat ? biases2 : biases, sb_total));
+  // The weight streams are issued once every wave of the workgroup has issued its operand
+  // loads: a CU's vector memory requests are served in order, and a wave whose small operand
+  // loads queue behind its neighbours' weight streams waits microseconds for them.  (A bare
+  // s_barrier: nothing here waits for the loads themselves.)
+  __builtin_amdgcn_s_barrier();
+  t.issue_w(make_rsrc(mat ? wq2 : wq, (int)((uint32_t)N * (uint32_t)(K * BITS / 8))));
+  t.stage();
+  float yacc[GemvTile<BITS, G64, STEPS, MR>::E];
+  t.fold(yacc);
+  gemv_reduce_store<NMAT>(lds, yacc, wave_all, W, lane, tid, NT, M, n0, N, y);
+}
+
 namespace {
 
 struct QmvPlan {
@@ -331,13 +385,12 @@ struct QmvPlan {
 constexpr int kStepChoices[] = {1, 2, 3, 4, 6, 8};
 
 // Picks the load steps per wave: among the counts that divide the row's load steps, fit a
-// workgroup of at most kMaxWaves waves and its LDS, the one whose workgroup comes closest to 8
-// waves (fewer steps on a tie).  Measured on the decode shapes (M = 1..8, K = 3072 and 8192, with
-// per-wave operand staging), about 8 waves of 3-8 steps finish first: a wave starts folding as
-// soon as its own operands arrive, and more, shorter waves spread the fold over the SIMDs, while
-// a 16-wave workgroup fills a CU on its own (128 registers per wave).  Eight steps with more than
-// one activation row exceed the 128 registers a 1024-thread workgroup allows (spills doubled the
-// time), so that combination is not used.
+// workgroup of at most kMaxWaves waves, its LDS and its registers (qmv_steps_fit), the one whose
+// workgroup comes closest to 8 waves (fewer steps on a tie).  Measured on the decode shapes
+// (M = 1..8, K = 3072 and 8192, with per-wave operand staging), about 8 waves of 3-8 steps finish
+// first: a wave starts folding as soon as its own operands arrive, and more, shorter waves spread
+// the fold over the SIMDs, while a 16-wave workgroup fills a CU on its own (128 registers per
+// wave).
 bool qmv_plan(int64_t M, int64_t K, int gs, int bits, int nmat, QmvPlan& p) {
   if (M < 1 || M > 8 || (bits != 4 && bits != 8) || (gs != 64 && gs != 128)) return false;
   const int64_t cpl = 512 / bits;
@@ -348,7 +401,7 @@ bool qmv_plan(int64_t M, int64_t K, int gs, int bits, int nmat, QmvPlan& p) {
   int64_t best_cost = 0;
   for (int steps : kStepChoices) {
     if (LS % steps != 0) continue;
-    if (steps == 8 && mr > 1) continue;
+    if (!qmv_steps_fit(bits, gs == 64, steps, mr)) continue;
     const int64_t waves = nmat * (LS / steps);
     if (waves > kMaxWaves) continue;
     // activation chunks a lane stages (registers): at most kCopySlots across the rows
@@ -395,18 +448,21 @@ static int launch_qmv_mfma(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
   return check_launch(NMAT == 2 ? "swiglu_qmv" : "qmv_mfma");
 }
 
+template <int BITS, bool G64, int STEPS, int MR, int NMAT>
+static int qmv_mr(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
+  if constexpr (qmv_steps_fit(BITS, G64, STEPS, MR))
+    return launch_qmv_mfma<BITS, G64, STEPS, MR, NMAT>(a, p, st);
+  else
+    return set_error(MLXQ_EINVAL, "qmv: %d load steps per wave with %d rows exceed the registers", STEPS, MR);
+}
+
 template <int BITS, bool G64, int STEPS, int NMAT>
 static int qmv_rows(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
-  if constexpr (STEPS == 8) {  // qmv_plan uses 8 steps for one activation row only
-    if (p.mr != 1) return set_error(MLXQ_EINVAL, "qmv: 8 load steps per wave need M = 1");
-    return launch_qmv_mfma<BITS, G64, 8, 1, NMAT>(a, p, st);
-  } else {
-    switch (p.mr) {
-      case 1: return launch_qmv_mfma<BITS, G64, STEPS, 1, NMAT>(a, p, st);
-      case 2: return launch_qmv_mfma<BITS, G64, STEPS, 2, NMAT>(a, p, st);
-      case 4: return launch_qmv_mfma<BITS, G64, STEPS, 4, NMAT>(a, p, st);
-      default: return launch_qmv_mfma<BITS, G64, STEPS, 8, NMAT>(a, p, st);
-    }
+  switch (p.mr) {
+    case 1: return qmv_mr<BITS, G64, STEPS, 1, NMAT>(a, p, st);
+    case 2: return qmv_mr<BITS, G64, STEPS, 2, NMAT>(a, p, st);
+    case 4: return qmv_mr<BITS, G64, STEPS, 4, NMAT>(a, p, st);
+    default: return qmv_mr<BITS, G64, STEPS, 8, NMAT>(a, p, st);
   }
 }
 

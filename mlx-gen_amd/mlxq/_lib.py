@@ -36,6 +36,7 @@ EXPORTS = (
     "mlxq_quantized_matmul",
     "mlxq_qmm",
     "mlxq_qmv",
+    "mlxq_qmv_valu",
     "mlxq_linear_workspace_size",
     "mlxq_linear_out_dtype",
     "mlxq_linear",
@@ -94,7 +95,7 @@ def load():
     lib.mlxq_dequantize.argtypes = [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _vp, _vp]
     lib.mlxq_quantized_matmul.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _vp, _int, _i64, _int,
                                           _int, _int, _vp, _vp]
-    for name in ("mlxq_qmm", "mlxq_qmv"):
+    for name in ("mlxq_qmm", "mlxq_qmv", "mlxq_qmv_valu"):
         getattr(lib, name).argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _vp, _int, _i64, _int, _int,
                                        _vp, _vp]
     lib.mlxq_linear_workspace_size.argtypes = [_int, _int, _i64, _i64, ctypes.POINTER(Epilogue)]
@@ -118,7 +119,7 @@ def load():
     lib.mlxq_embedding.argtypes = [_vp, _i64, _vp, _vp, _vp, _int, _i64, _i64, _int, _int, _vp, _int,
                                    _vp]
     for name in ("mlxq_quantize", "mlxq_dequantize", "mlxq_quantized_matmul", "mlxq_qmm",
-                 "mlxq_qmv", "mlxq_linear", "mlxq_linear_noalloc", "mlxq_packed_bits", "mlxq_embedding",
+                 "mlxq_qmv", "mlxq_qmv_valu", "mlxq_linear", "mlxq_linear_noalloc", "mlxq_packed_bits", "mlxq_embedding",
                  "mlxq_lora_residual", "mlxq_cast", "mlxq_swiglu", "mlxq_qmm_experts"):
         getattr(lib, name).restype = _int
     _lib = lib

@@ -180,6 +180,12 @@ def qmv(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int =
     return _mm("mlxq_qmv", x, wq, scales, biases, group_size, bits, out=out)
 
 
+def qmv_valu(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4, out=None):
+    """Force the VALU GEMV (no matrix cores; M <= 8), the kernel quantized_matmul runs for f32
+    operands and group size 32, on any operand dtypes."""
+    return _mm("mlxq_qmv_valu", x, wq, scales, biases, group_size, bits, out=out)
+
+
 def embedding(ids, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4,
               out_dtype=torch.float32):
     """TokenEmbedding::forward's quantized arm (src/nn.rs:42-58): gather the packed rows of ids

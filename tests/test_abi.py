@@ -93,6 +93,16 @@ def _ep(lib_mod, bias_dt=None, lora_dt=None, act=0, rank=16):
                          act, bias_dt if bias_dt is not None else 1, lora_dt if lora_dt is not None else 1)
 
 
+def test_qmv_valu_validation(lib):
+    from mlxq import _lib
+    p = ctypes.c_void_p(4096)
+    null = ctypes.c_void_p(0)
+    st = lib.mlxq_qmv_valu(p, 1, 9, 128, p, p, p, 1, 8, 64, 4, p, null)
+    assert st == _lib.MLXQ_EINVAL and b"GEMV limit" in lib.mlxq_last_error()
+    st = lib.mlxq_qmv_valu(p, 1, 2, 100, p, p, p, 1, 8, 64, 4, p, null)
+    assert st == _lib.MLXQ_EINVAL and b"multiple of group_size" in lib.mlxq_last_error()
+
+
 def test_linear_workspace_size(lib):
     from mlxq import _lib
     bf, f32 = _lib.MLXQ_BFLOAT16, _lib.MLXQ_FLOAT32
