@@ -14,6 +14,7 @@ Also reported (same JSON line):
   quantize     config 3 quantize pass (4 x [5120,5120] bf16 -> Q8 g64): GB/s;
   config1/3/5  the other BASELINE configs (quantize/dequantize/qmm, the Q8 projection, the LoRA sweep);
   experts      the stacked-expert MoE projections (one launch vs one linear per expert);
+  f32_mlp      config 2 on FLUX.1's f32 stream (f32 x and h, split-bf16 matrix-core GEMM);
   cpu_baseline the CPU oracle (fp64-accumulating C restatement, OpenMP) on a bounded row sample of
                the same up-projection, scaled to TFLOP/s.
 """
@@ -30,6 +31,7 @@ for _p in (ROOT, os.path.join(ROOT, "mlx-gen_amd")):
 
 METRIC = "qmatmul TFLOP/s (Q4 g64, FLUX MLP shape) + GEMV HBM GB/s, 1×MI355X"
 MFMA_BF16_PEAK_TFLOPS = 2516.6
+FP32_MFMA_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
 
 
@@ -41,7 +43,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extras", action="store_true", help="headline GEMM only")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
-    p.add_argument("--only", choices=("all", "mlp", "gemv", "quantize", "copy", "configs", "experts"),
+    p.add_argument("--only", choices=("all", "mlp", "gemv", "quantize", "copy", "configs", "experts", "f32"),
                    default="all",
                    help="run one leg only (for profiling); 'copy' is the plain-copy calibration "
                         "kernel for the HBM byte counters")
@@ -238,6 +240,32 @@ def graph_ms(torch, fn, inner=8, reps=5):
     torch.cuda.synchronize()
     del graph
     return e0.elapsed_time(e1) / (reps * inner)
+
+
+def bench_f32_mlp(mlxq, torch):
+    """Config 2's MLP on FLUX.1's f32 residual stream (mlx-gen-flux/src/model.rs:407-410): f32 x
+    [4608,3072] through the Q4-g64 up projection with mlx_rs::nn::gelu (f32), then the f32 h through
+    the down projection.  Both products are f32 (MLX's promotion) and run on the split-bf16 GEMM:
+    three bf16 MFMA passes per product, so its MFMA work is 3x the algorithmic flops."""
+    dev = torch.device("cuda:0")
+    M, K, F = 4608, 3072, 12288
+    x = gen_bf16((M, K), 1.0, 900, dev).float()
+    qu = mlxq.quantize(gen_bf16((F, K), 0.02, 901, dev), 64, 4)
+    qd = mlxq.quantize(gen_bf16((K, F), 0.02, 902, dev), 64, 4)
+    h = mlxq.linear(x, *qu, 64, 4, activation=mlxq.MLXQ_ACT_GELU)
+    y = torch.empty((M, K), dtype=torch.float32, device=dev)
+    up = lambda: mlxq.linear(x, *qu, 64, 4, activation=mlxq.MLXQ_ACT_GELU)
+    down = lambda: mlxq.quantized_matmul(h, *qd, True, 64, 4, out=y)
+    t_up = graph_ms(torch, up, inner=2, reps=3)
+    t_dn = graph_ms(torch, down, inner=2, reps=3)
+    flop = 2.0 * M * K * F
+    tf = 2 * flop / ((t_up + t_dn) * 1e-3) / 1e12
+    return {"up_ms": round(t_up, 4), "down_ms": round(t_dn, 4),
+            "up_TFLOPs": round(flop / (t_up * 1e-3) / 1e12, 1),
+            "down_TFLOPs": round(flop / (t_dn * 1e-3) / 1e12, 1),
+            "TFLOPs": round(tf, 1), "frac_of_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 3),
+            "bf16_mfma_frac": round(3 * tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "note": "f32 x and h; the up launch includes the f32 GELU epilogue pass"}
 
 
 def bench_config1(mlxq, torch):
@@ -460,6 +488,9 @@ def main():
     if args.only == "experts":
         print(json.dumps({"experts": bench_experts(mlxq, torch)}))
         return
+    if args.only == "f32":
+        print(json.dumps({"f32_mlp": bench_f32_mlp(mlxq, torch)}))
+        return
     if args.only == "configs":
         print(json.dumps({"config1": bench_config1(mlxq, torch), "config3": bench_config3(mlxq, torch),
                           "config5": bench_config5(mlxq, torch)}))
@@ -496,6 +527,7 @@ def main():
         res["config3"] = bench_config3(mlxq, torch)
         res["config5"] = bench_config5(mlxq, torch)
         res["experts"] = bench_experts(mlxq, torch)
+        res["f32_mlp"] = bench_f32_mlp(mlxq, torch)
     if not args.no_cpu and args.only == "all":
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(res))

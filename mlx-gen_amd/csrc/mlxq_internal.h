@@ -62,7 +62,8 @@ int run_quantize(const void* w, int dtype, int64_t N, int64_t K, int gs, int bit
                  void* s, void* b, hipStream_t st);
 int run_dequantize(const uint32_t* wq, const void* s, const void* b, int dtype, int64_t N, int64_t K,
                    int gs, int bits, void* out, hipStream_t st);
-// Exact-f32-dequant product; y in promote(x_dtype, sb_dtype).
+// The f32-dequant product; y in promote(x_dtype, sb_dtype): the GEMV for M <= 8 (exact f32), the
+// split-bf16 GEMM for larger M (f32 operands, within ~1e-5 relative of the f32 product).
 int run_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
             const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st);
 int run_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
@@ -90,6 +91,10 @@ int run_swiglu_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq_g, co
 // point for measuring it against the matrix-core GEMV).
 int run_qmv_valu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                  const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st);
+// Large-M GEMM for operands MLX computes in f32 (f32 x and/or f32 scales), f32 y, as three bf16
+// MFMA passes over two-term bf16 splits of x and of the f32-dequantized weights.
+int run_qmm_f32(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+                const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st);
 int run_embedding(const int32_t* ids, int64_t T, const uint32_t* wq, const void* s, const void* b,
                   int sb_dtype, int64_t vocab, int64_t hidden, int gs, int bits, void* out,
                   int out_dtype, hipStream_t st);

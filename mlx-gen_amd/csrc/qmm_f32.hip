@@ -1,0 +1,312 @@
+// qmm_f32.hip — large-M quantized GEMM in f32 (y[M,N] = x[M,K] . W^T, M > 8) on gfx950 matrix
+// cores, for the operand mixes MLX computes in f32: f32 activations (FLUX.1's f32 residual stream,
+// reference mlx-gen-flux/src/model.rs:407-410 into src/adapters.rs:301-317) and/or f32 scales.
+//
+// Semantics: MLX's quantized_matmul casts x, scales and biases to their result type (f32 here),
+// dequantizes every weight in f32 and accumulates in f32.  gfx950 has no f32 matrix rate worth
+// using (157 TFLOP/s dense), so each f32 operand is carried as two bf16 values whose sum holds it
+// to 16 significant bits:
+//     v_hi = bf16(v),  v_lo = bf16(v - v_hi)      (both round to nearest even)
+// and each product as three bf16 MFMAs accumulated in f32:
+//     x.w ~= x_hi.w_hi + x_hi.w_lo + x_lo.w_hi
+// The dropped x_lo.w_lo term and the two representation errors are each below 2^-16 of |x.w|, so
+// the result is within ~1e-5 relative (Frobenius) of the f32 product, against ~1e-3 for a plain
+// bf16 product.  With bf16 activations (f32 scales) x_lo is zero and the third pass is skipped.
+// Weights are dequantized exactly as fma(code, scale, bias) in f32 (scale and bias widened
+// exactly from bf16), then split.
+//
+// Structure: one 256-thread workgroup (4 waves, 2 x 2, one per SIMD) per 128 x 128 output tile, K
+// advanced 64 at a time through a double-buffered LDS holding the four bf16 tiles x_hi, x_lo,
+// w_hi, w_lo of a step (64 KB per buffer).  Activations are split and weights dequantized and
+// split once per workgroup as they are written to LDS; every wave reads its 64 x 64 sub-tile's
+// fragments from there.  Rows of 64 bf16 (128 B) with the 16-byte chunk XOR-swizzled by row & 7.
+// Fragment mapping for v_mfma_f32_32x32x16_bf16: lane l supplies row (l & 31) and 8 consecutive k
+// at chunk 2 kk + (l >> 5) for both operands; the f32x16 result holds column (l & 31) and rows
+// 8 (v >> 2) + 4 (l >> 5) + (v & 3).
+// Tile order: groups of 8 M-tiles by all N-tiles (M fastest), so the workgroups in flight share
+// weight panels and a few activation panels; consecutive workgroup ids are spread over the 8 XCDs,
+// so the order is remapped to give each XCD a contiguous slice of it.
+#include <type_traits>
+
+#include "mlxq_common.h"
+
+namespace mlxq {
+
+namespace {
+
+constexpr int kF32BM = 128, kF32BN = 128, kF32BK = 64;
+constexpr int kF32GroupM = 8;
+
+__device__ __forceinline__ int swz32(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
+
+// (v0, v1) -> {hi, lo}: the packed bf16 pairs of the two-term split of two values.
+__device__ __forceinline__ u32x2 split2(float v0, float v1) {
+  const uint32_t hi = pack_bf16x2(v0, v1);
+  return u32x2{hi, pack_bf16x2(v0 - __uint_as_float(hi << 16), v1 - __uint_as_float(hi & 0xffff0000u))};
+}
+
+__device__ __forceinline__ void f32_tile_coords(int64_t bid, int64_t tiles_m, int64_t tiles_n,
+                                                int64_t& tm, int64_t& tn) {
+  const int64_t T = tiles_m * tiles_n;
+  const int64_t per = T / 8;
+  int64_t L = bid;
+  if (bid < per * 8) L = (bid % 8) * per + bid / 8;
+  const int64_t span = kF32GroupM * tiles_n;
+  const int64_t g = L / span;
+  const int64_t gm0 = g * kF32GroupM;
+  const int64_t gsz = tiles_m - gm0 < kF32GroupM ? tiles_m - gm0 : kF32GroupM;
+  const int64_t idx = L - g * span;
+  tm = gm0 + idx % gsz;
+  tn = idx / gsz;
+}
+
+}  // namespace
+
+// XT: activation storage (float, or uint16_t bf16 bits); SB: scale/bias storage.  y is f32.
+template <typename XT, typename SB, int BITS, int GS>
+__global__ __launch_bounds__(256, 1) void qmm_f32_kernel(const XT* __restrict__ x, int64_t M,
+                                                         int64_t K, const uint32_t* __restrict__ wq,
+                                                         const SB* __restrict__ scales,
+                                                         const SB* __restrict__ biases, int64_t N,
+                                                         float* __restrict__ y) {
+  constexpr bool XLO = std::is_same<XT, float>::value;  // activations carry a low part
+  constexpr int BM = kF32BM, BN = kF32BN;
+  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+  constexpr int A_LD = BM * 8 / 256;         // 8-element activation chunks per thread per step
+  constexpr int B_CPR = BITS == 4 ? 2 : 4;   // 16-byte code chunks per weight row per step
+  constexpr int B_LD = BN * B_CPR / 256;     // code chunks per thread per step
+  constexpr int T_BYTES = BM * 128;          // one bf16 tile (BM == BN)
+  static_assert(BM == BN && A_LD >= 1 && B_LD >= 1, "tile shape");
+  // Per buffer: x_hi, x_lo, w_hi, w_lo.
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2][4 * T_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int64_t tm, tn;
+  f32_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int64_t bm0 = tm * BM, bn0 = tn * BN;
+  const int64_t kwords = K * BITS / 32;
+  const int64_t groups = K / GS;
+  const int ksteps = (int)((K + kF32BK - 1) / kF32BK);
+
+  // Staging registers: activation chunks (8 values each: two 16-byte f32 loads or one bf16 load)
+  // and packed code chunks with their group's scale and bias.
+  u32x4 a_reg[A_LD][XLO ? 2 : 1];
+  u32x4 b_reg[B_LD];
+  float s_reg[B_LD], z_reg[B_LD];
+
+  auto load_global = [&](int kt) {
+    const int64_t k0 = (int64_t)kt * kF32BK;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int id = tid + 256 * i;
+      const int row = id >> 3, c = id & 7;
+      const int64_t m = bm0 + row, k = k0 + c * 8;
+      const bool ok = m < M && k < K;  // K % 32 == 0, so a chunk never straddles K
+#pragma unroll
+      for (int h = 0; h < (XLO ? 2 : 1); ++h)
+        a_reg[i][h] = ok ? reinterpret_cast<const u32x4*>(x + m * K + k)[h] : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int id = tid + 256 * i;
+      const int row = id / B_CPR, j = id % B_CPR;
+      const int64_t n = bn0 + row;
+      const int64_t kc = k0 + j * (BITS == 4 ? 32 : 16);
+      if (n < N && kc < K) {
+        b_reg[i] = *reinterpret_cast<const u32x4*>(wq + n * kwords + kc * BITS / 32);
+        const int64_t g = n * groups + kc / GS;
+        s_reg[i] = SBLoad<SB>::ld(scales, g);
+        z_reg[i] = SBLoad<SB>::ld(biases, g);
+      } else {
+        b_reg[i] = u32x4{0u, 0u, 0u, 0u};
+        s_reg[i] = 0.0f;
+        z_reg[i] = 0.0f;
+      }
+    }
+  };
+
+  auto store_lds = [&](int buf) {
+    unsigned char* Ah = smem[buf];
+    unsigned char* Al = smem[buf] + T_BYTES;
+    unsigned char* Bh = smem[buf] + 2 * T_BYTES;
+    unsigned char* Bl = smem[buf] + 3 * T_BYTES;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int id = tid + 256 * i;
+      const int row = id >> 3, c = id & 7;
+      if constexpr (XLO) {
+        u32x4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const u32x4& src = a_reg[i][e >> 1];
+          const u32x2 p = split2(__uint_as_float(src[2 * (e & 1)]), __uint_as_float(src[2 * (e & 1) + 1]));
+          hi[e] = p[0];
+          lo[e] = p[1];
+        }
+        *reinterpret_cast<u32x4*>(Ah + swz32(row, c)) = hi;
+        *reinterpret_cast<u32x4*>(Al + swz32(row, c)) = lo;
+      } else {
+        *reinterpret_cast<u32x4*>(Ah + swz32(row, c)) = a_reg[i][0];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int id = tid + 256 * i;
+      const int row = id / B_CPR, j = id % B_CPR;
+      const float s = s_reg[i], z = z_reg[i];
+      if constexpr (BITS == 4) {
+        // 4 words x 8 nibbles = k [32j, 32j+32): word q -> chunk 4j+q, codes in natural order.
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t w = b_reg[i][q];
+          u32x4 hi, lo;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float c0 = (float)((w >> (8 * e)) & 0xfu);
+            const float c1 = (float)((w >> (8 * e + 4)) & 0xfu);
+            const u32x2 p = split2(fmaf(c0, s, z), fmaf(c1, s, z));
+            hi[e] = p[0];
+            lo[e] = p[1];
+          }
+          *reinterpret_cast<u32x4*>(Bh + swz32(row, 4 * j + q)) = hi;
+          *reinterpret_cast<u32x4*>(Bl + swz32(row, 4 * j + q)) = lo;
+        }
+      } else {
+        // 4 words x 4 bytes = k [16j, 16j+16): words 2p, 2p+1 -> chunk 2j+p.
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          u32x4 hi, lo;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t w = b_reg[i][2 * p + h];
+            const u32x2 p0 = split2(fmaf((float)(w & 0xffu), s, z), fmaf((float)((w >> 8) & 0xffu), s, z));
+            const u32x2 p1 = split2(fmaf((float)((w >> 16) & 0xffu), s, z), fmaf((float)(w >> 24), s, z));
+            hi[2 * h] = p0[0];
+            lo[2 * h] = p0[1];
+            hi[2 * h + 1] = p1[0];
+            lo[2 * h + 1] = p1[1];
+          }
+          *reinterpret_cast<u32x4*>(Bh + swz32(row, 2 * j + p)) = hi;
+          *reinterpret_cast<u32x4*>(Bl + swz32(row, 2 * j + p)) = lo;
+        }
+      }
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  load_global(0);
+  store_lds(0);
+  __syncthreads();
+
+  const int r32 = lane & 31, half = lane >> 5;
+  for (int kt = 0; kt < ksteps; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < ksteps) load_global(kt + 1);
+    const unsigned char* Ah = smem[buf];
+    const unsigned char* Al = smem[buf] + T_BYTES;
+    const unsigned char* Bh = smem[buf] + 2 * T_BYTES;
+    const unsigned char* Bl = smem[buf] + 3 * T_BYTES;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int c = kk * 2 + half;
+      bf16x8 ah[TM], al[TM], bh[TN], bl[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        ah[i] = *reinterpret_cast<const bf16x8*>(Ah + swz32(wm * WM + i * 32 + r32, c));
+        if constexpr (XLO) al[i] = *reinterpret_cast<const bf16x8*>(Al + swz32(wm * WM + i * 32 + r32, c));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        bh[j] = *reinterpret_cast<const bf16x8*>(Bh + swz32(wn * WN + j * 32 + r32, c));
+        bl[j] = *reinterpret_cast<const bf16x8*>(Bl + swz32(wn * WN + j * 32 + r32, c));
+      }
+      // Three passes over the independent accumulators, so no MFMA waits on its predecessor.
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh[j], ah[i], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bl[j], ah[i], acc[i][j], 0, 0, 0);
+      if constexpr (XLO) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh[j], al[i], acc[i][j], 0, 0, 0);
+      }
+    }
+    if (kt + 1 < ksteps) store_lds(buf ^ 1);
+    __syncthreads();
+  }
+
+  // acc[i][j] element v: column m = row of A's fragment (lane & 31), rows n = 8 (v >> 2) +
+  // 4 half + (v & 3) of B's fragment: the weight operand is MFMA's A side, so each lane holds four
+  // runs of 4 consecutive n for one m and stores them as 16-byte rows.
+  const bool vec_ok = (N % 4) == 0;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t m = bm0 + wm * WM + i * 32 + r32;
+    if (m >= M) continue;
+    float* yrow = y + m * N;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int64_t n = bn0 + wn * WN + j * 32 + 8 * a + 4 * half;
+        const f32x4 v = {acc[i][j][4 * a], acc[i][j][4 * a + 1], acc[i][j][4 * a + 2], acc[i][j][4 * a + 3]};
+        if (vec_ok && n + 3 < N) {
+          *reinterpret_cast<f32x4*>(yrow + n) = v;
+        } else {
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            if (n + b < N) yrow[n + b] = v[b];
+        }
+      }
+    }
+  }
+}
+
+template <typename XT, typename SB, int BITS, int GS>
+static int launch_qmm_f32(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+                          const void* b, int64_t N, void* y, hipStream_t st) {
+  const int64_t tiles = ((M + kF32BM - 1) / kF32BM) * ((N + kF32BN - 1) / kF32BN);
+  if (tiles == 0) return MLXQ_OK;
+  if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm_f32: problem too large");
+  hipLaunchKernelGGL((qmm_f32_kernel<XT, SB, BITS, GS>), dim3((unsigned)tiles), dim3(256), 0, st,
+                     (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (float*)y);
+  return check_launch("qmm_f32");
+}
+
+template <typename XT, typename SB>
+static int qmm_f32_bits_gs(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+                           const void* b, int64_t N, int gs, int bits, void* y, hipStream_t st) {
+#define MLXQ_F(B, G) \
+  if (bits == B && gs == G) return launch_qmm_f32<XT, SB, B, G>(x, M, K, wq, s, b, N, y, st);
+  MLXQ_F(4, 32) MLXQ_F(4, 64) MLXQ_F(4, 128) MLXQ_F(8, 32) MLXQ_F(8, 64) MLXQ_F(8, 128)
+#undef MLXQ_F
+  return set_error(MLXQ_EINVAL, "qmm_f32: unsupported bits=%d group_size=%d", bits, gs);
+}
+
+int run_qmm_f32(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
+                const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st) {
+  if (x_dtype == MLXQ_BFLOAT16 && sb_dtype == MLXQ_BFLOAT16)
+    return set_error(MLXQ_EINVAL, "qmm_f32: bf16 operands take the bf16 GEMM");
+  if (x_dtype == MLXQ_FLOAT32) {
+    if (sb_dtype == MLXQ_BFLOAT16) return qmm_f32_bits_gs<float, uint16_t>(x, M, K, wq, s, b, N, gs, bits, y, st);
+    return qmm_f32_bits_gs<float, float>(x, M, K, wq, s, b, N, gs, bits, y, st);
+  }
+  return qmm_f32_bits_gs<uint16_t, float>(x, M, K, wq, s, b, N, gs, bits, y, st);
+}
+
+}  // namespace mlxq

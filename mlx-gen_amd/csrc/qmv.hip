@@ -189,9 +189,15 @@ int run_qmv_valu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_
   return qmv_bits_gs<float, float>(x, M, K, wq, s, b, N, gs, bits, y, st);
 }
 
-// Exact-f32-dequant matmul for any M (M <= 8 is the decode GEMV; larger M tiles the grid in y).
+// The f32-dequant product for any M: the decode GEMV for M <= 8, the split-bf16 matrix-core GEMM
+// (qmm_f32.hip) above that.
 int run_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
             const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st) {
+  if (M > 8) {
+    if (x_dtype == MLXQ_BFLOAT16 && sb_dtype == MLXQ_BFLOAT16)
+      return set_error(MLXQ_EINVAL, "qmv: M=%lld exceeds the GEMV limit of 8", (long long)M);
+    return run_qmm_f32(x, x_dtype, M, K, wq, s, b, sb_dtype, N, gs, bits, y, st);
+  }
   // bf16 activations with 64/128 groups take the matrix-core GEMV; f32 activations and
   // group_size 32 take the VALU kernel above (same exact-f32 dequant semantics).
   if (qmv_mfma_applicable(x_dtype, sb_dtype, M, K, N, gs, bits))
