@@ -47,9 +47,11 @@ def parse():
                    default="all",
                    help="run one leg only (for profiling); 'copy' is the plain-copy calibration "
                         "kernel for the HBM byte counters")
+    p.add_argument("--pmc-sets", metavar="A,B", default=None,
+                   help="with --summarize-pmc: only these counter-set subdirectories (copy_* always read)")
     p.add_argument("--summarize-pmc", metavar="DIR",
-                   help="print the HBM traffic summary from rocprofv3 --pmc runs under DIR "
-                        "(subdirectories fetch/, write/, copy_fetch/, copy_write/) and exit")
+                   help="print the counter summary of the rocprofv3 --pmc runs under DIR (one "
+                        "subdirectory per counter set, see summarize_pmc) and exit")
     return p.parse_args()
 
 
@@ -401,7 +403,7 @@ def cpu_baseline(budget_s):
 
 
 COPY_BYTES = 1 << 30  # plain-copy calibration: 1 GiB read + 1 GiB written per launch
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qmm_wide_flux_mlp_hbm_traffic.txt")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qmm_wide_flux_mlp_counters.txt")
 
 
 def run_copy(torch, reps=5):
@@ -414,40 +416,82 @@ def run_copy(torch, reps=5):
     print(json.dumps({"copy_bytes": COPY_BYTES, "reps": reps}))
 
 
-def _pmc_values(d, counter):
-    """{kernel name: [per-dispatch counter values]} from a rocprofv3 --pmc csv directory."""
+def _pmc_table(d):
+    """{kernel name: {counter: [per-dispatch values]}} from the rocprofv3 --pmc csv files under d."""
     import csv
     import glob
     out = {}
     for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
         for r in csv.DictReader(open(f)):
-            if r["Counter_Name"] == counter:
-                out.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+            k = r["Kernel_Name"].split("(")[0].replace("void ", "")
+            out.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
     return out
 
 
-def summarize_pmc(d):
-    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the qmm kernels, scaled by what the same
-    counters read for a plain copy of COPY_BYTES."""
-    med = lambda v: sorted(v)[len(v) // 2]
+def _med(v):
+    v = sorted(v)
+    return v[len(v) // 2]
+
+
+SIMDS = 256 * 4  # MI355X: 256 CUs x 4 SIMDs; GRBM_GUI_ACTIVE is summed over its 8 XCDs
+
+
+def summarize_pmc(d, sets=None):
+    """Summary of the rocprofv3 --pmc runs under d, one subdirectory per counter set:
+    <leg>_mfma (SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_BF16),
+    <leg>_dram (TCC_EA0_RDREQ_DRAM_32B_sum TCC_EA0_WRREQ_WRITE_DRAM_32B_sum), <leg>_fetch (FETCH_SIZE),
+    <leg>_write (WRITE_SIZE), with leg 'copy' the 1 GiB plain-copy calibration.  Per mlxq kernel:
+    MFMA busy = busy cycles / (GUI-active cycles per XCD x SIMDs), bf16 MFMA flop = MOPS x 512,
+    memory-side read / write bytes = 32-byte requests x 32 scaled by the copy calibration, and
+    FETCH_SIZE / WRITE_SIZE (KiB per dispatch) scaled by the same.  Medians over dispatches."""
+    import glob
+    subs = {os.path.basename(p): _pmc_table(p) for p in sorted(glob.glob(os.path.join(d, "*"))) if os.path.isdir(p)}
+    keep = set(sets.split(",")) if sets else None
+    copy_ctr = lambda sub, c: max((_med(v[c]) for k, v in subs.get(sub, {}).items() if "copy" in k.lower() and c in v),
+                                  default=None)
     cal = {}
-    for c, sub in (("FETCH_SIZE", "copy_fetch"), ("WRITE_SIZE", "copy_write")):
-        vals = [med(v) for k, v in _pmc_values(os.path.join(d, sub), c).items() if "copy" in k]
-        cal[c] = (COPY_BYTES / 1024.0) / max(vals)
-    lines = [f"calibration (1 GiB plain copy): FETCH_SIZE x{cal['FETCH_SIZE']:.4f}, "
-             f"WRITE_SIZE x{cal['WRITE_SIZE']:.4f} (expected KiB / counted KiB)"]
-    total = []
-    fetch = _pmc_values(os.path.join(d, "fetch"), "FETCH_SIZE")
-    write = _pmc_values(os.path.join(d, "write"), "WRITE_SIZE")
-    for k in sorted(fetch):
-        if "qmm" not in k:
+    rd, wr = copy_ctr("copy_dram", "TCC_EA0_RDREQ_DRAM_32B_sum"), copy_ctr("copy_dram", "TCC_EA0_WRREQ_WRITE_DRAM_32B_sum")
+    cal["rd"] = COPY_BYTES / (rd * 32) if rd else 1.0
+    cal["wr"] = COPY_BYTES / (wr * 32) if wr else 1.0
+    fe, wi = copy_ctr("copy_fetch", "FETCH_SIZE"), copy_ctr("copy_write", "WRITE_SIZE")
+    cal["fetch"] = (COPY_BYTES / 1024.0) / fe if fe else None
+    cal["write"] = (COPY_BYTES / 1024.0) / wi if wi else None
+    lines = [f"calibration (1 GiB plain copy): DRAM read requests x32 B x{cal['rd']:.4f}, write x{cal['wr']:.4f}; "
+             f"FETCH_SIZE x{cal['fetch'] or 0:.4f}, WRITE_SIZE x{cal['write'] or 0:.4f} (expected / counted)"]
+    wide = []
+    for sub, tab in subs.items():
+        if sub.startswith("copy") or (keep is not None and sub not in keep):
             continue
-        f = med(fetch[k]) * 1024 * cal["FETCH_SIZE"]
-        w = med(write.get(k, [0.0])) * 1024 * cal["WRITE_SIZE"]
-        total.append(f + w)
-        lines.append(f"{k.split('(')[0]}: fetch {f / 1e6:.1f} MB  write {w / 1e6:.1f} MB  "
-                     f"({len(fetch[k])} dispatches)")
-    lines.append(f"traffic_bytes_per_launch: {int(sum(total) / max(len(total), 1))}")
+        for k in sorted(tab):
+            if "mlxq" not in k:
+                continue
+            c = tab[k]
+            n = len(next(iter(c.values())))
+            parts = []
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in c and "GRBM_GUI_ACTIVE" in c:
+                busy = _med(c["SQ_VALU_MFMA_BUSY_CYCLES"]) / (_med(c["GRBM_GUI_ACTIVE"]) / 8 * SIMDS)
+                parts.append(f"MFMA busy {100 * busy:.1f}%")
+            if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in c:
+                parts.append(f"bf16 MFMA {_med(c['SQ_INSTS_VALU_MFMA_MOPS_BF16']) * 512 / 1e9:.2f} GFLOP")
+            if "TCC_EA0_RDREQ_DRAM_32B_sum" in c:
+                r = _med(c["TCC_EA0_RDREQ_DRAM_32B_sum"]) * 32 * cal["rd"]
+                w = _med(c.get("TCC_EA0_WRREQ_WRITE_DRAM_32B_sum", [0.0])) * 32 * cal["wr"]
+                parts.append(f"memory-side read {r / 1e6:.2f} MB write {w / 1e6:.2f} MB")
+            if "FETCH_SIZE" in c and cal["fetch"]:
+                f = _med(c["FETCH_SIZE"]) * 1024 * cal["fetch"]
+                parts.append(f"FETCH_SIZE {f / 1e6:.2f} MB")
+                if "qmm_wide" in k:
+                    wide.append(("fetch", k, f))
+            if "WRITE_SIZE" in c and cal["write"]:
+                w = _med(c["WRITE_SIZE"]) * 1024 * cal["write"]
+                parts.append(f"WRITE_SIZE {w / 1e6:.2f} MB")
+                if "qmm_wide" in k:
+                    wide.append(("write", k, w))
+            lines.append(f"[{sub}] {k}: " + "; ".join(parts) + f" ({n} dispatches)")
+    kernels = sorted({k for _, k, _ in wide})
+    if kernels:
+        per = [sum(v for t, k2, v in wide if k2 == k) for k in kernels]
+        lines.append(f"traffic_bytes_per_launch: {int(sum(per) / len(per))}")
     print("\n".join(lines))
 
 
@@ -465,7 +509,7 @@ def read_traffic():
 def main():
     args = parse()
     if args.summarize_pmc:
-        summarize_pmc(args.summarize_pmc)
+        summarize_pmc(args.summarize_pmc, args.pmc_sets)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the quantized-linear "

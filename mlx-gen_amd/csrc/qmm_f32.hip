@@ -15,14 +15,14 @@
 // Weights are dequantized exactly as fma(code, scale, bias) in f32 (scale and bias widened
 // exactly from bf16), then split.
 //
-// Structure: one 256-thread workgroup (4 waves, 2 x 2, one per SIMD) per 128 x 128 output tile, K
-// advanced 64 at a time through a double-buffered LDS holding the four bf16 tiles x_hi, x_lo,
-// w_hi, w_lo of a step (64 KB per buffer).  Activations are split and weights dequantized and
-// split once per workgroup as they are written to LDS; every wave reads its 64 x 64 sub-tile's
-// fragments from there.  Rows of 64 bf16 (128 B) with the 16-byte chunk XOR-swizzled by row & 7.
+// Structure: a workgroup of 4 waves (2 x 2, 64 x 64 each) per 128 x 128 output tile, K advanced
+// BK = 32 at a time through a double-buffered LDS holding the four bf16 tiles x_hi, x_lo, w_hi,
+// w_lo of a step (32 KB per buffer, two workgroups per CU).  Activations are split and weights
+// dequantized and split once per workgroup as they are written to LDS; every wave reads its
+// sub-tile's fragments from there.  Rows of BK bf16 with the 16-byte chunks XOR-swizzled.
 // Fragment mapping for v_mfma_f32_32x32x16_bf16: lane l supplies row (l & 31) and 8 consecutive k
-// at chunk 2 kk + (l >> 5) for both operands; the f32x16 result holds column (l & 31) and rows
-// 8 (v >> 2) + 4 (l >> 5) + (v & 3).
+// at chunk 2 kk + (l >> 5) for both operands; with the weights as the A operand the f32x16 result
+// holds activation row (l & 31) and weight rows 8 (v >> 2) + 4 (l >> 5) + (v & 3).
 // Tile order: groups of 8 M-tiles by all N-tiles (M fastest), so the workgroups in flight share
 // weight panels and a few activation panels; consecutive workgroup ids are spread over the 8 XCDs,
 // so the order is remapped to give each XCD a contiguous slice of it.
@@ -34,10 +34,17 @@ namespace mlxq {
 
 namespace {
 
-constexpr int kF32BM = 128, kF32BN = 128, kF32BK = 64;
+constexpr int kF32BM = 128;
 constexpr int kF32GroupM = 8;
 
-__device__ __forceinline__ int swz32(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
+// Byte offset of 16-byte chunk `chunk` of tile row `row` for rows of BK bf16: 128-byte rows XOR
+// the chunk with row & 7, 64-byte rows with (row >> 1) & 3, so the fragment reads (one chunk of 8
+// or more consecutive rows) fall on distinct banks.
+template <int BK>
+__device__ __forceinline__ int swz32(int row, int chunk) {
+  if constexpr (BK == 64) return row * 128 + ((chunk ^ (row & 7)) << 4);
+  else return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
+}
 
 // (v0, v1) -> {hi, lo}: the packed bf16 pairs of the two-term split of two values.
 __device__ __forceinline__ u32x2 split2(float v0, float v1) {
@@ -63,80 +70,93 @@ __device__ __forceinline__ void f32_tile_coords(int64_t bid, int64_t tiles_m, in
 }  // namespace
 
 // XT: activation storage (float, or uint16_t bf16 bits); SB: scale/bias storage.  y is f32.
-template <typename XT, typename SB, int BITS, int GS>
-__global__ __launch_bounds__(256, 1) void qmm_f32_kernel(const XT* __restrict__ x, int64_t M,
+// WAVES: 4 (2 x 2 waves of 64 x 64) or 8 (2 x 4 waves of 64 x 32, two per SIMD).
+template <typename XT, typename SB, int BITS, int GS, int WAVES, int BN, int BK>
+__global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restrict__ x, int64_t M,
                                                          int64_t K, const uint32_t* __restrict__ wq,
                                                          const SB* __restrict__ scales,
                                                          const SB* __restrict__ biases, int64_t N,
                                                          float* __restrict__ y) {
   constexpr bool XLO = std::is_same<XT, float>::value;  // activations carry a low part
-  constexpr int BM = kF32BM, BN = kF32BN;
-  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
-  constexpr int A_LD = BM * 8 / 256;         // 8-element activation chunks per thread per step
-  constexpr int B_CPR = BITS == 4 ? 2 : 4;   // 16-byte code chunks per weight row per step
-  constexpr int B_LD = BN * B_CPR / 256;     // code chunks per thread per step
-  constexpr int T_BYTES = BM * 128;          // one bf16 tile (BM == BN)
-  static_assert(BM == BN && A_LD >= 1 && B_LD >= 1, "tile shape");
+  constexpr int BM = kF32BM, NT = WAVES * 64;
+  constexpr int WGN = WAVES / 2;             // waves along N
+  constexpr int WM = BM / 2, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+  constexpr int CPR = BK / 8;                // 16-byte bf16 chunks per tile row
+  constexpr int A_LD = BM * CPR / NT;        // 8-element activation chunks per thread per step
+  constexpr int CPT = BN * BK / NT;          // codes per thread per step
+  constexpr int WPT = CPT * BITS / 32;       // their packed words
+  constexpr int PPR = BK / CPT;              // threads per weight row
+  constexpr int TA = BM * BK * 2, TB = BN * BK * 2;  // bytes of one activation / weight tile
+  static_assert(A_LD >= 1 && TM >= 1 && TN >= 1 && CPT >= 8 && CPT <= 32 && PPR >= 1, "tile shape");
   // Per buffer: x_hi, x_lo, w_hi, w_lo.
-  __shared__ __attribute__((aligned(16))) unsigned char smem[2][4 * T_BYTES];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2][2 * TA + 2 * TB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int64_t tm, tn;
   f32_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int64_t bm0 = tm * BM, bn0 = tn * BN;
   const int64_t kwords = K * BITS / 32;
   const int64_t groups = K / GS;
-  const int ksteps = (int)((K + kF32BK - 1) / kF32BK);
+  const int ksteps = (int)((K + BK - 1) / BK);
 
   // Staging registers: activation chunks (8 values each: two 16-byte f32 loads or one bf16 load)
   // and packed code chunks with their group's scale and bias.
   u32x4 a_reg[A_LD][XLO ? 2 : 1];
-  u32x4 b_reg[B_LD];
-  float s_reg[B_LD], z_reg[B_LD];
+  uint32_t b_reg[WPT];
+  float s_reg, z_reg;
 
   auto load_global = [&](int kt) {
-    const int64_t k0 = (int64_t)kt * kF32BK;
+    const int64_t k0 = (int64_t)kt * BK;
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
-      const int id = tid + 256 * i;
-      const int row = id >> 3, c = id & 7;
+      const int id = tid + NT * i;
+      const int row = id / CPR, c = id % CPR;
       const int64_t m = bm0 + row, k = k0 + c * 8;
       const bool ok = m < M && k < K;  // K % 32 == 0, so a chunk never straddles K
 #pragma unroll
       for (int h = 0; h < (XLO ? 2 : 1); ++h)
         a_reg[i][h] = ok ? reinterpret_cast<const u32x4*>(x + m * K + k)[h] : u32x4{0u, 0u, 0u, 0u};
     }
-#pragma unroll
-    for (int i = 0; i < B_LD; ++i) {
-      const int id = tid + 256 * i;
-      const int row = id / B_CPR, j = id % B_CPR;
+    {  // CPT consecutive codes of one weight row (one group: CPT <= 32 <= group size)
+      const int row = tid / PPR, part = tid % PPR;
       const int64_t n = bn0 + row;
-      const int64_t kc = k0 + j * (BITS == 4 ? 32 : 16);
+      const int64_t kc = k0 + part * CPT;
       if (n < N && kc < K) {
-        b_reg[i] = *reinterpret_cast<const u32x4*>(wq + n * kwords + kc * BITS / 32);
+        const uint32_t* src = wq + n * kwords + kc * BITS / 32;
+        if constexpr (WPT == 1) {
+          b_reg[0] = src[0];
+        } else {
+#pragma unroll
+          for (int q = 0; q < WPT; q += 2) {
+            const u32x2 v = *reinterpret_cast<const u32x2*>(src + q);
+            b_reg[q] = v[0];
+            b_reg[q + 1] = v[1];
+          }
+        }
         const int64_t g = n * groups + kc / GS;
-        s_reg[i] = SBLoad<SB>::ld(scales, g);
-        z_reg[i] = SBLoad<SB>::ld(biases, g);
+        s_reg = SBLoad<SB>::ld(scales, g);
+        z_reg = SBLoad<SB>::ld(biases, g);
       } else {
-        b_reg[i] = u32x4{0u, 0u, 0u, 0u};
-        s_reg[i] = 0.0f;
-        z_reg[i] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < WPT; ++q) b_reg[q] = 0u;
+        s_reg = 0.0f;
+        z_reg = 0.0f;
       }
     }
   };
 
   auto store_lds = [&](int buf) {
     unsigned char* Ah = smem[buf];
-    unsigned char* Al = smem[buf] + T_BYTES;
-    unsigned char* Bh = smem[buf] + 2 * T_BYTES;
-    unsigned char* Bl = smem[buf] + 3 * T_BYTES;
+    unsigned char* Al = smem[buf] + TA;
+    unsigned char* Bh = smem[buf] + 2 * TA;
+    unsigned char* Bl = smem[buf] + 2 * TA + TB;
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
-      const int id = tid + 256 * i;
-      const int row = id >> 3, c = id & 7;
+      const int id = tid + NT * i;
+      const int row = id / CPR, c = id % CPR;
       if constexpr (XLO) {
         u32x4 hi, lo;
 #pragma unroll
@@ -146,42 +166,43 @@ __global__ __launch_bounds__(256, 1) void qmm_f32_kernel(const XT* __restrict__ 
           hi[e] = p[0];
           lo[e] = p[1];
         }
-        *reinterpret_cast<u32x4*>(Ah + swz32(row, c)) = hi;
-        *reinterpret_cast<u32x4*>(Al + swz32(row, c)) = lo;
+        *reinterpret_cast<u32x4*>(Ah + swz32<BK>(row, c)) = hi;
+        *reinterpret_cast<u32x4*>(Al + swz32<BK>(row, c)) = lo;
       } else {
-        *reinterpret_cast<u32x4*>(Ah + swz32(row, c)) = a_reg[i][0];
+        *reinterpret_cast<u32x4*>(Ah + swz32<BK>(row, c)) = a_reg[i][0];
       }
     }
-#pragma unroll
-    for (int i = 0; i < B_LD; ++i) {
-      const int id = tid + 256 * i;
-      const int row = id / B_CPR, j = id % B_CPR;
-      const float s = s_reg[i], z = z_reg[i];
+    {
+      const int row = tid / PPR, part = tid % PPR;
+      const float s = s_reg, z = z_reg;
+      // LDS chunk c holds k [8c, 8c + 8) of the step; this thread's codes start at chunk part*CPT/8.
+      const int c0 = part * CPT / 8;
       if constexpr (BITS == 4) {
-        // 4 words x 8 nibbles = k [32j, 32j+32): word q -> chunk 4j+q, codes in natural order.
+        // word q: codes 8q..8q+7 in natural order (low nibble first) -> chunk c0 + q
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t w = b_reg[i][q];
+        for (int q = 0; q < WPT; ++q) {
+          const uint32_t w = b_reg[q];
           u32x4 hi, lo;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float c0 = (float)((w >> (8 * e)) & 0xfu);
-            const float c1 = (float)((w >> (8 * e + 4)) & 0xfu);
-            const u32x2 p = split2(fmaf(c0, s, z), fmaf(c1, s, z));
+            const float c0f = (float)((w >> (8 * e)) & 0xfu);
+            const float c1f = (float)((w >> (8 * e + 4)) & 0xfu);
+            const u32x2 p = split2(fmaf(c0f, s, z), fmaf(c1f, s, z));
             hi[e] = p[0];
             lo[e] = p[1];
           }
-          *reinterpret_cast<u32x4*>(Bh + swz32(row, 4 * j + q)) = hi;
-          *reinterpret_cast<u32x4*>(Bl + swz32(row, 4 * j + q)) = lo;
+          *reinterpret_cast<u32x4*>(Bh + swz32<BK>(row, c0 + q)) = hi;
+          *reinterpret_cast<u32x4*>(Bl + swz32<BK>(row, c0 + q)) = lo;
         }
       } else {
-        // 4 words x 4 bytes = k [16j, 16j+16): words 2p, 2p+1 -> chunk 2j+p.
+        // words 2p, 2p+1: codes 8p..8p+7 -> chunk c0 + p
+        static_assert(WPT % 2 == 0, "Q8 words come in pairs");
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
+        for (int p = 0; p < WPT / 2; ++p) {
           u32x4 hi, lo;
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const uint32_t w = b_reg[i][2 * p + h];
+            const uint32_t w = b_reg[2 * p + h];
             const u32x2 p0 = split2(fmaf((float)(w & 0xffu), s, z), fmaf((float)((w >> 8) & 0xffu), s, z));
             const u32x2 p1 = split2(fmaf((float)((w >> 16) & 0xffu), s, z), fmaf((float)(w >> 24), s, z));
             hi[2 * h] = p0[0];
@@ -189,8 +210,8 @@ __global__ __launch_bounds__(256, 1) void qmm_f32_kernel(const XT* __restrict__ 
             hi[2 * h + 1] = p1[0];
             lo[2 * h + 1] = p1[1];
           }
-          *reinterpret_cast<u32x4*>(Bh + swz32(row, 2 * j + p)) = hi;
-          *reinterpret_cast<u32x4*>(Bl + swz32(row, 2 * j + p)) = lo;
+          *reinterpret_cast<u32x4*>(Bh + swz32<BK>(row, c0 + p)) = hi;
+          *reinterpret_cast<u32x4*>(Bl + swz32<BK>(row, c0 + p)) = lo;
         }
       }
     }
@@ -213,22 +234,22 @@ __global__ __launch_bounds__(256, 1) void qmm_f32_kernel(const XT* __restrict__ 
     const int buf = kt & 1;
     if (kt + 1 < ksteps) load_global(kt + 1);
     const unsigned char* Ah = smem[buf];
-    const unsigned char* Al = smem[buf] + T_BYTES;
-    const unsigned char* Bh = smem[buf] + 2 * T_BYTES;
-    const unsigned char* Bl = smem[buf] + 3 * T_BYTES;
+    const unsigned char* Al = smem[buf] + TA;
+    const unsigned char* Bh = smem[buf] + 2 * TA;
+    const unsigned char* Bl = smem[buf] + 2 * TA + TB;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 0; kk < BK / 16; ++kk) {
       const int c = kk * 2 + half;
       bf16x8 ah[TM], al[TM], bh[TN], bl[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        ah[i] = *reinterpret_cast<const bf16x8*>(Ah + swz32(wm * WM + i * 32 + r32, c));
-        if constexpr (XLO) al[i] = *reinterpret_cast<const bf16x8*>(Al + swz32(wm * WM + i * 32 + r32, c));
+        ah[i] = *reinterpret_cast<const bf16x8*>(Ah + swz32<BK>(wm * WM + i * 32 + r32, c));
+        if constexpr (XLO) al[i] = *reinterpret_cast<const bf16x8*>(Al + swz32<BK>(wm * WM + i * 32 + r32, c));
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        bh[j] = *reinterpret_cast<const bf16x8*>(Bh + swz32(wn * WN + j * 32 + r32, c));
-        bl[j] = *reinterpret_cast<const bf16x8*>(Bl + swz32(wn * WN + j * 32 + r32, c));
+        bh[j] = *reinterpret_cast<const bf16x8*>(Bh + swz32<BK>(wn * WN + j * 32 + r32, c));
+        bl[j] = *reinterpret_cast<const bf16x8*>(Bl + swz32<BK>(wn * WN + j * 32 + r32, c));
       }
       // Three passes over the independent accumulators, so no MFMA waits on its predecessor.
 #pragma unroll
@@ -280,11 +301,15 @@ __global__ __launch_bounds__(256, 1) void qmm_f32_kernel(const XT* __restrict__ 
 template <typename XT, typename SB, int BITS, int GS>
 static int launch_qmm_f32(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                           const void* b, int64_t N, void* y, hipStream_t st) {
-  const int64_t tiles = ((M + kF32BM - 1) / kF32BM) * ((N + kF32BN - 1) / kF32BN);
+  // 4 waves on 128 x 128 tiles with 32-deep K steps (64 KB of LDS, two workgroups per CU):
+  // 1225 us on the FLUX up shape (f32 x, Q4 g64, 284 TFLOP/s) against 1279 with 8 waves, 1336
+  // with 128 x 256 tiles (1 workgroup per CU) and 1614 with 64-deep steps (128 KB, 1 per CU).
+  constexpr int WAVES = 4, BN = 128, BK = 32;
+  const int64_t tiles = ((M + kF32BM - 1) / kF32BM) * ((N + BN - 1) / BN);
   if (tiles == 0) return MLXQ_OK;
   if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm_f32: problem too large");
-  hipLaunchKernelGGL((qmm_f32_kernel<XT, SB, BITS, GS>), dim3((unsigned)tiles), dim3(256), 0, st,
-                     (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (float*)y);
+  hipLaunchKernelGGL((qmm_f32_kernel<XT, SB, BITS, GS, WAVES, BN, BK>), dim3((unsigned)tiles), dim3(WAVES * 64),
+                     0, st, (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (float*)y);
   return check_launch("qmm_f32");
 }
 
