@@ -8,7 +8,9 @@
 // (src/quant.rs:92-116; mlx-gen-flux/src/convert.rs:46-78).
 #include <algorithm>
 #include <cctype>
+#include <cerrno>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <filesystem>
 #include <fstream>
@@ -48,9 +50,21 @@ struct Json {
 
 [[noreturn]] void bad_json(const std::string& what) { throw Error(MLXQ_EINVAL, "json: " + what); }
 
+// Nesting limit of the parser: safetensors headers and config files nest a few levels; a header
+// of nested brackets is rejected instead of exhausting the stack.
+constexpr int kMaxJsonDepth = 64;
+
+int hex_digit(char c) {
+  if (c >= '0' && c <= '9') return c - '0';
+  if (c >= 'a' && c <= 'f') return c - 'a' + 10;
+  if (c >= 'A' && c <= 'F') return c - 'A' + 10;
+  return -1;
+}
+
 struct JsonParser {
   const std::string& s;
   size_t i = 0;
+  int depth = 0;
   void ws() {
     while (i < s.size() && std::isspace((unsigned char)s[i])) ++i;
   }
@@ -85,7 +99,12 @@ struct JsonParser {
         case 't': out += '\t'; break;
         case 'u': {
           if (i + 4 > s.size()) bad_json("bad \\u escape");
-          unsigned cp = (unsigned)std::stoul(s.substr(i, 4), nullptr, 16);
+          unsigned cp = 0;
+          for (int k = 0; k < 4; ++k) {
+            const int d = hex_digit(s[i + k]);
+            if (d < 0) bad_json("bad \\u escape");
+            cp = cp * 16 + (unsigned)d;
+          }
           i += 4;
           if (cp < 0x80) out += (char)cp;  // config files here are ASCII; keep others as UTF-8
           else if (cp < 0x800) { out += (char)(0xc0 | (cp >> 6)); out += (char)(0x80 | (cp & 0x3f)); }
@@ -100,10 +119,11 @@ struct JsonParser {
   Json value() {
     const char c = peek();
     Json j;
+    if ((c == '{' || c == '[') && ++depth > kMaxJsonDepth) bad_json("nested too deeply");
     if (c == '{') {
       ++i;
       JsonObject o;
-      if (peek() == '}') { ++i; j.v = o; return j; }
+      if (peek() == '}') { ++i; j.v = o; --depth; return j; }
       while (true) {
         std::string k = str();
         expect(':');
@@ -113,10 +133,11 @@ struct JsonParser {
         break;
       }
       j.v = std::move(o);
+      --depth;
     } else if (c == '[') {
       ++i;
       JsonArray a;
-      if (peek() == ']') { ++i; j.v = a; return j; }
+      if (peek() == ']') { ++i; j.v = a; --depth; return j; }
       while (true) {
         a.push_back(value());
         if (peek() == ',') { ++i; continue; }
@@ -124,6 +145,7 @@ struct JsonParser {
         break;
       }
       j.v = std::move(a);
+      --depth;
     } else if (c == '"') {
       j.v = str();
     } else if (s.compare(i, 4, "true") == 0) { i += 4; j.v = true; }
@@ -139,8 +161,17 @@ struct JsonParser {
       if (e == i) bad_json("unexpected character");
       const std::string num = s.substr(i, e - i);
       i = e;
-      if (frac) j.v = std::stod(num);
-      else j.v = (int64_t)std::stoll(num);
+      char* end = nullptr;
+      errno = 0;
+      if (frac) {
+        const double d = std::strtod(num.c_str(), &end);
+        if (end != num.c_str() + num.size() || errno == ERANGE) bad_json("bad number " + num);
+        j.v = d;
+      } else {
+        const long long n = std::strtoll(num.c_str(), &end, 10);
+        if (end != num.c_str() + num.size() || errno == ERANGE) bad_json("bad integer " + num);
+        j.v = (int64_t)n;
+      }
     }
     return j;
   }
@@ -212,36 +243,52 @@ int64_t as_int(const Json* j, const std::string& what) {
 }  // namespace
 
 HostMap read_safetensors(const std::string& path) {
-  const std::string bytes = read_file(path);
-  if (bytes.size() < 8) throw Error(MLXQ_EINVAL, "safetensors: " + path + " is too short");
+  // The length and the JSON header are read first; each tensor's byte range is then read from the
+  // file straight into its buffer, so a multi-GB snapshot needs its own size in host memory once.
+  std::ifstream f(path, std::ios::binary | std::ios::ate);
+  if (!f) throw Error(MLXQ_EINVAL, "cannot open " + path);
+  const uint64_t size = (uint64_t)f.tellg();
+  if (size < 8) throw Error(MLXQ_EINVAL, "safetensors: " + path + " is too short");
+  f.seekg(0);
+  uint8_t len[8];
+  f.read((char*)len, 8);
   uint64_t n = 0;
-  for (int k = 7; k >= 0; --k) n = (n << 8) | (uint8_t)bytes[k];
-  if (n > bytes.size() - 8) throw Error(MLXQ_EINVAL, "safetensors: header length past the end of " + path);
-  const Json header = parse_json(bytes.substr(8, n));
+  for (int k = 7; k >= 0; --k) n = (n << 8) | len[k];
+  if (!f || n > size - 8) throw Error(MLXQ_EINVAL, "safetensors: header length past the end of " + path);
+  std::string head((size_t)n, '\0');
+  f.read(head.data(), (std::streamsize)n);
+  if (!f) throw Error(MLXQ_EINVAL, "safetensors: cannot read the header of " + path);
+  const Json header = parse_json(head);
   const auto* obj = std::get_if<JsonObject>(&header.v);
   if (!obj) throw Error(MLXQ_EINVAL, "safetensors: header is not an object");
-  const size_t base = 8 + n;
+  const uint64_t base = 8 + n;
   HostMap out;
   for (const auto& [name, desc] : *obj) {
     if (name == "__metadata__") continue;
     const Json* dt = desc.get("dtype");
     const Json* shape = desc.get("shape");
     const Json* offs = desc.get("data_offsets");
-    if (!dt || !std::holds_alternative<std::string>(dt->v) || !shape || !offs)
+    const auto* dims = shape ? std::get_if<JsonArray>(&shape->v) : nullptr;
+    const auto* o = offs ? std::get_if<JsonArray>(&offs->v) : nullptr;
+    if (!dt || !std::holds_alternative<std::string>(dt->v) || !dims || !o || o->size() != 2)
       throw Error(MLXQ_EINVAL, "safetensors: malformed entry " + name);
     HostTensor t;
     t.dtype = dtype_from_name(std::get<std::string>(dt->v));
-    int64_t count = 1;
-    for (const Json& d : std::get<JsonArray>(shape->v)) {
-      t.shape.push_back(as_int(&d, "shape of " + name));
-      count *= t.shape.back();
+    uint64_t count = 1;
+    for (const Json& d : *dims) {
+      const int64_t v = as_int(&d, "shape of " + name);
+      if (v < 0 || (v > 0 && count > (UINT64_MAX / 16) / (uint64_t)v))
+        throw Error(MLXQ_EINVAL, "safetensors: bad shape of " + name);
+      t.shape.push_back(v);
+      count *= (uint64_t)v;
     }
-    const auto& o = std::get<JsonArray>(offs->v);
-    if (o.size() != 2) throw Error(MLXQ_EINVAL, "safetensors: bad data_offsets of " + name);
-    const int64_t b = as_int(&o[0], "offset"), e = as_int(&o[1], "offset");
-    if (b < 0 || e < b || base + (size_t)e > bytes.size() || (size_t)(e - b) != count * dtype_size(t.dtype))
+    const int64_t b = as_int(&(*o)[0], "offset"), e = as_int(&(*o)[1], "offset");
+    if (b < 0 || e < b || (uint64_t)e > size - base || (uint64_t)(e - b) != count * dtype_size(t.dtype))
       throw Error(MLXQ_EINVAL, "safetensors: data range of " + name + " does not match its shape");
-    t.data.assign(bytes.begin() + base + b, bytes.begin() + base + e);
+    t.data.resize((size_t)(e - b));
+    f.seekg((std::streamoff)(base + (uint64_t)b));
+    f.read((char*)t.data.data(), (std::streamsize)t.data.size());
+    if (!f) throw Error(MLXQ_EINVAL, "safetensors: cannot read " + name + " from " + path);
     out.emplace(name, std::move(t));
   }
   return out;

@@ -200,6 +200,34 @@ static void cpu_cases(const fs::path& root) {
     threw = false;
     try { dtype_from_name("C64"); } catch (const Error&) { threw = true; }
     EXPECT(threw, "unknown dtype accepted");
+    // Headers that are well-formed bytes but wrong JSON shapes or values: every one is an
+    // mlxq::Error with MLXQ_EINVAL, never another exception type or a crash.
+    const std::vector<std::string> headers = {
+        "{\"x\":{\"dtype\":\"F32\",\"shape\":4,\"data_offsets\":[0,16]}}",          // shape not a list
+        "{\"x\":{\"dtype\":\"F32\",\"shape\":[4],\"data_offsets\":\"0\"}}",       // offsets not a list
+        "{\"x\":{\"dtype\":\"F32\",\"shape\":[-4],\"data_offsets\":[0,16]}}",       // negative dim
+        "{\"x\":{\"dtype\":\"F32\",\"shape\":[4],\"data_offsets\":[0,99999999999999999999]}}",
+        "{\"x\":{\"dtype\":\"F32\",\"shape\":[4294967296,4294967296],\"data_offsets\":[0,16]}}",
+        "{\"x\":{\"dtype\":\"F\\uZZ32\",\"shape\":[4],\"data_offsets\":[0,16]}}",   // bad \\u escape
+        "{\"x\":{\"dtype\":\"F32\",\"shape\":[4],\"data_offsets\":[0,1.5e999]}}",
+        std::string(5000, '[') + std::string(5000, ']'),                          // deep nesting
+    };
+    for (size_t h = 0; h < headers.size(); ++h) {
+      std::string file(8, '\0');
+      const uint64_t n = headers[h].size();
+      for (int k = 0; k < 8; ++k) file[k] = (char)(n >> (8 * k));
+      file += headers[h] + std::string(16, '\0');
+      std::ofstream(tmp / "bad2.safetensors", std::ios::binary) << file;
+      int status = -1;
+      try {
+        read_safetensors((tmp / "bad2.safetensors").string());
+      } catch (const Error& e) {
+        status = e.status;
+      } catch (...) {
+        status = -2;
+      }
+      EXPECT(status == MLXQ_EINVAL, "malformed header %zu gave status %d", h, status);
+    }
   }
 
   banner("write_quantized_config merges into an existing config");
