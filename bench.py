@@ -267,7 +267,7 @@ def bench_f32_mlp(mlxq, torch):
             "down_TFLOPs": round(flop / (t_dn * 1e-3) / 1e12, 1),
             "TFLOPs": round(tf, 1), "frac_of_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 3),
             "bf16_mfma_frac": round(3 * tf / MFMA_BF16_PEAK_TFLOPS, 4),
-            "note": "f32 x and h; the up launch includes the f32 GELU epilogue pass"}
+            "note": "f32 x and h; bias and GELU fused into the up GEMM epilogue"}
 
 
 def bench_config1(mlxq, torch):

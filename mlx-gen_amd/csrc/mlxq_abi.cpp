@@ -514,6 +514,15 @@ int mlxq_linear(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
     if ((rc = epilogue_table(a, st))) return rc;
     return run_linear_epilogue(a, st);
   }
+  // An f32 product at GEMM size fuses the bias and the activation (all in f32) unless a LoRA
+  // adapter needs the elementwise epilogue.
+  if (!p.d0_bf16 && M > 8 && !p.lora) {
+    F32Epilogue fe;
+    fe.bias = p.bias ? ep->bias : nullptr;
+    fe.bias_bf16 = p.bias && ep->bias_dtype == MLXQ_BFLOAT16;
+    fe.act = p.act;
+    return run_qmm_f32(x, x_dtype, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y, st, fe);
+  }
   // The product in D0, straight into y when y has that dtype; a bf16 product whose result
   // promotes to f32 goes through the workspace (the elementwise epilogue widens it into y).
   void* y0 = p.promoted() ? (char*)workspace + p.y0 : y;

@@ -91,10 +91,18 @@ int run_swiglu_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq_g, co
 // point for measuring it against the matrix-core GEMV).
 int run_qmv_valu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                  const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st);
+// The f32 epilogue the f32 GEMM can fuse: y + bias (bias in its own dtype, the sum in f32), then
+// an activation evaluated in f32 (mlxq_activation; the sequence of linear_epilogue_kernel in f32).
+struct F32Epilogue {
+  const void* bias = nullptr;  // [N]
+  bool bias_bf16 = false;
+  int act = 0;                 // mlxq_activation
+};
 // Large-M GEMM for operands MLX computes in f32 (f32 x and/or f32 scales), f32 y, as three bf16
 // MFMA passes over two-term bf16 splits of x and of the f32-dequantized weights.
 int run_qmm_f32(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
-                const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st);
+                const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st,
+                const F32Epilogue& epi = F32Epilogue{});
 int run_embedding(const int32_t* ids, int64_t T, const uint32_t* wq, const void* s, const void* b,
                   int sb_dtype, int64_t vocab, int64_t hidden, int gs, int bits, void* out,
                   int out_dtype, hipStream_t st);

@@ -70,13 +70,14 @@ __device__ __forceinline__ void f32_tile_coords(int64_t bid, int64_t tiles_m, in
 }  // namespace
 
 // XT: activation storage (float, or uint16_t bf16 bits); SB: scale/bias storage.  y is f32.
-// WAVES: 4 (2 x 2 waves of 64 x 64) or 8 (2 x 4 waves of 64 x 32, two per SIMD).
-template <typename XT, typename SB, int BITS, int GS, int WAVES, int BN, int BK>
+// WAVES: 4 (2 x 2 waves of 64 x 64) or 8 (2 x 4 waves of 64 x 32, two per SIMD).  EPI: the f32
+// epilogue (dense bias in its own dtype, then the f32 activation) is applied before the store.
+template <typename XT, typename SB, int BITS, int GS, int WAVES, int BN, int BK, bool EPI>
 __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restrict__ x, int64_t M,
                                                          int64_t K, const uint32_t* __restrict__ wq,
                                                          const SB* __restrict__ scales,
                                                          const SB* __restrict__ biases, int64_t N,
-                                                         float* __restrict__ y) {
+                                                         float* __restrict__ y, F32Epilogue epi) {
   constexpr bool XLO = std::is_same<XT, float>::value;  // activations carry a low part
   constexpr int BM = kF32BM, NT = WAVES * 64;
   constexpr int WGN = WAVES / 2;             // waves along N
@@ -275,6 +276,30 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
   // 4 half + (v & 3) of B's fragment: the weight operand is MFMA's A side, so each lane holds four
   // runs of 4 consecutive n for one m and stores them as 16-byte rows.
   const bool vec_ok = (N % 4) == 0;
+  // The f32 epilogue of LinearBase::forward + the caller's activation (reference
+  // src/adapters.rs:318-320, mlx-gen-flux/src/transformer.rs:975): y + bias in f32, then the
+  // activation evaluated in f32 — the same arithmetic as the elementwise epilogue kernel.
+  [[maybe_unused]] float bcol[TN][16];
+  if constexpr (EPI) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t n = bn0 + wn * WN + j * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+        const int64_t nc = n < N ? n : N - 1;  // columns past N are never stored
+        bcol[j][v] = epi.bias == nullptr ? 0.0f
+                     : epi.bias_bf16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(epi.bias)[nc])
+                                     : static_cast<const float*>(epi.bias)[nc];
+      }
+  }
+  auto finish = [&](float o, float bv) {
+    if constexpr (EPI) {
+      if (epi.bias) o += bv;
+      if (epi.act == MLXQ_ACT_GELU || epi.act == MLXQ_ACT_GELU_EXACT) o = gelu_erf(o);
+      else if (epi.act == MLXQ_ACT_GELU_TANH) o = gelu_tanh<false>(o);
+    }
+    return o;
+  };
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int64_t m = bm0 + wm * WM + i * 32 + r32;
@@ -285,7 +310,9 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
         const int64_t n = bn0 + wn * WN + j * 32 + 8 * a + 4 * half;
-        const f32x4 v = {acc[i][j][4 * a], acc[i][j][4 * a + 1], acc[i][j][4 * a + 2], acc[i][j][4 * a + 3]};
+        f32x4 v;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) v[b] = finish(acc[i][j][4 * a + b], EPI ? bcol[j][4 * a + b] : 0.0f);
         if (vec_ok && n + 3 < N) {
           *reinterpret_cast<f32x4*>(yrow + n) = v;
         } else {
@@ -300,7 +327,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
 
 template <typename XT, typename SB, int BITS, int GS>
 static int launch_qmm_f32(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
-                          const void* b, int64_t N, void* y, hipStream_t st) {
+                          const void* b, int64_t N, void* y, const F32Epilogue& epi, hipStream_t st) {
   // 4 waves on 128 x 128 tiles with 32-deep K steps (64 KB of LDS, two workgroups per CU):
   // 1225 us on the FLUX up shape (f32 x, Q4 g64, 284 TFLOP/s) against 1279 with 8 waves, 1336
   // with 128 x 256 tiles (1 workgroup per CU) and 1614 with 64-deep steps (128 KB, 1 per CU).
@@ -308,30 +335,39 @@ static int launch_qmm_f32(const void* x, int64_t M, int64_t K, const uint32_t* w
   const int64_t tiles = ((M + kF32BM - 1) / kF32BM) * ((N + BN - 1) / BN);
   if (tiles == 0) return MLXQ_OK;
   if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm_f32: problem too large");
-  hipLaunchKernelGGL((qmm_f32_kernel<XT, SB, BITS, GS, WAVES, BN, BK>), dim3((unsigned)tiles), dim3(WAVES * 64),
-                     0, st, (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (float*)y);
+  if (epi.bias || epi.act != MLXQ_ACT_NONE)
+    hipLaunchKernelGGL((qmm_f32_kernel<XT, SB, BITS, GS, WAVES, BN, BK, true>), dim3((unsigned)tiles),
+                       dim3(WAVES * 64), 0, st, (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N,
+                       (float*)y, epi);
+  else
+    hipLaunchKernelGGL((qmm_f32_kernel<XT, SB, BITS, GS, WAVES, BN, BK, false>), dim3((unsigned)tiles),
+                       dim3(WAVES * 64), 0, st, (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N,
+                       (float*)y, epi);
   return check_launch("qmm_f32");
 }
 
 template <typename XT, typename SB>
 static int qmm_f32_bits_gs(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
-                           const void* b, int64_t N, int gs, int bits, void* y, hipStream_t st) {
+                           const void* b, int64_t N, int gs, int bits, void* y, const F32Epilogue& epi,
+                           hipStream_t st) {
 #define MLXQ_F(B, G) \
-  if (bits == B && gs == G) return launch_qmm_f32<XT, SB, B, G>(x, M, K, wq, s, b, N, y, st);
+  if (bits == B && gs == G) return launch_qmm_f32<XT, SB, B, G>(x, M, K, wq, s, b, N, y, epi, st);
   MLXQ_F(4, 32) MLXQ_F(4, 64) MLXQ_F(4, 128) MLXQ_F(8, 32) MLXQ_F(8, 64) MLXQ_F(8, 128)
 #undef MLXQ_F
   return set_error(MLXQ_EINVAL, "qmm_f32: unsupported bits=%d group_size=%d", bits, gs);
 }
 
 int run_qmm_f32(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
-                const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st) {
+                const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st,
+                const F32Epilogue& epi) {
   if (x_dtype == MLXQ_BFLOAT16 && sb_dtype == MLXQ_BFLOAT16)
     return set_error(MLXQ_EINVAL, "qmm_f32: bf16 operands take the bf16 GEMM");
   if (x_dtype == MLXQ_FLOAT32) {
-    if (sb_dtype == MLXQ_BFLOAT16) return qmm_f32_bits_gs<float, uint16_t>(x, M, K, wq, s, b, N, gs, bits, y, st);
-    return qmm_f32_bits_gs<float, float>(x, M, K, wq, s, b, N, gs, bits, y, st);
+    if (sb_dtype == MLXQ_BFLOAT16)
+      return qmm_f32_bits_gs<float, uint16_t>(x, M, K, wq, s, b, N, gs, bits, y, epi, st);
+    return qmm_f32_bits_gs<float, float>(x, M, K, wq, s, b, N, gs, bits, y, epi, st);
   }
-  return qmm_f32_bits_gs<uint16_t, float>(x, M, K, wq, s, b, N, gs, bits, y, st);
+  return qmm_f32_bits_gs<uint16_t, float>(x, M, K, wq, s, b, N, gs, bits, y, epi, st);
 }
 
 }  // namespace mlxq

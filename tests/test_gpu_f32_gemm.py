@@ -87,3 +87,35 @@ def test_f32_flux_mlp_up_every_tile_band(mlxq, act):
                         sb_bf16=True)
     rel, peak = assert_close(got, ref, f"f32 flux up act={act}")
     assert rel < 1e-4
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3])
+@pytest.mark.parametrize("bias_dt", ["f32", "bf16", None])
+def test_f32_fused_epilogue_matches_elementwise(mlxq, act, bias_dt):
+    """The f32 GEMM applies the bias and the activation before its store; a LoRA adapter sends the
+    same linear through the product followed by the elementwise epilogue kernel instead.  With a
+    zero B factor the residual adds exactly 0.0 in f32, so both routes must agree bit for bit
+    (bias in either dtype, every activation), and both must match the oracle's f32 linear."""
+    banner("f32 fused epilogue", act, bias_dt)
+    rng = np.random.default_rng(77 + act)
+    M, K, N = 200, 512, 262
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = oracle.bf16_round((rng.standard_normal((N, K)) * 0.05).astype(np.float32))
+    rwq, rs, rb = oracle.quantize(w, 64, 4, sb_bf16=True)
+    bias = None
+    if bias_dt is not None:
+        bias = (rng.standard_normal(N) * 0.5).astype(np.float32)
+        if bias_dt == "bf16":
+            bias = oracle.bf16_round(bias)
+    gb = None if bias is None else to_gpu(bias, _tdt(bias_dt))
+    args = (to_gpu(x, torch.float32), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), 64, 4)
+    fused = mlxq.linear(*args, bias=gb, activation=act)
+    la = to_gpu((rng.standard_normal((K, 4)) * 0.1).astype(np.float32), torch.float32)
+    lb = torch.zeros((4, N), dtype=torch.float32, device=la.device)
+    split = mlxq.linear(*args, bias=gb, lora_a=la, lora_b=lb, lora_scale=1.0, activation=act)
+    assert fused.dtype == torch.float32 and split.dtype == torch.float32
+    assert torch.equal(fused, split), "fused f32 epilogue differs from the elementwise epilogue"
+    ref = oracle.linear(x, rwq, rs, rb, 64, 4, w_bf16=False, act_bf16=False, bias=bias, act=act,
+                        sb_bf16=True, bias_bf16=(bias_dt == "bf16"))
+    rel, peak = assert_close(to_np(fused), ref, f"f32 fused epilogue act={act} bias={bias_dt}")
+    assert rel < 1e-4
