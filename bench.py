@@ -15,6 +15,7 @@ Also reported (same JSON line):
   config1/3/5  the other BASELINE configs (quantize/dequantize/qmm, the Q8 projection, the LoRA sweep);
   experts      the stacked-expert MoE projections (one launch vs one linear per expert);
   f32_mlp      config 2 on FLUX.1's f32 stream (f32 x and h, split-bf16 matrix-core GEMM);
+  dense_bf16_reference  context only: the library dense bf16 GEMM (torch.mm) on the same shapes;
   cpu_baseline the CPU oracle (fp64-accumulating C restatement, OpenMP) on a bounded row sample of
                the same up-projection, scaled to TFLOP/s.
 """
@@ -43,7 +44,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extras", action="store_true", help="headline GEMM only")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
-    p.add_argument("--only", choices=("all", "mlp", "gemv", "quantize", "copy", "configs", "experts", "f32"),
+    p.add_argument("--only", choices=("all", "mlp", "gemv", "quantize", "copy", "configs", "experts", "f32",
+                                       "dense"),
                    default="all",
                    help="run one leg only (for profiling); 'copy' is the plain-copy calibration "
                         "kernel for the HBM byte counters")
@@ -268,6 +270,42 @@ def bench_f32_mlp(mlxq, torch):
             "TFLOPs": round(tf, 1), "frac_of_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 3),
             "bf16_mfma_frac": round(3 * tf / MFMA_BF16_PEAK_TFLOPS, 4),
             "note": "f32 x and h; bias and GELU fused into the up GEMM epilogue"}
+
+
+def bench_dense_reference(torch):
+    """Context for the roofline fraction, not part of the path: the library dense bf16 GEMM
+    (torch.mm on hipBLASLt) on config 2's two shapes with the bf16 weights themselves (no
+    quantization, no dequantization, no GELU).  The right operand is W^T made contiguous [K, N]."""
+    dev = torch.device("cuda:0")
+    M, K, F = 4608, 3072, 12288
+    x = gen_bf16((M, K), 1.0, 0, dev)
+    wu_t = gen_bf16((F, K), 0.02, 1, dev).t().contiguous()
+    wd_t = gen_bf16((K, F), 0.02, 2, dev).t().contiguous()
+    h = gen_bf16((M, F), 1.0, 3, dev)
+    yu = torch.empty((M, F), dtype=torch.bfloat16, device=dev)
+    yd = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    def ev_ms(fn, reps=20):  # plain launches between events (no graph capture of library calls)
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    t_up = ev_ms(lambda: torch.mm(x, wu_t, out=yu))
+    t_dn = ev_ms(lambda: torch.mm(h, wd_t, out=yd))
+    flop = 2.0 * M * K * F
+    tf = 2 * flop / ((t_up + t_dn) * 1e-3) / 1e12
+    return {"up_ms": round(t_up, 4), "down_ms": round(t_dn, 4),
+            "up_TFLOPs": round(flop / (t_up * 1e-3) / 1e12, 1),
+            "down_TFLOPs": round(flop / (t_dn * 1e-3) / 1e12, 1),
+            "TFLOPs": round(tf, 1), "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "note": "torch.mm (hipBLASLt) on dense bf16 weights of the config-2 shapes: the vendor "
+                    "GEMM without dequantization, for context only"}
 
 
 def bench_config1(mlxq, torch):
@@ -535,6 +573,9 @@ def main():
     if args.only == "f32":
         print(json.dumps({"f32_mlp": bench_f32_mlp(mlxq, torch)}))
         return
+    if args.only == "dense":
+        print(json.dumps({"dense_bf16_reference": bench_dense_reference(torch)}))
+        return
     if args.only == "configs":
         print(json.dumps({"config1": bench_config1(mlxq, torch), "config3": bench_config3(mlxq, torch),
                           "config5": bench_config5(mlxq, torch)}))
@@ -572,6 +613,7 @@ def main():
         res["config5"] = bench_config5(mlxq, torch)
         res["experts"] = bench_experts(mlxq, torch)
         res["f32_mlp"] = bench_f32_mlp(mlxq, torch)
+        res["dense_bf16_reference"] = bench_dense_reference(torch)
     if not args.no_cpu and args.only == "all":
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(res))
