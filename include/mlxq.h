@@ -244,6 +244,21 @@ int mlxq_lora_residual(const void* x, int x_dtype, int64_t M, int64_t K, const v
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * One LoKr adapter on an already computed output — the Adapter::Lokr arm of Adapter::residual
+ * (src/adapters.rs:263-266) in AdaptableLinear::forward's residual sum (:543-549):
+ *   d = delta cast to x_dtype;  r = x . d^T in x_dtype (f32 accumulation, rounded once);
+ *   r = r * scale (scale cast to x_dtype first);  y_out = y_in + r in promote(y_dtype, x_dtype).
+ * delta [N, K] in delta_dtype is the reconstructed kron delta (reconstruct_lokr_delta,
+ * src/adapters.rs:26-128; the reference stores it bf16).  K must be a multiple of 32.  y_out may be
+ * y_in when the sum keeps y_dtype; otherwise the two must not overlap.  workspace:
+ * mlxq_lokr_residual_workspace_size() bytes (the f32 product, M*N*4).
+ */
+size_t mlxq_lokr_residual_workspace_size(int x_dtype, int64_t M, int64_t N);
+int mlxq_lokr_residual(const void* x, int x_dtype, int64_t M, int64_t K, const void* delta,
+                       int delta_dtype, int64_t N, float scale, const void* y_in, int y_dtype,
+                       void* y_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Element-wise dtype conversion f32 <-> bf16 (round to nearest even) — the `as_dtype(Bfloat16)`
  * casts that precede packing in AdaptableLinear::quantize (src/adapters.rs:508-521) and
  * quant::quantize_map (src/quant.rs:140).  src/dst 4-byte aligned.

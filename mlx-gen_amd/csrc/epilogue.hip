@@ -252,6 +252,8 @@ __global__ void linear_epilogue_kernel(LinearEpilogueArgs a) {
     for (int k = 0; k < a.R; ++k)
       r = fmaf(ld_any(a.xa, a.dr_bf16, m * a.R + k), ld_any(a.lbt, a.dr_bf16, n * a.R + k), r);
     o = rnd_if(a.d2_bf16, o + rnd_if(a.dr_bf16, rnd_if(a.dr_bf16, r) * a.lora_scale));
+  } else if (a.res) {
+    o = rnd_if(a.d2_bf16, o + rnd_if(a.dr_bf16, rnd_if(a.dr_bf16, a.res[t]) * a.lora_scale));
   }
   const bool act_bf16 = a.d2_bf16;  // the activation's input dtype
   if (a.act == MLXQ_ACT_GELU) {

@@ -331,6 +331,59 @@ size_t mlxq_lora_residual_workspace_size(int x_dtype, int lora_dtype, int64_t M,
   return align256((size_t)(M * R * 4)) + align256((size_t)(N * R * 4));
 }
 
+size_t mlxq_lokr_residual_workspace_size(int x_dtype, int64_t M, int64_t N) {
+  (void)x_dtype;
+  if (M <= 0 || N <= 0) return 0;
+  return align256((size_t)(M * N * 4));  // the f32 product x . delta^T
+}
+
+int mlxq_lokr_residual(const void* x, int x_dtype, int64_t M, int64_t K, const void* delta,
+                       int delta_dtype, int64_t N, float scale, const void* y_in, int y_dtype,
+                       void* y_out, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc;
+  if ((rc = check_dtype("lokr_residual", "x", x_dtype)) ||
+      (rc = check_dtype("lokr_residual", "delta", delta_dtype)) ||
+      (rc = check_dtype("lokr_residual", "y", y_dtype)))
+    return rc;
+  if (M < 0 || K <= 0 || N < 0)
+    return set_error(MLXQ_EINVAL, "lokr_residual: bad shape M=%lld K=%lld N=%lld", (long long)M,
+                     (long long)K, (long long)N);
+  if (K % 32 != 0)
+    return set_error(MLXQ_EUNSUPPORTED, "lokr_residual: K=%lld is not a multiple of 32 (a quantized "
+                                        "base's K is a multiple of its group size)", (long long)K);
+  if (M == 0 || N == 0) return MLXQ_OK;
+  if (!x || !delta || !y_in || !y_out) return set_error(MLXQ_EINVAL, "lokr_residual: null operand");
+  if ((rc = check_aligned("lokr_residual", "x", x)) || (rc = check_aligned("lokr_residual", "delta", delta)))
+    return rc;
+  // The residual runs in the activation dtype (delta cast to it); the sum promotes with y.
+  const bool dr_bf16 = x_dtype == MLXQ_BFLOAT16;
+  const bool out_bf16 = y_dtype == MLXQ_BFLOAT16 && dr_bf16;
+  if (y_in == y_out && out_bf16 != (y_dtype == MLXQ_BFLOAT16))
+    return set_error(MLXQ_EINVAL, "lokr_residual: the sum promotes to float32 and cannot overwrite the "
+                                  "bfloat16 y_in in place");
+  const size_t need = mlxq_lokr_residual_workspace_size(x_dtype, M, N);
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error(MLXQ_EINVAL, "lokr_residual: workspace of %zu bytes is smaller than the %zu required",
+                     workspace_bytes, need);
+  if ((rc = check_aligned("lokr_residual", "workspace", workspace))) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = run_dense_f32(x, x_dtype, M, K, delta, delta_dtype, N, (float*)workspace, st))) return rc;
+  LinearEpilogueArgs a;
+  a.y_in = y_in;
+  a.y_in_bf16 = y_dtype == MLXQ_BFLOAT16;
+  a.y_out = y_out;
+  a.y_out_bf16 = out_bf16;
+  a.M = M;
+  a.N = N;
+  a.d1_bf16 = a.y_in_bf16;
+  a.res = (const float*)workspace;
+  a.dr_bf16 = dr_bf16;
+  a.lora_scale = dr_bf16 ? bf16_scalar(scale) : scale;
+  a.d2_bf16 = out_bf16;
+  return run_linear_epilogue(a, st);
+}
+
 int mlxq_swiglu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq_gate,
                 const void* scales_gate, const void* biases_gate, const uint32_t* wq_up,
                 const void* scales_up, const void* biases_up, int sb_dtype, int64_t F,

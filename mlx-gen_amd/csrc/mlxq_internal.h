@@ -45,6 +45,8 @@ struct LinearEpilogueArgs {
   bool d2_bf16 = true;         // y + r rounds to bf16
   int act = 0;                 // mlxq_activation
   const uint16_t* act_table = nullptr;  // bf16 table of act when the activation runs in bf16
+  const float* res = nullptr;  // [M, N] f32 product of a dense residual (LoKr), R must be 0: r is
+                               // this value rounded to DR, then scaled like the LoRA residual
 };
 
 // A stacked launch over `count` matrices of the same shape (the experts of an [E, out, ...] pack):
@@ -103,6 +105,10 @@ struct F32Epilogue {
 int run_qmm_f32(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                 const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st,
                 const F32Epilogue& epi = F32Epilogue{});
+// y[M, N] f32 = x[M, K] . d^T for a dense d [N, K] in d_dtype, cast to bf16 against bf16 x, on
+// the matrix cores (bf16 passes over two-term splits of the f32 operands).  K % 32 == 0.
+int run_dense_f32(const void* x, int x_dtype, int64_t M, int64_t K, const void* d, int d_dtype,
+                  int64_t N, float* y, hipStream_t st);
 int run_embedding(const int32_t* ids, int64_t T, const uint32_t* wq, const void* s, const void* b,
                   int sb_dtype, int64_t vocab, int64_t hidden, int gs, int bits, void* out,
                   int out_dtype, hipStream_t st);

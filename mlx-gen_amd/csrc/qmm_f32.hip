@@ -72,13 +72,22 @@ __device__ __forceinline__ void f32_tile_coords(int64_t bid, int64_t tiles_m, in
 // XT: activation storage (float, or uint16_t bf16 bits); SB: scale/bias storage.  y is f32.
 // WAVES: 4 (2 x 2 waves of 64 x 64) or 8 (2 x 4 waves of 64 x 32, two per SIMD).  EPI: the f32
 // epilogue (dense bias in its own dtype, then the f32 activation) is applied before the store.
-template <typename XT, typename SB, int BITS, int GS, int WAVES, int BN, int BK, bool EPI>
+// WT: uint32_t for packed codes (wq, scales, biases); uint16_t (bf16) or float for a dense [N, K]
+// weight matrix passed in wq's place (scales, biases, BITS and GS unused), the LoKr residual's
+// x . delta^T.  A dense f32 matrix against bf16 activations is rounded to bf16 first (MLX casts
+// the delta to the activation dtype).
+template <typename XT, typename SB, int BITS, int GS, int WAVES, int BN, int BK, bool EPI,
+          typename WT = uint32_t>
 __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restrict__ x, int64_t M,
                                                          int64_t K, const uint32_t* __restrict__ wq,
                                                          const SB* __restrict__ scales,
                                                          const SB* __restrict__ biases, int64_t N,
                                                          float* __restrict__ y, F32Epilogue epi) {
   constexpr bool XLO = std::is_same<XT, float>::value;  // activations carry a low part
+  constexpr bool DENSE = !std::is_same<WT, uint32_t>::value;
+  // Weights carry a low part unless they are bf16 values: dequantized codes are f32, and a dense
+  // f32 matrix keeps its low part against f32 activations.
+  constexpr bool WLO = !DENSE || (std::is_same<WT, float>::value && XLO);
   constexpr int BM = kF32BM, NT = WAVES * 64;
   constexpr int WGN = WAVES / 2;             // waves along N
   constexpr int WM = BM / 2, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
@@ -88,6 +97,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
   constexpr int WPT = CPT * BITS / 32;       // their packed words
   constexpr int PPR = BK / CPT;              // threads per weight row
   constexpr int TA = BM * BK * 2, TB = BN * BK * 2;  // bytes of one activation / weight tile
+  constexpr int DV = DENSE ? CPT * (int)sizeof(WT) / 16 : 1;  // 16-byte loads of dense weights
   static_assert(A_LD >= 1 && TM >= 1 && TN >= 1 && CPT >= 8 && CPT <= 32 && PPR >= 1, "tile shape");
   // Per buffer: x_hi, x_lo, w_hi, w_lo.
   __shared__ __attribute__((aligned(16))) unsigned char smem[2][2 * TA + 2 * TB];
@@ -108,6 +118,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
   u32x4 a_reg[A_LD][XLO ? 2 : 1];
   uint32_t b_reg[WPT];
   float s_reg, z_reg;
+  [[maybe_unused]] u32x4 d_reg[DV];
 
   auto load_global = [&](int kt) {
     const int64_t k0 = (int64_t)kt * BK;
@@ -121,7 +132,15 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
       for (int h = 0; h < (XLO ? 2 : 1); ++h)
         a_reg[i][h] = ok ? reinterpret_cast<const u32x4*>(x + m * K + k)[h] : u32x4{0u, 0u, 0u, 0u};
     }
-    {  // CPT consecutive codes of one weight row (one group: CPT <= 32 <= group size)
+    if constexpr (DENSE) {  // CPT consecutive values of one weight row
+      const int row = tid / PPR, part = tid % PPR;
+      const int64_t n = bn0 + row;
+      const int64_t kc = k0 + part * CPT;
+      const bool ok = n < N && kc < K;
+      const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const WT*>(wq) + n * K + kc);
+#pragma unroll
+      for (int q = 0; q < DV; ++q) d_reg[q] = ok ? src[q] : u32x4{0u, 0u, 0u, 0u};
+    } else {  // CPT consecutive codes of one weight row (one group: CPT <= 32 <= group size)
       const int row = tid / PPR, part = tid % PPR;
       const int64_t n = bn0 + row;
       const int64_t kc = k0 + part * CPT;
@@ -173,7 +192,32 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
         *reinterpret_cast<u32x4*>(Ah + swz32<BK>(row, c)) = a_reg[i][0];
       }
     }
-    {
+    if constexpr (DENSE) {
+      const int row = tid / PPR, part = tid % PPR;
+      const int c0 = part * CPT / 8;
+#pragma unroll
+      for (int p = 0; p < CPT / 8; ++p) {
+        if constexpr (std::is_same<WT, uint16_t>::value) {
+          *reinterpret_cast<u32x4*>(Bh + swz32<BK>(row, c0 + p)) = d_reg[p];
+        } else {
+          u32x4 hi, lo;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const u32x4& src = d_reg[2 * p + (e >> 1)];
+            const float v0 = __uint_as_float(src[2 * (e & 1)]), v1 = __uint_as_float(src[2 * (e & 1) + 1]);
+            if constexpr (WLO) {
+              const u32x2 q = split2(v0, v1);
+              hi[e] = q[0];
+              lo[e] = q[1];
+            } else {
+              hi[e] = pack_bf16x2(v0, v1);
+            }
+          }
+          *reinterpret_cast<u32x4*>(Bh + swz32<BK>(row, c0 + p)) = hi;
+          if constexpr (WLO) *reinterpret_cast<u32x4*>(Bl + swz32<BK>(row, c0 + p)) = lo;
+        }
+      }
+    } else {
       const int row = tid / PPR, part = tid % PPR;
       const float s = s_reg, z = z_reg;
       // LDS chunk c holds k [8c, 8c + 8) of the step; this thread's codes start at chunk part*CPT/8.
@@ -250,17 +294,19 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         bh[j] = *reinterpret_cast<const bf16x8*>(Bh + swz32<BK>(wn * WN + j * 32 + r32, c));
-        bl[j] = *reinterpret_cast<const bf16x8*>(Bl + swz32<BK>(wn * WN + j * 32 + r32, c));
+        if constexpr (WLO) bl[j] = *reinterpret_cast<const bf16x8*>(Bl + swz32<BK>(wn * WN + j * 32 + r32, c));
       }
       // Three passes over the independent accumulators, so no MFMA waits on its predecessor.
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh[j], ah[i], acc[i][j], 0, 0, 0);
+      if constexpr (WLO) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bl[j], ah[i], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bl[j], ah[i], acc[i][j], 0, 0, 0);
+      }
       if constexpr (XLO) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -368,6 +414,31 @@ int run_qmm_f32(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
     return qmm_f32_bits_gs<float, float>(x, M, K, wq, s, b, N, gs, bits, y, epi, st);
   }
   return qmm_f32_bits_gs<uint16_t, float>(x, M, K, wq, s, b, N, gs, bits, y, epi, st);
+}
+
+// y[M, N] (f32) = x . d^T for a dense [N, K] matrix d (bf16 or f32; cast to bf16 against bf16
+// x), on the same tiles: one bf16 pass for bf16 x with a bf16 (or bf16-cast) d, two for f32 x
+// with bf16 d (d is exact in bf16), three for f32 x with f32 d.  K % 32 == 0.
+int run_dense_f32(const void* x, int x_dtype, int64_t M, int64_t K, const void* d, int d_dtype,
+                  int64_t N, float* y, hipStream_t st) {
+  constexpr int WAVES = 4, BN = 128, BK = 32;
+  if (K % BK != 0) return set_error(MLXQ_EINVAL, "dense product: K=%lld is not a multiple of 32", (long long)K);
+  const int64_t tiles = ((M + kF32BM - 1) / kF32BM) * ((N + BN - 1) / BN);
+  if (tiles == 0) return MLXQ_OK;
+  if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "dense product: problem too large");
+  const F32Epilogue none{};
+#define MLXQ_D(XT, WT)                                                                                    \
+  hipLaunchKernelGGL((qmm_f32_kernel<XT, float, 4, 32, WAVES, BN, BK, false, WT>), dim3((unsigned)tiles), \
+                     dim3(WAVES * 64), 0, st, (const XT*)x, M, K, (const uint32_t*)d, nullptr, nullptr, N, y, none)
+  if (x_dtype == MLXQ_BFLOAT16) {
+    if (d_dtype == MLXQ_BFLOAT16) MLXQ_D(uint16_t, uint16_t);
+    else MLXQ_D(uint16_t, float);
+  } else {
+    if (d_dtype == MLXQ_BFLOAT16) MLXQ_D(float, uint16_t);
+    else MLXQ_D(float, float);
+  }
+#undef MLXQ_D
+  return check_launch("dense_f32");
 }
 
 }  // namespace mlxq

@@ -393,7 +393,7 @@ Dtype AdaptableLinear::out_dtype(Dtype x_dtype) const {
   const QuantizedLinear& q = *quantized_;
   Dtype d = promote(x_dtype, q.scales.dtype());
   if (q.bias) d = promote(d, q.bias->dtype());
-  for (const Adapter& ad : adapters_) d = promote(d, promote(x_dtype, ad.a.dtype()));
+  for (const Adapter& ad : adapters_) d = promote(d, ad.is_lokr() ? x_dtype : promote(x_dtype, ad.a.dtype()));
   return d;
 }
 
@@ -403,20 +403,22 @@ Array AdaptableLinear::forward_impl(const Array& x, const Array* out_arg, hipStr
                 "AdaptableLinear: the dense base is not on the quantized path; call quantize() first");
   const QuantizedLinear& q = *quantized_;
   for (const Adapter& ad : adapters_)
-    if (ad.a.ndim() != 2 || ad.a.dim(1) > 256)
+    if (!ad.is_lokr() && (ad.a.ndim() != 2 || ad.a.dim(1) > 256))
       throw Error(MLXQ_EUNSUPPORTED, "AdaptableLinear: LoRA rank above 256");
   if (adapters_.empty()) return q.forward_fused(x, nullptr, MLXQ_ACT_NONE, s, out_arg);
-  // The first adapter rides in mlxq_linear's epilogue, later ones are added one at a time
+  // A leading LoRA adapter rides in mlxq_linear's epilogue, the others are added one at a time
   // (out = out + residual, src/adapters.rs:545-547), each sum in MLX's promoted dtype.  Every
   // workspace is the layer's own (kept between calls), so nothing here waits for the device, and
   // with a caller's output nothing is allocated after the first call: a result that promotes
   // from bf16 to f32 part-way down the stack keeps its bf16 part in a layer-owned buffer.
   const Dtype final_dt = out_dtype(x.dtype());
+  const Adapter* fused = adapters_[0].is_lokr() ? nullptr : &adapters_[0];
+  const size_t rest = fused ? 1 : 0;  // first adapter applied one at a time
   const Array* first_out = out_arg;
   Array mid;
-  if (out_arg && adapters_.size() > 1) {
-    const Dtype d1 = promote(promote(x.dtype(), q.scales.dtype()),
-                             promote(q.bias ? q.bias->dtype() : x.dtype(), promote(x.dtype(), adapters_[0].a.dtype())));
+  if (out_arg && adapters_.size() > rest) {
+    Dtype d1 = promote(promote(x.dtype(), q.scales.dtype()), q.bias ? q.bias->dtype() : x.dtype());
+    if (fused) d1 = promote(d1, promote(x.dtype(), fused->a.dtype()));
     if (d1 != final_dt) {
       if (!mid_ || mid_->shape() != out_arg->shape() || mid_->dtype() != d1)
         mid_ = std::make_shared<Array>(Array::empty(out_arg->shape(), d1));
@@ -424,11 +426,24 @@ Array AdaptableLinear::forward_impl(const Array& x, const Array* out_arg, hipStr
       first_out = &mid;
     }
   }
-  Array y = q.forward_fused(x, &adapters_[0], MLXQ_ACT_NONE, s, first_out);
+  Array y = q.forward_fused(x, fused, MLXQ_ACT_NONE, s, first_out);
   const int xdt = abi_dtype(x.dtype(), "AdaptableLinear::forward");
   const int64_t K = x.dim(-1), N = q.weight.dim(0), M = K > 0 ? x.size() / K : 0;
-  for (size_t i = 1; i < adapters_.size(); ++i) {
+  for (size_t i = rest; i < adapters_.size(); ++i) {
     const Adapter& ad = adapters_[i];
+    if (ad.is_lokr()) {
+      if (ad.delta.ndim() != 2 || ad.delta.dim(0) != N || ad.delta.dim(1) != K)
+        throw Error(MLXQ_EINVAL, "AdaptableLinear: a LoKr delta must be [out, in]");
+      const Dtype odt = promote(y.dtype(), x.dtype());
+      Array out = odt == y.dtype() ? y : (out_arg ? *out_arg : Array::empty(y.shape(), odt));
+      Array& ws = grow_workspace(workspace_, mlxq_lokr_residual_workspace_size(xdt, M, N));
+      check(mlxq_lokr_residual(x.data(), xdt, M, K, ad.delta.data(),
+                               abi_dtype(ad.delta.dtype(), "AdaptableLinear::forward"), N, ad.scale,
+                               y.data(), abi_dtype(y.dtype(), "AdaptableLinear::forward"), out.data(),
+                               ws.data(), ws.nbytes(), s));
+      y = out;
+      continue;
+    }
     if (ad.a.ndim() != 2 || ad.b.ndim() != 2 || ad.a.dim(0) != K || ad.b.dim(1) != N ||
         ad.a.dim(1) != ad.b.dim(0) || ad.a.dtype() != ad.b.dtype())
       throw Error(MLXQ_EINVAL, "AdaptableLinear: LoRA factors must be A [in, r] and B [r, out] of one dtype");

@@ -90,11 +90,26 @@ Array quantized_matmul(const Array& x, const Array& wq, const Array& scales, con
 int packed_bits(const Array& wq, const Array& scales, int group_size);
 
 // ---- layers ---------------------------------------------------------------------------------
-// LoRA adapter: residual = scale * (x.A).B with A [in, r], B [r, out] (alpha/rank folded in B,
-// src/adapters/loader.rs:568-599).
+// One adapter of AdaptableLinear's stack (enum Adapter, src/adapters.rs:231-270):
+//   LoRA: residual = scale * (x.A).B with A [in, r], B [r, out] (alpha/rank folded in B,
+//         src/adapters/loader.rs:568-599), the factors in their file dtype;
+//   LoKr: residual = scale * x . delta^T with delta [out, in] the reconstructed kron delta
+//         (reconstruct_lokr_delta, src/adapters.rs:26-128), cast to the activation dtype.
 struct Adapter {
-  Array a, b;
+  Array a, b;  // LoRA factors
   float scale = 1.0f;
+  Array delta;  // LoKr delta (kind == Kind::Lokr)
+  enum class Kind { Lora, Lokr } kind = Kind::Lora;
+
+  static Adapter lora(Array a, Array b, float scale) { return Adapter{std::move(a), std::move(b), scale}; }
+  static Adapter lokr(Array delta, float scale) {
+    Adapter r;
+    r.delta = std::move(delta);
+    r.scale = scale;
+    r.kind = Kind::Lokr;
+    return r;
+  }
+  bool is_lokr() const { return kind == Kind::Lokr; }
 };
 
 struct QuantizedLinear {
@@ -148,7 +163,7 @@ class AdaptableLinear {
   std::optional<Array> dense_weight_, dense_bias_;
   std::optional<QuantizedLinear> quantized_;
   std::vector<Adapter> adapters_;
-  mutable std::shared_ptr<Array> workspace_;  // mlxq_lora_residual staging, grown on demand
+  mutable std::shared_ptr<Array> workspace_;  // mlxq_{lora,lokr}_residual staging, grown on demand
   mutable std::shared_ptr<Array> mid_;        // a bf16 partial sum before an f32 adapter
 };
 

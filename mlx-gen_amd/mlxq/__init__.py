@@ -8,17 +8,17 @@ All compute runs in libmlxq_hip.so (hand-written HIP for gfx950) through its C A
 from ._lib import (MLXQ_ACT_GELU, MLXQ_ACT_GELU_EXACT, MLXQ_ACT_GELU_TANH, MLXQ_ACT_NONE,
                    MLXQ_BFLOAT16, MLXQ_FLOAT32, MlxqError, LIB_PATH, load)
 from .ops import (DEFAULT_GROUP_SIZE, dequantize, embedding, linear, linear_out_dtype,
-                  linear_workspace_size, lora_residual, packed_bits, promote, qmm, qmm_experts, qmv,
+                  linear_workspace_size, lokr_residual, lora_residual, packed_bits, promote, qmm, qmm_experts, qmv,
                   qmv_valu, quantize, quantized_matmul, swiglu)
-from .nn import (Adapter, AdaptableLinear, QuantizedLinear, StackedExperts, TokenEmbedding,
+from .nn import (Adapter, AdaptableLinear, LokrAdapter, QuantizedLinear, StackedExperts, TokenEmbedding,
                  has_packed_experts, lin, load_packed_experts, quantize_map)
 from . import io
 
 __all__ = [
     "MLXQ_ACT_GELU", "MLXQ_ACT_GELU_EXACT", "MLXQ_ACT_GELU_TANH", "MLXQ_ACT_NONE", "MLXQ_BFLOAT16",
     "MLXQ_FLOAT32", "MlxqError", "LIB_PATH", "load", "DEFAULT_GROUP_SIZE", "dequantize", "embedding",
-    "linear", "linear_out_dtype", "linear_workspace_size", "lora_residual", "packed_bits", "promote",
+    "linear", "linear_out_dtype", "linear_workspace_size", "lokr_residual", "lora_residual", "packed_bits", "promote",
     "qmm", "qmm_experts", "qmv", "qmv_valu", "quantize",
-    "quantized_matmul", "swiglu", "Adapter", "AdaptableLinear", "QuantizedLinear", "StackedExperts",
+    "quantized_matmul", "swiglu", "Adapter", "AdaptableLinear", "LokrAdapter", "QuantizedLinear", "StackedExperts",
     "TokenEmbedding", "has_packed_experts", "lin", "load_packed_experts", "quantize_map", "io",
 ]

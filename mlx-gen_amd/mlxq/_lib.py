@@ -45,6 +45,8 @@ EXPORTS = (
     "mlxq_embedding",
     "mlxq_lora_residual",
     "mlxq_lora_residual_workspace_size",
+    "mlxq_lokr_residual",
+    "mlxq_lokr_residual_workspace_size",
     "mlxq_cast",
     "mlxq_swiglu",
     "mlxq_qmm_experts",
@@ -111,6 +113,10 @@ def load():
     lib.mlxq_packed_bits.argtypes = [_i64, _i64, _int]
     lib.mlxq_lora_residual.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _int, _i64, _i64,
                                        ctypes.c_float, _vp, _int, _vp, _vp, ctypes.c_size_t, _vp]
+    lib.mlxq_lokr_residual_workspace_size.argtypes = [_int, _i64, _i64]
+    lib.mlxq_lokr_residual_workspace_size.restype = ctypes.c_size_t
+    lib.mlxq_lokr_residual.argtypes = [_vp, _int, _i64, _i64, _vp, _int, _i64, ctypes.c_float, _vp,
+                                       _int, _vp, _vp, ctypes.c_size_t, _vp]
     lib.mlxq_cast.argtypes = [_vp, _int, _vp, _int, _i64, _vp]
     lib.mlxq_qmm_experts.argtypes = [_vp, _int, _int, _i64, _i64, _i64, _vp, _vp, _vp, _int, _vp,
                                      _int, _i64, _int, _int, _vp, _vp]
@@ -120,7 +126,8 @@ def load():
                                    _vp]
     for name in ("mlxq_quantize", "mlxq_dequantize", "mlxq_quantized_matmul", "mlxq_qmm",
                  "mlxq_qmv", "mlxq_qmv_valu", "mlxq_linear", "mlxq_linear_noalloc", "mlxq_packed_bits", "mlxq_embedding",
-                 "mlxq_lora_residual", "mlxq_cast", "mlxq_swiglu", "mlxq_qmm_experts"):
+                 "mlxq_lora_residual", "mlxq_lokr_residual", "mlxq_cast", "mlxq_swiglu",
+                 "mlxq_qmm_experts"):
         getattr(lib, name).restype = _int
     _lib = lib
     return lib

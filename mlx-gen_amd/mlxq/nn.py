@@ -1,7 +1,8 @@
 """Layer surface over the mlxq ops, mirroring the reference's quantized-linear seam.
 
   QuantizedLinear   ~ mlx_rs::nn::QuantizedLinear (try_from_linear used at src/adapters.rs:533-537)
-  Adapter           ~ src/adapters.rs:231-270 (LoRA arm; residual = scale * (x.A).B)
+  Adapter           ~ src/adapters.rs:231-270, LoRA arm (residual = scale * (x.A).B)
+  LokrAdapter       ~ src/adapters.rs:231-270, LoKr arm (residual = scale * x.delta^T)
   AdaptableLinear   ~ src/adapters.rs:330-549 (dense / quantized base + adapter stack)
   quantize_map      ~ src/quant.rs:125-149 (offline converter primitive)
   TokenEmbedding    ~ src/nn.rs:20-101 (dense or packed table; forward gathers + dequantizes)
@@ -70,12 +71,27 @@ class Adapter:
 
 
 @dataclass
+class LokrAdapter:
+    """LoKr adapter (Adapter::Lokr, src/adapters.rs:234-235): residual = scale * x . delta^T with
+    delta [out, in] the reconstructed kron delta (reconstruct_lokr_delta, :26-128; stored bf16),
+    cast to the activation dtype (:263-266)."""
+    delta: torch.Tensor
+    scale: float = 1.0
+
+    def residual(self, x: torch.Tensor) -> torch.Tensor:
+        """The dense-base arm's residual, in x's dtype with the scale cast to it.  Over a quantized
+        base the library applies it instead (ops.lokr_residual)."""
+        r = x @ self.delta.to(x.dtype).t()
+        return r * torch.tensor(self.scale, dtype=x.dtype, device=r.device)
+
+
+@dataclass
 class AdaptableLinear:
     """A linear base (dense or quantized) plus a stack of adapters: base(x) + sum residual(x)."""
     dense_weight: Optional[torch.Tensor] = None
     dense_bias: Optional[torch.Tensor] = None
     quantized: Optional[QuantizedLinear] = None
-    adapters: List[Adapter] = field(default_factory=list)
+    adapters: List[object] = field(default_factory=list)  # Adapter (LoRA) or LokrAdapter
 
     @classmethod
     def dense(cls, weight: torch.Tensor, bias: Optional[torch.Tensor] = None):
@@ -85,10 +101,10 @@ class AdaptableLinear:
     def from_quantized_parts(cls, weight, scales, biases, bias, group_size: int, bits: int):
         return cls(quantized=QuantizedLinear(weight, scales, biases, bias, group_size, bits))
 
-    def push(self, adapter: Adapter) -> None:
+    def push(self, adapter) -> None:
         self.adapters.append(adapter)
 
-    def set_adapters(self, adapters: List[Adapter]) -> None:
+    def set_adapters(self, adapters: List[object]) -> None:
         self.adapters = list(adapters)
 
     def is_quantized(self) -> bool:
@@ -113,21 +129,27 @@ class AdaptableLinear:
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.quantized is not None:
-            # src/adapters.rs:543-549 over the quantized base, all in the library: the first
-            # adapter rides in mlxq_linear's epilogue, each further one is one mlxq_lora_residual
-            # (out = out + residual, promoted as MLX promotes).  Factors keep their dtype.
+            # src/adapters.rs:543-549 over the quantized base, all in the library: a leading LoRA
+            # adapter rides in mlxq_linear's epilogue, each further adapter is one
+            # mlxq_lora_residual / mlxq_lokr_residual (out = out + residual, promoted as MLX
+            # promotes).  Factors and deltas keep their dtype.
             q = self.quantized
             for ad in self.adapters:
-                if ad.a.shape[1] > 256:
+                if isinstance(ad, Adapter) and ad.a.shape[1] > 256:
                     raise MlxqError(MLXQ_EUNSUPPORTED, "AdaptableLinear: LoRA rank above 256")
             if not self.adapters:
                 return q.forward(x)
-            first = self.adapters[0]
+            first = self.adapters[0] if isinstance(self.adapters[0], Adapter) else None
             out = ops.linear(x, q.weight, q.scales, q.biases, q.group_size, q.bits, bias=q.bias,
-                             lora_a=first.a, lora_b=first.b, lora_scale=first.scale,
+                             lora_a=None if first is None else first.a,
+                             lora_b=None if first is None else first.b,
+                             lora_scale=1.0 if first is None else first.scale,
                              activation=MLXQ_ACT_NONE)
-            for ad in self.adapters[1:]:
-                out = ops.lora_residual(x, out, ad.a, ad.b, ad.scale)
+            for ad in self.adapters[1:] if first is not None else self.adapters:
+                if isinstance(ad, LokrAdapter):
+                    out = ops.lokr_residual(x, out, ad.delta, ad.scale)
+                else:
+                    out = ops.lora_residual(x, out, ad.a, ad.b, ad.scale)
             return out
         else:
             w = self.dense_weight

@@ -385,6 +385,38 @@ def lora_residual(x, y, lora_a, lora_b, lora_scale: float = 1.0, workspace=None)
     return out
 
 
+def lokr_residual(x, y, delta, scale: float = 1.0, workspace=None):
+    """out = y + scale * x . delta^T — one LoKr adapter of AdaptableLinear::forward's stack
+    (src/adapters.rs:543-549, Adapter::residual's Lokr arm :263-266) on an already computed y.
+    delta [out, in] (the reconstructed kron delta, stored bf16 by the reference) is cast to x's
+    dtype and the residual runs in x's dtype; the sum in promote(y, x) (in place when that is y's
+    dtype)."""
+    _float_dtype("lokr_residual", "x", x)
+    _float_dtype("lokr_residual", "y", y)
+    _float_dtype("lokr_residual", "delta", delta)
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    N = y.shape[-1]
+    if y.numel() != M * N:
+        _bad("lokr_residual", f"y has {y.numel()} elements, x implies {M} rows of {N}")
+    if delta.dim() != 2 or tuple(delta.shape) != (N, K):
+        _bad("lokr_residual", f"delta must be [{N}, {K}], got {tuple(delta.shape)}")
+    delta = delta.contiguous()
+    _need_gpu(x, y, delta)
+    y_in = y.contiguous()
+    odt = promote(y.dtype, x.dtype)
+    out = y_in if odt == y.dtype else torch.empty(y.shape, dtype=odt, device=y.device)
+    lib = _lib.load()
+    need = int(lib.mlxq_lokr_residual_workspace_size(_dt(x2), M, N))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    check(lib.mlxq_lokr_residual(_ptr(x2), _dt(x2), M, K, _ptr(delta), _dt(delta), N, float(scale),
+                                 _ptr(y_in), _dt(y_in), _ptr(out), _ptr(workspace), need,
+                                 _stream(x.device)))
+    return out
+
+
 def packed_bits(wq, scales, group_size: int) -> int:
     """quant::packed_bits (src/quant.rs:38-41), returning an error instead of panicking."""
     if wq.dim() != 2 or scales.dim() != 2:

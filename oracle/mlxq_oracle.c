@@ -24,6 +24,11 @@
  *                      bf16/f32 promotion (src/adapters.rs:243-252); its rounding points follow
  *                      MLX's per-op rounding (not pinned by a golden: parity unpinned for the
  *                      bf16 rounding points).
+ *   oracle_lokr_residual  pinned: the reference's LoKr tests (src/adapters.rs:695-764, 1089-1119:
+ *                      the 2x2 kron delta, a bf16 residual within 5e-2 of the f32 one, scale 0 is
+ *                      a bit-exact no-op, LoRA + LoKr stacks sum their residuals) and the
+ *                      closed form x . delta^T of a rank-1 (kron of vectors) delta; the bf16
+ *                      rounding points are parity unpinned (MLX per-op rounding, as elsewhere).
  *   oracle_gelu_erf / oracle_silu: textbook closed forms (special values tested).
  *   oracle_gelu_exact  the op sequence of src/nn.rs:344-355 in the input dtype; in f32 pinned by
  *                      its distance to the closed form, in bf16 parity unpinned (rounding points).
@@ -353,6 +358,35 @@ int oracle_swiglu_mlp(const float* x, int64_t M, int64_t K, const uint32_t* wq_g
     free(g);
     free(u);
     return rc;
+}
+
+/*
+ * One LoKr adapter of AdaptableLinear::forward's residual sum (reference src/adapters.rs:543-549)
+ * through Adapter::residual's Lokr arm (:263-266):
+ *   d  = delta.as_dtype(x)          DX = x's dtype (bf16 when x_bf16)
+ *   r  = x . d^T                    in DX (double accumulate, rounded once)
+ *   r2 = r * scale                  scale cast to DX first (the dtype-matched scalar, :268-269)
+ *   y  = y_in + r2                  in promote(y_in, DX)
+ * delta [N,K] row-major (the reconstructed kron delta, :26-128).  *out_bf16 receives whether y's
+ * dtype is bf16.
+ */
+int oracle_lokr_residual(const float* x, int64_t M, int64_t K, const float* delta, int64_t N,
+                         float scale, int x_bf16, const float* y_in, int y_bf16, float* y,
+                         int* out_bf16) {
+    const int dout = y_bf16 && x_bf16;
+    const float sc = rnd(scale, x_bf16);
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t n = 0; n < N; ++n) {
+            double acc = 0.0;
+            for (int64_t k = 0; k < K; ++k)
+                acc += (double)x[m * K + k] * (double)rnd(delta[n * K + k], x_bf16);
+            const float r = rnd((float)acc, x_bf16);
+            y[m * N + n] = rnd(y_in[m * N + n] + rnd(r * sc, x_bf16), dout);
+        }
+    }
+    if (out_bf16) *out_bf16 = dout;
+    return ORACLE_OK;
 }
 
 int oracle_num_threads(void) {

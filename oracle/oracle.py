@@ -49,6 +49,8 @@ def lib():
         l.oracle_swiglu_mlp.argtypes = [_f32p, _i64, _i64, _u32p, _f32p, _f32p, _u32p, _f32p, _f32p,
                                         _i64, _u32p, _f32p, _f32p, _i64, _int, _int, _int, _int,
                                         _f32p, _f32p]
+        l.oracle_lokr_residual.argtypes = [_f32p, _i64, _i64, _f32p, _i64, ctypes.c_float, _int, _f32p,
+                                           _int, _f32p, ctypes.POINTER(_int)]
         l.oracle_gelu_erf.argtypes = [ctypes.c_float, _int]
         l.oracle_gelu_erf.restype = ctypes.c_float
         l.oracle_gelu_tanh.argtypes = [ctypes.c_float, _int]
@@ -181,6 +183,22 @@ def swiglu_mlp(x, gate, up, down, group_size=64, bits=4, w_bf16=False, act_bf16=
                                    int(act_bf16), h.ctypes.data_as(_f32p),
                                    y.ctypes.data_as(_f32p)), "swiglu_mlp")
     return h, y
+
+
+def lokr_residual(x, y_in, delta, scale=1.0, x_bf16=True, y_bf16=True, return_dtype=False):
+    """y_in + scale * x . delta^T, one LoKr adapter step of AdaptableLinear::forward (the residual
+    in x's dtype, the sum in promote(y, x)).  Values are passed as the f32 numbers they hold."""
+    x, xp = _f32(x)
+    y_in, yp = _f32(y_in)
+    delta, dp = _f32(delta)
+    M, K = x.shape
+    N = delta.shape[0]
+    assert delta.shape == (N, K) and y_in.shape == (M, N)
+    y = np.empty((M, N), np.float32)
+    ob = _int(0)
+    _check(lib().oracle_lokr_residual(xp, M, K, dp, N, float(scale), int(x_bf16), yp, int(y_bf16),
+                                      y.ctypes.data_as(_f32p), ctypes.byref(ob)), "lokr_residual")
+    return (y, bool(ob.value)) if return_dtype else y
 
 
 def gelu_erf(v, out_bf16=True):

@@ -36,6 +36,9 @@ int oracle_linear(const float* x, int64_t M, int64_t K, const uint32_t* wq, cons
                   int sb_bf16, const float* bias, int bias_bf16, const float* lora_a,
                   const float* lora_b, int64_t rank, int lora_bf16, float lora_scale, int act,
                   float* y, int* out_bf16);
+int oracle_lokr_residual(const float* x, int64_t M, int64_t K, const float* delta, int64_t N,
+                         float scale, int x_bf16, const float* y_in, int y_bf16, float* y,
+                         int* out_bf16);
 }
 
 namespace fs = std::filesystem;
@@ -408,6 +411,58 @@ static void gpu_cases(const fs::path& root) {
     (void)hipGraphExecDestroy(exec);
     (void)hipGraphDestroy(graph);
     (void)hipStreamDestroy(st);
+  }
+
+  banner("AdaptableLinear: LoKr adapters (bf16 LoRA + LoKr stack, LoKr first on an f32 stream, scale 0)");
+  {
+    std::mt19937 rng(13);
+    const int64_t M = 150, K = 256, N = 200, R = 16;
+    std::vector<float> w = bf16_normal(rng, N * K, 0.02f), xb = bf16_normal(rng, M * K, 1.0f);
+    std::vector<float> a = bf16_normal(rng, K * R, 0.02f), b = bf16_normal(rng, R * N, 0.02f);
+    std::vector<float> delta = bf16_normal(rng, N * K, 0.01f);  // stored bf16, as the reference does
+    QuantizedLinear q = QuantizedLinear::try_from_linear(bf16_array(w, {N, K}), std::nullopt, 64, 4);
+    std::vector<uint32_t> wq(N * K / 8);
+    std::vector<float> sc(N * K / 64), zz(N * K / 64);
+    oracle_quantize(w.data(), N, K, 64, 4, 1, wq.data(), sc.data(), zz.data());
+    // bf16 x: base + LoRA (fused), then + LoKr (residual and sum in bf16)
+    AdaptableLinear l = AdaptableLinear::from_quantized_parts(q.weight, q.scales, q.biases, std::nullopt, 64, 4);
+    l.push(Adapter::lora(bf16_array(a, {K, R}), bf16_array(b, {R, N}), 0.5f));
+    l.push(Adapter::lokr(bf16_array(delta, {N, K}), 0.7f));
+    Array y = l.forward(bf16_array(xb, {M, K}));
+    EXPECT(y.dtype() == Dtype::Bfloat16 && y.shape() == std::vector<int64_t>({M, N}), "lora+lokr output");
+    std::vector<float> ref(M * N), ref2(M * N);
+    oracle_linear(xb.data(), M, K, wq.data(), sc.data(), zz.data(), N, 64, 4, 1, 1, 1, nullptr, 1, a.data(),
+                  b.data(), R, 1, 0.5f, 0, ref.data(), nullptr);
+    int ob = -1;
+    oracle_lokr_residual(xb.data(), M, K, delta.data(), N, 0.7f, 1, ref.data(), 1, ref2.data(), &ob);
+    EXPECT(ob == 1, "oracle dtype");
+    double e = rel_fro(host_f32(y), ref2);
+    EXPECT(e < 2e-3, "lora+lokr relFro %.3e", e);
+    // f32 x (FLUX.1's stream): LoKr first (nothing fused), the delta widened exactly, all in f32
+    std::vector<float> xf(M * K);
+    std::normal_distribution<float> nd(0.0f, 1.0f);
+    for (auto& v : xf) v = nd(rng);
+    AdaptableLinear lf = AdaptableLinear::from_quantized_parts(q.weight, q.scales, q.biases, std::nullopt, 64, 4);
+    lf.push(Adapter::lokr(bf16_array(delta, {N, K}), 1.25f));
+    const Array xin = Array::from_host(xf.data(), {M, K}, Dtype::Float32);
+    Array yf = lf.forward(xin);
+    EXPECT(yf.dtype() == Dtype::Float32, "f32 stream output");
+    oracle_linear(xf.data(), M, K, wq.data(), sc.data(), zz.data(), N, 64, 4, 0, 0, 1, nullptr, 1, nullptr,
+                  nullptr, 0, 1, 1.0f, 0, ref.data(), nullptr);
+    oracle_lokr_residual(xf.data(), M, K, delta.data(), N, 1.25f, 0, ref.data(), 0, ref2.data(), &ob);
+    EXPECT(ob == 0, "oracle f32 dtype");
+    e = rel_fro(host_f32(yf), ref2);
+    EXPECT(e < 1e-4, "f32 lokr relFro %.3e", e);
+    // scale 0 is a bit-exact no-op (src/adapters.rs:717-728)
+    AdaptableLinear l0 = AdaptableLinear::from_quantized_parts(q.weight, q.scales, q.biases, std::nullopt, 64, 4);
+    const Array base = l0.forward(xin);
+    l0.push(Adapter::lokr(bf16_array(delta, {N, K}), 0.0f));
+    EXPECT(host_f32(l0.forward(xin)) == host_f32(base), "scale-0 LoKr changed the output");
+    // a wrongly shaped delta is an error, not a crash
+    l0.push(Adapter::lokr(bf16_array(delta, {K, N}), 1.0f));
+    bool threw = false;
+    try { l0.forward(xin); } catch (const Error& err) { threw = err.status == MLXQ_EINVAL; }
+    EXPECT(threw, "a [in, out] delta accepted");
   }
 
   banner("fused SwiGLU decode and the stacked expert projection");

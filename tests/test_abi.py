@@ -118,6 +118,32 @@ def test_linear_workspace_size(lib):
     # An f32 product is written straight into y: nothing to stage.
     assert ws(f32, bf, 64, 128, _ep(lib, bias_dt=f32, act=_lib.MLXQ_ACT_GELU)) == 0
     assert lib.mlxq_lora_residual_workspace_size(bf, f32, 4608, 3072, 16) == 4608 * 64 + 3072 * 64
+    # LoKr: the f32 product x . delta^T, padded to 256 B.
+    assert lib.mlxq_lokr_residual_workspace_size(bf, 4608, 3072) == 4608 * 3072 * 4
+    assert lib.mlxq_lokr_residual_workspace_size(f32, 3, 5) == 256
+    assert lib.mlxq_lokr_residual_workspace_size(bf, 0, 5) == 0
+
+
+def test_lokr_residual_validation(lib):
+    """mlxq_lokr_residual rejects bad dtypes, shapes, K not a multiple of 32, a promoted in-place
+    sum and a short workspace before touching the device."""
+    from mlxq import _lib
+    bf, f32 = _lib.MLXQ_BFLOAT16, _lib.MLXQ_FLOAT32
+    p = ctypes.c_void_p(4096)
+    call = lambda xd, M, K, dd, N, yd, yout, ws, wsb: lib.mlxq_lokr_residual(
+        p, xd, M, K, p, dd, N, 0.5, p, yd, yout, ws, wsb, None)
+    assert call(7, 4, 64, bf, 8, bf, p, p, 1 << 20) == _lib.MLXQ_EINVAL
+    assert b"dtype" in lib.mlxq_last_error()
+    assert call(bf, 4, 64, 9, 8, bf, p, p, 1 << 20) == _lib.MLXQ_EINVAL
+    assert call(bf, -1, 64, bf, 8, bf, p, p, 1 << 20) == _lib.MLXQ_EINVAL
+    assert call(bf, 4, 48, bf, 8, bf, p, p, 1 << 20) == _lib.MLXQ_EUNSUPPORTED
+    assert b"multiple of 32" in lib.mlxq_last_error()
+    assert call(bf, 0, 64, bf, 8, bf, p, p, 0) == _lib.MLXQ_OK       # empty: nothing to do
+    # bf16 y + an f32 residual promotes to f32: cannot overwrite y_in in place
+    assert call(f32, 4, 64, bf, 8, bf, p, p, 1 << 20) == _lib.MLXQ_EINVAL
+    assert b"in place" in lib.mlxq_last_error()
+    assert call(bf, 4, 64, bf, 8, bf, p, p, 16) == _lib.MLXQ_EINVAL
+    assert b"workspace" in lib.mlxq_last_error()
 
 
 def test_linear_out_dtype_follows_mlx_promotion(lib):
@@ -179,6 +205,8 @@ def test_wrappers_reject_bad_shapes_before_launch():
     rejected(lambda: ops.swiglu(x, (wq4, s, s), (wq8, s, s), 64, 4), "words per row")
     rejected(lambda: ops.lora_residual(x, torch.zeros((3, N), dtype=bf), torch.zeros((K + 1, 8), dtype=bf),
                                        torch.zeros((8, N), dtype=bf)), "LoRA")
+    rejected(lambda: ops.lokr_residual(x, torch.zeros((3, N), dtype=bf), torch.zeros((K, N), dtype=bf)),
+             "delta")
     rejected(lambda: ops.dequantize(wq4, s[:, :3], s[:, :3], 64, 4), "scales/biases")
 
 

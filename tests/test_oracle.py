@@ -313,3 +313,70 @@ def test_stack_split_commutes_with_packing():
             per = oracle.quantize(w[e], 64, bits, sb_bf16=True)
             for a, b in zip(stacked, per):
                 assert np.array_equal(a[e * N:(e + 1) * N], b)
+
+
+def _lokr_2x2():
+    """The reference's lokr_2x2 fixture (src/adapters.rs:695-708): reconstruct_lokr_delta(alpha 8,
+    rank 4, [2, 2], w1 = [[0.5], [0.6]], w2 = [[0.7, 0.8]], bf16) = bf16(2 * kron(w1, w2)), the
+    kron and the scale taken in f32 (src/adapters.rs:117-119)."""
+    w1 = np.array([[0.5], [0.6]], np.float32)
+    w2 = np.array([[0.7, 0.8]], np.float32)
+    return oracle.bf16_round((np.kron(w1, w2).astype(np.float32) * np.float32(8.0 / 4.0)).reshape(2, 2))
+
+
+def test_lokr_delta_fixture_hand_values():
+    """2 * [[0.35, 0.4], [0.42, 0.48]] rounded to 8 significant bits: 0.7 = 1.0110011|0011.. x 2^-1
+    rounds down to 0.69921875, 0.8 = 1.1001100|1100.. up to 0.80078125, 0.84 = 1.1010111|0000.. down
+    to 0.83984375, 0.96 = 1.1110101|1100.. up to 0.9609375."""
+    np.testing.assert_array_equal(_lokr_2x2(), np.array([[0.69921875, 0.80078125],
+                                                          [0.83984375, 0.9609375]], np.float32))
+
+
+def test_lokr_residual_reference_known_answers():
+    """The reference's LoKr tests on the oracle (src/adapters.rs:711-764): a bf16-input residual of
+    the 2x2 delta at scale 0.5 stays bf16 and is within 5e-2 of the f32 one; the products are exact
+    here, so the hand-computed values hold bit for bit; scale 0 is a bit-exact no-op."""
+    delta = _lokr_2x2()
+    x32 = np.array([[1.0, -2.0], [0.5, 0.25], [-1.0, 2.0]], np.float32)
+    zero = np.zeros((3, 2), np.float32)
+    got, out_bf16 = oracle.lokr_residual(x32, zero, delta, 0.5, x_bf16=True, y_bf16=True,
+                                         return_dtype=True)
+    assert out_bf16
+    want = (x32.astype(np.float64) @ delta.astype(np.float64).T * 0.5).astype(np.float32)
+    np.testing.assert_allclose(got, oracle.bf16_round(want), rtol=5e-2, atol=5e-2)
+    # row 0: r = (0.69921875 - 1.6015625, 0.83984375 - 1.921875) = (-0.90234375, -1.08203125); the
+    # second needs 9 significant bits (1.0001010|1) and ties to even at -1.078125; times 0.5:
+    np.testing.assert_array_equal(got[0], np.array([-0.451171875, -0.5390625], np.float32))
+    y = oracle.bf16_round(np.array([[0.1, 0.2], [0.3, 0.4], [1.5, -7.0]], np.float32))
+    np.testing.assert_array_equal(oracle.lokr_residual(x32, y, delta, 0.0), y)
+    np.testing.assert_array_equal(oracle.lokr_residual(x32, y, delta, 0.0, x_bf16=False, y_bf16=False), y)
+
+
+@pytest.mark.parametrize("x_dt,y_dt,delta_dt", [("bf16", "bf16", "bf16"), ("f32", "f32", "bf16"),
+                                                ("bf16", "f32", "bf16"), ("f32", "bf16", "f32"),
+                                                ("bf16", "bf16", "f32")])
+def test_lokr_residual_matches_torch_promotion(x_dt, y_dt, delta_dt):
+    """oracle.lokr_residual against Adapter::residual's Lokr arm and the sum of
+    AdaptableLinear::forward (src/adapters.rs:263-269, :545-547) as torch ops on operands of the
+    stated dtypes: delta.to(x.dtype), matmul (float64, rounded to x's dtype), times the scale cast to
+    x's dtype, then y + r with torch's (= MLX's) promotion.  Bit-exact."""
+    import torch
+    rng = np.random.default_rng(len(x_dt + y_dt + delta_dt))
+    M, K, N = 5, 64, 24
+    bf, f32 = torch.bfloat16, torch.float32
+    tdt = {"bf16": bf, "f32": f32}
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    y = rng.standard_normal((M, N)).astype(np.float32)
+    delta = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    x = oracle.bf16_round(x) if x_dt == "bf16" else x
+    y = oracle.bf16_round(y) if y_dt == "bf16" else y
+    delta = oracle.bf16_round(delta) if delta_dt == "bf16" else delta
+    got, out_bf16 = oracle.lokr_residual(x, y, delta, 0.3, x_bf16=x_dt == "bf16", y_bf16=y_dt == "bf16",
+                                         return_dtype=True)
+    t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a)).to(dt)
+    d = t(delta, tdt[delta_dt]).to(tdt[x_dt])
+    r = t(x.astype(np.float64) @ d.double().numpy().T, f32).to(tdt[x_dt])
+    r = r * torch.tensor(0.3, dtype=f32).to(tdt[x_dt])
+    out = t(y, tdt[y_dt]) + r
+    assert out_bf16 == (out.dtype == bf)
+    np.testing.assert_array_equal(got, out.float().numpy())
