@@ -267,12 +267,13 @@ static int launch_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, c
   return check_launch("qmm");
 }
 
+// 128 x 128 tiles for every shape: the 256 x 256 form held part of its tile in scratch (8-32
+// bytes per lane) and measured no faster where it applied (same box, K % 64 == 32 with group size
+// 32: M = N = 4096, K = 4064 Q4 262 vs 270 us, with GELU 287 vs 286; M = 2048, N = 8192 Q8 289 vs
+// 270; M = 8192, N = 4096, K = 1056 Q4 with GELU 201 vs 170, 256 x 256 first).
 template <typename SB, int BITS, int GS>
 static int qmm_tile(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                     const void* b, int64_t N, void* y, const QmmEpilogue& epi, hipStream_t st) {
-  // Large problems take the 256x256 tile; small ones a 128x128 tile so more CUs get work.
-  const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
-  if (big_tiles >= 256) return launch_qmm<SB, BITS, GS, 256, 256>(x, M, K, wq, s, b, N, y, epi, st);
   return launch_qmm<SB, BITS, GS, 128, 128>(x, M, K, wq, s, b, N, y, epi, st);
 }
 
