@@ -13,10 +13,10 @@
 //     buffer load per 32-column sub-tile per K step for Q4, two for Q8) and dequantizes them into
 //     the MFMA operand registers — no LDS round trip, and each weight is dequantized exactly once
 //     per workgroup because no two waves share columns;
-//   * activations: the 256x64 bf16 tile is staged global -> registers -> LDS through a 3-deep
-//     ring (one barrier per K step) and every wave reads all of it.  16-byte chunks are
-//     XOR-swizzled by f(row) = (row & 7) ^ ((row >> 3) & 1), which keeps both the 16-lane
-//     fragment reads (16 rows, one chunk) and the row-wise tile writes on distinct banks;
+//   * activations: the 256x64 bf16 tile goes global -> LDS by direct-to-LDS buffer loads into a
+//     4-stage ring, issued two K steps ahead (one barrier per K step), and every wave reads all of
+//     it.  16-byte chunks are XOR-swizzled by f(row) = (row & 7) ^ ((row >> 3) & 1) on the source
+//     side, which keeps the 16-lane fragment reads (16 rows, one chunk) on distinct banks;
 //   * the MFMA takes the weight fragment as its A operand (rows = n) and the activation fragment
 //     as B (columns = m), so each lane's f32x16 result holds 4 runs of 4 consecutive n for one m
 //     and the epilogue writes 8-byte (4 x bf16) row segments directly.
