@@ -30,8 +30,9 @@
  *     output the same way).  mlxq_linear_out_dtype gives the dtype y must have.
  *   - Re-entrant per stream.  Process-wide state, all of it per device and written once: the two
  *     GELU tables (device memory in the code object, filled by the first GELU GEMM on a device),
- *     the cached CU count, the device address of mlxq_linear_noalloc's static scratch (guarded
- *     by a mutex), plus the thread-local error string.
+ *     the cached CU count, the decode GEMV's raised dynamic-LDS limit (atomic flags), the device
+ *     address of mlxq_linear_noalloc's static scratch (guarded by a mutex), plus the thread-local
+ *     error string.
  */
 #ifndef MLXQ_H
 #define MLXQ_H

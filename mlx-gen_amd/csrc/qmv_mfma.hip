@@ -28,6 +28,8 @@
 // A workgroup owns 16 weight rows; its waves split K and reduce through LDS at the end.
 // Q4 k-order inside an 8-run is [0,2,4,6,1,3,5,7] (low nibbles first, see unpack_q4); the
 // activation rows are permuted to match with v_perm_b32 as they are copied into LDS.
+#include <atomic>
+
 #include "mlxq_common.h"
 
 namespace mlxq {
@@ -434,12 +436,16 @@ struct QmvArgs {
 
 template <int BITS, bool G64, int STEPS, int MR, int NMAT>
 static int launch_qmv_mfma(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
-  static bool attr_set = false;
-  if (!attr_set) {
+  // The dynamic-LDS limit is raised once per device (any thread may get here first; setting it
+  // twice is harmless).
+  static std::atomic<bool> attr_set[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(MLXQ_EDEVICE, "qmv: no current device");
+  if (dev < 0 || dev >= 64 || !attr_set[dev].load(std::memory_order_acquire)) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_mfma_kernel<BITS, G64, STEPS, MR, NMAT>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds) != hipSuccess)
       return set_error(MLXQ_EDEVICE, "qmv: hipFuncSetAttribute failed");
-    attr_set = true;
+    if (dev >= 0 && dev < 64) attr_set[dev].store(true, std::memory_order_release);
   }
   hipLaunchKernelGGL((qmv_mfma_kernel<BITS, G64, STEPS, MR, NMAT>), dim3((unsigned)((a.N + 15) / 16)),
                      dim3(p.waves * 64), p.lds, st, (const uint16_t*)a.x, (int)a.M, (int)a.K, a.wq,
