@@ -81,7 +81,9 @@ class LokrAdapter:
     def residual(self, x: torch.Tensor) -> torch.Tensor:
         """The dense-base arm's residual, in x's dtype with the scale cast to it.  Over a quantized
         base the library applies it instead (ops.lokr_residual)."""
-        r = x @ self.delta.to(x.dtype).t()
+        # the transposed operand made contiguous: batched bf16 products on a transposed view are
+        # avoided on this platform
+        r = x @ self.delta.to(x.dtype).t().contiguous()
         return r * torch.tensor(self.scale, dtype=x.dtype, device=r.device)
 
 
@@ -155,9 +157,9 @@ class AdaptableLinear:
             w = self.dense_weight
             if self.dense_bias is not None:
                 out = torch.addmm(self.dense_bias.to(x.dtype), x.reshape(-1, x.shape[-1]),
-                                  w.to(x.dtype).t()).reshape(*x.shape[:-1], w.shape[0])
+                                  w.to(x.dtype).t().contiguous()).reshape(*x.shape[:-1], w.shape[0])
             else:
-                out = x @ w.to(x.dtype).t()
+                out = x @ w.to(x.dtype).t().contiguous()
         for ad in self.adapters:
             out = out + ad.residual(x)
         return out
