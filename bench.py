@@ -39,8 +39,8 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extras", action="store_true", help="headline GEMM only")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -187,13 +187,17 @@ def bench_gemv(mlxq, torch, reps=20):
     return out
 
 
+QUANT_SETS = 2  # config-3 weight sets rotated (8 x 52 MB read + 8 x 28 MB written: > 256 MB MALL)
+
+
 def bench_quantize(mlxq, torch, iters=10):
-    """Config 3 quantize pass: 4 x [5120,5120] bf16 -> Q8 g64 (321.1 MB algorithmic)."""
+    """Config 3 quantize pass: 4 x [5120,5120] bf16 -> Q8 g64 (321.1 MB algorithmic), timed over
+    QUANT_SETS distinct sets of four weights so the Infinity Cache cannot hold one pass's data."""
     dev = torch.device("cuda:0")
-    ws = [gen_bf16((5120, 5120), 0.02, 200 + i, dev) for i in range(4)]
+    ws = [gen_bf16((5120, 5120), 0.02, 200 + i, dev) for i in range(4 * QUANT_SETS)]
     outs = [(torch.empty((5120, 1280), dtype=torch.int32, device=dev),
              torch.empty((5120, 80), dtype=torch.bfloat16, device=dev),
-             torch.empty((5120, 80), dtype=torch.bfloat16, device=dev)) for _ in range(4)]
+             torch.empty((5120, 80), dtype=torch.bfloat16, device=dev)) for _ in ws]
     from mlxq import _lib
     import ctypes
     lib = _lib.load()
@@ -208,7 +212,7 @@ def bench_quantize(mlxq, torch, iters=10):
     # Every weight writes its own preallocated outputs: outputs allocated per call inside a graph
     # reuse one freed buffer, whose repeated writes then stay in the caches (~15 % faster, not
     # the traffic of a real conversion).
-    ms = graph_ms(torch, run, inner=2, reps=iters)
+    ms = graph_ms(torch, run, inner=1, reps=iters) / QUANT_SETS
     nbytes = 4 * (5120 * 5120 * 2 + 5120 * 5120 + 5120 * 80 * 4)
     # Reference point: a plain device copy of each weight into its own buffer, same method.
     dsts = [torch.empty_like(w) for w in ws]
@@ -216,14 +220,15 @@ def bench_quantize(mlxq, torch, iters=10):
     def copy():
         for w, d in zip(ws, dsts):
             d.copy_(w)
-    ms_c = graph_ms(torch, copy, inner=2, reps=iters)
+    ms_c = graph_ms(torch, copy, inner=1, reps=iters) / QUANT_SETS
     cbytes = 4 * 2 * 5120 * 5120 * 2
     return {"us_per_pass": ms * 1e3, "GBs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes,
             "frac_of_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "copy_GBs": round(cbytes / (ms_c * 1e-3) / 1e9, 1),
             "frac_of_copy_rate": round(nbytes / (ms * 1e-3) / (cbytes / (ms_c * 1e-3)), 4),
-            "note": "4 launches per pass, each weight into its own outputs; copy_GBs: torch copy_ of "
-                    "the same four weights into their own buffers, same timing"}
+            "note": "4 launches per pass, each weight into its own outputs, passes rotated over "
+                    f"{QUANT_SETS} weight sets; copy_GBs: torch copy_ of the same weights into their "
+                    "own buffers, same timing"}
 
 
 def graph_ms(torch, fn, inner=8, reps=5):
@@ -315,21 +320,50 @@ def bench_dense_reference(torch):
                     "GEMM without dequantization, for context only"}
 
 
+CONFIG1_COPIES = 16  # distinct config-1 weights rotated (16 x 24 MB > the 256 MB Infinity Cache)
+
+
 def bench_config1(mlxq, torch):
-    """Config 1 round trip: W[3072,3072] bf16 -> Q4 g64, dequantize, x[256,3072] . W^T."""
+    """Config 1 round trip: W[3072,3072] bf16 -> Q4 g64, dequantize, x[256,3072] . W^T.  Each op is
+    timed over CONFIG1_COPIES distinct weights (each with its own outputs), one launch per weight,
+    so a weight's 24 MB are not served from the Infinity Cache by the previous launch."""
     dev = torch.device("cuda:0")
-    w = gen_bf16((3072, 3072), 0.02, 300, dev)
+    ws = [gen_bf16((3072, 3072), 0.02, 300 + 7 * i, dev) for i in range(CONFIG1_COPIES)]
     x = gen_bf16((256, 3072), 1.0, 301, dev)
-    q = mlxq.quantize(w, 64, 4)
+    qs = [mlxq.quantize(w, 64, 4) for w in ws]
+    qo = [tuple(torch.empty_like(t) for t in q) for q in qs]
+    do = [torch.empty_like(w) for w in ws]
+    yo = torch.empty((256, 3072), dtype=torch.bfloat16, device=dev)
+    from mlxq import _lib
+    import ctypes
+    lib = _lib.load()
+
+    def quant():
+        sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        for w, (wq, sc, bi) in zip(ws, qo):
+            _lib.check(lib.mlxq_quantize(w.data_ptr(), 1, 3072, 3072, 64, 4, wq.data_ptr(), sc.data_ptr(),
+                                         bi.data_ptr(), sp))
+
+    def deq():
+        sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        for (wq, sc, bi), d in zip(qs, do):
+            _lib.check(lib.mlxq_dequantize(wq.data_ptr(), sc.data_ptr(), bi.data_ptr(), 1, 3072, 3072, 64, 4,
+                                           d.data_ptr(), sp))
+
+    def mm():
+        for q in qs:
+            mlxq.quantized_matmul(x, *q, True, 64, 4, out=yo)
     qbytes = 3072 * 3072 * 2 + 3072 * 3072 // 2 + 3072 * 48 * 4
-    t_q = graph_ms(torch, lambda: mlxq.quantize(w, 64, 4))
-    t_d = graph_ms(torch, lambda: mlxq.dequantize(*q, 64, 4))
-    t_m = graph_ms(torch, lambda: mlxq.quantized_matmul(x, *q, True, 64, 4))
+    n = len(ws)
+    t_q = graph_ms(torch, quant, inner=1, reps=10) / n
+    t_d = graph_ms(torch, deq, inner=1, reps=10) / n
+    t_m = graph_ms(torch, mm, inner=1, reps=10) / n
     flop = 2.0 * 256 * 3072 * 3072
     return {"quantize_us": round(t_q * 1e3, 2), "quantize_GBs": round(qbytes / (t_q * 1e-3) / 1e9, 1),
             "dequantize_us": round(t_d * 1e3, 2), "dequantize_GBs": round(qbytes / (t_d * 1e-3) / 1e9, 1),
             "qmm_us": round(t_m * 1e3, 2), "qmm_TFLOPs": round(flop / (t_m * 1e-3) / 1e12, 1),
-            "note": "24.2 MB per quantize/dequantize: latency-bound at this size"}
+            "note": f"per launch, rotated over {CONFIG1_COPIES} distinct weights (HIP graph, gaps "
+                    "included); 24.2 MB per quantize/dequantize: latency-bound at this size"}
 
 
 def bench_config3(mlxq, torch):
@@ -341,7 +375,10 @@ def bench_config3(mlxq, torch):
     ws = [gen_bf16((D, D), 0.02, 401 + i, dev) for i in range(4)]
     qs = [mlxq.quantize(w, 64, 8) for w in ws]
     ys = [torch.empty((M, D), dtype=torch.bfloat16, device=dev) for _ in range(4)]
-    qouts = [tuple(torch.empty_like(t) for t in q) for q in qs]  # each weight its own outputs
+    # The quantize pass is timed over QUANT_SETS weight sets (the four weights plus copies) so the
+    # Infinity Cache cannot hold a pass's data, each weight into its own outputs.
+    wq_all = ws + [gen_bf16((D, D), 0.02, 451 + i, dev) for i in range(4 * (QUANT_SETS - 1))]
+    qouts = [tuple(torch.empty_like(t) for t in qs[0]) for _ in wq_all]
     from mlxq import _lib
     import ctypes
     lib = _lib.load()
@@ -352,11 +389,11 @@ def bench_config3(mlxq, torch):
 
     def quant():
         sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        for w, (wq, sc, bi) in zip(ws, qouts):
+        for w, (wq, sc, bi) in zip(wq_all, qouts):
             _lib.check(lib.mlxq_quantize(w.data_ptr(), 1, D, D, 64, 8, wq.data_ptr(), sc.data_ptr(),
                                          bi.data_ptr(), sp))
     t_p = graph_ms(torch, proj, inner=2, reps=3)
-    t_q = graph_ms(torch, quant, inner=4, reps=3)
+    t_q = graph_ms(torch, quant, inner=1, reps=5) / QUANT_SETS
     flop = 4 * 2.0 * M * D * D
     qbytes = 4 * (D * D * 2 + D * D + D * (D // 64) * 4)
     return {"qmm_ms": round(t_p, 3), "qmm_TFLOPs": round(flop / (t_p * 1e-3) / 1e12, 1),
