@@ -22,6 +22,9 @@
 namespace mlxq {
 
 constexpr int BK = 64;
+// Grids of at least this many 128 x 128 tiles (and under 128 tiles of 256 x 128) take the wide
+// kernel's 128 x 128 form instead of the K-split kernel.
+constexpr int64_t kQmmMidMinTiles = 136;
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
 
@@ -283,11 +286,15 @@ int run_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void*
   // The wide kernel needs K % 64 == 0 and enough tiles to occupy the CUs: 256x256 tiles, or
   // below 128 of those 256x128 tiles with 4 waves (which beat the K-split kernel from 128 such
   // tiles on: M = 512, N = 12288, K = 3072 52 vs 84 us; M = 2048, N = 3072, K = 8192 120 vs
-  // 204 us; below it lost: M = 1024, N = 3072 46 vs 43 us at 96 tiles).  Small or ragged-K
-  // problems take the K-split or the 128/256-tile kernel below.
+  // 204 us; below it lost: M = 1024, N = 3072 46 vs 43 us at 96 tiles), and below that
+  // 128x128 tiles with 4 waves from kQmmMidMinTiles such tiles on (M = 1024, N = K = 3072, 192
+  // tiles: 32 vs 44 us; M = 768, 144 tiles: 31 vs 42 us; even at 128 tiles, M = 512,
+  // N = K = 4096: 38 vs 37 us; at 48 tiles 29 vs 15 us).  Small or ragged-K problems take the
+  // K-split or the 128/256-tile kernel below.
   const int64_t wide_tiles = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t narrow_tiles = ((M + 255) / 256) * ((N + 127) / 128);
-  if (K % 64 == 0 && (wide_tiles >= 128 || narrow_tiles >= 128) &&
+  const int64_t mid_tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  if (K % 64 == 0 && (wide_tiles >= 128 || narrow_tiles >= 128 || mid_tiles >= kQmmMidMinTiles) &&
       qmm_wide_fits(M, K, N, gs, bits, sb_dtype == MLXQ_BFLOAT16 ? 2 : 4))
     return run_qmm_wide(x, M, K, wq, s, b, sb_dtype, N, gs, bits, y, epi, st);
   // Small grids with a long K: the K-split kernel (64x64 tiles, 8 waves each taking a slice of

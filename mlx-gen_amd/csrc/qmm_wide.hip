@@ -38,7 +38,7 @@ namespace mlxq {
 
 namespace {
 
-constexpr int kBM = 256;  // LDS activation tile rows (a BM < 256 tile leaves the last rows unused)
+constexpr int kBM = 256;  // rows of the large tiles' LDS activation ring (224-row tiles use 256)
 constexpr int kBN = 256;
 constexpr int kGroupM = 4;
 constexpr int kStages = 4;  // activation LDS ring depth (power of two)
@@ -168,10 +168,13 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   constexpr int TMW = BM / 32;           // m sub-tiles per wave (all BM rows)
   constexpr int TNW = BN / WAVES / 32;  // n sub-tiles per wave
   constexpr int WPL = BITS;              // packed words per lane per n sub-tile per K step (4 or 8)
-  constexpr int A_PER = kBM * 8 / NT;    // 16-byte activation chunks per thread per K step
+  // LDS activation ring rows: the tile's rows, or 256 for 224-row tiles (whose 8 waves fill rows
+  // in blocks of 64: the last 32 ring rows repeat the tile's last row and are never read).
+  constexpr int RB = BM == 224 ? kBM : BM;
+  constexpr int A_PER = RB * 8 / NT;     // 16-byte activation chunks per thread per K step
   constexpr int A_ROWS = NT / 8;         // row stride between a thread's chunks
-  static_assert(TNW >= 1 && A_PER >= 1 && A_ROWS % 16 == 0 && BM % 32 == 0 && BM <= kBM,
-                "tile/wave shape");
+  static_assert(TNW >= 1 && A_PER >= 1 && A_PER * NT == RB * 8 && A_ROWS % 16 == 0 && BM % 32 == 0 &&
+                    BM <= RB, "tile/wave shape");
   // bf16 scales/biases are staged through LDS in blocks of 8 groups (SPB K steps): per wave and
   // 32-column sub-tile, two 1 KB buffers of [32 rows x 8 scales][32 rows x 8 biases], plus one
   // 1 KB sink per wave for the placeholder loads (see load_b).
@@ -181,12 +184,15 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   constexpr int kSzBytes = SZ_LDS ? WAVES * TNW * 2048 + WAVES * 1024 : 0;
   // The epilogue reuses the ring (and scale region) for the output tile, BM rows of BN bf16 at
   // a 528-byte pitch; the dense bias sits after both.
-  constexpr int kRing = kStages * kBM * 128 + kSzBytes;
+  constexpr int kRing = kStages * RB * 128 + kSzBytes;
   constexpr int kOut = BM * (BN * 2 + 16);
-  constexpr int kMain = kRing > kOut ? kRing : kOut;
+  // A GELU epilogue copies its 128 KB bf16 table to the start of this region.
+  constexpr int kTab = (FUSED && ACT != kFusedActNone) ? 65536 * 2 : 0;
+  constexpr int kMain0 = kRing > kOut ? kRing : kOut;
+  constexpr int kMain = kMain0 > kTab ? kMain0 : kTab;
   __shared__ __attribute__((aligned(16))) unsigned char lds_all[kMain + BN * 4];
-  auto smem = reinterpret_cast<unsigned char (*)[kBM * 128]>(lds_all);
-  unsigned char* const sz_lds = lds_all + kStages * kBM * 128;
+  auto smem = reinterpret_cast<unsigned char (*)[RB * 128]>(lds_all);
+  unsigned char* const sz_lds = lds_all + kStages * RB * 128;
 
   // Stacked launch: grid.y selects the matrix (expert); one matrix has all strides zero.
   if (gridDim.y > 1) {
@@ -236,7 +242,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   // load moves 1 KB per wave: lane L's 16 bytes land at block + 16 L.  Wave wv's round i fills
   // the block of rows A_ROWS i + 8 wv .. +7, so lane L loads the chunk of row
   // A_ROWS i + 8 wv + (L >> 3) that belongs at position L & 7 under the swizzle, i.e. global
-  // chunk (L & 7) ^ f(row).  All kBM LDS rows are filled (uniform code); rows at or past BM
+  // chunk (L & 7) ^ f(row).  All RB LDS rows are filled (uniform code); rows at or past BM
   // repeat the tile's last row and are never read.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   uint32_t a_goff[A_PER];
@@ -787,9 +793,19 @@ static int launch_wide(const void* x, int64_t M, int64_t K, const uint32_t* wq, 
   // tile; other layouts keep 256 rows.
   constexpr bool kBf16 = std::is_same<SB, uint16_t>::value;
   const bool szl = kBf16 && (K / GS) % 8 == 0 && qmm_wide_sb_reach(s, b, N * (K / GS) * 2, 2);
-  // Grids under 128 tiles of 256 x 256 (mid-size prefill) take 256 x 128 tiles with 4 waves:
-  // the same 256 x 32 strip per wave, twice the tiles.
+  // Grids under 128 tiles of 256 x 256 take 256 x 128 tiles with 4 waves (the same 256 x 32
+  // strip per wave, twice the tiles), and grids under 128 of those 128 x 128 tiles with 4 waves
+  // of 128 x 32 and a ring of 128 rows (mid-size prefill).
   const bool narrow = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN) * bat.count < 128;
+  const bool mid = narrow && ((M + kBM - 1) / kBM) * ((N + 127) / 128) * bat.count < 128;
+  if (mid) {
+    const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+    if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm: problem too large");
+    if constexpr (kBf16) {
+      if (szl) return launch_wide_w<SB, BITS, GS, 4, 128, true, 128>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+    }
+    return launch_wide_w<SB, BITS, GS, 4, 128, false, 128>(x, M, K, wq, s, b, N, y, epi, st, tiles, bat);
+  }
   if (narrow) {
     const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + 127) / 128);
     if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm: problem too large");

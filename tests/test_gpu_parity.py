@@ -224,6 +224,11 @@ WIDE_CASES = [
     (600, 1024, 6000, 32, 8),    # narrow, ragged M and N
     (1030, 512, 4100, 64, 4),    # narrow, N % 8 != 0: direct stores
     (1030, 576, 4097, 64, 4),    # narrow, N % 4 != 0: element stores, K / gs = 9: regs
+    # Under 128 of those but at least 136 tiles of 128x128 (4 waves, 128-row ring, "mid"):
+    (1024, 3072, 3072, 64, 4),   # mid, 192 tiles
+    (768, 1024, 3072, 32, 8),    # mid, 144 tiles
+    (1000, 512, 3000, 128, 4),   # mid, ragged M and N
+    (1030, 576, 2049, 64, 4),    # mid, N % 4 != 0: element stores, K / gs = 9: regs
 ]
 @pytest.mark.parametrize("M,K,N,gs,bits", WIDE_CASES)
 def test_qmm_wide_vs_oracle(mlxq, M, K, N, gs, bits):
@@ -239,12 +244,14 @@ def test_qmm_wide_vs_oracle(mlxq, M, K, N, gs, bits):
 
 @pytest.mark.parametrize("M,K,N,gs,bits", [(2048, 192, 4096, 64, 4), (2048, 64, 4096, 32, 4),
                                            (2100, 320, 4352, 64, 8), (2048, 512, 4096, 128, 8),
-                                           (1024, 256, 4096, 64, 4), (128, 1024, 512, 64, 4),
+                                           (1024, 256, 4096, 64, 4), (1024, 256, 3072, 64, 4),
+                                           (1000, 320, 3000, 64, 8), (128, 1024, 512, 64, 4),
                                            (200, 768, 300, 32, 8)])
 def test_qmm_wide_f32_scales(mlxq, M, K, N, gs, bits):
     """bf16 activations with f32 scales/biases: the wide kernel's register-loaded scale path,
     any K % 64 == 0 (K/64 = 3, 1, 5 and 8 steps cover both prologue parities), its 256x128
-    form (M = 1024), and the K-split kernel's per-step scale loads (M = 128, 200)."""
+    form (M = 1024, N = 4096), its 128x128 form (N = 3072 and the ragged 1000 x 3000) and the
+    K-split kernel's per-step scale loads (M = 128, 200)."""
     banner("qmm wide f32 scales", M, K, N, gs, bits)
     rng = np.random.default_rng(M + K + N + 7 * bits)
     x = bf16_normal(rng, (M, K))
@@ -264,7 +271,7 @@ ODD_GRID_CASES = [
     # M, K, N, gs, bits, act, bias
     (2304, 4096, 4096, 64, 4, 0, False),   # 144 tiles: one round at 56 %
     (2304, 1024, 4096, 64, 8, 3, True),    # bias + exact GELU
-    (1000, 2048, 6000, 32, 4, 2, True),    # ragged M and N (tiled kernel), tanh GELU
+    (1000, 2048, 6000, 32, 4, 2, True),    # ragged M and N (256x128 tiles), tanh GELU
     (4608, 3072, 4352, 64, 4, 0, False),   # 357 224-row tiles: two rounds at 70 %
 ]
 
@@ -289,11 +296,12 @@ def test_qmm_odd_grids(mlxq, M, K, N, gs, bits, act, bias):
     assert_close(to_np(y1)[rows], ref, f"odd grid M={M} K={K} N={N}")
 
 
-@pytest.mark.parametrize("M,N", [(2100, 4200), (1100, 4200), (2100, 4100)])
+@pytest.mark.parametrize("M,N", [(2100, 4200), (1100, 4200), (2100, 4100), (1024, 3000)])
 @pytest.mark.parametrize("act,scale", [(0, 1.0), (3, 1.0), (2, 1.0), (0, 0.75), (3, 1.5)])
 def test_linear_wide_bias_lora_act(mlxq, act, scale, M, N):
     """Fused bias + LoRA + activation epilogue on 256x256 tiles (M = 2100), on 256x128 tiles
-    with 4 waves (M = 1100: 85 wide tiles, 165 narrow ones) and with ragged N (4100), with LoRA
+    with 4 waves (M = 1100: 85 wide tiles, 165 narrow ones), on 128x128 tiles (M = 1024,
+    N = 3000: 96 narrow tiles, 192 of 128x128) and with ragged N (4100), with LoRA
     scales other than 1 (their product rounding runs only then)."""
     banner("linear wide epilogue", act, scale, M, N)
     rng = np.random.default_rng(77 + act + M + N)
