@@ -29,6 +29,7 @@
 // Q4 k-order inside an 8-run is [0,2,4,6,1,3,5,7] (low nibbles first, see unpack_q4); the
 // activation rows are permuted to match with v_perm_b32 as they are copied into LDS.
 #include <atomic>
+#include <type_traits>
 
 #include "mlxq_common.h"
 
@@ -262,54 +263,74 @@ struct GemvTile {
       for (int e = 0; e < E; ++e) yacc[e] = fmaf(s, acc[e], fmaf(zc, xsum[e], yacc[e]));
     };
 
-    // Activation runs: only lanes of A rows c16 < M read them (at M = 1 that is 4 lanes of 64, a
-    // sixteenth of the LDS traffic).  The other lanes keep their previous (finite) contents: an A
-    // row m >= M only feeds result row m, which is never stored.
-    const bool row_lane = c16 < M;
-    bf16x8 a[NM];
-#pragma unroll
-    for (int i = 0; i < NM; ++i) a[i] = bf16x8{};
+    // Activation runs: every lane reads, lanes of A rows c16 >= M the run of row 0 (an A row
+    // m >= M only feeds result row m, which is never stored).  The 16 lanes of a quarter then read
+    // at most M distinct addresses (broadcast); a read restricted to the lanes of rows < M cost
+    // the compiler ten 64-bit register copies per step to keep the other lanes' operands.
+    using SZ = typename std::conditional<BITS == 4 && G64, f32x4, f32x2>::type;
+    bf16x8 a[STEPS][NM];
+    SZ p[STEPS];
+    f32x4 acc[STEPS][2], xsum[STEPS][2];
 
+    // A step's LDS operands: its activation runs and its (s, zc) pairs.
+    auto read_step = [&](int d) {
 #pragma unroll
-    for (int d = 0; d < STEPS; ++d) {
-      // Scheduling fences around each step's MFMAs: without them the scheduler interleaves
-      // steps and keeps several steps' operands and partial sums live at once (the Q4 g64
-      // decode kernels then ran out of registers).
-      __builtin_amdgcn_sched_barrier(0);
-      if (row_lane) {
-#pragma unroll
-        for (int i = 0; i < NM; ++i) a[i] = *reinterpret_cast<const bf16x8*>(xa[i] + d * (CPL * 2));
+      for (int i = 0; i < NM; ++i) a[d][i] = *reinterpret_cast<const bf16x8*>(xa[i] + d * (CPL * 2));
+      if constexpr (BITS == 4 && G64) {
+        p[d] = *reinterpret_cast<const f32x4*>(sz + 4 * d);  // groups 2ls, 2ls+1
+      } else {
+        // Q4/128 and Q8/64: one group per step; Q8/128: a group every two steps
+        const int gl = (BITS == 4 || G64) ? d : ((ls0 + d) >> 1) - g0;
+        p[d] = *reinterpret_cast<const f32x2*>(sz + 2 * gl);
       }
+    };
+    // A step's products: NM MFMAs x . codes and NM MFMAs x . ones (the group sums).
+    auto mfma_step = [&](int d) {
       uint32_t w[4] = {wv[d][0], wv[d][1], wv[d][2], wv[d][3]};
       if constexpr (BITS == 4 && G64) {
         swap_lane_halves(w[0], w[2]);
         swap_lane_halves(w[1], w[3]);
       }
-      f32x4 acc[2], xsum[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        acc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        xsum[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        acc[d][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        xsum[d][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       }
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
         const int h = (BITS == 4 && G64) ? i >> 1 : 0;
         const bf16x8 b = BITS == 4 ? unpack_q4(w[i]) : cvt_q8(w[2 * i], w[2 * i + 1]);
-        acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b, acc[h], 0, 0, 0);
-        xsum[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], ones, xsum[h], 0, 0, 0);
+        acc[d][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][i], b, acc[d][h], 0, 0, 0);
+        xsum[d][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][i], ones, xsum[d][h], 0, 0, 0);
       }
-      __builtin_amdgcn_sched_barrier(0);
+    };
+    // A step's fold into the result.  The result is pinned after each fold: otherwise the
+    // compiler sinks every fold below the last step and keeps all steps' products live at once.
+    auto fold_step = [&](int d) {
       if constexpr (BITS == 4 && G64) {
-        const f32x4 p = *reinterpret_cast<const f32x4*>(sz + 4 * d);  // groups 2ls, 2ls+1
-        fold1(acc[0], xsum[0], p[0], p[1]);
-        fold1(acc[1], xsum[1], p[2], p[3]);
+        fold1(acc[d][0], xsum[d][0], p[d][0], p[d][1]);
+        fold1(acc[d][1], xsum[d][1], p[d][2], p[d][3]);
       } else {
-        // Q4/128 and Q8/64: one group per step; Q8/128: a group every two steps
-        const int gl = (BITS == 4 || G64) ? d : ((ls0 + d) >> 1) - g0;
-        const f32x2 p = *reinterpret_cast<const f32x2*>(sz + 2 * gl);
-        fold1(acc[0], xsum[0], p[0], p[1]);
+        fold1(acc[d][0], xsum[d][0], p[d][0], p[d][1]);
       }
+#pragma unroll
+      for (int e = 0; e < E; ++e) asm volatile("" : "+v"(yacc[e]));
+    };
+
+    // Software pipeline over the steps: iteration d reads step d+1's LDS operands, runs step d's
+    // MFMAs (waiting for its weight load only) and folds step d-1, whose products have completed
+    // meanwhile, so the LDS-read and MFMA latencies of consecutive steps overlap.  Scheduling
+    // fences between iterations keep at most two steps' operands live.
+    read_step(0);
+#pragma unroll
+    for (int d = 0; d < STEPS; ++d) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (d + 1 < STEPS) read_step(d + 1 < STEPS ? d + 1 : d);
+      mfma_step(d);
+      if (d > 0) fold_step(d - 1);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    fold_step(STEPS - 1);
   }
 };
 
@@ -388,11 +409,12 @@ constexpr int kStepChoices[] = {1, 2, 3, 4, 6, 8};
 
 // Picks the load steps per wave: among the counts that divide the row's load steps, fit a
 // workgroup of at most kMaxWaves waves, its LDS and its registers (qmv_steps_fit), the one whose
-// workgroup comes closest to 8 waves (fewer steps on a tie).  Measured on the decode shapes
-// (M = 1..8, K = 3072 and 8192, with per-wave operand staging), about 8 waves of 3-8 steps finish
-// first: a wave starts folding as soon as its own operands arrive, and more, shorter waves spread
-// the fold over the SIMDs, while a 16-wave workgroup fills a CU on its own (128 registers per
-// wave).
+// workgroup comes closest to 12 waves (fewer steps on a tie).  Measured on the decode shapes
+// (M = 1..8, K = 3072 and 8192, per-wave operand staging, pipelined fold), 8-12 waves of 3-8 steps
+// finish first: a wave starts folding as soon as its own operands arrive, and more, shorter waves
+// spread the fold's VALU work (which bounds the last waves' tail) over the SIMDs, while a 16-wave
+// workgroup fills a CU on its own (128 registers per wave).  12 against 8: the down GEMV
+// (K = 8192) 6.10 -> 5.84 us, gate (K = 3072) 5.40 -> 5.28 us, SwiGLU unchanged; 16 was no better.
 bool qmv_plan(int64_t M, int64_t K, int gs, int bits, int nmat, QmvPlan& p) {
   if (M < 1 || M > 8 || (bits != 4 && bits != 8) || (gs != 64 && gs != 128)) return false;
   const int64_t cpl = 512 / bits;
@@ -412,7 +434,7 @@ bool qmv_plan(int64_t M, int64_t K, int gs, int bits, int nmat, QmvPlan& p) {
     const int64_t red = waves * 16 * 17 * 4;
     const int64_t lds = operands > red ? operands : red;
     if (lds > kMaxLds) continue;
-    const int64_t cost = waves > 8 ? waves - 8 : 8 - waves;
+    const int64_t cost = waves > 12 ? waves - 12 : 12 - waves;
     if (found && cost >= best_cost) continue;
     found = true;
     best_cost = cost;
