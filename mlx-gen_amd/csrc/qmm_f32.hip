@@ -19,7 +19,8 @@
 // BK = 32 at a time through a double-buffered LDS holding the four bf16 tiles x_hi, x_lo, w_hi,
 // w_lo of a step (32 KB per buffer, two workgroups per CU).  Activations are split and weights
 // dequantized and split once per workgroup as they are written to LDS; every wave reads its
-// sub-tile's fragments from there.  Rows of BK bf16 with the 16-byte chunks XOR-swizzled.
+// sub-tile's fragments from there.  Global loads run two steps ahead of their use (two register
+// slots), so a step's MFMAs and the next step's split/dequant never wait on memory.  Rows of BK bf16 with the 16-byte chunks XOR-swizzled.
 // Fragment mapping for v_mfma_f32_32x32x16_bf16: lane l supplies row (l & 31) and 8 consecutive k
 // at chunk 2 kk + (l >> 5) for both operands; with the weights as the A operand the f32x16 result
 // holds activation row (l & 31) and weight rows 8 (v >> 2) + 4 (l >> 5) + (v & 3).
@@ -113,62 +114,55 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
   const int64_t groups = K / GS;
   const int ksteps = (int)((K + BK - 1) / BK);
 
-  // Staging registers: activation chunks (8 values each: two 16-byte f32 loads or one bf16 load)
-  // and packed code chunks with their group's scale and bias.
-  u32x4 a_reg[A_LD][XLO ? 2 : 1];
-  uint32_t b_reg[WPT];
-  float s_reg, z_reg;
-  [[maybe_unused]] u32x4 d_reg[DV];
+  // Staging registers, two slots (steps of even / odd parity): activation chunks (8 values each:
+  // two 16-byte f32 loads or one bf16 load) and packed code chunks with their group's scale and
+  // bias.  The loads are unconditional (rows past M / N are clamped; their products only reach
+  // outputs that are never stored, and every step's k range lies inside K), so the loop is
+  // straight-line code and each wait covers exactly the loads it needs.
+  u32x4 a_reg[2][A_LD][XLO ? 2 : 1];
+  uint32_t b_reg[2][WPT];
+  float s_reg[2], z_reg[2];
+  [[maybe_unused]] u32x4 d_reg[2][DV];
 
-  auto load_global = [&](int kt) {
+  auto load_global = [&](int kt, auto SLOT) {
+    constexpr int sl = decltype(SLOT)::value;
     const int64_t k0 = (int64_t)kt * BK;
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
       const int id = tid + NT * i;
       const int row = id / CPR, c = id % CPR;
-      const int64_t m = bm0 + row, k = k0 + c * 8;
-      const bool ok = m < M && k < K;  // K % 32 == 0, so a chunk never straddles K
+      const int64_t m = bm0 + row < M ? bm0 + row : M - 1;
+      const int64_t k = k0 + c * 8;  // K % 32 == 0: a chunk never straddles K
 #pragma unroll
-      for (int h = 0; h < (XLO ? 2 : 1); ++h)
-        a_reg[i][h] = ok ? reinterpret_cast<const u32x4*>(x + m * K + k)[h] : u32x4{0u, 0u, 0u, 0u};
+      for (int h = 0; h < (XLO ? 2 : 1); ++h) a_reg[sl][i][h] = reinterpret_cast<const u32x4*>(x + m * K + k)[h];
     }
+    const int row = tid / PPR, part = tid % PPR;
+    const int64_t n = bn0 + row < N ? bn0 + row : N - 1;
+    const int64_t kc = k0 + part * CPT;
     if constexpr (DENSE) {  // CPT consecutive values of one weight row
-      const int row = tid / PPR, part = tid % PPR;
-      const int64_t n = bn0 + row;
-      const int64_t kc = k0 + part * CPT;
-      const bool ok = n < N && kc < K;
       const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const WT*>(wq) + n * K + kc);
 #pragma unroll
-      for (int q = 0; q < DV; ++q) d_reg[q] = ok ? src[q] : u32x4{0u, 0u, 0u, 0u};
+      for (int q = 0; q < DV; ++q) d_reg[sl][q] = src[q];
     } else {  // CPT consecutive codes of one weight row (one group: CPT <= 32 <= group size)
-      const int row = tid / PPR, part = tid % PPR;
-      const int64_t n = bn0 + row;
-      const int64_t kc = k0 + part * CPT;
-      if (n < N && kc < K) {
-        const uint32_t* src = wq + n * kwords + kc * BITS / 32;
-        if constexpr (WPT == 1) {
-          b_reg[0] = src[0];
-        } else {
-#pragma unroll
-          for (int q = 0; q < WPT; q += 2) {
-            const u32x2 v = *reinterpret_cast<const u32x2*>(src + q);
-            b_reg[q] = v[0];
-            b_reg[q + 1] = v[1];
-          }
-        }
-        const int64_t g = n * groups + kc / GS;
-        s_reg = SBLoad<SB>::ld(scales, g);
-        z_reg = SBLoad<SB>::ld(biases, g);
+      const uint32_t* src = wq + n * kwords + kc * BITS / 32;
+      if constexpr (WPT == 1) {
+        b_reg[sl][0] = src[0];
       } else {
 #pragma unroll
-        for (int q = 0; q < WPT; ++q) b_reg[q] = 0u;
-        s_reg = 0.0f;
-        z_reg = 0.0f;
+        for (int q = 0; q < WPT; q += 2) {
+          const u32x2 v = *reinterpret_cast<const u32x2*>(src + q);
+          b_reg[sl][q] = v[0];
+          b_reg[sl][q + 1] = v[1];
+        }
       }
+      const int64_t g = n * groups + kc / GS;
+      s_reg[sl] = SBLoad<SB>::ld(scales, g);
+      z_reg[sl] = SBLoad<SB>::ld(biases, g);
     }
   };
 
-  auto store_lds = [&](int buf) {
+  auto store_lds = [&](int buf, auto SLOT) {
+    constexpr int sl = decltype(SLOT)::value;
     unsigned char* Ah = smem[buf];
     unsigned char* Al = smem[buf] + TA;
     unsigned char* Bh = smem[buf] + 2 * TA;
@@ -181,7 +175,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
         u32x4 hi, lo;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const u32x4& src = a_reg[i][e >> 1];
+          const u32x4& src = a_reg[sl][i][e >> 1];
           const u32x2 p = split2(__uint_as_float(src[2 * (e & 1)]), __uint_as_float(src[2 * (e & 1) + 1]));
           hi[e] = p[0];
           lo[e] = p[1];
@@ -189,7 +183,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
         *reinterpret_cast<u32x4*>(Ah + swz32<BK>(row, c)) = hi;
         *reinterpret_cast<u32x4*>(Al + swz32<BK>(row, c)) = lo;
       } else {
-        *reinterpret_cast<u32x4*>(Ah + swz32<BK>(row, c)) = a_reg[i][0];
+        *reinterpret_cast<u32x4*>(Ah + swz32<BK>(row, c)) = a_reg[sl][i][0];
       }
     }
     if constexpr (DENSE) {
@@ -198,12 +192,12 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
 #pragma unroll
       for (int p = 0; p < CPT / 8; ++p) {
         if constexpr (std::is_same<WT, uint16_t>::value) {
-          *reinterpret_cast<u32x4*>(Bh + swz32<BK>(row, c0 + p)) = d_reg[p];
+          *reinterpret_cast<u32x4*>(Bh + swz32<BK>(row, c0 + p)) = d_reg[sl][p];
         } else {
           u32x4 hi, lo;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const u32x4& src = d_reg[2 * p + (e >> 1)];
+            const u32x4& src = d_reg[sl][2 * p + (e >> 1)];
             const float v0 = __uint_as_float(src[2 * (e & 1)]), v1 = __uint_as_float(src[2 * (e & 1) + 1]);
             if constexpr (WLO) {
               const u32x2 q = split2(v0, v1);
@@ -219,14 +213,14 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
       }
     } else {
       const int row = tid / PPR, part = tid % PPR;
-      const float s = s_reg, z = z_reg;
+      const float s = s_reg[sl], z = z_reg[sl];
       // LDS chunk c holds k [8c, 8c + 8) of the step; this thread's codes start at chunk part*CPT/8.
       const int c0 = part * CPT / 8;
       if constexpr (BITS == 4) {
         // word q: codes 8q..8q+7 in natural order (low nibble first) -> chunk c0 + q
 #pragma unroll
         for (int q = 0; q < WPT; ++q) {
-          const uint32_t w = b_reg[q];
+          const uint32_t w = b_reg[sl][q];
           u32x4 hi, lo;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -247,7 +241,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
           u32x4 hi, lo;
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const uint32_t w = b_reg[2 * p + h];
+            const uint32_t w = b_reg[sl][2 * p + h];
             const u32x2 p0 = split2(fmaf((float)(w & 0xffu), s, z), fmaf((float)((w >> 8) & 0xffu), s, z));
             const u32x2 p1 = split2(fmaf((float)((w >> 16) & 0xffu), s, z), fmaf((float)(w >> 24), s, z));
             hi[2 * h] = p0[0];
@@ -270,14 +264,11 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  load_global(0);
-  store_lds(0);
-  __syncthreads();
-
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
   const int r32 = lane & 31, half = lane >> 5;
-  for (int kt = 0; kt < ksteps; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < ksteps) load_global(kt + 1);
+  // Step kt's products from LDS buffer kt & 1.
+  auto mfma_step = [&](int buf) {
     const unsigned char* Ah = smem[buf];
     const unsigned char* Al = smem[buf] + TA;
     const unsigned char* Bh = smem[buf] + 2 * TA;
@@ -314,9 +305,29 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
           for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh[j], al[i], acc[i][j], 0, 0, 0);
       }
     }
-    if (kt + 1 < ksteps) store_lds(buf ^ 1);
+  };
+  // Software pipeline, global loads two steps ahead of their use: iteration kt issues step kt+2's
+  // loads into the register slot step kt has vacated, then runs step kt's MFMAs from one LDS buffer
+  // while step kt+1's operands (loaded during iteration kt-1) are split, dequantized and written
+  // into the other, so the split/dequant VALU work overlaps the MFMAs instead of following them.
+  // Past the last step the loads repeat the last step (in bounds, never used) and the writes fill
+  // the idle buffer, which keeps the body free of branches.
+  auto body = [&](int kt, auto SLOT, auto NSLOT) {
+    load_global(kt + 2 < ksteps ? kt + 2 : ksteps - 1, SLOT);
+    mfma_step(kt & 1);
+    store_lds((kt + 1) & 1, NSLOT);
     __syncthreads();
+  };
+  load_global(0, S0{});
+  load_global(ksteps > 1 ? 1 : 0, S1{});
+  store_lds(0, S0{});
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 1 < ksteps; kt += 2) {
+    body(kt, S0{}, S1{});
+    body(kt + 1, S1{}, S0{});
   }
+  if (kt < ksteps) body(kt, S0{}, S1{});
 
   // acc[i][j] element v: column m = row of A's fragment (lane & 31), rows n = 8 (v >> 2) +
   // 4 half + (v & 3) of B's fragment: the weight operand is MFMA's A side, so each lane holds four
