@@ -51,6 +51,12 @@ def parse():
                         "kernel for the HBM byte counters")
     p.add_argument("--pmc-sets", metavar="A,B", default=None,
                    help="with --summarize-pmc: only these counter-set subdirectories (copy_* always read)")
+    p.add_argument("--summarize-trace", metavar="DIR",
+                   help="print per-launch-shape duration statistics of the mlxq kernels in the "
+                        "rocprofv3 --kernel-trace csv files under DIR and exit")
+    p.add_argument("--trace-skip", type=int, default=0, metavar="N",
+                   help="with --summarize-trace: leave out each launch shape's first N launches "
+                        "(the warm-up steps), so the averages cover the timed launches")
     p.add_argument("--summarize-pmc", metavar="DIR",
                    help="print the counter summary of the rocprofv3 --pmc runs under DIR (one "
                         "subdirectory per counter set, see summarize_pmc) and exit")
@@ -583,6 +589,35 @@ def summarize_pmc(d, sets=None):
     print("\n".join(lines))
 
 
+def summarize_trace(d, skip=0):
+    """Per mlxq kernel and launch shape (grid in workgroups x workgroup size) of the rocprofv3
+    --kernel-trace csv files under d: launch count and average / median / minimum duration, over
+    the launches after each shape's first `skip` (in start-time order)."""
+    import csv
+    import glob
+    shapes = {}
+    for f in glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            name = r["Kernel_Name"].replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
+            if "mlxq" not in name:
+                continue
+            wg = int(r["Workgroup_Size_X"]) * int(r.get("Workgroup_Size_Y", 1) or 1)
+            grid = int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"]))
+            gy = int(r.get("Grid_Size_Y", 1) or 1) // max(1, int(r.get("Workgroup_Size_Y", 1) or 1))
+            key = (name, grid if gy <= 1 else f"{grid} x {gy}", wg)
+            shapes.setdefault(key, []).append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    lines = []
+    durs = {}
+    for key, ts in shapes.items():
+        ts.sort()
+        kept = ts[skip:] if len(ts) > skip else ts
+        durs[key] = [(e - b) / 1e3 for b, e in kept]
+    for (name, grid, wg), v in sorted(durs.items(), key=lambda kv: -sum(kv[1]) / len(kv[1])):
+        lines.append(f"  {name}  grid {grid} x {wg}: launches {len(v)}  avg {sum(v) / len(v):.2f} us  "
+                     f"median {_med(v):.2f} us  min {min(v):.2f}")
+    print("\n".join(lines))
+
+
 def read_traffic():
     """HBM bytes per qmm launch from the committed rocprofv3 --pmc summary, or None."""
     try:
@@ -596,6 +631,9 @@ def read_traffic():
 
 def main():
     args = parse()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args.trace_skip)
+        return
     if args.summarize_pmc:
         summarize_pmc(args.summarize_pmc, args.pmc_sets)
         return
