@@ -15,9 +15,10 @@
 // Weights are dequantized exactly as fma(code, scale, bias) in f32 (scale and bias widened
 // exactly from bf16), then split.
 //
-// Structure: a workgroup of 4 waves (2 x 2, 64 x 64 each) per 128 x 128 output tile, K advanced
-// BK = 32 at a time through a double-buffered LDS holding the four bf16 tiles x_hi, x_lo, w_hi,
-// w_lo of a step (32 KB per buffer, two workgroups per CU).  Activations are split and weights
+// Structure: a workgroup of 8 waves (2 x 4, 64 x 64 each) per 128 x 256 output tile (the LoKr
+// dense product: 4 waves, 2 x 2, per 128 x 128 tile), K advanced BK = 32 at a time through a
+// double-buffered LDS holding the four bf16 tiles x_hi, x_lo, w_hi, w_lo of a step (48 KB per
+// buffer, one workgroup per CU; 32 KB and two for the dense product).  Activations are split and weights
 // dequantized and split once per workgroup as they are written to LDS; every wave reads its
 // sub-tile's fragments from there.  Global loads run two steps ahead of their use (two register
 // slots), so a step's MFMAs and the next step's split/dequant never wait on memory.  Rows of BK bf16 with the 16-byte chunks XOR-swizzled.
@@ -385,10 +386,13 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
 template <typename XT, typename SB, int BITS, int GS>
 static int launch_qmm_f32(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                           const void* b, int64_t N, void* y, const F32Epilogue& epi, hipStream_t st) {
-  // 4 waves on 128 x 128 tiles with 32-deep K steps (64 KB of LDS, two workgroups per CU):
-  // 1225 us on the FLUX up shape (f32 x, Q4 g64, 284 TFLOP/s) against 1279 with 8 waves, 1336
-  // with 128 x 256 tiles (1 workgroup per CU) and 1614 with 64-deep steps (128 KB, 1 per CU).
-  constexpr int WAVES = 4, BN = 128, BK = 32;
+  // 8 waves (2 x 4 of 64 x 64) on 128 x 256 tiles with 32-deep K steps (96 KB of LDS, one
+  // workgroup per CU).  With loads two steps ahead, same-box A/B on the FLUX shapes (f32 x, Q4
+  // g64, up / down in ms): this form 1.103 / 1.346; 4 waves on 128 x 128 (two workgroups per CU)
+  // 1.199 / 1.348; 8 waves on 128 x 128 1.200 / 1.362; 4 waves on 128 x 256 1.433 / 1.729.
+  // (Before the prefetch rework the 128 x 128 four-wave form had led: 1225 us on the up shape
+  // against 1279 with 8 waves, 1336 with 128 x 256 tiles, 1614 with 64-deep steps.)
+  constexpr int WAVES = 8, BN = 256, BK = 32;
   const int64_t tiles = ((M + kF32BM - 1) / kF32BM) * ((N + BN - 1) / BN);
   if (tiles == 0) return MLXQ_OK;
   if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm_f32: problem too large");
