@@ -401,6 +401,230 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   gemv_reduce_store<NMAT>(lds, yacc, wave_all, W, lane, tid, NT, M, n0, N, y);
 }
 
+// ---------------------------------------------------------------------------------------------
+// M = 1, Q4: one weight row per wave.
+//
+// A wave streams its whole row (its gate and up rows in the SwiGLU form) in contiguous 512-byte
+// loads, 8 bytes per lane, all issued up front, and computes the row's dot product alone: no
+// split-K partials, no reduction through LDS, and no workgroup barrier after the one that
+// publishes the staged activations.  (Streaming rows whole measured 3.66-3.70 us for the down
+// codes against 4.08 us for the 16-row x 64-byte loads of the tile kernel above.)
+//
+// A 512-byte load holds 16 columns of 64 codes.  Lane L reads bytes [32n + 8q, +8) with
+// n = L & 15, q = L >> 4: codes [16q, 16q + 16) of column n, i.e. its two words feed two MFMAs
+// (v_mfma_f32_16x16x32_bf16) whose B column n is column n's 64 codes.  The A operand's row m is
+// the activation run of column m (16 different K slices of the one activation row), so the
+// product's diagonal C[n][n] is column n's dot product sum x*(128+c), and the off-diagonal
+// entries are discarded.  C[n][n] sits in lane n + 16 (n >> 2), register n & 3: 16 lanes of the
+// wave fold one column each per load,
+//   y += s*C[n][n] + (b - 128 s)*X[column],
+// with X the column's activation sum (computed once per workgroup while staging).  The wave's
+// 16 partial sums are added at the end with row shifts and lane reads.
+constexpr int kRowColPitch = 144;  // LDS bytes per 64-element activation column (128 + pad)
+
+// Whether the one-row kernel takes a problem (bf16 x and scales are checked by the caller).
+__host__ __device__ constexpr bool qmv_row_fits(int64_t M, int64_t K, int gs, int bits) {
+  return M == 1 && bits == 4 && (gs == 64 || gs == 128) && K % 1024 == 0 && K >= 1024 && K <= 16384;
+}
+
+// LDS bytes of a one-row workgroup: the activation columns, their sums and each wave's (s, zc)
+// table per matrix.
+__host__ __device__ constexpr int qmv_row_lds(int LS, bool g64, int nmat, int wpb) {
+  return LS * 16 * kRowColPitch + LS * 16 * 4 + wpb * nmat * (g64 ? LS * 16 : LS * 8) * 8;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+
+// Contract (checked on the host by qmv_row_plan): M = 1, K = 1024 LS, bf16 x/scales/biases, Q4
+// codes, group 64 or 128, 8..16 waves per workgroup, dynamic LDS of qmv_row_lds bytes, every
+// buffer < 2 GiB.  NMAT = 2: wave f streams gate row f and up row f and writes
+// round(round(silu(round(g))) * round(u)) (qwen3.rs:178-181); else round(y).
+template <bool G64, int LS, int NMAT>
+__global__ __launch_bounds__(1024) void qmv_row_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ biases, const uint32_t* __restrict__ wq2,
+    const uint16_t* __restrict__ scales2, const uint16_t* __restrict__ biases2, int N,
+    uint16_t* __restrict__ y) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  constexpr int K = 1024 * LS;
+  constexpr int C = 16 * LS;                  // 64-code columns per row
+  constexpr int G = G64 ? C : C / 2;          // groups per row
+  constexpr int RB = 512 * LS;                // bytes per packed row
+  constexpr int XCH = 128 * LS;               // 16-byte activation chunks
+  constexpr int XPT = (XCH + 511) / 512;      // ... per thread (at least 8 waves)
+  constexpr int SBPL = (G + 127) / 128;       // scale/bias word pairs per lane
+  const int NT = blockDim.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row = blockIdx.x * (NT >> 6) + wave;
+  const int r = row < N ? row : N - 1;  // waves past N take part in the staging, store nothing
+  unsigned char* xs = lds;
+  float* xsum = reinterpret_cast<float*>(lds + C * kRowColPitch);
+  float* tab = xsum + C + wave * NMAT * G * 2;
+
+  // Operand loads first (they queue ahead of the weight streams), then every weight load.
+  const auto rx = make_rsrc(x, K * 2);
+  u32x4 cx[XPT];
+#pragma unroll
+  for (int j = 0; j < XPT; ++j) {
+    const int ch = tid + j * NT;
+    cx[j] = load16(rx, ch < XCH ? (uint32_t)ch * 16u : kOob);
+  }
+  const int sb_bytes = (int)((uint32_t)N * (uint32_t)G * 2u);
+  uint32_t cs[NMAT][SBPL], cb[NMAT][SBPL];
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat) {
+    const auto rs = make_rsrc(mat ? scales2 : scales, sb_bytes);
+    const auto rz = make_rsrc(mat ? biases2 : biases, sb_bytes);
+#pragma unroll
+    for (int i = 0; i < SBPL; ++i) {
+      const int g0 = 2 * lane + 128 * i;
+      const uint32_t off = g0 < G ? ((uint32_t)r * (uint32_t)G + (uint32_t)g0) * 2u : kOob;
+      cs[mat][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+      cb[mat][i] = __builtin_amdgcn_raw_buffer_load_b32(rz, off, 0, 0);
+    }
+  }
+  // Every wave's activation loads go ahead of all weight streams in the CU's in-order memory
+  // queue: the staging below needs the whole workgroup's (a bare s_barrier, no memory wait).
+  __builtin_amdgcn_s_barrier();
+  // Weight loads in fold order (step d of every matrix before step d + 1), so a step's operands
+  // arrive together.
+  u32x2 wv[NMAT][LS];
+  const uint32_t lo = 32u * (uint32_t)(lane & 15) + 8u * (uint32_t)(lane >> 4);
+  const int w_bytes = (int)((uint32_t)N * (uint32_t)RB);
+  const __amdgpu_buffer_rsrc_t rw[2] = {make_rsrc(wq, w_bytes), make_rsrc(NMAT == 2 ? wq2 : wq, w_bytes)};
+#pragma unroll
+  for (int d = 0; d < LS; ++d) {
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat)
+      wv[mat][d] = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw[mat], (uint32_t)r * (uint32_t)RB + (uint32_t)d * 512u + lo, 0, 0));
+  }
+
+  // Activation columns (runs permuted to the unpacked code order) and their sums: the 8 chunks
+  // of a column sit in 8 consecutive lanes of one wave (NT is a multiple of 64).
+#pragma unroll
+  for (int j = 0; j < XPT; ++j) {
+    const int ch = tid + j * NT;
+    const u32x4 v = cx[j];
+    float t = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t += __uint_as_float(v[e] << 16) + __uint_as_float(v[e] & 0xffff0000u);
+    t += dpp_f32<0xb1>(t);   // quad_perm [1,0,3,2]
+    t += dpp_f32<0x4e>(t);   // quad_perm [2,3,0,1]: every lane holds its quad's sum
+    t += dpp_f32<0x104>(t);  // row_shl:4: lane 8k adds lane 8k+4's quad
+    // (only lanes 8k, the column's first chunk, store the sum)
+    if (ch < XCH) {
+      *reinterpret_cast<u32x4*>(xs + (ch >> 3) * kRowColPitch + (ch & 7) * 16) = perm_q4(v);
+      if ((ch & 7) == 0) xsum[ch >> 3] = t;
+    }
+  }
+  // Publish the activations with LDS-only fences: a __syncthreads() release fence would also
+  // wait for every outstanding weight load.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  // The wave's (s, b - 128 s) pairs per group, f32, after the barrier: only this wave reads them,
+  // so the workgroup waits for the activations alone, not for every wave's scale loads.
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat) {
+#pragma unroll
+    for (int i = 0; i < SBPL; ++i) {
+      const int g0 = 2 * lane + 128 * i;
+      if (g0 < G) {
+        const float s0 = __uint_as_float(cs[mat][i] << 16), s1 = __uint_as_float(cs[mat][i] & 0xffff0000u);
+        const float b0 = __uint_as_float(cb[mat][i] << 16), b1 = __uint_as_float(cb[mat][i] & 0xffff0000u);
+        *reinterpret_cast<f32x4*>(tab + (mat * G + g0) * 2) =
+            f32x4{s0, fmaf(-128.0f, s0, b0), s1, fmaf(-128.0f, s1, b1)};
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+
+  // Load d covers columns 16d .. 16d+15.  Lane (m, q) = (L & 15, L >> 4) reads A runs 2q, 2q+1 of
+  // column 16d + m, and folds column 16d + n (n = m) from register e = L & 3 of the product.
+  const int m = lane & 15, q = lane >> 4, e = lane & 3;
+  const unsigned char* xa = xs + m * kRowColPitch + q * 32;
+  bf16x8 a[LS][2];
+  f32x2 p[LS][NMAT];
+  float xg[LS];
+  f32x4 acc[LS][NMAT];
+  float ya[NMAT];
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat) ya[mat] = 0.0f;
+  auto read_step = [&](int d) {
+    a[d][0] = *reinterpret_cast<const bf16x8*>(xa + d * 16 * kRowColPitch);
+    a[d][1] = *reinterpret_cast<const bf16x8*>(xa + d * 16 * kRowColPitch + 16);
+    const int col = 16 * d + m;
+    const int g = G64 ? col : col >> 1;
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat) p[d][mat] = *reinterpret_cast<const f32x2*>(tab + (mat * G + g) * 2);
+    xg[d] = xsum[col];
+  };
+  auto mfma_step = [&](int d) {
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat) {
+      const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][0], unpack_q4(wv[mat][d][0]),
+                                                              f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+      acc[d][mat] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][1], unpack_q4(wv[mat][d][1]), c, 0, 0, 0);
+    }
+  };
+  auto fold_step = [&](int d) {
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat) {
+      const f32x4 c = acc[d][mat];
+      float v = e == 1 ? c[1] : c[0];
+      v = e == 2 ? c[2] : v;
+      v = e == 3 ? c[3] : v;
+      ya[mat] = fmaf(p[d][mat][0], v, fmaf(p[d][mat][1], xg[d], ya[mat]));
+      asm volatile("" : "+v"(ya[mat]));
+    }
+  };
+  read_step(0);
+#pragma unroll
+  for (int d = 0; d < LS; ++d) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (d + 1 < LS) read_step(d + 1 < LS ? d + 1 : d);
+    mfma_step(d);
+    if (d > 0) fold_step(d - 1);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  fold_step(LS - 1);
+
+  // The 16 diagonal lanes (n + 16 (n >> 2)) hold the partial sums: a row-shift scan leaves each
+  // 16-lane row's sum in its lane 15.
+  const bool diag = q == (m >> 2);
+  float tot[NMAT];
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat) {
+    float v = diag ? ya[mat] : 0.0f;
+    v += dpp_f32<0x111>(v);
+    v += dpp_f32<0x112>(v);
+    v += dpp_f32<0x114>(v);
+    v += dpp_f32<0x118>(v);
+    tot[mat] = (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 15)) +
+                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31))) +
+               (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 47)) +
+                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63)));
+  }
+  if (lane == 0 && row < N) {
+    float v = tot[0];
+    if constexpr (NMAT == 2) {
+      // each op rounded to bf16 as the reference's separate ops are (qwen3.rs:178-181)
+      const float g = round_bf16(v);
+      const float sg = round_bf16(g / (1.0f + expf(-g)));
+      v = sg * round_bf16(tot[1]);
+    }
+    y[row] = f32_to_bf16_bits(v);
+  }
+}
+
 namespace {
 
 struct QmvPlan {
@@ -518,6 +742,78 @@ static int qmv_kind(const QmvArgs& a, int gs, int bits, const QmvPlan& p, hipStr
   return qmv_steps<4, false, NMAT>(a, p, st);
 }
 
+// CUs of the current device (cached per device).
+static int64_t gemv_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int cus = cached[dev].load(std::memory_order_relaxed);
+  if (cus <= 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[dev].store(cus, std::memory_order_relaxed);
+  }
+  return cus;
+}
+
+// Waves (rows) per one-row workgroup.  SwiGLU (two rows per wave): 8, i.e. the staging barrier
+// among fewer waves (K = 3072, F = 8192: 7.7 -> 7.1 us against 16 waves; 4 was no better).
+// One matrix: the largest of 16, 12, 8 whose workgroup count is a multiple of the CU count
+// (N = 3072: 12 -> 256 workgroups, 5.1 us against 5.5 at 8 and 5.9 at 16; N = 8192: 16), else 16.
+static int qmv_row_wpb(int64_t N, int nmat) {
+  if (nmat == 2) return 8;
+  const int64_t cus = gemv_cus();
+  for (int w : {16, 12, 8})
+    if (((N + w - 1) / w) % cus == 0) return w;
+  return 16;
+}
+
+template <bool G64, int LS, int NMAT>
+static int launch_qmv_row(const QmvArgs& a, hipStream_t st) {
+  static std::atomic<bool> attr_set[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(MLXQ_EDEVICE, "qmv: no current device");
+  if (dev < 0 || dev >= 64 || !attr_set[dev].load(std::memory_order_acquire)) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_row_kernel<G64, LS, NMAT>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds) != hipSuccess)
+      return set_error(MLXQ_EDEVICE, "qmv: hipFuncSetAttribute failed");
+    if (dev >= 0 && dev < 64) attr_set[dev].store(true, std::memory_order_release);
+  }
+  const int wpb = qmv_row_wpb(a.N, NMAT);
+  const int lds = qmv_row_lds(LS, G64, NMAT, wpb);
+  hipLaunchKernelGGL((qmv_row_kernel<G64, LS, NMAT>), dim3((unsigned)((a.N + wpb - 1) / wpb)), dim3(wpb * 64),
+                     lds, st, (const uint16_t*)a.x, a.wq, (const uint16_t*)a.s, (const uint16_t*)a.b, a.wq2,
+                     (const uint16_t*)a.s2, (const uint16_t*)a.b2, (int)a.N, (uint16_t*)a.y);
+  return check_launch(NMAT == 2 ? "swiglu_qmv_row" : "qmv_row");
+}
+
+template <bool G64, int NMAT>
+static int qmv_row_ls(const QmvArgs& a, hipStream_t st) {
+  switch (a.K / 1024) {
+    case 1: return launch_qmv_row<G64, 1, NMAT>(a, st);
+    case 2: return launch_qmv_row<G64, 2, NMAT>(a, st);
+    case 3: return launch_qmv_row<G64, 3, NMAT>(a, st);
+    case 4: return launch_qmv_row<G64, 4, NMAT>(a, st);
+    case 5: return launch_qmv_row<G64, 5, NMAT>(a, st);
+    case 6: return launch_qmv_row<G64, 6, NMAT>(a, st);
+    case 7: return launch_qmv_row<G64, 7, NMAT>(a, st);
+    case 8: return launch_qmv_row<G64, 8, NMAT>(a, st);
+    case 9: return launch_qmv_row<G64, 9, NMAT>(a, st);
+    case 10: return launch_qmv_row<G64, 10, NMAT>(a, st);
+    case 11: return launch_qmv_row<G64, 11, NMAT>(a, st);
+    case 12: return launch_qmv_row<G64, 12, NMAT>(a, st);
+    case 13: return launch_qmv_row<G64, 13, NMAT>(a, st);
+    case 14: return launch_qmv_row<G64, 14, NMAT>(a, st);
+    case 15: return launch_qmv_row<G64, 15, NMAT>(a, st);
+    default: return launch_qmv_row<G64, 16, NMAT>(a, st);
+  }
+}
+
+template <int NMAT>
+static int qmv_row(const QmvArgs& a, int gs, hipStream_t st) {
+  return gs == 64 ? qmv_row_ls<true, NMAT>(a, st) : qmv_row_ls<false, NMAT>(a, st);
+}
+
 static bool buffers_fit(int64_t M, int64_t K, int64_t N) {
   const int64_t lim = (int64_t)1 << 31;  // every buffer (Q8 weights: N*K bytes) under 2 GiB
   return N * K < lim && M * K * 2 < lim;
@@ -531,10 +827,11 @@ bool qmv_mfma_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int64_
 
 int run_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
                  int64_t N, int gs, int bits, void* y, hipStream_t st) {
+  const QmvArgs a = {x, M, K, N, wq, s, b, nullptr, nullptr, nullptr, y};
+  if (qmv_row_fits(M, K, gs, bits)) return qmv_row<1>(a, gs, st);
   QmvPlan p;
   if (!qmv_plan(M, K, gs, bits, 1, p))
     return set_error(MLXQ_EINVAL, "qmv: no GEMV plan for M=%lld K=%lld", (long long)M, (long long)K);
-  const QmvArgs a = {x, M, K, N, wq, s, b, nullptr, nullptr, nullptr, y};
   return qmv_kind<1>(a, gs, bits, p, st);
 }
 
@@ -547,11 +844,12 @@ bool swiglu_qmv_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int6
 int run_swiglu_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq_g, const void* s_g,
                    const void* b_g, const uint32_t* wq_u, const void* s_u, const void* b_u, int64_t F,
                    int gs, int bits, void* h, hipStream_t st) {
+  const QmvArgs a = {x, M, K, F, wq_g, s_g, b_g, wq_u, s_u, b_u, h};
+  if (qmv_row_fits(M, K, gs, bits)) return qmv_row<2>(a, gs, st);
   QmvPlan p;
   if (!qmv_plan(M, K, gs, bits, 2, p))
     return set_error(MLXQ_EUNSUPPORTED, "swiglu: no fused GEMV plan for M=%lld K=%lld", (long long)M,
                      (long long)K);
-  const QmvArgs a = {x, M, K, F, wq_g, s_g, b_g, wq_u, s_u, b_u, h};
   return qmv_kind<2>(a, gs, bits, p, st);
 }
 
