@@ -422,52 +422,56 @@ def _close_to_exact(y, ref, what):
     assert worst <= 1.0, what
 
 
-# M = 1, Q4, K a multiple of 1024: the one-row-per-wave kernel (K from 1 to 16 loads per row,
-# N not a multiple of the 8/12/16 rows of a workgroup, N below one workgroup).
+# Q4, K a multiple of 1024: at M = 1 the one-row-per-wave kernel (K from 1 to 16 loads per row,
+# N not a multiple of the 8/12/16 rows of a workgroup, N below one workgroup); M = 2..4 run the
+# 16-row tile kernel on the same shapes, held to the same bound.
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 @pytest.mark.parametrize("K,N,gs", [(1024, 77, 64), (3072, 8192, 128), (5120, 1000, 64), (8192, 3072, 128),
                                     (16384, 40, 64), (16384, 24, 128), (2048, 5, 64), (7168, 2051, 64)])
-def test_qmv_one_row_kernel_vs_exact(mlxq, K, N, gs):
-    banner("qmv one row", K, N, gs)
-    rng = np.random.default_rng(K + 3 * N + gs)
-    x = bf16_normal(rng, (1, K))
+def test_qmv_one_row_kernel_vs_exact(mlxq, M, K, N, gs):
+    banner("qmv one row", M, K, N, gs)
+    rng = np.random.default_rng(K + 3 * N + gs + 101 * M)
+    x = bf16_normal(rng, (M, K))
     w = bf16_normal(rng, (N, K), 0.02)
     rwq, rs, rb = oracle.quantize(w, gs, 4, sb_bf16=True)
     y = to_np(mlxq.quantized_matmul(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), True, gs, 4))
     exact = oracle.quantized_matmul(x, rwq, rs, rb, gs, 4, w_bf16=False, out_bf16=False)
-    _close_to_exact(y, exact, f"one-row K={K} N={N} gs={gs}")
-    assert_close(y, oracle.bf16_round(exact), f"one-row K={K} N={N} gs={gs}")
+    _close_to_exact(y, exact, f"one-row M={M} K={K} N={N} gs={gs}")
+    assert_close(y, oracle.bf16_round(exact), f"one-row M={M} K={K} N={N} gs={gs}")
 
 
 @pytest.mark.parametrize("K,N,gs", [(3072, 8192, 64), (8192, 3072, 64), (4096, 520, 128)])
 def test_qmv_one_row_kernel_matches_tile_kernel(mlxq, K, N, gs):
-    """The one-row kernel (M = 1) and the 16-row tile kernel (the same row twice, M = 2) compute
-    the same exact-f32 product: their bf16 outputs agree to the same bound."""
+    """The one-row kernel (M = 1) and the 16-row tile kernel (M = 2..4 and 8, different wave plans)
+    compute the same exact-f32 product: the first M rows of an M = 8 launch bound the M-row
+    launches of the same rows."""
     banner("qmv one row vs tile", K, N, gs)
     rng = np.random.default_rng(K + N)
-    x = bf16_normal(rng, (1, K))
+    x = bf16_normal(rng, (8, K))
     w = bf16_normal(rng, (N, K), 0.02)
     wq, s, b = [to_gpu(a) if i else wq_to_gpu(a) for i, a in enumerate(oracle.quantize(w, gs, 4, sb_bf16=True))]
-    y1 = to_np(mlxq.quantized_matmul(to_gpu(x), wq, s, b, True, gs, 4))
-    y2 = to_np(mlxq.quantized_matmul(to_gpu(np.concatenate([x, x])), wq, s, b, True, gs, 4))
-    assert np.array_equal(y2[0], y2[1])
-    _close_to_exact(y1[0], y2[0].astype(np.float64), f"one-row vs tile K={K} N={N}")
-    print(f"    bit-identical outputs: {np.mean(y1[0] == y2[0]) * 100:.2f} %", flush=True)
+    y8 = to_np(mlxq.quantized_matmul(to_gpu(x), wq, s, b, True, gs, 4))
+    for M in (1, 2, 3, 4):
+        yM = to_np(mlxq.quantized_matmul(to_gpu(x[:M]), wq, s, b, True, gs, 4))
+        _close_to_exact(yM, y8[:M].astype(np.float64), f"rows vs tile M={M} K={K} N={N}")
+        print(f"    M={M} bit-identical outputs: {np.mean(yM == y8[:M]) * 100:.2f} %", flush=True)
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 @pytest.mark.parametrize("K,F,gs", [(3072, 8192, 64), (4096, 77, 128), (1024, 1000, 64)])
-def test_swiglu_one_row_kernel_vs_exact(mlxq, K, F, gs):
-    """SwiGLU at M = 1 on the one-row kernel (gate row f and up row f in one wave): h against the
-    op-by-op rounding of the exact gate and up products."""
-    banner("swiglu one row", K, F, gs)
-    rng = np.random.default_rng(K + F + gs + 1)
-    x = bf16_normal(rng, (1, K))
+def test_swiglu_one_row_kernel_vs_exact(mlxq, M, K, F, gs):
+    """SwiGLU at M = 1 on the one-row kernel (gate row f and up row f in one wave), M = 2..4 on the
+    tile kernel: h against the op-by-op rounding of the exact gate and up products."""
+    banner("swiglu one row", M, K, F, gs)
+    rng = np.random.default_rng(K + F + gs + 1 + 7 * M)
+    x = bf16_normal(rng, (M, K))
     tg, tu = [oracle.quantize(bf16_normal(rng, (F, K), 0.02), gs, 4, sb_bf16=True) for _ in range(2)]
     h = to_np(mlxq.swiglu(to_gpu(x), [wq_to_gpu(tg[0]), to_gpu(tg[1]), to_gpu(tg[2])],
                           [wq_to_gpu(tu[0]), to_gpu(tu[1]), to_gpu(tu[2])], gs, 4))
     gr = oracle.quantized_matmul(x, *tg, gs, 4, w_bf16=False, out_bf16=True)
     ur = oracle.quantized_matmul(x, *tu, gs, 4, w_bf16=False, out_bf16=True)
     ref = oracle.bf16_round(oracle.bf16_round(np.vectorize(oracle.silu)(gr).astype(np.float32)) * ur)
-    assert_close(h, ref, f"swiglu one row K={K} F={F}")
+    assert_close(h, ref, f"swiglu one row M={M} K={K} F={F}")
     print(f"    bit-identical outputs: {np.mean(h == ref) * 100:.2f} %", flush=True)
     assert np.mean(h == ref) > 0.95
 
