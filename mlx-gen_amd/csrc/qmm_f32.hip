@@ -383,6 +383,291 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
   }
 }
 
+// The factored form for group sizes 64 and 128: since
+//     x . w = sum_g ( s_g * sum_{k in g} x_k c_k  +  b_g * X_g ),   X_g = sum_{k in g} x_k,
+// the codes c (small integers, exact in bf16) are the weight operand and only the activations are
+// split: x_hi.c + x_lo.c is two MFMA passes for f32 x (one for bf16 x) instead of three, with no
+// dequantization or weight split.  Each group's product accumulates in `acc` (the first MFMA of a
+// group starts from zero) and is folded into the running f32 sum y by two FMAs per output with the
+// group's scale and bias (one per weight row) and activation sum (one per activation row), which
+// the staging threads leave in two small LDS tables next to the step's tiles.  The loop is
+// unrolled by the group's GS/32 steps, so group starts and ends are compile-time positions.
+// Tiles, waves, buffers and the load pipeline are those of qmm_f32_kernel (128 x 256, 8 waves of
+// 64 x 64, 32-deep K steps, loads two steps ahead).
+template <typename XT, typename SB, int BITS, int GS, bool EPI>
+__global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x, int64_t M, int64_t K,
+                                                   const uint32_t* __restrict__ wq,
+                                                   const SB* __restrict__ scales,
+                                                   const SB* __restrict__ biases, int64_t N,
+                                                   float* __restrict__ y, F32Epilogue epi) {
+  constexpr bool XLO = std::is_same<XT, float>::value;  // activations carry a low part
+  constexpr int WAVES = 8, BN = 256, BK = 32;
+  constexpr int BM = kF32BM, NT = WAVES * 64;
+  constexpr int WGN = WAVES / 2;
+  constexpr int WM = BM / 2, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+  constexpr int CPR = BK / 8;                // 16-byte bf16 chunks per tile row
+  constexpr int CPT = BN * BK / NT;          // codes per thread per step (16)
+  constexpr int WPT = CPT * BITS / 32;       // their packed words
+  constexpr int PPR = BK / CPT;              // threads per weight row (2)
+  constexpr int GSTEP = GS / BK;             // steps per group (2 or 4)
+  constexpr int TA = BM * BK * 2, TB = BN * BK * 2;
+  constexpr int OFF_SB = 2 * TA + TB, OFF_X = OFF_SB + BN * 8, BUF = OFF_X + BM * 4;
+  static_assert(BM * CPR == NT && GSTEP >= 2 && GSTEP % 2 == 0 && WPT >= 1, "tile shape");
+  // Per buffer: x_hi, x_lo, codes, then the (s, b) pairs of the tile's weight rows and the
+  // activation sums of its rows for the group the buffer's step closes.
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2][BUF];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int64_t tm, tn;
+  f32_tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int64_t bm0 = tm * BM, bn0 = tn * BN;
+  const int64_t kwords = K * BITS / 32;
+  const int64_t groups = K / GS;
+  const int ksteps = (int)(K / BK);  // a multiple of GSTEP (K % GS == 0)
+
+  // Staging registers, two slots (see qmm_f32_kernel): thread tid stages activation row tid / 4,
+  // chunk tid % 4, and codes CPT of weight row tid / 2 with that row's scale and bias.
+  u32x4 a_reg[2][XLO ? 2 : 1];
+  uint32_t b_reg[2][WPT];
+  float s_reg[2], z_reg[2];
+  float xrun = 0.0f;  // the staged row's activation sum over the current group's steps so far
+
+  auto load_global = [&](int kt, auto SLOT) {
+    constexpr int sl = decltype(SLOT)::value;
+    const int64_t k0 = (int64_t)kt * BK;
+    {
+      const int row = tid / CPR, c = tid % CPR;
+      const int64_t m = bm0 + row < M ? bm0 + row : M - 1;
+#pragma unroll
+      for (int h = 0; h < (XLO ? 2 : 1); ++h)
+        a_reg[sl][h] = reinterpret_cast<const u32x4*>(x + m * K + k0 + c * 8)[h];
+    }
+    const int row = tid / PPR, part = tid % PPR;
+    const int64_t n = bn0 + row < N ? bn0 + row : N - 1;
+    const int64_t kc = k0 + part * CPT;
+    const uint32_t* src = wq + n * kwords + kc * BITS / 32;
+    if constexpr (WPT == 1) {
+      b_reg[sl][0] = src[0];
+    } else {
+#pragma unroll
+      for (int q = 0; q < WPT; q += 2) {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(src + q);
+        b_reg[sl][q] = v[0];
+        b_reg[sl][q + 1] = v[1];
+      }
+    }
+    const int64_t g = n * groups + kc / GS;
+    s_reg[sl] = SBLoad<SB>::ld(scales, g);
+    z_reg[sl] = SBLoad<SB>::ld(biases, g);
+  };
+
+  // Step `POS` (its position in its group) from register slot SLOT into LDS buffer buf.
+  auto store_lds = [&](int buf, auto SLOT, auto POS) {
+    constexpr int sl = decltype(SLOT)::value;
+    constexpr int pos = decltype(POS)::value;
+    unsigned char* Ah = smem[buf];
+    unsigned char* Al = smem[buf] + TA;
+    unsigned char* Bc = smem[buf] + 2 * TA;
+    {
+      const int row = tid / CPR, c = tid % CPR;
+      float t = 0.0f;
+      if constexpr (XLO) {
+        u32x4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const u32x4& src = a_reg[sl][e >> 1];
+          const float v0 = __uint_as_float(src[2 * (e & 1)]), v1 = __uint_as_float(src[2 * (e & 1) + 1]);
+          t += v0 + v1;
+          const u32x2 p = split2(v0, v1);
+          hi[e] = p[0];
+          lo[e] = p[1];
+        }
+        *reinterpret_cast<u32x4*>(Ah + swz32<BK>(row, c)) = hi;
+        *reinterpret_cast<u32x4*>(Al + swz32<BK>(row, c)) = lo;
+      } else {
+        const u32x4 v = a_reg[sl][0];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t += __uint_as_float(v[e] << 16) + __uint_as_float(v[e] & 0xffff0000u);
+        *reinterpret_cast<u32x4*>(Ah + swz32<BK>(row, c)) = v;
+      }
+      // the row's sum over this step: its 4 chunks sit in 4 consecutive lanes
+      t += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0xb1, 0xf, 0xf, true));
+      t += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0x4e, 0xf, 0xf, true));
+      xrun = pos == 0 ? t : xrun + t;
+      if constexpr (pos == GSTEP - 1) {
+        if (c == 0) reinterpret_cast<float*>(smem[buf] + OFF_X)[row] = xrun;
+      }
+    }
+    const int row = tid / PPR, part = tid % PPR;
+    const int c0 = part * CPT / 8;  // LDS chunk c holds k [8c, 8c + 8) of the step
+    if constexpr (BITS == 4) {
+      // word q: codes 8q..8q+7 in natural order (low nibble first) -> chunk c0 + q, as bf16(c)
+#pragma unroll
+      for (int q = 0; q < WPT; ++q) {
+        const uint32_t w = b_reg[sl][q];
+        u32x4 cv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          cv[e] = pack_bf16x2((float)((w >> (8 * e)) & 0xfu), (float)((w >> (8 * e + 4)) & 0xfu));
+        *reinterpret_cast<u32x4*>(Bc + swz32<BK>(row, c0 + q)) = cv;
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < WPT / 2; ++p) {
+        u32x4 cv;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t w = b_reg[sl][2 * p + h];
+          cv[2 * h] = pack_bf16x2((float)(w & 0xffu), (float)((w >> 8) & 0xffu));
+          cv[2 * h + 1] = pack_bf16x2((float)((w >> 16) & 0xffu), (float)(w >> 24));
+        }
+        *reinterpret_cast<u32x4*>(Bc + swz32<BK>(row, c0 + p)) = cv;
+      }
+    }
+    if constexpr (pos == GSTEP - 1) {
+      if (part == 0) *reinterpret_cast<f32x2*>(smem[buf] + OFF_SB + row * 8) = f32x2{s_reg[sl], z_reg[sl]};
+    }
+  };
+
+  f32x16 acc[TM][TN], yv[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) yv[i][j][v] = 0.0f;
+
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  const int r32 = lane & 31, half = lane >> 5;
+  // Step products from LDS buffer buf; the first MFMA of a group's first step starts from zero.
+  auto mfma_step = [&](int buf, auto FIRST) {
+    constexpr bool first = decltype(FIRST)::value;
+    const unsigned char* Ah = smem[buf];
+    const unsigned char* Al = smem[buf] + TA;
+    const unsigned char* Bc = smem[buf] + 2 * TA;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int c = kk * 2 + half;
+      bf16x8 ah[TM], al[TM], bc[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        ah[i] = *reinterpret_cast<const bf16x8*>(Ah + swz32<BK>(wm * WM + i * 32 + r32, c));
+        if constexpr (XLO) al[i] = *reinterpret_cast<const bf16x8*>(Al + swz32<BK>(wm * WM + i * 32 + r32, c));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bc[j] = *reinterpret_cast<const bf16x8*>(Bc + swz32<BK>(wn * WN + j * 32 + r32, c));
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          if (first && kk == 0) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bc[j], ah[i], f32x16{}, 0, 0, 0);
+          else acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bc[j], ah[i], acc[i][j], 0, 0, 0);
+        }
+      if constexpr (XLO) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bc[j], al[i], acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+  // y += s * acc + b * X for the group closed by buffer buf's step.  Element v of acc[i][j]:
+  // activation row wm WM + 32 i + r32, weight row wn WN + 32 j + 8 (v >> 2) + 4 half + (v & 3).
+  auto fold = [&](int buf) {
+    const float* sb = reinterpret_cast<const float*>(smem[buf] + OFF_SB);
+    const float* xs = reinterpret_cast<const float*>(smem[buf] + OFF_X);
+    float xg[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) xg[i] = xs[wm * WM + i * 32 + r32];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int n0 = wn * WN + j * 32 + 8 * t + 4 * half;
+        const f32x4 p0 = *reinterpret_cast<const f32x4*>(sb + 2 * n0);
+        const f32x4 p1 = *reinterpret_cast<const f32x4*>(sb + 2 * n0 + 4);
+        const float sv[4] = {p0[0], p0[2], p1[0], p1[2]}, zv[4] = {p0[1], p0[3], p1[1], p1[3]};
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            yv[i][j][4 * t + u] = fmaf(sv[u], acc[i][j][4 * t + u], fmaf(zv[u], xg[i], yv[i][j][4 * t + u]));
+      }
+  };
+  // One group: GSTEP steps, loads two steps ahead (clamped to the last step past the end).
+  auto body = [&](int kt, auto SLOT, auto NSLOT, auto POS) {
+    constexpr int pos = decltype(POS)::value;
+    load_global(kt + 2 < ksteps ? kt + 2 : ksteps - 1, SLOT);
+    mfma_step(kt & 1, std::integral_constant<bool, pos == 0>{});
+    if constexpr (pos == GSTEP - 1) fold(kt & 1);
+    store_lds((kt + 1) & 1, NSLOT, std::integral_constant<int, (pos + 1) % GSTEP>{});
+    __syncthreads();
+  };
+  load_global(0, S0{});
+  load_global(ksteps > 1 ? 1 : 0, S1{});
+  store_lds(0, S0{}, std::integral_constant<int, 0>{});
+  __syncthreads();
+  for (int kt = 0; kt < ksteps; kt += GSTEP) {
+    body(kt, S0{}, S1{}, std::integral_constant<int, 0>{});
+    body(kt + 1, S1{}, S0{}, std::integral_constant<int, 1>{});
+    if constexpr (GSTEP == 4) {
+      body(kt + 2, S0{}, S1{}, std::integral_constant<int, 2>{});
+      body(kt + 3, S1{}, S0{}, std::integral_constant<int, 3>{});
+    }
+  }
+
+  // Epilogue as in qmm_f32_kernel: y + bias in f32, then the activation in f32.
+  const bool vec_ok = (N % 4) == 0;
+  [[maybe_unused]] float bcol[TN][16];
+  if constexpr (EPI) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t n = bn0 + wn * WN + j * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+        const int64_t nc = n < N ? n : N - 1;  // columns past N are never stored
+        bcol[j][v] = epi.bias == nullptr ? 0.0f
+                     : epi.bias_bf16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(epi.bias)[nc])
+                                     : static_cast<const float*>(epi.bias)[nc];
+      }
+  }
+  auto finish = [&](float o, float bv) {
+    if constexpr (EPI) {
+      if (epi.bias) o += bv;
+      if (epi.act == MLXQ_ACT_GELU || epi.act == MLXQ_ACT_GELU_EXACT) o = gelu_erf(o);
+      else if (epi.act == MLXQ_ACT_GELU_TANH) o = gelu_tanh<false>(o);
+    }
+    return o;
+  };
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t m = bm0 + wm * WM + i * 32 + r32;
+    if (m >= M) continue;
+    float* yrow = y + m * N;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int64_t n = bn0 + wn * WN + j * 32 + 8 * a + 4 * half;
+        f32x4 v;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) v[b] = finish(yv[i][j][4 * a + b], EPI ? bcol[j][4 * a + b] : 0.0f);
+        if (vec_ok && n + 3 < N) {
+          *reinterpret_cast<f32x4*>(yrow + n) = v;
+        } else {
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            if (n + b < N) yrow[n + b] = v[b];
+        }
+      }
+    }
+  }
+}
+
 template <typename XT, typename SB, int BITS, int GS>
 static int launch_qmm_f32(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                           const void* b, int64_t N, void* y, const F32Epilogue& epi, hipStream_t st) {
@@ -396,6 +681,15 @@ static int launch_qmm_f32(const void* x, int64_t M, int64_t K, const uint32_t* w
   const int64_t tiles = ((M + kF32BM - 1) / kF32BM) * ((N + BN - 1) / BN);
   if (tiles == 0) return MLXQ_OK;
   if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm_f32: problem too large");
+  if constexpr (GS >= 64) {  // the factored form (codes as the weight operand)
+    if (epi.bias || epi.act != MLXQ_ACT_NONE)
+      hipLaunchKernelGGL((qmm_f32c_kernel<XT, SB, BITS, GS, true>), dim3((unsigned)tiles), dim3(WAVES * 64), 0,
+                         st, (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (float*)y, epi);
+    else
+      hipLaunchKernelGGL((qmm_f32c_kernel<XT, SB, BITS, GS, false>), dim3((unsigned)tiles), dim3(WAVES * 64), 0,
+                         st, (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (float*)y, epi);
+    return check_launch("qmm_f32");
+  }
   if (epi.bias || epi.act != MLXQ_ACT_NONE)
     hipLaunchKernelGGL((qmm_f32_kernel<XT, SB, BITS, GS, WAVES, BN, BK, true>), dim3((unsigned)tiles),
                        dim3(WAVES * 64), 0, st, (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N,
