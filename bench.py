@@ -14,7 +14,7 @@ Also reported (same JSON line):
   quantize     config 3 quantize pass (4 x [5120,5120] bf16 -> Q8 g64): GB/s;
   config1/3/5  the other BASELINE configs (quantize/dequantize/qmm, the Q8 projection, the LoRA sweep);
   experts      the stacked-expert MoE projections (one launch vs one linear per expert);
-  f32_mlp      config 2 on FLUX.1's f32 stream (f32 x and h, split-bf16 matrix-core GEMM);
+  f32_mlp      config 2 on FLUX.1's f32 stream (f32 x and h, f32 matrix-core GEMM on split bf16);
   dense_bf16_reference  context only: the library dense bf16 GEMM (torch.mm) on the same shapes;
   cpu_baseline the CPU oracle (fp64-accumulating C restatement, OpenMP) on a bounded row sample of
                the same up-projection, scaled to TFLOP/s.
@@ -267,8 +267,9 @@ def graph_ms(torch, fn, inner=8, reps=5):
 def bench_f32_mlp(mlxq, torch):
     """Config 2's MLP on FLUX.1's f32 residual stream (mlx-gen-flux/src/model.rs:407-410): f32 x
     [4608,3072] through the Q4-g64 up projection with mlx_rs::nn::gelu (f32), then the f32 h through
-    the down projection.  Both products are f32 (MLX's promotion) and run on the split-bf16 GEMM:
-    three bf16 MFMA passes per product, so its MFMA work is 3x the algorithmic flops."""
+    the down projection.  Both products are f32 (MLX's promotion) and run on the factored f32 GEMM
+    (group size 64): the codes as exact bf16 operands against the two-term split of x, two bf16
+    MFMA passes per product, so its MFMA work is 2x the algorithmic flops."""
     dev = torch.device("cuda:0")
     M, K, F = 4608, 3072, 12288
     x = gen_bf16((M, K), 1.0, 900, dev).float()
@@ -286,8 +287,9 @@ def bench_f32_mlp(mlxq, torch):
             "up_TFLOPs": round(flop / (t_up * 1e-3) / 1e12, 1),
             "down_TFLOPs": round(flop / (t_dn * 1e-3) / 1e12, 1),
             "TFLOPs": round(tf, 1), "frac_of_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 3),
-            "bf16_mfma_frac": round(3 * tf / MFMA_BF16_PEAK_TFLOPS, 4),
-            "note": "f32 x and h; bias and GELU fused into the up GEMM epilogue"}
+            "bf16_mfma_frac": round(2 * tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "note": "f32 x and h; bias and GELU fused into the up GEMM epilogue; two bf16 MFMA "
+                    "passes per product (bf16_mfma_frac counts both)"}
 
 
 def bench_dense_reference(torch):

@@ -13,7 +13,9 @@
 // the result is within ~1e-5 relative (Frobenius) of the f32 product, against ~1e-3 for a plain
 // bf16 product.  With bf16 activations (f32 scales) x_lo is zero and the third pass is skipped.
 // Weights are dequantized exactly as fma(code, scale, bias) in f32 (scale and bias widened
-// exactly from bf16), then split.
+// exactly from bf16), then split.  That three-pass kernel serves group size 32 and the LoKr dense
+// product; group sizes 64 and 128 take the factored kernel further down (qmm_f32c_kernel: the
+// codes themselves as exact bf16 operands, two passes for f32 x).
 //
 // Structure: a workgroup of 8 waves (2 x 4, 64 x 64 each) per 128 x 256 output tile (the LoKr
 // dense product: 4 waves, 2 x 2, per 128 x 128 tile), K advanced BK = 32 at a time through a
