@@ -1,5 +1,9 @@
 // qmv_mfma.hip — decode GEMV y[M,N] = x[M,K] . W^T for M <= 8 on gfx950 matrix cores.
 //
+// Two kernels: the 16-row tile kernel described here (M = 2..8, Q8, and K not a multiple of
+// 1024), and, further down, the one-row kernel that serves M = 1 with Q4 codes (one weight row per
+// wave, no split-K reduction).  Both compute the same exact-f32 factored form.
+//
 // The path is HBM-bound and small (a few MB per call), so the kernel is built around the load
 // shape the memory system streams best and around latency: every 16-byte weight load a wave
 // needs is issued up front, each load covers 16 rows x 64 contiguous bytes (4 lanes per row), the
