@@ -396,7 +396,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
 // unrolled by the group's GS/32 steps, so group starts and ends are compile-time positions.
 // Tiles, waves, buffers and the load pipeline are those of qmm_f32_kernel (128 x 256, 8 waves of
 // 64 x 64, 32-deep K steps, loads two steps ahead).
-template <typename XT, typename SB, int BITS, int GS, bool EPI>
+template <typename XT, typename SB, int BITS, int GS, bool EPI, bool BMF>
 __global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x, int64_t M, int64_t K,
                                                    const uint32_t* __restrict__ wq,
                                                    const SB* __restrict__ scales,
@@ -418,6 +418,14 @@ __global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x,
   // Per buffer: x_hi, x_lo, codes, then the (s, b) pairs of the tile's weight rows and the
   // activation sums of its rows for the group the buffer's step closes.
   __shared__ __attribute__((aligned(16))) unsigned char smem[2][BUF];
+  // BMF (bf16 scales, K / GS a multiple of 16): the bias term b.X goes to the matrix cores, 16
+  // groups at a time: each group's bf16 biases per weight row and hi/lo split activation sums per
+  // activation row wait in 16-group tables (rows of 32 bytes), and every 16th group adds
+  // b[n, g..g+15] . X[g..g+15, m] into y with one MFMA pair per block.  The per-group fold is then
+  // one FMA per output, y += s * acc.
+  constexpr int BT = BN * 32, XT_ = BM * 32;
+  static_assert(!BMF || std::is_same<SB, uint16_t>::value, "bias MFMA needs bf16 biases (exact bf16 operands)");
+  __shared__ __attribute__((aligned(16))) unsigned char btab[BMF ? BT + 2 * XT_ : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -466,8 +474,8 @@ __global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x,
     z_reg[sl] = SBLoad<SB>::ld(biases, g);
   };
 
-  // Step `POS` (its position in its group) from register slot SLOT into LDS buffer buf.
-  auto store_lds = [&](int buf, auto SLOT, auto POS) {
+  // Step `POS` (its position in its group `grp`) from register slot SLOT into LDS buffer buf.
+  auto store_lds = [&](int buf, auto SLOT, auto POS, int grp) {
     constexpr int sl = decltype(SLOT)::value;
     constexpr int pos = decltype(POS)::value;
     unsigned char* Ah = smem[buf];
@@ -500,7 +508,15 @@ __global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x,
       t += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0x4e, 0xf, 0xf, true));
       xrun = pos == 0 ? t : xrun + t;
       if constexpr (pos == GSTEP - 1) {
-        if (c == 0) reinterpret_cast<float*>(smem[buf] + OFF_X)[row] = xrun;
+        if (c == 0) {
+          reinterpret_cast<float*>(smem[buf] + OFF_X)[row] = xrun;
+          if constexpr (BMF) {
+            const uint16_t hb = f32_to_bf16_bits(xrun);
+            const uint16_t lb = f32_to_bf16_bits(xrun - bf16_bits_to_f32(hb));
+            reinterpret_cast<uint16_t*>(btab + BT)[row * 16 + (grp & 15)] = hb;
+            reinterpret_cast<uint16_t*>(btab + BT + XT_)[row * 16 + (grp & 15)] = lb;
+          }
+        }
       }
     }
     const int row = tid / PPR, part = tid % PPR;
@@ -530,7 +546,11 @@ __global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x,
       }
     }
     if constexpr (pos == GSTEP - 1) {
-      if (part == 0) *reinterpret_cast<f32x2*>(smem[buf] + OFF_SB + row * 8) = f32x2{s_reg[sl], z_reg[sl]};
+      if (part == 0) {
+        *reinterpret_cast<f32x2*>(smem[buf] + OFF_SB + row * 8) = f32x2{s_reg[sl], z_reg[sl]};
+        if constexpr (BMF)
+          reinterpret_cast<uint16_t*>(btab)[row * 16 + (grp & 15)] = (uint16_t)(__float_as_uint(z_reg[sl]) >> 16);
+      }
     }
   };
 
@@ -579,12 +599,14 @@ __global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x,
   };
   // y += s * acc + b * X for the group closed by buffer buf's step.  Element v of acc[i][j]:
   // activation row wm WM + 32 i + r32, weight row wn WN + 32 j + 8 (v >> 2) + 4 half + (v & 3).
-  auto fold = [&](int buf) {
+  auto fold = [&](int buf, int grp) {
     const float* sb = reinterpret_cast<const float*>(smem[buf] + OFF_SB);
     const float* xs = reinterpret_cast<const float*>(smem[buf] + OFF_X);
     float xg[TM];
+    if constexpr (!BMF) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) xg[i] = xs[wm * WM + i * 32 + r32];
+      for (int i = 0; i < TM; ++i) xg[i] = xs[wm * WM + i * 32 + r32];
+    }
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -596,22 +618,45 @@ __global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x,
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int u = 0; u < 4; ++u)
-            yv[i][j][4 * t + u] = fmaf(sv[u], acc[i][j][4 * t + u], fmaf(zv[u], xg[i], yv[i][j][4 * t + u]));
+          for (int u = 0; u < 4; ++u) {
+            if constexpr (BMF) yv[i][j][4 * t + u] = fmaf(sv[u], acc[i][j][4 * t + u], yv[i][j][4 * t + u]);
+            else yv[i][j][4 * t + u] = fmaf(sv[u], acc[i][j][4 * t + u], fmaf(zv[u], xg[i], yv[i][j][4 * t + u]));
+          }
       }
+    if constexpr (BMF) {
+      if ((grp & 15) == 15) {  // the 16-group batch is complete: y += b . X on the matrix cores
+        const unsigned char* bt = btab;
+        const unsigned char* xh = btab + BT;
+        const unsigned char* xl = btab + BT + XT_;
+        bf16x8 bf[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(bt + (wn * WN + j * 32 + r32) * 32 + half * 16);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int rr = (wm * WM + i * 32 + r32) * 32 + half * 16;
+          const bf16x8 ah = *reinterpret_cast<const bf16x8*>(xh + rr);
+          const bf16x8 al = *reinterpret_cast<const bf16x8*>(xl + rr);
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            yv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j], ah, yv[i][j], 0, 0, 0);
+            yv[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j], al, yv[i][j], 0, 0, 0);
+          }
+        }
+      }
+    }
   };
   // One group: GSTEP steps, loads two steps ahead (clamped to the last step past the end).
   auto body = [&](int kt, auto SLOT, auto NSLOT, auto POS) {
     constexpr int pos = decltype(POS)::value;
     load_global(kt + 2 < ksteps ? kt + 2 : ksteps - 1, SLOT);
     mfma_step(kt & 1, std::integral_constant<bool, pos == 0>{});
-    if constexpr (pos == GSTEP - 1) fold(kt & 1);
-    store_lds((kt + 1) & 1, NSLOT, std::integral_constant<int, (pos + 1) % GSTEP>{});
+    if constexpr (pos == GSTEP - 1) fold(kt & 1, kt / GSTEP);
+    store_lds((kt + 1) & 1, NSLOT, std::integral_constant<int, (pos + 1) % GSTEP>{}, (kt + 1) / GSTEP);
     __syncthreads();
   };
   load_global(0, S0{});
   load_global(ksteps > 1 ? 1 : 0, S1{});
-  store_lds(0, S0{}, std::integral_constant<int, 0>{});
+  store_lds(0, S0{}, std::integral_constant<int, 0>{}, 0);
   __syncthreads();
   for (int kt = 0; kt < ksteps; kt += GSTEP) {
     body(kt, S0{}, S1{}, std::integral_constant<int, 0>{});
@@ -684,12 +729,21 @@ static int launch_qmm_f32(const void* x, int64_t M, int64_t K, const uint32_t* w
   if (tiles == 0) return MLXQ_OK;
   if (tiles > 0x7fffffff) return set_error(MLXQ_EINVAL, "qmm_f32: problem too large");
   if constexpr (GS >= 64) {  // the factored form (codes as the weight operand)
-    if (epi.bias || epi.act != MLXQ_ACT_NONE)
-      hipLaunchKernelGGL((qmm_f32c_kernel<XT, SB, BITS, GS, true>), dim3((unsigned)tiles), dim3(WAVES * 64), 0,
-                         st, (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (float*)y, epi);
-    else
-      hipLaunchKernelGGL((qmm_f32c_kernel<XT, SB, BITS, GS, false>), dim3((unsigned)tiles), dim3(WAVES * 64), 0,
-                         st, (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (float*)y, epi);
+    const bool epi_on = epi.bias || epi.act != MLXQ_ACT_NONE;
+    const bool bmf = std::is_same<SB, uint16_t>::value && (K / GS) % 16 == 0;
+#define MLXQ_F32C(E, B)                                                                                 \
+  hipLaunchKernelGGL((qmm_f32c_kernel<XT, SB, BITS, GS, E, B>), dim3((unsigned)tiles), dim3(WAVES * 64), 0, st, \
+                     (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (float*)y, epi)
+    if constexpr (std::is_same<SB, uint16_t>::value) {
+      if (bmf) {
+        if (epi_on) MLXQ_F32C(true, true);
+        else MLXQ_F32C(false, true);
+        return check_launch("qmm_f32");
+      }
+    }
+    if (epi_on) MLXQ_F32C(true, false);
+    else MLXQ_F32C(false, false);
+#undef MLXQ_F32C
     return check_launch("qmm_f32");
   }
   if (epi.bias || epi.act != MLXQ_ACT_NONE)
