@@ -392,7 +392,8 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
 // dequantization or weight split.  Each group's product accumulates in `acc` (the first MFMA of a
 // group starts from zero) and is folded into the running f32 sum y by two FMAs per output with the
 // group's scale and bias (one per weight row) and activation sum (one per activation row), which
-// the staging threads leave in two small LDS tables next to the step's tiles.  The loop is
+// the staging threads leave in two small LDS tables next to the step's tiles (with bf16 scales and
+// K / GS a multiple of 16, one FMA: the bias term runs on the matrix cores, see BMF).  The loop is
 // unrolled by the group's GS/32 steps, so group starts and ends are compile-time positions.
 // Tiles, waves, buffers and the load pipeline are those of qmm_f32_kernel (128 x 256, 8 waves of
 // 64 x 64, 32-deep K steps, loads two steps ahead).
