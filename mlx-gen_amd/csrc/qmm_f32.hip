@@ -397,25 +397,26 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
 // unrolled by the group's GS/32 steps, so group starts and ends are compile-time positions.
 // Tiles, waves, buffers and the load pipeline are those of qmm_f32_kernel (128 x 256, 8 waves of
 // 64 x 64, 32-deep K steps, loads two steps ahead).
-template <typename XT, typename SB, int BITS, int GS, bool EPI, bool BMF>
-__global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x, int64_t M, int64_t K,
+template <typename XT, typename SB, int BITS, int GS, bool EPI, bool BMF, int WAVES, int BN>
+__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void qmm_f32c_kernel(const XT* __restrict__ x, int64_t M, int64_t K,
                                                    const uint32_t* __restrict__ wq,
                                                    const SB* __restrict__ scales,
                                                    const SB* __restrict__ biases, int64_t N,
                                                    float* __restrict__ y, F32Epilogue epi) {
   constexpr bool XLO = std::is_same<XT, float>::value;  // activations carry a low part
-  constexpr int WAVES = 8, BN = 256, BK = 32;
+  constexpr int BK = 32;
   constexpr int BM = kF32BM, NT = WAVES * 64;
   constexpr int WGN = WAVES / 2;
   constexpr int WM = BM / 2, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
   constexpr int CPR = BK / 8;                // 16-byte bf16 chunks per tile row
+  constexpr int A_LD = BM * CPR / NT;        // activation chunks per thread per step (1 or 2)
   constexpr int CPT = BN * BK / NT;          // codes per thread per step (16)
   constexpr int WPT = CPT * BITS / 32;       // their packed words
   constexpr int PPR = BK / CPT;              // threads per weight row (2)
   constexpr int GSTEP = GS / BK;             // steps per group (2 or 4)
   constexpr int TA = BM * BK * 2, TB = BN * BK * 2;
   constexpr int OFF_SB = 2 * TA + TB, OFF_X = OFF_SB + BN * 8, BUF = OFF_X + BM * 4;
-  static_assert(BM * CPR == NT && GSTEP >= 2 && GSTEP % 2 == 0 && WPT >= 1, "tile shape");
+  static_assert(A_LD * NT == BM * CPR && CPT == 16 && GSTEP >= 2 && GSTEP % 2 == 0 && WPT >= 1, "tile shape");
   // Per buffer: x_hi, x_lo, codes, then the (s, b) pairs of the tile's weight rows and the
   // activation sums of its rows for the group the buffer's step closes.
   __shared__ __attribute__((aligned(16))) unsigned char smem[2][BUF];
@@ -439,22 +440,25 @@ __global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x,
   const int64_t groups = K / GS;
   const int ksteps = (int)(K / BK);  // a multiple of GSTEP (K % GS == 0)
 
-  // Staging registers, two slots (see qmm_f32_kernel): thread tid stages activation row tid / 4,
-  // chunk tid % 4, and codes CPT of weight row tid / 2 with that row's scale and bias.
-  u32x4 a_reg[2][XLO ? 2 : 1];
+  // Staging registers, two slots (see qmm_f32_kernel): thread tid stages activation chunks
+  // id = tid + NT i (row id / 4, chunk id % 4), and codes CPT of weight row tid / 2 with that row's
+  // scale and bias.
+  u32x4 a_reg[2][A_LD][XLO ? 2 : 1];
   uint32_t b_reg[2][WPT];
   float s_reg[2], z_reg[2];
-  float xrun = 0.0f;  // the staged row's activation sum over the current group's steps so far
+  float xrun[A_LD];  // each staged row's activation sum over the current group's steps so far
 
   auto load_global = [&](int kt, auto SLOT) {
     constexpr int sl = decltype(SLOT)::value;
     const int64_t k0 = (int64_t)kt * BK;
-    {
-      const int row = tid / CPR, c = tid % CPR;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int id = tid + NT * i;
+      const int row = id / CPR, c = id % CPR;
       const int64_t m = bm0 + row < M ? bm0 + row : M - 1;
 #pragma unroll
       for (int h = 0; h < (XLO ? 2 : 1); ++h)
-        a_reg[sl][h] = reinterpret_cast<const u32x4*>(x + m * K + k0 + c * 8)[h];
+        a_reg[sl][i][h] = reinterpret_cast<const u32x4*>(x + m * K + k0 + c * 8)[h];
     }
     const int row = tid / PPR, part = tid % PPR;
     const int64_t n = bn0 + row < N ? bn0 + row : N - 1;
@@ -482,14 +486,16 @@ __global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x,
     unsigned char* Ah = smem[buf];
     unsigned char* Al = smem[buf] + TA;
     unsigned char* Bc = smem[buf] + 2 * TA;
-    {
-      const int row = tid / CPR, c = tid % CPR;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int id = tid + NT * i;
+      const int row = id / CPR, c = id % CPR;
       float t = 0.0f;
       if constexpr (XLO) {
         u32x4 hi, lo;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const u32x4& src = a_reg[sl][e >> 1];
+          const u32x4& src = a_reg[sl][i][e >> 1];
           const float v0 = __uint_as_float(src[2 * (e & 1)]), v1 = __uint_as_float(src[2 * (e & 1) + 1]);
           t += v0 + v1;
           const u32x2 p = split2(v0, v1);
@@ -499,7 +505,7 @@ __global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x,
         *reinterpret_cast<u32x4*>(Ah + swz32<BK>(row, c)) = hi;
         *reinterpret_cast<u32x4*>(Al + swz32<BK>(row, c)) = lo;
       } else {
-        const u32x4 v = a_reg[sl][0];
+        const u32x4 v = a_reg[sl][i][0];
 #pragma unroll
         for (int e = 0; e < 4; ++e) t += __uint_as_float(v[e] << 16) + __uint_as_float(v[e] & 0xffff0000u);
         *reinterpret_cast<u32x4*>(Ah + swz32<BK>(row, c)) = v;
@@ -507,13 +513,13 @@ __global__ __launch_bounds__(512) void qmm_f32c_kernel(const XT* __restrict__ x,
       // the row's sum over this step: its 4 chunks sit in 4 consecutive lanes
       t += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0xb1, 0xf, 0xf, true));
       t += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0x4e, 0xf, 0xf, true));
-      xrun = pos == 0 ? t : xrun + t;
+      xrun[i] = pos == 0 ? t : xrun[i] + t;
       if constexpr (pos == GSTEP - 1) {
         if (c == 0) {
-          reinterpret_cast<float*>(smem[buf] + OFF_X)[row] = xrun;
+          reinterpret_cast<float*>(smem[buf] + OFF_X)[row] = xrun[i];
           if constexpr (BMF) {
-            const uint16_t hb = f32_to_bf16_bits(xrun);
-            const uint16_t lb = f32_to_bf16_bits(xrun - bf16_bits_to_f32(hb));
+            const uint16_t hb = f32_to_bf16_bits(xrun[i]);
+            const uint16_t lb = f32_to_bf16_bits(xrun[i] - bf16_bits_to_f32(hb));
             reinterpret_cast<uint16_t*>(btab + BT)[row * 16 + (grp & 15)] = hb;
             reinterpret_cast<uint16_t*>(btab + BT + XT_)[row * 16 + (grp & 15)] = lb;
           }
@@ -732,8 +738,13 @@ static int launch_qmm_f32(const void* x, int64_t M, int64_t K, const uint32_t* w
   if constexpr (GS >= 64) {  // the factored form (codes as the weight operand)
     const bool epi_on = epi.bias || epi.act != MLXQ_ACT_NONE;
     const bool bmf = std::is_same<SB, uint16_t>::value && (K / GS) % 16 == 0;
+    // 8 waves on 128 x 256 tiles, as the three-pass kernel.  4 waves on 128 x 128 (two workgroups
+    // per CU, so the two waves of a SIMD fold at different times) measured slower on the FLUX
+    // shapes (same box: up 0.850 -> 0.926 ms, down 0.948 -> 1.020 ms).
+    constexpr int CW = 8, CBN = 256;
+    const int64_t ctiles = ((M + kF32BM - 1) / kF32BM) * ((N + CBN - 1) / CBN);
 #define MLXQ_F32C(E, B)                                                                                 \
-  hipLaunchKernelGGL((qmm_f32c_kernel<XT, SB, BITS, GS, E, B>), dim3((unsigned)tiles), dim3(WAVES * 64), 0, st, \
+  hipLaunchKernelGGL((qmm_f32c_kernel<XT, SB, BITS, GS, E, B, CW, CBN>), dim3((unsigned)ctiles), dim3(CW * 64), 0, st, \
                      (const XT*)x, M, K, wq, (const SB*)s, (const SB*)b, N, (float*)y, epi)
     if constexpr (std::is_same<SB, uint16_t>::value) {
       if (bmf) {
