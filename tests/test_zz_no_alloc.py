@@ -3,8 +3,9 @@ caller workspace, through the C ABI.
 
 Both entry points run the same kernels, so outputs must be bit-identical.  Two calls in a row on
 the scratch array, the second with a smaller problem (stale contents of the first call must not
-leak into it), on the fused GEMM epilogue (M > 8, rank <= 16), the GEMV path (M <= 8) and a wide
-adapter (rank 24: plain GEMM + elementwise epilogue).  A problem needing more scratch than the
+leak into it), on the fused GEMM epilogue (M > 8, rank <= 16), the GEMV paths (the 16-row tile
+kernel at M = 5, the one-row kernel at M = 1) and a wide adapter (rank 24: plain GEMM +
+elementwise epilogue).  A problem needing more scratch than the
 array holds is rejected before any device work.
 """
 import ctypes
@@ -64,6 +65,7 @@ def _run(mlxq, c, noalloc, scale, act):
     ((600, 1024, 2304, 16), (300, 512, 520, 16)),   # fused GEMM epilogue twice
     ((256, 512, 1040, 24), (40, 256, 136, 8)),      # rank 24 elementwise, then rank 8 fused
     ((300, 512, 1000, 16), (5, 512, 264, 16)),      # GEMM, then the GEMV path
+    ((1, 2048, 520, 16), (1, 1024, 264, 16)),       # the one-row GEMV path (M = 1) twice
 ])
 def test_noalloc_matches_workspace_entry_point(mlxq, first, second):
     rng = np.random.default_rng(sum(first) + sum(second))
