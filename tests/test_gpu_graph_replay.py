@@ -1,5 +1,6 @@
 """The hot-path entry points captured in a HIP graph (as a serving loop or the bench runs them):
-every replay must reproduce the eager outputs bit for bit.
+every replay must reproduce the eager outputs bit for bit; and run from two streams at once, each
+stream's outputs must equal what it computes alone (no shared mutable device state).
 
 Captured: the M = 1 decode MLP (SwiGLU launch + down GEMV, the one-row kernel), a wide-GEMM
 linear with bias and the exact GELU, the f32 GEMM with its matrix-core bias term, and a quantize.
@@ -83,3 +84,34 @@ def test_graph_replays_match_eager(mlxq):
             assert torch.equal(o, e), f"replay {rep}: {name} differs from the eager result"
         print(f"    replay {rep}: all {len(outs)} outputs bit-identical", flush=True)
     del graph
+
+
+def test_two_streams_at_once_match_sequential(mlxq):
+    """Re-entrancy per stream: two streams running different decode MLPs, wide GELU linears and f32
+    GEMMs at the same time (each stream on its own weights, its launches interleaved with the
+    other's) produce what each produces alone."""
+    banner("two streams at once")
+    a, b = _inputs(mlxq), _inputs(mlxq)
+    rng = np.random.default_rng(7)
+    b["x1"] = to_gpu(bf16_normal(rng, (1, 3072)))
+    b["xw"] = to_gpu(bf16_normal(rng, (1024, 3072)))
+    b["xf"] = to_gpu(rng.standard_normal((256, 3072)).astype(np.float32), torch.float32)
+    ref_a = [t.clone() for t in _run(mlxq, a)]
+    ref_b = [t.clone() for t in _run(mlxq, b)]
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    sa.wait_stream(torch.cuda.current_stream())
+    sb.wait_stream(torch.cuda.current_stream())
+    outs_a, outs_b = [], []
+    for _ in range(3):
+        with torch.cuda.stream(sa):
+            outs_a.append(_run(mlxq, a))
+        with torch.cuda.stream(sb):
+            outs_b.append(_run(mlxq, b))
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for o, e in zip(outs_a[rep], ref_a):
+            assert torch.equal(o, e), f"stream a, round {rep}"
+        for o, e in zip(outs_b[rep], ref_b):
+            assert torch.equal(o, e), f"stream b, round {rep}"
+    print("    both streams bit-identical to their sequential results", flush=True)
