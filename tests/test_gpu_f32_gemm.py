@@ -32,7 +32,8 @@ def _tdt(name):
 # (M, N, K, gs, bits, x dtype, scales dtype): ragged M and N (N % 4 != 0), every group size,
 # Q4 and Q8, f32 or bf16 scales, bf16 x against f32 scales, the M = 9 boundary.  Group sizes 64
 # and 128 run the factored kernel; with bf16 scales and K / gs a multiple of 16 its bias term goes
-# through the batched MFMA (the last three cases: one, three and two 16-group batches).
+# through the batched MFMA (the last four cases: one, three, two and one 16-group batches, the
+# last at the M = 9 boundary).
 CASES = [
     (200, 198, 512, 64, 4, "f32", "bf16"),
     (130, 264, 1024, 32, 8, "f32", "f32"),
@@ -43,6 +44,7 @@ CASES = [
     (200, 262, 1024, 64, 4, "f32", "bf16"),
     (137, 300, 3072, 64, 8, "f32", "bf16"),
     (260, 520, 4096, 128, 4, "f32", "bf16"),
+    (9, 100, 1024, 64, 4, "f32", "bf16"),
 ]
 
 
