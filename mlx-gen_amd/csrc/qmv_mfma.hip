@@ -761,7 +761,7 @@ static int64_t gemv_cus() {
 }
 
 // Waves (rows) per one-row workgroup.  SwiGLU (two rows per wave): 8, i.e. the staging barrier
-// among fewer waves (K = 3072, F = 8192: 7.7 -> 7.1 us against 16 waves; 4 was no better).
+// among fewer waves (K = 3072, F = 8192: 7.7 -> 7.1 us against 16 waves; 4 measured slower).
 // One matrix: the largest of 16, 12, 8 whose workgroup count is a multiple of the CU count
 // (N = 3072: 12 -> 256 workgroups, 5.1 us against 5.5 at 8 and 5.9 at 16; N = 8192: 16), else 16.
 static int qmv_row_wpb(int64_t N, int nmat) {
