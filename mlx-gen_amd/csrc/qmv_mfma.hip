@@ -763,13 +763,17 @@ static int64_t gemv_cus() {
 // Waves (rows) per one-row workgroup.  SwiGLU (two rows per wave): 8, i.e. the staging barrier
 // among fewer waves (K = 3072, F = 8192: 7.7 -> 7.1 us against 16 waves; 4 measured slower).
 // One matrix: the largest of 16, 12, 8 whose workgroup count is a multiple of the CU count
-// (N = 3072: 12 -> 256 workgroups, 5.1 us against 5.5 at 8 and 5.9 at 16; N = 8192: 16), else 16.
+// (N = 3072: 12 -> 256 workgroups, 5.1 us against 5.5 at 8 and 5.9 at 16; N = 8192: 16); else
+// the largest that still gives every CU a workgroup; else 8, the most workgroups (N = 1536,
+// K = 16384: 16 rows left 96 workgroups on 256 CUs).
 static int qmv_row_wpb(int64_t N, int nmat) {
   if (nmat == 2) return 8;
   const int64_t cus = gemv_cus();
   for (int w : {16, 12, 8})
     if (((N + w - 1) / w) % cus == 0) return w;
-  return 16;
+  for (int w : {16, 12, 8})
+    if ((N + w - 1) / w >= cus) return w;
+  return 8;
 }
 
 template <bool G64, int LS, int NMAT>
