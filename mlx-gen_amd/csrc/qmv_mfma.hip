@@ -34,6 +34,7 @@
 // activation rows are permuted to match with v_perm_b32 as they are copied into LDS.
 #include <atomic>
 #include <type_traits>
+#include <utility>
 
 #include "mlxq_common.h"
 
@@ -419,16 +420,25 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
 // (v_mfma_f32_16x16x32_bf16) whose B column n is column n's 64 codes.  The A operand's row m is
 // the activation run of column m (16 different K slices of the one activation row), so the
 // product's diagonal C[n][n] is column n's dot product sum x*(128+c), and the off-diagonal
-// entries are discarded.  C[n][n] sits in lane n + 16 (n >> 2), register n & 3: 16 lanes of the
+// entries are discarded.  A row of K codes takes LS = ceil(K / 1024) loads; when K is not a
+// multiple of 1024 the last load's upper columns reach into the next row (or past the buffer end,
+// where the loads return zero), and those columns fold exactly zero: their staged activations,
+// activation sums and (s, b - 128 s) table entries are all zero.  C[n][n] sits in lane n + 16 (n >> 2), register n & 3: 16 lanes of the
 // wave fold one column each per load,
 //   y += s*C[n][n] + (b - 128 s)*X[column],
 // with X the column's activation sum (computed once per workgroup while staging).  The wave's
 // 16 partial sums are added at the end with row shifts and lane reads.
 constexpr int kRowColPitch = 144;  // LDS bytes per 64-element activation column (128 + pad)
 
-// Whether the one-row kernel takes a problem (bf16 x and scales are checked by the caller).
-__host__ __device__ constexpr bool qmv_row_fits(int64_t M, int64_t K, int gs, int bits) {
-  return M == 1 && bits == 4 && (gs == 64 || gs == 128) && K % 1024 == 0 && K >= 1024 && K <= 16384;
+// Loads per row (K <= 1024 times this): 32 for one matrix, 16 for the SwiGLU pair, whose wave
+// holds two rows' codes in registers.
+constexpr int kRowMaxLoads[2] = {32, 16};
+
+// Whether the one-row kernel takes a problem (bf16 x and scales are checked by the caller): the
+// group count per row must be even (scales and biases are read as group pairs, 4-byte aligned).
+__host__ __device__ constexpr bool qmv_row_fits(int64_t M, int64_t K, int gs, int bits, int nmat) {
+  return M == 1 && bits == 4 && (gs == 64 || gs == 128) && K % (2 * gs) == 0 && K >= 1024 &&
+         K <= 1024 * kRowMaxLoads[nmat - 1];
 }
 
 // LDS bytes of a one-row workgroup: the activation columns, their sums and each wave's (s, zc)
@@ -442,24 +452,24 @@ __device__ __forceinline__ float dpp_f32(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
 }
 
-// Contract (checked on the host by qmv_row_plan): M = 1, K = 1024 LS, bf16 x/scales/biases, Q4
-// codes, group 64 or 128, 8..16 waves per workgroup, dynamic LDS of qmv_row_lds bytes, every
-// buffer < 2 GiB.  NMAT = 2: wave f streams gate row f and up row f and writes
+// Contract (checked on the host by qmv_row_fits): M = 1, 1024 (LS - 1) < K <= 1024 LS, an even
+// number of groups per row, bf16 x/scales/biases, Q4 codes, group 64 or 128, 8..16 waves per
+// workgroup, dynamic LDS of qmv_row_lds bytes, every buffer < 2 GiB.  NMAT = 2: wave f streams gate row f and up row f and writes
 // round(round(silu(round(g))) * round(u)) (qwen3.rs:178-181); else round(y).
 template <bool G64, int LS, int NMAT>
 __global__ __launch_bounds__(1024) void qmv_row_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint32_t* __restrict__ wq2,
-    const uint16_t* __restrict__ scales2, const uint16_t* __restrict__ biases2, int N,
+    const uint16_t* __restrict__ scales2, const uint16_t* __restrict__ biases2, int K, int N,
     uint16_t* __restrict__ y) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  constexpr int K = 1024 * LS;
-  constexpr int C = 16 * LS;                  // 64-code columns per row
-  constexpr int G = G64 ? C : C / 2;          // groups per row
-  constexpr int RB = 512 * LS;                // bytes per packed row
-  constexpr int XCH = 128 * LS;               // 16-byte activation chunks
+  constexpr int C = 16 * LS;                  // 64-code columns per row, padded to whole loads
+  constexpr int G = G64 ? C : C / 2;          // groups per padded row (table entries)
+  constexpr int XCH = 128 * LS;               // 16-byte activation chunks of the padded row
   constexpr int XPT = (XCH + 511) / 512;      // ... per thread (at least 8 waves)
   constexpr int SBPL = (G + 127) / 128;       // scale/bias word pairs per lane
+  const int Gr = K / (G64 ? 64 : 128);        // groups per row
+  const uint32_t RB = (uint32_t)K / 2u;       // bytes per packed row
   const int NT = blockDim.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -470,7 +480,8 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
   float* xsum = reinterpret_cast<float*>(lds + C * kRowColPitch);
   float* tab = xsum + C + wave * NMAT * G * 2;
 
-  // Operand loads first (they queue ahead of the weight streams), then every weight load.
+  // Operand loads first (they queue ahead of the weight streams), then every weight load.  The
+  // activation chunks past K read as zeros (past the resource's end).
   const auto rx = make_rsrc(x, K * 2);
   u32x4 cx[XPT];
 #pragma unroll
@@ -478,7 +489,7 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
     const int ch = tid + j * NT;
     cx[j] = load16(rx, ch < XCH ? (uint32_t)ch * 16u : kOob);
   }
-  const int sb_bytes = (int)((uint32_t)N * (uint32_t)G * 2u);
+  const int sb_bytes = (int)((uint32_t)N * (uint32_t)Gr * 2u);
   uint32_t cs[NMAT][SBPL], cb[NMAT][SBPL];
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat) {
@@ -487,7 +498,7 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
 #pragma unroll
     for (int i = 0; i < SBPL; ++i) {
       const int g0 = 2 * lane + 128 * i;
-      const uint32_t off = g0 < G ? ((uint32_t)r * (uint32_t)G + (uint32_t)g0) * 2u : kOob;
+      const uint32_t off = g0 < Gr ? ((uint32_t)r * (uint32_t)Gr + (uint32_t)g0) * 2u : kOob;
       cs[mat][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
       cb[mat][i] = __builtin_amdgcn_raw_buffer_load_b32(rz, off, 0, 0);
     }
@@ -499,14 +510,14 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
   // arrive together.
   u32x2 wv[NMAT][LS];
   const uint32_t lo = 32u * (uint32_t)(lane & 15) + 8u * (uint32_t)(lane >> 4);
-  const int w_bytes = (int)((uint32_t)N * (uint32_t)RB);
+  const int w_bytes = (int)((uint32_t)N * RB);
   const __amdgpu_buffer_rsrc_t rw[2] = {make_rsrc(wq, w_bytes), make_rsrc(NMAT == 2 ? wq2 : wq, w_bytes)};
 #pragma unroll
   for (int d = 0; d < LS; ++d) {
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat)
       wv[mat][d] = __builtin_bit_cast(
-          u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw[mat], (uint32_t)r * (uint32_t)RB + (uint32_t)d * 512u + lo, 0, 0));
+          u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw[mat], (uint32_t)r * RB + (uint32_t)d * 512u + lo, 0, 0));
   }
 
   // Activation columns (runs permuted to the unpacked code order) and their sums: the 8 chunks
@@ -533,7 +544,8 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   // The wave's (s, b - 128 s) pairs per group, f32, after the barrier: only this wave reads them,
-  // so the workgroup waits for the activations alone, not for every wave's scale loads.
+  // so the workgroup waits for the activations alone, not for every wave's scale loads.  Groups
+  // past the row's end get (0, 0) (their loads returned zero).
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat) {
 #pragma unroll
@@ -762,22 +774,29 @@ static int64_t gemv_cus() {
 
 // Waves (rows) per one-row workgroup.  SwiGLU (two rows per wave): 8, i.e. the staging barrier
 // among fewer waves (K = 3072, F = 8192: 7.7 -> 7.1 us against 16 waves; 4 measured slower).
-// One matrix: the largest of 16, 12, 8 whose workgroup count is a multiple of the CU count
-// (N = 3072: 12 -> 256 workgroups, 5.1 us against 5.5 at 8 and 5.9 at 16; N = 8192: 16); else
-// the largest that still gives every CU a workgroup; else 8, the most workgroups (N = 1536,
-// K = 16384: 16 rows left 96 workgroups on 256 CUs).
+// One matrix: of 16, 12 and 8 the one whose busiest CU streams the fewest rows,
+// ceil(ceil(N / w) / CUs) * w, the larger on a tie.  Measured over 14 shapes (K = 2048..28672,
+// N = 1536..8192) the launch time follows that count: N = 3072 takes 12 (4.74 us against 4.94 at 8
+// and 5.37 at 16), N = 5120 takes 12 (K = 13824: 13.6 us against 15.1 at 16), N = 1536 takes 8
+// (3.99 against 5.29 at 16), N = 3584 and 8192 take 16.
 static int qmv_row_wpb(int64_t N, int nmat) {
   if (nmat == 2) return 8;
   const int64_t cus = gemv_cus();
-  for (int w : {16, 12, 8})
-    if (((N + w - 1) / w) % cus == 0) return w;
-  for (int w : {16, 12, 8})
-    if ((N + w - 1) / w >= cus) return w;
-  return 8;
+  int best = 16;
+  int64_t best_rows = 0;
+  for (int w : {16, 12, 8}) {
+    const int64_t rows = ((N + w - 1) / w + cus - 1) / cus * w;
+    if (best_rows == 0 || rows < best_rows) {
+      best = w;
+      best_rows = rows;
+    }
+  }
+  return best;
 }
 
 template <bool G64, int LS, int NMAT>
 static int launch_qmv_row(const QmvArgs& a, hipStream_t st) {
+  static_assert(qmv_row_lds(LS, G64, NMAT, 16) <= kMaxLds, "one-row workgroup exceeds the LDS");
   static std::atomic<bool> attr_set[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return set_error(MLXQ_EDEVICE, "qmv: no current device");
@@ -791,35 +810,22 @@ static int launch_qmv_row(const QmvArgs& a, hipStream_t st) {
   const int lds = qmv_row_lds(LS, G64, NMAT, wpb);
   hipLaunchKernelGGL((qmv_row_kernel<G64, LS, NMAT>), dim3((unsigned)((a.N + wpb - 1) / wpb)), dim3(wpb * 64),
                      lds, st, (const uint16_t*)a.x, a.wq, (const uint16_t*)a.s, (const uint16_t*)a.b, a.wq2,
-                     (const uint16_t*)a.s2, (const uint16_t*)a.b2, (int)a.N, (uint16_t*)a.y);
+                     (const uint16_t*)a.s2, (const uint16_t*)a.b2, (int)a.K, (int)a.N, (uint16_t*)a.y);
   return check_launch(NMAT == 2 ? "swiglu_qmv_row" : "qmv_row");
 }
 
-template <bool G64, int NMAT>
-static int qmv_row_ls(const QmvArgs& a, hipStream_t st) {
-  switch (a.K / 1024) {
-    case 1: return launch_qmv_row<G64, 1, NMAT>(a, st);
-    case 2: return launch_qmv_row<G64, 2, NMAT>(a, st);
-    case 3: return launch_qmv_row<G64, 3, NMAT>(a, st);
-    case 4: return launch_qmv_row<G64, 4, NMAT>(a, st);
-    case 5: return launch_qmv_row<G64, 5, NMAT>(a, st);
-    case 6: return launch_qmv_row<G64, 6, NMAT>(a, st);
-    case 7: return launch_qmv_row<G64, 7, NMAT>(a, st);
-    case 8: return launch_qmv_row<G64, 8, NMAT>(a, st);
-    case 9: return launch_qmv_row<G64, 9, NMAT>(a, st);
-    case 10: return launch_qmv_row<G64, 10, NMAT>(a, st);
-    case 11: return launch_qmv_row<G64, 11, NMAT>(a, st);
-    case 12: return launch_qmv_row<G64, 12, NMAT>(a, st);
-    case 13: return launch_qmv_row<G64, 13, NMAT>(a, st);
-    case 14: return launch_qmv_row<G64, 14, NMAT>(a, st);
-    case 15: return launch_qmv_row<G64, 15, NMAT>(a, st);
-    default: return launch_qmv_row<G64, 16, NMAT>(a, st);
-  }
+// Launchers by loads per row (1 .. kRowMaxLoads).
+template <bool G64, int NMAT, int... L>
+static int qmv_row_ls(const QmvArgs& a, hipStream_t st, std::integer_sequence<int, L...>) {
+  using Launch = int (*)(const QmvArgs&, hipStream_t);
+  static constexpr Launch launch[] = {&launch_qmv_row<G64, L + 1, NMAT>...};
+  return launch[(a.K + 1023) / 1024 - 1](a, st);
 }
 
 template <int NMAT>
 static int qmv_row(const QmvArgs& a, int gs, hipStream_t st) {
-  return gs == 64 ? qmv_row_ls<true, NMAT>(a, st) : qmv_row_ls<false, NMAT>(a, st);
+  constexpr auto ls = std::make_integer_sequence<int, kRowMaxLoads[NMAT - 1]>{};
+  return gs == 64 ? qmv_row_ls<true, NMAT>(a, st, ls) : qmv_row_ls<false, NMAT>(a, st, ls);
 }
 
 static bool buffers_fit(int64_t M, int64_t K, int64_t N) {
@@ -830,13 +836,13 @@ static bool buffers_fit(int64_t M, int64_t K, int64_t N) {
 bool qmv_mfma_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int64_t N, int gs, int bits) {
   if (x_dtype != MLXQ_BFLOAT16 || sb_dtype != MLXQ_BFLOAT16 || !buffers_fit(M, K, N)) return false;
   QmvPlan p;
-  return qmv_plan(M, K, gs, bits, 1, p);
+  return qmv_row_fits(M, K, gs, bits, 1) || qmv_plan(M, K, gs, bits, 1, p);
 }
 
 int run_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* s, const void* b,
                  int64_t N, int gs, int bits, void* y, hipStream_t st) {
   const QmvArgs a = {x, M, K, N, wq, s, b, nullptr, nullptr, nullptr, y};
-  if (qmv_row_fits(M, K, gs, bits)) return qmv_row<1>(a, gs, st);
+  if (qmv_row_fits(M, K, gs, bits, 1)) return qmv_row<1>(a, gs, st);
   QmvPlan p;
   if (!qmv_plan(M, K, gs, bits, 1, p))
     return set_error(MLXQ_EINVAL, "qmv: no GEMV plan for M=%lld K=%lld", (long long)M, (long long)K);
@@ -846,14 +852,14 @@ int run_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* wq, const 
 bool swiglu_qmv_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int64_t F, int gs, int bits) {
   if (x_dtype != MLXQ_BFLOAT16 || sb_dtype != MLXQ_BFLOAT16 || !buffers_fit(M, K, F)) return false;
   QmvPlan p;
-  return qmv_plan(M, K, gs, bits, 2, p);
+  return qmv_row_fits(M, K, gs, bits, 2) || qmv_plan(M, K, gs, bits, 2, p);
 }
 
 int run_swiglu_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq_g, const void* s_g,
                    const void* b_g, const uint32_t* wq_u, const void* s_u, const void* b_u, int64_t F,
                    int gs, int bits, void* h, hipStream_t st) {
   const QmvArgs a = {x, M, K, F, wq_g, s_g, b_g, wq_u, s_u, b_u, h};
-  if (qmv_row_fits(M, K, gs, bits)) return qmv_row<2>(a, gs, st);
+  if (qmv_row_fits(M, K, gs, bits, 2)) return qmv_row<2>(a, gs, st);
   QmvPlan p;
   if (!qmv_plan(M, K, gs, bits, 2, p))
     return set_error(MLXQ_EUNSUPPORTED, "swiglu: no fused GEMV plan for M=%lld K=%lld", (long long)M,

@@ -440,6 +440,43 @@ def test_qmv_one_row_kernel_vs_exact(mlxq, M, K, N, gs):
     assert_close(y, oracle.bf16_round(exact), f"one-row M={M} K={K} N={N} gs={gs}")
 
 
+@pytest.mark.parametrize("K,N,gs", [(1152, 33, 64), (11008, 300, 64), (8960, 257, 128), (13824, 130, 64),
+                                    (18944, 100, 64), (29568, 48, 64), (32768, 40, 128), (2560, 4097, 128)])
+def test_qmv_one_row_kernel_ragged_k(mlxq, K, N, gs):
+    """M = 1, Q4, K not a multiple of 1024 (an even group count per row), up to 32 loads per row:
+    the last load of a row is partial, its upper columns reach into the next row's codes (past the
+    buffer's end for the last row) and must fold exactly zero.  The activation row sits in a longer
+    buffer whose tail past K is NaN, so a read past K shows in every output."""
+    banner("qmv one row ragged K", K, N, gs)
+    rng = np.random.default_rng(K + 5 * N + gs)
+    x = bf16_normal(rng, (1, K))
+    w = bf16_normal(rng, (N, K), 0.02)
+    rwq, rs, rb = oracle.quantize(w, gs, 4, sb_bf16=True)
+    xbig = torch.full((1, K + 2048), float("nan"), dtype=torch.bfloat16, device="cuda")
+    xbig[:, :K] = to_gpu(x)
+    y = to_np(mlxq.quantized_matmul(xbig[:, :K], wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), True, gs, 4))
+    exact = oracle.quantized_matmul(x, rwq, rs, rb, gs, 4, w_bf16=False, out_bf16=False)
+    _close_to_exact(y, exact, f"one-row ragged K={K} N={N} gs={gs}")
+    assert_close(y, oracle.bf16_round(exact), f"one-row ragged K={K} N={N} gs={gs}")
+
+
+@pytest.mark.parametrize("K,F,gs", [(3584, 300, 64), (2560, 129, 128), (15488, 24, 64)])
+def test_swiglu_one_row_kernel_ragged_k(mlxq, K, F, gs):
+    """The SwiGLU pair at M = 1 with K not a multiple of 1024 (up to 16 loads per row)."""
+    banner("swiglu one row ragged K", K, F, gs)
+    rng = np.random.default_rng(K + F + gs + 3)
+    x = bf16_normal(rng, (1, K))
+    tg, tu = [oracle.quantize(bf16_normal(rng, (F, K), 0.02), gs, 4, sb_bf16=True) for _ in range(2)]
+    h = to_np(mlxq.swiglu(to_gpu(x), [wq_to_gpu(tg[0]), to_gpu(tg[1]), to_gpu(tg[2])],
+                          [wq_to_gpu(tu[0]), to_gpu(tu[1]), to_gpu(tu[2])], gs, 4))
+    gr = oracle.quantized_matmul(x, *tg, gs, 4, w_bf16=False, out_bf16=True)
+    ur = oracle.quantized_matmul(x, *tu, gs, 4, w_bf16=False, out_bf16=True)
+    ref = oracle.bf16_round(oracle.bf16_round(np.vectorize(oracle.silu)(gr).astype(np.float32)) * ur)
+    assert_close(h, ref, f"swiglu one row ragged K={K} F={F}")
+    print(f"    bit-identical outputs: {np.mean(h == ref) * 100:.2f} %", flush=True)
+    assert np.mean(h == ref) > 0.95
+
+
 @pytest.mark.parametrize("K,N,gs", [(3072, 8192, 64), (8192, 3072, 64), (4096, 520, 128)])
 def test_qmv_one_row_kernel_matches_tile_kernel(mlxq, K, N, gs):
     """The one-row kernel (M = 1) and the 16-row tile kernel (M = 2..4 and 8, different wave plans)
