@@ -131,24 +131,32 @@ __host__ __device__ constexpr int qmv_wave_lds(int bits, bool g64, int steps, in
   return M * (steps * (512 / bits) * 2 + 16) + 16 * sz_pitch(qmv_wave_groups(bits, g64, steps)) * 4;
 }
 
-// One 16-row GEMV tile as seen by one wave: the wave's K range of load steps, the operand
-// registers between the issue of its loads and their use, and its private LDS region.
+// One 16-row GEMV tile as seen by one wave: the wave's K range of T load steps, the operand
+// registers between the issue of its loads and their use, and its private LDS region.  The
+// weights pass through a ring of STEPS load registers: the first STEPS steps are issued up front
+// and each register is reloaded with step d + STEPS as soon as step d's MFMAs have read it (T = 2
+// STEPS reaches twice the K of one register round at the same register count).  The last wave's
+// range may run past K: its activations there load as zero (so those steps' products and group
+// sums are zero, whatever codes the weight loads find past the row's end) and so do the scales
+// and biases of groups past the row's end.
 // Contract of every kernel built from it (checked on the host by qmv_plan):
 // 1 <= M <= MR, K % (512/BITS) == 0, K % group == 0, bf16 scales and biases, the row's
-// K*BITS/512 load steps split evenly over the waves of one matrix (STEPS each), dynamic LDS of at
-// least max(waves * qmv_wave_lds, waves * 16 * 17 * 4) bytes, every buffer < 2 GiB.
-template <int BITS, bool G64, int STEPS, int MR>
+// K*BITS/512 load steps covered by the waves of one matrix (T each, the last wave's range may end
+// past K), dynamic LDS of at least max(waves * qmv_wave_lds, waves * 16 * 17 * 4) bytes, every
+// buffer < 2 GiB.
+template <int BITS, bool G64, int STEPS, int MR, int T>
 struct GemvTile {
+  static_assert(T >= STEPS, "ring shorter than the wave's steps");
   static constexpr int CPL = 512 / BITS;          // codes per row in one 64-byte load step
   static constexpr int GS = G64 ? 64 : 128;       // group size
   static constexpr int NM = BITS == 4 ? 4 : 2;    // MFMAs per load step
   static constexpr int E = MR < 4 ? MR : 4;       // result registers per lane that can hold a row < M
-  static constexpr int XCH = STEPS * CPL / 8;     // 16-byte activation chunks per row in the wave's range
+  static constexpr int XCH = T * CPL / 8;         // 16-byte activation chunks per row in the wave's range
   static constexpr int XSL = (XCH + 63) / 64;     // ... per lane
-  static constexpr int NGW = qmv_wave_groups(BITS, G64, STEPS);
+  static constexpr int NGW = qmv_wave_groups(BITS, G64, T);
   static constexpr int PW = sz_pitch(NGW);        // (s, zc) table row pitch, floats
   static constexpr int SBL = (16 * NGW + 63) / 64;  // scale entries per lane
-  static constexpr int XW = STEPS * CPL * 2 + 16;   // LDS pitch of the wave's activation rows
+  static constexpr int XW = T * CPL * 2 + 16;       // LDS pitch of the wave's activation rows
 
   int lane, c16, q, n0, M, K, N, G, ls0, kb, g0;
   unsigned char* wl;  // this wave's LDS region: activation rows, then the (s, zc) table
@@ -156,6 +164,8 @@ struct GemvTile {
   u32x4 cx[MR][XSL];
   uint32_t cs[SBL], cz[SBL];
   u32x4 wv[STEPS];
+  __amdgpu_buffer_rsrc_t rw;
+  uint32_t w_base;
 
   // wave_all: the wave's index in the workgroup (selects its LDS region); wave: its index among
   // the waves of its matrix (selects its K range); rows [n0, n0 + 16) of an [N, K] matrix.
@@ -169,7 +179,7 @@ struct GemvTile {
     K = K_;
     N = N_;
     G = K / GS;
-    ls0 = wave * STEPS;
+    ls0 = wave * T;
     kb = ls0 * CPL;
     g0 = kb / GS;
     wl = lds + wave_all * (M * XW + 16 * PW * 4);
@@ -184,7 +194,7 @@ struct GemvTile {
 #pragma unroll
         for (int j = 0; j < XSL; ++j) {
           const int c = lane + 64 * j;
-          cx[m][j] = load16(rx, c < XCH ? (uint32_t)((m * K + kb + c * 8) * 2) : kOob);
+          cx[m][j] = load16(rx, c < XCH && kb + c * 8 < K ? (uint32_t)((m * K + kb + c * 8) * 2) : kOob);
         }
       }
     }
@@ -203,12 +213,13 @@ struct GemvTile {
     }
   }
 
-  // The wave's whole weight stream: 16 rows x 64 contiguous bytes per load, rows past N clamped
-  // (never stored).
-  __device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t rw) {
+  // The wave's first STEPS weight loads: 16 rows x 64 contiguous bytes per load, rows past N
+  // clamped (never stored).
+  __device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t rw_) {
+    rw = rw_;
     const int n = n0 + c16;
     const int nn = n < N ? n : N - 1;
-    const uint32_t w_base = (uint32_t)nn * (uint32_t)(K * BITS / 8) + (uint32_t)(ls0 * 64 + q * 16);
+    w_base = (uint32_t)nn * (uint32_t)(K * BITS / 8) + (uint32_t)(ls0 * 64 + q * 16);
 #pragma unroll
     for (int d = 0; d < STEPS; ++d) wv[d] = load16(rw, w_base + (uint32_t)d * 64u);
   }
@@ -245,7 +256,7 @@ struct GemvTile {
 
   // Per load step: NM MFMAs x . codes and NM MFMAs x . ones (group sums), then the fold of
   // each group, y += s*acc + zc*X.  yacc[e] is result row 4q + e of column c16.
-  __device__ __forceinline__ void fold(float (&yacc)[E]) const {
+  __device__ __forceinline__ void fold(float (&yacc)[E]) {
     const unsigned char* xa[NM];  // this lane's activation run for MFMA i at the wave's first step
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
@@ -273,9 +284,9 @@ struct GemvTile {
     // at most M distinct addresses (broadcast); a read restricted to the lanes of rows < M cost
     // the compiler ten 64-bit register copies per step to keep the other lanes' operands.
     using SZ = typename std::conditional<BITS == 4 && G64, f32x4, f32x2>::type;
-    bf16x8 a[STEPS][NM];
-    SZ p[STEPS];
-    f32x4 acc[STEPS][2], xsum[STEPS][2];
+    bf16x8 a[T][NM];
+    SZ p[T];
+    f32x4 acc[T][2], xsum[T][2];
 
     // A step's LDS operands: its activation runs and its (s, zc) pairs.
     auto read_step = [&](int d) {
@@ -289,9 +300,11 @@ struct GemvTile {
         p[d] = *reinterpret_cast<const f32x2*>(sz + 2 * gl);
       }
     };
-    // A step's products: NM MFMAs x . codes and NM MFMAs x . ones (the group sums).
+    // A step's products: NM MFMAs x . codes and NM MFMAs x . ones (the group sums); then the ring
+    // register is reloaded with step d + STEPS.
     auto mfma_step = [&](int d) {
-      uint32_t w[4] = {wv[d][0], wv[d][1], wv[d][2], wv[d][3]};
+      const int slot = d % STEPS;
+      uint32_t w[4] = {wv[slot][0], wv[slot][1], wv[slot][2], wv[slot][3]};
       if constexpr (BITS == 4 && G64) {
         swap_lane_halves(w[0], w[2]);
         swap_lane_halves(w[1], w[3]);
@@ -308,6 +321,7 @@ struct GemvTile {
         acc[d][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][i], b, acc[d][h], 0, 0, 0);
         xsum[d][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][i], ones, xsum[d][h], 0, 0, 0);
       }
+      if (d + STEPS < T) wv[slot] = load16(rw, w_base + (uint32_t)(d + STEPS) * 64u);
     };
     // A step's fold into the result.  The result is pinned after each fold: otherwise the
     // compiler sinks every fold below the last step and keeps all steps' products live at once.
@@ -328,14 +342,14 @@ struct GemvTile {
     // fences between iterations keep at most two steps' operands live.
     read_step(0);
 #pragma unroll
-    for (int d = 0; d < STEPS; ++d) {
+    for (int d = 0; d < T; ++d) {
       __builtin_amdgcn_sched_barrier(0);
-      if (d + 1 < STEPS) read_step(d + 1 < STEPS ? d + 1 : d);
+      if (d + 1 < T) read_step(d + 1 < T ? d + 1 : d);
       mfma_step(d);
       if (d > 0) fold_step(d - 1);
     }
     __builtin_amdgcn_sched_barrier(0);
-    fold_step(STEPS - 1);
+    fold_step(T - 1);
   }
 };
 
@@ -374,7 +388,7 @@ __device__ __forceinline__ void gemv_reduce_store(unsigned char* lds, const floa
 // Each wave stages only its own operands (its K range of the activations, the scales and biases
 // of its groups) into its own LDS region, so it starts on its weights as soon as its own operands
 // land; the only workgroup barrier is the final split-K reduction.
-template <int BITS, bool G64, int STEPS, int MR, int NMAT>
+template <int BITS, bool G64, int STEPS, int MR, int NMAT, int RING>
 __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
     const uint16_t* __restrict__ x, int M, int K, const uint32_t* __restrict__ wq,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
@@ -388,7 +402,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   const int W = (NT >> 6) / NMAT;  // waves per matrix
   const int mat = NMAT == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave_all / W);
   const int n0 = blockIdx.x * 16;
-  GemvTile<BITS, G64, STEPS, MR> t(lane, wave_all, wave_all - mat * W, n0, M, K, N, lds);
+  using Tile = GemvTile<BITS, G64, STEPS, MR, STEPS * RING>;
+  Tile t(lane, wave_all, wave_all - mat * W, n0, M, K, N, lds);
   const int sb_total = (int)(((uint32_t)N * (uint32_t)t.G * 2u + 3u) & ~3u);  // whole dwords
   t.issue_x(make_rsrc(x, M * K * 2));
   t.issue_sb(make_rsrc(mat ? scales2 : scales, sb_total), make_rsrc(mat ? biases2 : biases, sb_total));
@@ -401,7 +416,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   if constexpr (NMAT == 1) __builtin_amdgcn_s_barrier();
   t.issue_w(make_rsrc(mat ? wq2 : wq, (int)((uint32_t)N * (uint32_t)(K * BITS / 8))));
   t.stage();
-  float yacc[GemvTile<BITS, G64, STEPS, MR>::E];
+  float yacc[Tile::E];
   t.fold(yacc);
   gemv_reduce_store<NMAT>(lds, yacc, wave_all, W, lane, tid, NT, M, n0, N, y);
 }
@@ -644,10 +659,17 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
 namespace {
 
 struct QmvPlan {
-  int waves, steps, mr, lds;  // waves: all waves of the workgroup (per matrix x matrices)
+  int waves, steps, ring, mr, lds;  // waves: all waves of the workgroup (per matrix x matrices)
+  int rows;                         // activation rows per launch: M, or 4 or 2 when M is split
 };
 
 constexpr int kStepChoices[] = {1, 2, 3, 4, 6, 8};
+
+// Whether a kernel with a ring of `ring` rounds exists: two rounds only for Q4, 4..8 load
+// registers, at most four activation rows (more rows split into launches of four).
+constexpr bool qmv_ring_built(int bits, int steps, int mr, int ring) {
+  return ring == 1 || (ring == 2 && bits == 4 && steps >= 4 && mr <= 4);
+}
 
 // Picks the load steps per wave: among the counts that divide the row's load steps, fit a
 // workgroup of at most kMaxWaves waves, its LDS and its registers (qmv_steps_fit), the one whose
@@ -657,32 +679,56 @@ constexpr int kStepChoices[] = {1, 2, 3, 4, 6, 8};
 // spread the fold's VALU work (which bounds the last waves' tail) over the SIMDs, while a 16-wave
 // workgroup fills a CU on its own (128 registers per wave).  12 against 8: the down GEMV
 // (K = 8192) 6.10 -> 5.84 us, gate (K = 3072) 5.40 -> 5.28 us, SwiGLU unchanged; 16 was no better.
+//
+// When no count divides the row's load steps within those limits (K = 11008: 86 steps of Q4),
+// the waves take ceil(steps / waves) each and the last one's range ends past K (cost as above,
+// then the fewest padded steps); failing that, each wave takes two rounds of its load registers
+// (ring 2: twice the K at the same registers).  A launch holds its activation rows whole in LDS
+// (M x K x 2 bytes), so rows that fit no plan go out as launches of four, else two rows (M = 8,
+// K = 18944: four launches of two rows 46 us against 85 us on the VALU GEMV; single rows would
+// stream the weights M times and lose to it).
+static bool qmv_plan_rows(int64_t M, int64_t K, int gs, int bits, int nmat, QmvPlan& p) {
+  const int64_t cpl = 512 / bits;
+  const int64_t LS = K / cpl;
+  const int mr = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
+  for (int pass = 0; pass < 3; ++pass) {  // exact; ragged; ragged with two rounds
+    const int ring = pass == 2 ? 2 : 1;
+    bool found = false;
+    int64_t best_cost = 0, best_pad = 0;
+    for (int steps : kStepChoices) {
+      if (!qmv_steps_fit(bits, gs == 64, steps, mr) || !qmv_ring_built(bits, steps, mr, ring)) continue;
+      const int64_t t = (int64_t)steps * ring;  // load steps per wave
+      if (pass == 0 && LS % t != 0) continue;
+      const int64_t wpm = (LS + t - 1) / t;
+      const int64_t waves = nmat * wpm;
+      if (waves > kMaxWaves) continue;
+      // activation chunks a lane stages (registers): at most kCopySlots across the rows
+      if (mr * ((t * cpl / 8 + 63) / 64) > kCopySlots) continue;
+      const int64_t operands = waves * (int64_t)qmv_wave_lds(bits, gs == 64, (int)t, (int)M);
+      const int64_t red = waves * 16 * 17 * 4;
+      const int64_t lds = operands > red ? operands : red;
+      if (lds > kMaxLds) continue;
+      const int64_t cost = waves > 12 ? waves - 12 : 12 - waves;
+      const int64_t pad = wpm * t - LS;
+      if (found && (cost > best_cost || (cost == best_cost && pad >= best_pad))) continue;
+      found = true;
+      best_cost = cost;
+      best_pad = pad;
+      p = {(int)waves, steps, ring, mr, (int)lds, (int)M};
+    }
+    if (found) return true;
+  }
+  return false;
+}
+
 bool qmv_plan(int64_t M, int64_t K, int gs, int bits, int nmat, QmvPlan& p) {
   if (M < 1 || M > 8 || (bits != 4 && bits != 8) || (gs != 64 && gs != 128)) return false;
   const int64_t cpl = 512 / bits;
   if (K <= 0 || K % cpl != 0 || K % gs != 0) return false;
-  const int64_t LS = K / cpl;
-  const int mr = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
-  bool found = false;
-  int64_t best_cost = 0;
-  for (int steps : kStepChoices) {
-    if (LS % steps != 0) continue;
-    if (!qmv_steps_fit(bits, gs == 64, steps, mr)) continue;
-    const int64_t waves = nmat * (LS / steps);
-    if (waves > kMaxWaves) continue;
-    // activation chunks a lane stages (registers): at most kCopySlots across the rows
-    if (mr * ((steps * cpl / 8 + 63) / 64) > kCopySlots) continue;
-    const int64_t operands = waves * (int64_t)qmv_wave_lds(bits, gs == 64, steps, (int)M);
-    const int64_t red = waves * 16 * 17 * 4;
-    const int64_t lds = operands > red ? operands : red;
-    if (lds > kMaxLds) continue;
-    const int64_t cost = waves > 12 ? waves - 12 : 12 - waves;
-    if (found && cost >= best_cost) continue;
-    found = true;
-    best_cost = cost;
-    p = {(int)waves, steps, mr, (int)lds};
-  }
-  return found;
+  if (qmv_plan_rows(M, K, gs, bits, nmat, p)) return true;
+  for (int rows : {4, 2})  // launches of fewer rows
+    if (M > rows && qmv_plan_rows(rows, K, gs, bits, nmat, p)) return true;
+  return false;
 }
 
 // Device operands of one launch (the second matrix is used by the SwiGLU form only).
@@ -698,7 +744,7 @@ struct QmvArgs {
 
 }  // namespace
 
-template <int BITS, bool G64, int STEPS, int MR, int NMAT>
+template <int BITS, bool G64, int STEPS, int MR, int NMAT, int RING>
 static int launch_qmv_mfma(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
   // The dynamic-LDS limit is raised once per device (any thread may get here first; setting it
   // twice is harmless).
@@ -706,12 +752,12 @@ static int launch_qmv_mfma(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return set_error(MLXQ_EDEVICE, "qmv: no current device");
   if (dev < 0 || dev >= 64 || !attr_set[dev].load(std::memory_order_acquire)) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_mfma_kernel<BITS, G64, STEPS, MR, NMAT>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_mfma_kernel<BITS, G64, STEPS, MR, NMAT, RING>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds) != hipSuccess)
       return set_error(MLXQ_EDEVICE, "qmv: hipFuncSetAttribute failed");
     if (dev >= 0 && dev < 64) attr_set[dev].store(true, std::memory_order_release);
   }
-  hipLaunchKernelGGL((qmv_mfma_kernel<BITS, G64, STEPS, MR, NMAT>), dim3((unsigned)((a.N + 15) / 16)),
+  hipLaunchKernelGGL((qmv_mfma_kernel<BITS, G64, STEPS, MR, NMAT, RING>), dim3((unsigned)((a.N + 15) / 16)),
                      dim3(p.waves * 64), p.lds, st, (const uint16_t*)a.x, (int)a.M, (int)a.K, a.wq,
                      (const uint16_t*)a.s, (const uint16_t*)a.b, a.wq2, (const uint16_t*)a.s2,
                      (const uint16_t*)a.b2, (int)a.N, (uint16_t*)a.y);
@@ -720,10 +766,14 @@ static int launch_qmv_mfma(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
 
 template <int BITS, bool G64, int STEPS, int MR, int NMAT>
 static int qmv_mr(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
-  if constexpr (qmv_steps_fit(BITS, G64, STEPS, MR))
-    return launch_qmv_mfma<BITS, G64, STEPS, MR, NMAT>(a, p, st);
-  else
+  if constexpr (qmv_steps_fit(BITS, G64, STEPS, MR)) {
+    if (p.ring == 1) return launch_qmv_mfma<BITS, G64, STEPS, MR, NMAT, 1>(a, p, st);
+    if constexpr (qmv_ring_built(BITS, STEPS, MR, 2))
+      if (p.ring == 2) return launch_qmv_mfma<BITS, G64, STEPS, MR, NMAT, 2>(a, p, st);
+    return set_error(MLXQ_EINVAL, "qmv: no kernel with %d load rounds for this plan", p.ring);
+  } else {
     return set_error(MLXQ_EINVAL, "qmv: %d load steps per wave with %d rows exceed the registers", STEPS, MR);
+  }
 }
 
 template <int BITS, bool G64, int STEPS, int NMAT>
@@ -846,7 +896,14 @@ int run_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* wq, const 
   QmvPlan p;
   if (!qmv_plan(M, K, gs, bits, 1, p))
     return set_error(MLXQ_EINVAL, "qmv: no GEMV plan for M=%lld K=%lld", (long long)M, (long long)K);
-  return qmv_kind<1>(a, gs, bits, p, st);
+  if (p.rows == M) return qmv_kind<1>(a, gs, bits, p, st);
+  for (int64_t m0 = 0; m0 < M; m0 += p.rows) {  // launches of p.rows activation rows
+    const int64_t rows = M - m0 < p.rows ? M - m0 : p.rows;
+    const int rc = run_qmv_mfma(static_cast<const uint16_t*>(x) + m0 * K, rows, K, wq, s, b, N, gs, bits,
+                                static_cast<uint16_t*>(y) + m0 * N, st);
+    if (rc != MLXQ_OK) return rc;
+  }
+  return MLXQ_OK;
 }
 
 bool swiglu_qmv_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int64_t F, int gs, int bits) {
@@ -864,7 +921,14 @@ int run_swiglu_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq_g, co
   if (!qmv_plan(M, K, gs, bits, 2, p))
     return set_error(MLXQ_EUNSUPPORTED, "swiglu: no fused GEMV plan for M=%lld K=%lld", (long long)M,
                      (long long)K);
-  return qmv_kind<2>(a, gs, bits, p, st);
+  if (p.rows == M) return qmv_kind<2>(a, gs, bits, p, st);
+  for (int64_t m0 = 0; m0 < M; m0 += p.rows) {  // launches of p.rows activation rows
+    const int64_t rows = M - m0 < p.rows ? M - m0 : p.rows;
+    const int rc = run_swiglu_qmv(static_cast<const uint16_t*>(x) + m0 * K, rows, K, wq_g, s_g, b_g, wq_u, s_u,
+                                  b_u, F, gs, bits, static_cast<uint16_t*>(h) + m0 * F, st);
+    if (rc != MLXQ_OK) return rc;
+  }
+  return MLXQ_OK;
 }
 
 }  // namespace mlxq
