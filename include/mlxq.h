@@ -222,7 +222,7 @@ int mlxq_qmm_experts(const void* x, int x_dtype, int x_per_expert, int64_t E, in
  *   h = round(round(silu(round(x.Wg^T))) * round(x.Wu^T))      (round() to bf16)
  * Decode form only: bf16 x and scales, 1 <= M <= 8, group_size 64 or 128, K a multiple of
  * 512/bits within the fused kernels' reach (Q4: K <= 16384 at M = 1, 12288 at M = 2..8; Q8:
- * 4096 at M = 1, 3072 at M = 2..8); anything else returns MLXQ_EUNSUPPORTED (callers then run
+ * 8192 at M = 1, 6144 at M = 2..8); anything else returns MLXQ_EUNSUPPORTED (callers then run
  * the two linears).
  * This entry point has no single counterpart in the reference; it replaces a three-op sequence.
  */

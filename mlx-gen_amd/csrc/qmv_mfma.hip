@@ -665,10 +665,10 @@ struct QmvPlan {
 
 constexpr int kStepChoices[] = {1, 2, 3, 4, 6, 8};
 
-// Whether a kernel with a ring of `ring` rounds exists: two rounds only for Q4, 4..8 load
-// registers, at most four activation rows (more rows split into launches of four).
+// Whether a kernel with a ring of `ring` rounds exists: two rounds only with 4..8 load registers
+// and at most four activation rows (more rows split into launches of four or two).
 constexpr bool qmv_ring_built(int bits, int steps, int mr, int ring) {
-  return ring == 1 || (ring == 2 && bits == 4 && steps >= 4 && mr <= 4);
+  return ring == 1 || (ring == 2 && (bits == 4 || bits == 8) && steps >= 4 && mr <= 4);
 }
 
 // Picks the load steps per wave: among the counts that divide the row's load steps, fit a

@@ -460,16 +460,17 @@ def test_qmv_one_row_kernel_ragged_k(mlxq, K, N, gs):
     assert_close(y, oracle.bf16_round(exact), f"one-row ragged K={K} N={N} gs={gs}")
 
 
-@pytest.mark.parametrize("M", [2, 3, 4, 5, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("K,N,gs,bits", [(11008, 300, 64, 4), (14336, 257, 64, 4), (8960, 130, 128, 4),
                                          (16384, 64, 128, 4), (24576, 40, 64, 4), (1088, 70, 64, 8),
-                                         (18944, 33, 64, 4)])
+                                         (18944, 33, 64, 4), (11008, 200, 64, 8), (4224, 90, 128, 8)])
 def test_qmv_tile_kernel_long_and_ragged_k(mlxq, M, K, N, gs, bits):
-    """M = 2..8 where K's load steps have no even split over the tile kernel's waves or exceed one
-    register round: the last wave's range runs past K (K = 11008, 8960 and the Q8 K = 1088), waves
-    take two rounds of their load registers (M = 3..8 at K = 11008 / 14336 / 16384, M = 2 at
-    18944 and 24576), and rows that fit no plan go out as launches of four rows (M = 5, 8 at
-    K = 11008 / 14336) or two rows (M = 3..8 at K = 18944 and 24576).  The activations sit in a
+    """M = 2..8 (and Q8 at M = 1) where K's load steps have no even split over the tile kernel's
+    waves or exceed one register round: the last wave's range runs past K (K = 11008, 8960 and the
+    Q8 K = 1088, 4224), waves take two rounds of their load registers (M = 3..8 at K = 11008 /
+    14336 / 16384, M = 2 at 18944 and 24576, Q8 K = 11008), and rows that fit no plan go out as
+    launches of four rows (M = 5, 8 at K = 11008 / 14336) or two rows (M = 3..8 at K = 18944 and
+    24576).  Q4 at M = 1 runs the one-row kernel on the same shapes.  The activations sit in a
     longer buffer whose tail is NaN, so a read past M x K shows, and a read past K within a row
     takes the next row's values and moves the result."""
     banner("qmv tile long / ragged K", M, K, N, gs, bits)
@@ -487,29 +488,30 @@ def test_qmv_tile_kernel_long_and_ragged_k(mlxq, M, K, N, gs, bits):
 
 
 @pytest.mark.parametrize("M", [2, 3, 4, 5, 8])
-@pytest.mark.parametrize("K,F,gs", [(5120, 300, 64), (7168, 130, 64), (12288, 40, 128), (20480, 24, 64)])
-def test_swiglu_tile_kernel_long_and_ragged_k(mlxq, M, K, F, gs):
+@pytest.mark.parametrize("K,F,gs,bits", [(5120, 300, 64, 4), (7168, 130, 64, 4), (12288, 40, 128, 4),
+                                         (20480, 24, 64, 4), (6144, 48, 128, 8)])
+def test_swiglu_tile_kernel_long_and_ragged_k(mlxq, M, K, F, gs, bits):
     """The SwiGLU launch at M = 2..8 past the exact wave splits: the last wave's range past K
     (K = 5120 at M = 2), two register rounds per wave (K = 7168, K = 5120 at M >= 3, K = 12288 at
     M = 2), launches of four rows (M = 5, 8 at K = 5120 / 7168) and of two rows (M = 3..8 at
-    K = 12288); K = 20480 fits no fused plan at M >= 2 and must be refused (MLXQ_EUNSUPPORTED),
-    not run."""
-    banner("swiglu tile long K", M, K, F, gs)
+    K = 12288), Q8 at K = 6144 (two rounds); K = 20480 fits no fused plan at M >= 2 and must be
+    refused (MLXQ_EUNSUPPORTED), not run."""
+    banner("swiglu tile long K", M, K, F, gs, bits)
     rng = np.random.default_rng(M + K + F + gs)
     x = bf16_normal(rng, (M, K))
-    tg, tu = [oracle.quantize(bf16_normal(rng, (F, K), 0.02), gs, 4, sb_bf16=True) for _ in range(2)]
+    tg, tu = [oracle.quantize(bf16_normal(rng, (F, K), 0.02), gs, bits, sb_bf16=True) for _ in range(2)]
     args = (to_gpu(x), [wq_to_gpu(tg[0]), to_gpu(tg[1]), to_gpu(tg[2])],
-            [wq_to_gpu(tu[0]), to_gpu(tu[1]), to_gpu(tu[2])], gs, 4)
+            [wq_to_gpu(tu[0]), to_gpu(tu[1]), to_gpu(tu[2])], gs, bits)
     if K == 20480:
         with pytest.raises(mlxq.MlxqError) as ei:
             mlxq.swiglu(*args)
         assert ei.value.status == mlxq._lib.MLXQ_EUNSUPPORTED
         return
     h = to_np(mlxq.swiglu(*args))
-    gr = oracle.quantized_matmul(x, *tg, gs, 4, w_bf16=False, out_bf16=True)
-    ur = oracle.quantized_matmul(x, *tu, gs, 4, w_bf16=False, out_bf16=True)
+    gr = oracle.quantized_matmul(x, *tg, gs, bits, w_bf16=False, out_bf16=True)
+    ur = oracle.quantized_matmul(x, *tu, gs, bits, w_bf16=False, out_bf16=True)
     ref = oracle.bf16_round(oracle.bf16_round(np.vectorize(oracle.silu)(gr).astype(np.float32)) * ur)
-    assert_close(h, ref, f"swiglu tile long K M={M} K={K} F={F}")
+    assert_close(h, ref, f"swiglu tile long K M={M} K={K} F={F} b={bits}")
     print(f"    bit-identical outputs: {np.mean(h == ref) * 100:.2f} %", flush=True)
     assert np.mean(h == ref) > 0.95
 
