@@ -45,10 +45,11 @@ def parse():
     p.add_argument("--no-extras", action="store_true", help="headline GEMM only")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--only", choices=("all", "mlp", "gemv", "quantize", "copy", "configs", "experts", "f32",
-                                       "dense"),
+                                       "dense", "gemv_long"),
                    default="all",
                    help="run one leg only (for profiling); 'copy' is the plain-copy calibration "
-                        "kernel for the HBM byte counters")
+                        "kernel for the HBM byte counters; 'gemv_long' (not part of 'all') times "
+                        "the decode GEMV over long and ragged K")
     p.add_argument("--pmc-sets", metavar="A,B", default=None,
                    help="with --summarize-pmc: only these counter-set subdirectories (copy_* always read)")
     p.add_argument("--summarize-trace", metavar="DIR",
@@ -190,6 +191,47 @@ def bench_gemv(mlxq, torch, reps=20):
                    "3 matrix-core GEMV launches (gate, up, down); the fused form (SwiGLU gate/up "
                    "launch + down launch); and, for the kernel-choice A/B, 3 VALU GEMV launches "
                    "(mlxq_qmv_valu); per-kernel durations are in profiles/")
+    return out
+
+
+GEMV_LONG_SHAPES = ((11008, 4096), (14336, 4096), (13824, 5120), (18944, 3584))
+
+
+def bench_gemv_long(mlxq, torch, reps=10):
+    """Decode GEMVs over the long and ragged K of common decoder down projections (Q4 g64,
+    M = 1, 2, 4, 8): the matrix-core path (one-row kernel at M = 1; tile kernel with a ragged last
+    wave, two-round load rings or launches of four / two rows at M >= 2) against the VALU GEMV on
+    the same weights.  Weight copies rotate past the 256 MB Infinity Cache; one graph replay runs
+    every copy once."""
+    dev = torch.device("cuda:0")
+    out = {}
+    for K, N in GEMV_LONG_SHAPES:
+        wbytes = N * K // 2 + N * (K // 64) * 4
+        ncopy = max(2, -(-320_000_000 // wbytes))
+        copies = [mlxq.quantize(gen_bf16((N, K), 0.02, 200 + c, dev), 64, 4) for c in range(ncopy)]
+        torch.cuda.synchronize()
+        for M in (1, 2, 4, 8):
+            x = gen_bf16((M, K), 1.0, 9, dev)
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+            def mfma():
+                for w in copies:
+                    mlxq.qmv(x, *w, 64, 4, out=y)
+
+            def valu():
+                for w in copies:
+                    mlxq.qmv_valu(x, *w, 64, 4, out=y)
+
+            us = graph_ms(torch, mfma, inner=1, reps=reps) * 1e3 / ncopy
+            usv = graph_ms(torch, valu, inner=1, reps=reps) * 1e3 / ncopy
+            nbytes = wbytes + 2 * M * K + 2 * M * N
+            out[f"M{M}_K{K}_N{N}"] = {"us": round(us, 2), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                      "valu_us": round(usv, 2),
+                                      "valu_GBs": round(nbytes / (usv * 1e-6) / 1e9, 1)}
+        del copies
+        torch.cuda.empty_cache()
+    out["note"] = ("per launch (a launch sequence when M is split), replayed from a HIP graph over "
+                   "rotated weight copies; valu: mlxq_qmv_valu on the same operands")
     return out
 
 
@@ -653,6 +695,9 @@ def main():
         return
     if args.only == "gemv":
         print(json.dumps({"gemv": bench_gemv(mlxq, torch)}))
+        return
+    if args.only == "gemv_long":
+        print(json.dumps({"gemv_long": bench_gemv_long(mlxq, torch)}))
         return
     if args.only == "quantize":
         print(json.dumps({"quantize": bench_quantize(mlxq, torch)}))
