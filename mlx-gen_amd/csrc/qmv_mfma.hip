@@ -27,6 +27,9 @@
 //   * Q4, group 64: lanes q = 0,1 hold group 2t and lanes q = 2,3 group 2t+1.  Two
 //     v_permlane32_swap ops exchange words 2,3 of the low lane half with words 0,1 of the high
 //     half, after which words 0,1 of every lane belong to group 2t and words 2,3 to group 2t+1.
+//   * Q4, group 32: lane quarter q holds group 4t+q whole.  The same two swaps followed by two
+//     v_permlane16_swap ops (odd 16-lane rows against even rows) transpose the 4 x 4 block of
+//     (quarter, word), after which word i of every lane belongs to group 4t+i.
 // Each lane reads the activation run matching its code run from LDS (per-lane offsets below).
 // The 16x16 result holds column n = lane&15 for rows m = 4q + e.
 // A workgroup owns 16 weight rows; its waves split K and reduce through LDS at the end.
@@ -100,6 +103,14 @@ __device__ __forceinline__ void swap_lane_halves(uint32_t& lo_keep, uint32_t& hi
   hi_keep = r[1];
 }
 
+// v_permlane16_swap_b32: the odd 16-lane rows (1, 3) of `even_keep` trade places with the even
+// rows (0, 2) of `odd_keep`; row 2k keeps its own `even_keep`, row 2k + 1 its own `odd_keep`.
+__device__ __forceinline__ void swap_lane_rows(uint32_t& even_keep, uint32_t& odd_keep) {
+  const auto r = __builtin_amdgcn_permlane16_swap(even_keep, odd_keep, false, false);
+  even_keep = r[0];
+  odd_keep = r[1];
+}
+
 // Row pitch in floats of the per-row (s, zc) pair table in LDS: at least 2G, a multiple of 4 (the
 // fold reads 16 bytes) and an odd multiple of 4, so the 16 rows read in one step (one per lane)
 // land on 16 distinct 16-byte bank quads.  A pitch of exactly 2G puts every row on the same banks
@@ -113,22 +124,23 @@ __host__ __device__ constexpr int sz_pitch(int G) {
 // registers per lane of a 1024-thread workgroup (the counts the compiler reports for these
 // kernels): 8 steps only with one row, and for Q4 with group 64 (two groups per step) 6 steps
 // with at most two rows.  Larger combinations spilled (and spills doubled a launch's time).
-constexpr bool qmv_steps_fit(int bits, bool g64, int steps, int mr) {
-  return !(steps == 8 && mr > 1) && !(bits == 4 && g64 && steps == 6 && mr > 2);
+constexpr bool qmv_steps_fit(int bits, int gs, int steps, int mr) {
+  return !(steps == 8 && mr > 1) && !(bits == 4 && gs == 64 && steps == 6 && mr > 2) &&
+         !(gs == 32 && steps > 4);
 }
 
 }  // namespace
 
 // Scale/bias group slots one wave keeps: the groups its load steps touch (a group 128 of Q8 spans
 // two steps and may straddle two waves, hence the spare slot).
-__host__ __device__ constexpr int qmv_wave_groups(int bits, bool g64, int steps) {
-  return bits == 8 && !g64 ? (steps + 2) / 2 : (bits == 4 && g64 ? 2 * steps : steps);
+__host__ __device__ constexpr int qmv_wave_groups(int bits, int gs, int steps) {
+  return bits == 8 ? (gs == 128 ? (steps + 2) / 2 : steps) : steps * (128 / gs);
 }
 
 // Bytes of LDS one wave owns: its activation rows (M rows of steps * 64 bytes of codes' worth of
 // activations, padded so rows start on different banks) and its (s, zc) table.
-__host__ __device__ constexpr int qmv_wave_lds(int bits, bool g64, int steps, int M) {
-  return M * (steps * (512 / bits) * 2 + 16) + 16 * sz_pitch(qmv_wave_groups(bits, g64, steps)) * 4;
+__host__ __device__ constexpr int qmv_wave_lds(int bits, int gs, int steps, int M) {
+  return M * (steps * (512 / bits) * 2 + 16) + 16 * sz_pitch(qmv_wave_groups(bits, gs, steps)) * 4;
 }
 
 // One 16-row GEMV tile as seen by one wave: the wave's K range of T load steps, the operand
@@ -144,16 +156,18 @@ __host__ __device__ constexpr int qmv_wave_lds(int bits, bool g64, int steps, in
 // K*BITS/512 load steps covered by the waves of one matrix (T each, the last wave's range may end
 // past K), dynamic LDS of at least max(waves * qmv_wave_lds, waves * 16 * 17 * 4) bytes, every
 // buffer < 2 GiB.
-template <int BITS, bool G64, int STEPS, int MR, int T>
+template <int BITS, int GS, int STEPS, int MR, int T>
 struct GemvTile {
   static_assert(T >= STEPS, "ring shorter than the wave's steps");
   static constexpr int CPL = 512 / BITS;          // codes per row in one 64-byte load step
-  static constexpr int GS = G64 ? 64 : 128;       // group size
+  static constexpr bool G64 = GS == 64, G32 = GS == 32;
+  static_assert(!G32 || BITS == 4, "group 32 is built for Q4 only");
+  static constexpr int NACC = G32 ? 4 : 2;        // group accumulators per load step
   static constexpr int NM = BITS == 4 ? 4 : 2;    // MFMAs per load step
   static constexpr int E = MR < 4 ? MR : 4;       // result registers per lane that can hold a row < M
   static constexpr int XCH = T * CPL / 8;         // 16-byte activation chunks per row in the wave's range
   static constexpr int XSL = (XCH + 63) / 64;     // ... per lane
-  static constexpr int NGW = qmv_wave_groups(BITS, G64, T);
+  static constexpr int NGW = qmv_wave_groups(BITS, GS, T);
   static constexpr int PW = sz_pitch(NGW);        // (s, zc) table row pitch, floats
   static constexpr int SBL = (16 * NGW + 63) / 64;  // scale entries per lane
   static constexpr int XW = T * CPL * 2 + 16;       // LDS pitch of the wave's activation rows
@@ -262,6 +276,7 @@ struct GemvTile {
     for (int i = 0; i < NM; ++i) {
       int k;
       if constexpr (BITS == 8) k = 16 * q + 8 * i;
+      else if constexpr (G32) k = 32 * i + 8 * q;  // after the word transpose: MFMA i = group i
       else if constexpr (!G64) k = 32 * q + 8 * i;
       else if (i < 2) k = (q < 2 ? 32 * q : 32 * (q - 2) + 16) + 8 * i;
       else k = (q < 2 ? 64 + 32 * q : 32 * q + 16) + 8 * (i - 2);
@@ -286,13 +301,17 @@ struct GemvTile {
     using SZ = typename std::conditional<BITS == 4 && G64, f32x4, f32x2>::type;
     bf16x8 a[T][NM];
     SZ p[T];
-    f32x4 acc[T][2], xsum[T][2];
+    f32x4 p32[T][2];  // group 32: the (s, zc) pairs of the step's four groups
+    f32x4 acc[T][NACC], xsum[T][NACC];
 
     // A step's LDS operands: its activation runs and its (s, zc) pairs.
     auto read_step = [&](int d) {
 #pragma unroll
       for (int i = 0; i < NM; ++i) a[d][i] = *reinterpret_cast<const bf16x8*>(xa[i] + d * (CPL * 2));
-      if constexpr (BITS == 4 && G64) {
+      if constexpr (G32) {
+        p32[d][0] = *reinterpret_cast<const f32x4*>(sz + 8 * d);  // groups 4ls, 4ls+1
+        p32[d][1] = *reinterpret_cast<const f32x4*>(sz + 8 * d + 4);  // groups 4ls+2, 4ls+3
+      } else if constexpr (BITS == 4 && G64) {
         p[d] = *reinterpret_cast<const f32x4*>(sz + 4 * d);  // groups 2ls, 2ls+1
       } else {
         // Q4/128 and Q8/64: one group per step; Q8/128: a group every two steps
@@ -308,15 +327,23 @@ struct GemvTile {
       if constexpr (BITS == 4 && G64) {
         swap_lane_halves(w[0], w[2]);
         swap_lane_halves(w[1], w[3]);
+      } else if constexpr (G32) {
+        // Quarter q's 16 bytes are group q of the step (words = 8-code runs).  Transpose the
+        // 4 x 4 (quarter, word) block: afterwards word i of quarter q is run q of group i, so
+        // MFMA i covers group i alone.
+        swap_lane_halves(w[0], w[2]);
+        swap_lane_halves(w[1], w[3]);
+        swap_lane_rows(w[0], w[1]);
+        swap_lane_rows(w[2], w[3]);
       }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < NACC; ++h) {
         acc[d][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         xsum[d][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       }
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
-        const int h = (BITS == 4 && G64) ? i >> 1 : 0;
+        const int h = G32 ? i : ((BITS == 4 && G64) ? i >> 1 : 0);
         const bf16x8 b = BITS == 4 ? unpack_q4(w[i]) : cvt_q8(w[2 * i], w[2 * i + 1]);
         acc[d][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][i], b, acc[d][h], 0, 0, 0);
         xsum[d][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][i], ones, xsum[d][h], 0, 0, 0);
@@ -326,7 +353,12 @@ struct GemvTile {
     // A step's fold into the result.  The result is pinned after each fold: otherwise the
     // compiler sinks every fold below the last step and keeps all steps' products live at once.
     auto fold_step = [&](int d) {
-      if constexpr (BITS == 4 && G64) {
+      if constexpr (G32) {
+        fold1(acc[d][0], xsum[d][0], p32[d][0][0], p32[d][0][1]);
+        fold1(acc[d][1], xsum[d][1], p32[d][0][2], p32[d][0][3]);
+        fold1(acc[d][2], xsum[d][2], p32[d][1][0], p32[d][1][1]);
+        fold1(acc[d][3], xsum[d][3], p32[d][1][2], p32[d][1][3]);
+      } else if constexpr (BITS == 4 && G64) {
         fold1(acc[d][0], xsum[d][0], p[d][0], p[d][1]);
         fold1(acc[d][1], xsum[d][1], p[d][2], p[d][3]);
       } else {
@@ -388,7 +420,7 @@ __device__ __forceinline__ void gemv_reduce_store(unsigned char* lds, const floa
 // Each wave stages only its own operands (its K range of the activations, the scales and biases
 // of its groups) into its own LDS region, so it starts on its weights as soon as its own operands
 // land; the only workgroup barrier is the final split-K reduction.
-template <int BITS, bool G64, int STEPS, int MR, int NMAT, int RING>
+template <int BITS, int GS, int STEPS, int MR, int NMAT, int RING>
 __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
     const uint16_t* __restrict__ x, int M, int K, const uint32_t* __restrict__ wq,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
@@ -402,7 +434,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   const int W = (NT >> 6) / NMAT;  // waves per matrix
   const int mat = NMAT == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave_all / W);
   const int n0 = blockIdx.x * 16;
-  using Tile = GemvTile<BITS, G64, STEPS, MR, STEPS * RING>;
+  using Tile = GemvTile<BITS, GS, STEPS, MR, STEPS * RING>;
   Tile t(lane, wave_all, wave_all - mat * W, n0, M, K, N, lds);
   const int sb_total = (int)(((uint32_t)N * (uint32_t)t.G * 2u + 3u) & ~3u);  // whole dwords
   t.issue_x(make_rsrc(x, M * K * 2));
@@ -666,9 +698,10 @@ struct QmvPlan {
 constexpr int kStepChoices[] = {1, 2, 3, 4, 6, 8};
 
 // Whether a kernel with a ring of `ring` rounds exists: two rounds only with 4..8 load registers
-// and at most four activation rows (more rows split into launches of four or two).
-constexpr bool qmv_ring_built(int bits, int steps, int mr, int ring) {
-  return ring == 1 || (ring == 2 && (bits == 4 || bits == 8) && steps >= 4 && mr <= 4);
+// and at most four activation rows (two with group 32, whose four-row ring spilled; more rows
+// split into launches of four or two).
+constexpr bool qmv_ring_built(int bits, int gs, int steps, int mr, int ring) {
+  return ring == 1 || (ring == 2 && (bits == 4 || bits == 8) && steps >= 4 && mr <= (gs == 32 ? 2 : 4));
 }
 
 // Picks the load steps per wave: among the counts that divide the row's load steps, fit a
@@ -696,7 +729,7 @@ static bool qmv_plan_rows(int64_t M, int64_t K, int gs, int bits, int nmat, QmvP
     bool found = false;
     int64_t best_cost = 0, best_pad = 0;
     for (int steps : kStepChoices) {
-      if (!qmv_steps_fit(bits, gs == 64, steps, mr) || !qmv_ring_built(bits, steps, mr, ring)) continue;
+      if (!qmv_steps_fit(bits, gs, steps, mr) || !qmv_ring_built(bits, gs, steps, mr, ring)) continue;
       const int64_t t = (int64_t)steps * ring;  // load steps per wave
       if (pass == 0 && LS % t != 0) continue;
       const int64_t wpm = (LS + t - 1) / t;
@@ -704,7 +737,7 @@ static bool qmv_plan_rows(int64_t M, int64_t K, int gs, int bits, int nmat, QmvP
       if (waves > kMaxWaves) continue;
       // activation chunks a lane stages (registers): at most kCopySlots across the rows
       if (mr * ((t * cpl / 8 + 63) / 64) > kCopySlots) continue;
-      const int64_t operands = waves * (int64_t)qmv_wave_lds(bits, gs == 64, (int)t, (int)M);
+      const int64_t operands = waves * (int64_t)qmv_wave_lds(bits, gs, (int)t, (int)M);
       const int64_t red = waves * 16 * 17 * 4;
       const int64_t lds = operands > red ? operands : red;
       if (lds > kMaxLds) continue;
@@ -722,7 +755,8 @@ static bool qmv_plan_rows(int64_t M, int64_t K, int gs, int bits, int nmat, QmvP
 }
 
 bool qmv_plan(int64_t M, int64_t K, int gs, int bits, int nmat, QmvPlan& p) {
-  if (M < 1 || M > 8 || (bits != 4 && bits != 8) || (gs != 64 && gs != 128)) return false;
+  if (M < 1 || M > 8 || (bits != 4 && bits != 8)) return false;
+  if (gs != 64 && gs != 128 && !(gs == 32 && bits == 4)) return false;
   const int64_t cpl = 512 / bits;
   if (K <= 0 || K % cpl != 0 || K % gs != 0) return false;
   if (qmv_plan_rows(M, K, gs, bits, nmat, p)) return true;
@@ -744,7 +778,7 @@ struct QmvArgs {
 
 }  // namespace
 
-template <int BITS, bool G64, int STEPS, int MR, int NMAT, int RING>
+template <int BITS, int GS, int STEPS, int MR, int NMAT, int RING>
 static int launch_qmv_mfma(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
   // The dynamic-LDS limit is raised once per device (any thread may get here first; setting it
   // twice is harmless).
@@ -752,60 +786,61 @@ static int launch_qmv_mfma(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return set_error(MLXQ_EDEVICE, "qmv: no current device");
   if (dev < 0 || dev >= 64 || !attr_set[dev].load(std::memory_order_acquire)) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_mfma_kernel<BITS, G64, STEPS, MR, NMAT, RING>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_mfma_kernel<BITS, GS, STEPS, MR, NMAT, RING>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds) != hipSuccess)
       return set_error(MLXQ_EDEVICE, "qmv: hipFuncSetAttribute failed");
     if (dev >= 0 && dev < 64) attr_set[dev].store(true, std::memory_order_release);
   }
-  hipLaunchKernelGGL((qmv_mfma_kernel<BITS, G64, STEPS, MR, NMAT, RING>), dim3((unsigned)((a.N + 15) / 16)),
+  hipLaunchKernelGGL((qmv_mfma_kernel<BITS, GS, STEPS, MR, NMAT, RING>), dim3((unsigned)((a.N + 15) / 16)),
                      dim3(p.waves * 64), p.lds, st, (const uint16_t*)a.x, (int)a.M, (int)a.K, a.wq,
                      (const uint16_t*)a.s, (const uint16_t*)a.b, a.wq2, (const uint16_t*)a.s2,
                      (const uint16_t*)a.b2, (int)a.N, (uint16_t*)a.y);
   return check_launch(NMAT == 2 ? "swiglu_qmv" : "qmv_mfma");
 }
 
-template <int BITS, bool G64, int STEPS, int MR, int NMAT>
+template <int BITS, int GS, int STEPS, int MR, int NMAT>
 static int qmv_mr(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
-  if constexpr (qmv_steps_fit(BITS, G64, STEPS, MR)) {
-    if (p.ring == 1) return launch_qmv_mfma<BITS, G64, STEPS, MR, NMAT, 1>(a, p, st);
-    if constexpr (qmv_ring_built(BITS, STEPS, MR, 2))
-      if (p.ring == 2) return launch_qmv_mfma<BITS, G64, STEPS, MR, NMAT, 2>(a, p, st);
+  if constexpr (qmv_steps_fit(BITS, GS, STEPS, MR)) {
+    if (p.ring == 1) return launch_qmv_mfma<BITS, GS, STEPS, MR, NMAT, 1>(a, p, st);
+    if constexpr (qmv_ring_built(BITS, GS, STEPS, MR, 2))
+      if (p.ring == 2) return launch_qmv_mfma<BITS, GS, STEPS, MR, NMAT, 2>(a, p, st);
     return set_error(MLXQ_EINVAL, "qmv: no kernel with %d load rounds for this plan", p.ring);
   } else {
     return set_error(MLXQ_EINVAL, "qmv: %d load steps per wave with %d rows exceed the registers", STEPS, MR);
   }
 }
 
-template <int BITS, bool G64, int STEPS, int NMAT>
+template <int BITS, int GS, int STEPS, int NMAT>
 static int qmv_rows(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
   switch (p.mr) {
-    case 1: return qmv_mr<BITS, G64, STEPS, 1, NMAT>(a, p, st);
-    case 2: return qmv_mr<BITS, G64, STEPS, 2, NMAT>(a, p, st);
-    case 4: return qmv_mr<BITS, G64, STEPS, 4, NMAT>(a, p, st);
-    default: return qmv_mr<BITS, G64, STEPS, 8, NMAT>(a, p, st);
+    case 1: return qmv_mr<BITS, GS, STEPS, 1, NMAT>(a, p, st);
+    case 2: return qmv_mr<BITS, GS, STEPS, 2, NMAT>(a, p, st);
+    case 4: return qmv_mr<BITS, GS, STEPS, 4, NMAT>(a, p, st);
+    default: return qmv_mr<BITS, GS, STEPS, 8, NMAT>(a, p, st);
   }
 }
 
-template <int BITS, bool G64, int NMAT>
+template <int BITS, int GS, int NMAT>
 static int qmv_steps(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
   switch (p.steps) {
-    case 1: return qmv_rows<BITS, G64, 1, NMAT>(a, p, st);
-    case 2: return qmv_rows<BITS, G64, 2, NMAT>(a, p, st);
-    case 3: return qmv_rows<BITS, G64, 3, NMAT>(a, p, st);
-    case 4: return qmv_rows<BITS, G64, 4, NMAT>(a, p, st);
-    case 6: return qmv_rows<BITS, G64, 6, NMAT>(a, p, st);
-    default: return qmv_rows<BITS, G64, 8, NMAT>(a, p, st);
+    case 1: return qmv_rows<BITS, GS, 1, NMAT>(a, p, st);
+    case 2: return qmv_rows<BITS, GS, 2, NMAT>(a, p, st);
+    case 3: return qmv_rows<BITS, GS, 3, NMAT>(a, p, st);
+    case 4: return qmv_rows<BITS, GS, 4, NMAT>(a, p, st);
+    case 6: return qmv_rows<BITS, GS, 6, NMAT>(a, p, st);
+    default: return qmv_rows<BITS, GS, 8, NMAT>(a, p, st);
   }
 }
 
 template <int NMAT>
 static int qmv_kind(const QmvArgs& a, int gs, int bits, const QmvPlan& p, hipStream_t st) {
   if (bits == 8) {
-    if (gs == 64) return qmv_steps<8, true, NMAT>(a, p, st);
-    return qmv_steps<8, false, NMAT>(a, p, st);
+    if (gs == 64) return qmv_steps<8, 64, NMAT>(a, p, st);
+    return qmv_steps<8, 128, NMAT>(a, p, st);
   }
-  if (gs == 64) return qmv_steps<4, true, NMAT>(a, p, st);
-  return qmv_steps<4, false, NMAT>(a, p, st);
+  if (gs == 32) return qmv_steps<4, 32, NMAT>(a, p, st);
+  if (gs == 64) return qmv_steps<4, 64, NMAT>(a, p, st);
+  return qmv_steps<4, 128, NMAT>(a, p, st);
 }
 
 // CUs of the current device (cached per device).

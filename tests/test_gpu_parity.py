@@ -487,6 +487,42 @@ def test_qmv_tile_kernel_long_and_ragged_k(mlxq, M, K, N, gs, bits):
     assert_close(y, oracle.bf16_round(exact), f"tile long K M={M} K={K} N={N} gs={gs} b={bits}")
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("K,N", [(3072, 300), (8192, 130), (11008, 70), (14336, 40), (512, 33), (16384, 24)])
+def test_qmv_group32_on_matrix_cores(mlxq, M, K, N):
+    """Q4 with group 32 on the tile kernel (it ran the VALU GEMV before): each lane quarter's 16
+    bytes are one whole group, and a 4 x 4 transpose of (quarter, word) by permlane swaps puts
+    each MFMA on one group.  Exact splits (K = 3072, 8192, 512), the ragged last wave (11008), two
+    register rounds (11008, 14336, 16384) and launches of two rows (M >= 3 at K >= 11008)."""
+    banner("qmv group 32", M, K, N)
+    rng = np.random.default_rng(M * 5 + K + N + 32)
+    x = bf16_normal(rng, (M, K))
+    w = bf16_normal(rng, (N, K), 0.02)
+    rwq, rs, rb = oracle.quantize(w, 32, 4, sb_bf16=True)
+    y = to_np(mlxq.quantized_matmul(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), True, 32, 4))
+    exact = oracle.quantized_matmul(x, rwq, rs, rb, 32, 4, w_bf16=False, out_bf16=False)
+    _close_to_exact(y, exact, f"group 32 M={M} K={K} N={N}")
+    assert_close(y, oracle.bf16_round(exact), f"group 32 M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+@pytest.mark.parametrize("K,F", [(3072, 200), (8192, 64), (5120, 100)])
+def test_swiglu_group32(mlxq, M, K, F):
+    """The fused SwiGLU launch with Q4 group 32 (two-row launches at M >= 3 for K = 8192)."""
+    banner("swiglu group 32", M, K, F)
+    rng = np.random.default_rng(M + K + F + 32)
+    x = bf16_normal(rng, (M, K))
+    tg, tu = [oracle.quantize(bf16_normal(rng, (F, K), 0.02), 32, 4, sb_bf16=True) for _ in range(2)]
+    h = to_np(mlxq.swiglu(to_gpu(x), [wq_to_gpu(tg[0]), to_gpu(tg[1]), to_gpu(tg[2])],
+                          [wq_to_gpu(tu[0]), to_gpu(tu[1]), to_gpu(tu[2])], 32, 4))
+    gr = oracle.quantized_matmul(x, *tg, 32, 4, w_bf16=False, out_bf16=True)
+    ur = oracle.quantized_matmul(x, *tu, 32, 4, w_bf16=False, out_bf16=True)
+    ref = oracle.bf16_round(oracle.bf16_round(np.vectorize(oracle.silu)(gr).astype(np.float32)) * ur)
+    assert_close(h, ref, f"swiglu group 32 M={M} K={K} F={F}")
+    print(f"    bit-identical outputs: {np.mean(h == ref) * 100:.2f} %", flush=True)
+    assert np.mean(h == ref) > 0.95
+
+
 @pytest.mark.parametrize("M", [2, 3, 4, 5, 8])
 @pytest.mark.parametrize("K,F,gs,bits", [(5120, 300, 64, 4), (7168, 130, 64, 4), (12288, 40, 128, 4),
                                          (20480, 24, 64, 4), (6144, 48, 128, 8)])
