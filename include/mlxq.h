@@ -220,10 +220,10 @@ int mlxq_qmm_experts(const void* x, int x_dtype, int x_per_expert, int64_t E, in
  * with gate/up quantized linears [F,K] sharing x [M,K]; one launch streams both weight matrices
  * (launches of four or two activation rows when the M rows do not fit one workgroup):
  *   h = round(round(silu(round(x.Wg^T))) * round(x.Wu^T))      (round() to bf16)
- * Decode form only: bf16 x and scales, 1 <= M <= 8, group_size 64 or 128 (or 32 with Q4), K a
- * multiple of 512/bits within the fused kernels' reach (Q4: K <= 16384 at M = 1, 12288 at
- * M = 2..8, 8192 with group 32; Q8: 8192 at M = 1, 6144 at M = 2..8); anything else returns
- * MLXQ_EUNSUPPORTED (callers then run the two linears).
+ * Decode form only: bf16 x and scales, 1 <= M <= 8, group_size 32, 64 or 128, K a multiple of
+ * 512/bits within the fused kernels' reach (Q4: K <= 16384 at M = 1, 12288 at M = 2..8, 8192
+ * with group 32; Q8: 8192 at M = 1, 6144 at M = 2..8, 4096 with group 32); anything else
+ * returns MLXQ_EUNSUPPORTED (callers then run the two linears).
  * This entry point has no single counterpart in the reference; it replaces a three-op sequence.
  */
 int mlxq_swiglu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq_gate,

@@ -400,8 +400,8 @@ int mlxq_swiglu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
   if (!swiglu_qmv_applicable(x_dtype, sb_dtype, M, K, F, group_size, bits))
     return set_error(MLXQ_EUNSUPPORTED,
                      "swiglu: the fused decode form takes bf16 x and scales, 1 <= M <= 8, group_size "
-                     "64 or 128 (or 32 with bits 4) and K a multiple of %d whose activation rows and "
-                     "load steps fit one workgroup (got M=%lld K=%lld)", 512 / bits, (long long)M,
+                     "32, 64 or 128 and K a multiple of %d whose activation rows and load steps fit "
+                     "one workgroup (got M=%lld K=%lld)", 512 / bits, (long long)M,
                      (long long)K);
   return run_swiglu_qmv(x, M, K, wq_gate, scales_gate, biases_gate, wq_up, scales_up, biases_up, F,
                         group_size, bits, h, (hipStream_t)stream);

@@ -27,6 +27,8 @@
 //   * Q4, group 64: lanes q = 0,1 hold group 2t and lanes q = 2,3 group 2t+1.  Two
 //     v_permlane32_swap ops exchange words 2,3 of the low lane half with words 0,1 of the high
 //     half, after which words 0,1 of every lane belong to group 2t and words 2,3 to group 2t+1.
+//   * Q8, group 32: lanes q = 0,1 hold group 2t and q = 2,3 group 2t+1; the same two swaps as
+//     for Q4 group 64 make words 0,1 (MFMA 0) group 2t and words 2,3 (MFMA 1) group 2t+1.
 //   * Q4, group 32: lane quarter q holds group 4t+q whole.  The same two swaps followed by two
 //     v_permlane16_swap ops (odd 16-lane rows against even rows) transpose the 4 x 4 block of
 //     (quarter, word), after which word i of every lane belongs to group 4t+i.
@@ -134,7 +136,7 @@ constexpr bool qmv_steps_fit(int bits, int gs, int steps, int mr) {
 // Scale/bias group slots one wave keeps: the groups its load steps touch (a group 128 of Q8 spans
 // two steps and may straddle two waves, hence the spare slot).
 __host__ __device__ constexpr int qmv_wave_groups(int bits, int gs, int steps) {
-  return bits == 8 ? (gs == 128 ? (steps + 2) / 2 : steps) : steps * (128 / gs);
+  return bits == 8 ? (gs == 128 ? (steps + 2) / 2 : steps * (64 / gs)) : steps * (128 / gs);
 }
 
 // Bytes of LDS one wave owns: its activation rows (M rows of steps * 64 bytes of codes' worth of
@@ -161,8 +163,10 @@ struct GemvTile {
   static_assert(T >= STEPS, "ring shorter than the wave's steps");
   static constexpr int CPL = 512 / BITS;          // codes per row in one 64-byte load step
   static constexpr bool G64 = GS == 64, G32 = GS == 32;
-  static_assert(!G32 || BITS == 4, "group 32 is built for Q4 only");
-  static constexpr int NACC = G32 ? 4 : 2;        // group accumulators per load step
+  static constexpr bool Q4G32 = BITS == 4 && G32;  // four groups per step, one per lane quarter
+  // two groups per step, one per lane half (Q4 group 64, Q8 group 32)
+  static constexpr bool PAIR = (BITS == 4 && G64) || (BITS == 8 && G32);
+  static constexpr int NACC = Q4G32 ? 4 : 2;      // group accumulators per load step
   static constexpr int NM = BITS == 4 ? 4 : 2;    // MFMAs per load step
   static constexpr int E = MR < 4 ? MR : 4;       // result registers per lane that can hold a row < M
   static constexpr int XCH = T * CPL / 8;         // 16-byte activation chunks per row in the wave's range
@@ -275,7 +279,8 @@ struct GemvTile {
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
       int k;
-      if constexpr (BITS == 8) k = 16 * q + 8 * i;
+      if constexpr (BITS == 8 && G32) k = (q < 2 ? 16 * q : 16 * (q - 2) + 8) + 32 * i;
+      else if constexpr (BITS == 8) k = 16 * q + 8 * i;
       else if constexpr (G32) k = 32 * i + 8 * q;  // after the word transpose: MFMA i = group i
       else if constexpr (!G64) k = 32 * q + 8 * i;
       else if (i < 2) k = (q < 2 ? 32 * q : 32 * (q - 2) + 16) + 8 * i;
@@ -298,7 +303,7 @@ struct GemvTile {
     // m >= M only feeds result row m, which is never stored).  The 16 lanes of a quarter then read
     // at most M distinct addresses (broadcast); a read restricted to the lanes of rows < M cost
     // the compiler ten 64-bit register copies per step to keep the other lanes' operands.
-    using SZ = typename std::conditional<BITS == 4 && G64, f32x4, f32x2>::type;
+    using SZ = typename std::conditional<PAIR, f32x4, f32x2>::type;
     bf16x8 a[T][NM];
     SZ p[T];
     f32x4 p32[T][2];  // group 32: the (s, zc) pairs of the step's four groups
@@ -308,10 +313,10 @@ struct GemvTile {
     auto read_step = [&](int d) {
 #pragma unroll
       for (int i = 0; i < NM; ++i) a[d][i] = *reinterpret_cast<const bf16x8*>(xa[i] + d * (CPL * 2));
-      if constexpr (G32) {
+      if constexpr (Q4G32) {
         p32[d][0] = *reinterpret_cast<const f32x4*>(sz + 8 * d);  // groups 4ls, 4ls+1
         p32[d][1] = *reinterpret_cast<const f32x4*>(sz + 8 * d + 4);  // groups 4ls+2, 4ls+3
-      } else if constexpr (BITS == 4 && G64) {
+      } else if constexpr (PAIR) {
         p[d] = *reinterpret_cast<const f32x4*>(sz + 4 * d);  // groups 2ls, 2ls+1
       } else {
         // Q4/128 and Q8/64: one group per step; Q8/128: a group every two steps
@@ -324,10 +329,10 @@ struct GemvTile {
     auto mfma_step = [&](int d) {
       const int slot = d % STEPS;
       uint32_t w[4] = {wv[slot][0], wv[slot][1], wv[slot][2], wv[slot][3]};
-      if constexpr (BITS == 4 && G64) {
+      if constexpr (PAIR) {  // Q8 group 32: words 0,1 and 2,3 are its two MFMAs' pairs
         swap_lane_halves(w[0], w[2]);
         swap_lane_halves(w[1], w[3]);
-      } else if constexpr (G32) {
+      } else if constexpr (Q4G32) {
         // Quarter q's 16 bytes are group q of the step (words = 8-code runs).  Transpose the
         // 4 x 4 (quarter, word) block: afterwards word i of quarter q is run q of group i, so
         // MFMA i covers group i alone.
@@ -343,7 +348,7 @@ struct GemvTile {
       }
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
-        const int h = G32 ? i : ((BITS == 4 && G64) ? i >> 1 : 0);
+        const int h = (Q4G32 || (BITS == 8 && G32)) ? i : ((BITS == 4 && G64) ? i >> 1 : 0);
         const bf16x8 b = BITS == 4 ? unpack_q4(w[i]) : cvt_q8(w[2 * i], w[2 * i + 1]);
         acc[d][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][i], b, acc[d][h], 0, 0, 0);
         xsum[d][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][i], ones, xsum[d][h], 0, 0, 0);
@@ -353,12 +358,12 @@ struct GemvTile {
     // A step's fold into the result.  The result is pinned after each fold: otherwise the
     // compiler sinks every fold below the last step and keeps all steps' products live at once.
     auto fold_step = [&](int d) {
-      if constexpr (G32) {
+      if constexpr (Q4G32) {
         fold1(acc[d][0], xsum[d][0], p32[d][0][0], p32[d][0][1]);
         fold1(acc[d][1], xsum[d][1], p32[d][0][2], p32[d][0][3]);
         fold1(acc[d][2], xsum[d][2], p32[d][1][0], p32[d][1][1]);
         fold1(acc[d][3], xsum[d][3], p32[d][1][2], p32[d][1][3]);
-      } else if constexpr (BITS == 4 && G64) {
+      } else if constexpr (PAIR) {
         fold1(acc[d][0], xsum[d][0], p[d][0], p[d][1]);
         fold1(acc[d][1], xsum[d][1], p[d][2], p[d][3]);
       } else {
@@ -756,7 +761,7 @@ static bool qmv_plan_rows(int64_t M, int64_t K, int gs, int bits, int nmat, QmvP
 
 bool qmv_plan(int64_t M, int64_t K, int gs, int bits, int nmat, QmvPlan& p) {
   if (M < 1 || M > 8 || (bits != 4 && bits != 8)) return false;
-  if (gs != 64 && gs != 128 && !(gs == 32 && bits == 4)) return false;
+  if (gs != 32 && gs != 64 && gs != 128) return false;
   const int64_t cpl = 512 / bits;
   if (K <= 0 || K % cpl != 0 || K % gs != 0) return false;
   if (qmv_plan_rows(M, K, gs, bits, nmat, p)) return true;
@@ -835,6 +840,7 @@ static int qmv_steps(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
 template <int NMAT>
 static int qmv_kind(const QmvArgs& a, int gs, int bits, const QmvPlan& p, hipStream_t st) {
   if (bits == 8) {
+    if (gs == 32) return qmv_steps<8, 32, NMAT>(a, p, st);
     if (gs == 64) return qmv_steps<8, 64, NMAT>(a, p, st);
     return qmv_steps<8, 128, NMAT>(a, p, st);
   }

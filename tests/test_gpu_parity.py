@@ -488,35 +488,38 @@ def test_qmv_tile_kernel_long_and_ragged_k(mlxq, M, K, N, gs, bits):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
-@pytest.mark.parametrize("K,N", [(3072, 300), (8192, 130), (11008, 70), (14336, 40), (512, 33), (16384, 24)])
-def test_qmv_group32_on_matrix_cores(mlxq, M, K, N):
-    """Q4 with group 32 on the tile kernel (it ran the VALU GEMV before): each lane quarter's 16
+@pytest.mark.parametrize("K,N,bits", [(3072, 300, 4), (8192, 130, 4), (11008, 70, 4), (14336, 40, 4),
+                                      (512, 33, 4), (16384, 24, 4), (3072, 200, 8), (8192, 64, 8),
+                                      (4160, 90, 8)])
+def test_qmv_group32_on_matrix_cores(mlxq, M, K, N, bits):
+    """Group 32 on the tile kernel (it ran the VALU GEMV before).  Q4: each lane quarter's 16
     bytes are one whole group, and a 4 x 4 transpose of (quarter, word) by permlane swaps puts
-    each MFMA on one group.  Exact splits (K = 3072, 8192, 512), the ragged last wave (11008), two
-    register rounds (11008, 14336, 16384) and launches of two rows (M >= 3 at K >= 11008)."""
-    banner("qmv group 32", M, K, N)
-    rng = np.random.default_rng(M * 5 + K + N + 32)
+    each MFMA on one group; exact splits (K = 3072, 8192, 512), the ragged last wave (11008), two
+    register rounds (11008, 14336, 16384) and launches of two rows (M >= 3 at K >= 11008).  Q8:
+    each lane half holds one group and two half swaps regroup the word pairs (K = 4160 ragged)."""
+    banner("qmv group 32", M, K, N, bits)
+    rng = np.random.default_rng(M * 5 + K + N + 32 + bits)
     x = bf16_normal(rng, (M, K))
     w = bf16_normal(rng, (N, K), 0.02)
-    rwq, rs, rb = oracle.quantize(w, 32, 4, sb_bf16=True)
-    y = to_np(mlxq.quantized_matmul(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), True, 32, 4))
-    exact = oracle.quantized_matmul(x, rwq, rs, rb, 32, 4, w_bf16=False, out_bf16=False)
-    _close_to_exact(y, exact, f"group 32 M={M} K={K} N={N}")
-    assert_close(y, oracle.bf16_round(exact), f"group 32 M={M} K={K} N={N}")
+    rwq, rs, rb = oracle.quantize(w, 32, bits, sb_bf16=True)
+    y = to_np(mlxq.quantized_matmul(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), True, 32, bits))
+    exact = oracle.quantized_matmul(x, rwq, rs, rb, 32, bits, w_bf16=False, out_bf16=False)
+    _close_to_exact(y, exact, f"group 32 M={M} K={K} N={N} b={bits}")
+    assert_close(y, oracle.bf16_round(exact), f"group 32 M={M} K={K} N={N} b={bits}")
 
 
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
-@pytest.mark.parametrize("K,F", [(3072, 200), (8192, 64), (5120, 100)])
-def test_swiglu_group32(mlxq, M, K, F):
-    """The fused SwiGLU launch with Q4 group 32 (two-row launches at M >= 3 for K = 8192)."""
-    banner("swiglu group 32", M, K, F)
-    rng = np.random.default_rng(M + K + F + 32)
+@pytest.mark.parametrize("K,F,bits", [(3072, 200, 4), (8192, 64, 4), (5120, 100, 4), (3072, 96, 8)])
+def test_swiglu_group32(mlxq, M, K, F, bits):
+    """The fused SwiGLU launch with group 32 (two-row launches at M >= 3 for Q4 K = 8192)."""
+    banner("swiglu group 32", M, K, F, bits)
+    rng = np.random.default_rng(M + K + F + 32 + bits)
     x = bf16_normal(rng, (M, K))
-    tg, tu = [oracle.quantize(bf16_normal(rng, (F, K), 0.02), 32, 4, sb_bf16=True) for _ in range(2)]
+    tg, tu = [oracle.quantize(bf16_normal(rng, (F, K), 0.02), 32, bits, sb_bf16=True) for _ in range(2)]
     h = to_np(mlxq.swiglu(to_gpu(x), [wq_to_gpu(tg[0]), to_gpu(tg[1]), to_gpu(tg[2])],
-                          [wq_to_gpu(tu[0]), to_gpu(tu[1]), to_gpu(tu[2])], 32, 4))
-    gr = oracle.quantized_matmul(x, *tg, 32, 4, w_bf16=False, out_bf16=True)
-    ur = oracle.quantized_matmul(x, *tu, 32, 4, w_bf16=False, out_bf16=True)
+                          [wq_to_gpu(tu[0]), to_gpu(tu[1]), to_gpu(tu[2])], 32, bits))
+    gr = oracle.quantized_matmul(x, *tg, 32, bits, w_bf16=False, out_bf16=True)
+    ur = oracle.quantized_matmul(x, *tu, 32, bits, w_bf16=False, out_bf16=True)
     ref = oracle.bf16_round(oracle.bf16_round(np.vectorize(oracle.silu)(gr).astype(np.float32)) * ur)
     assert_close(h, ref, f"swiglu group 32 M={M} K={K} F={F}")
     print(f"    bit-identical outputs: {np.mean(h == ref) * 100:.2f} %", flush=True)
