@@ -47,6 +47,12 @@ extern "C" {
 typedef enum {
   MLXQ_FLOAT32 = 0,
   MLXQ_BFLOAT16 = 1,
+  /* fp16 is taken as the activation x of quantized_matmul, qmv, qmv_valu, linear, linear_noalloc,
+   * lora_residual and qmm_experts: the dtype SDXL's U-Net, CLIP encoders and ControlNets run in
+   * (mlx-gen-sdxl/src/model.rs:216) over bf16-packed weights (src/adapters.rs:508-537).  MLX
+   * promotes fp16 against bf16 or f32 to f32, so those products and their results are f32.
+   * Elsewhere (weights, scales, biases, LoRA factors, outputs) fp16 returns MLXQ_EUNSUPPORTED. */
+  MLXQ_FLOAT16 = 2,
 } mlxq_dtype;
 
 typedef enum {
@@ -65,8 +71,11 @@ typedef enum {
   /* tanh-approximate GELU as separate ops in the input dtype, src/nn.rs:321-329 (FLUX
    * single-stream FFN and GeluApprox, mlx-gen-flux/src/transformer.rs:506,708,979) */
   MLXQ_ACT_GELU_TANH = 2,
-  /* dtype-preserving exact GELU, src/nn.rs:344-355 gelu_exact (x * (1 + erf(x / sqrt2))) / 2 as
-   * separate ops in the input dtype; the GELU of most crates' FFNs (bernini, boogu, pid, svd, ...) */
+  /* dtype-preserving exact GELU, src/nn.rs:344-355 gelu_exact (x * (1 + erf(x / sqrt2))) / 2; the
+   * GELU of most crates' FFNs (bernini, boogu, pid, svd, ...).  In bf16 each op of the sequence is
+   * rounded to bf16 (the uncompiled op sequence).  The reference runs it under compile(f, true),
+   * whose fused kernel its own comments say rounds 16-bit types differently from the separate ops
+   * (src/nn.rs:339-343): bf16 parity with the reference is unpinned.  f32 is unaffected. */
   MLXQ_ACT_GELU_EXACT = 3,
 } mlxq_activation;
 
@@ -97,8 +106,9 @@ int mlxq_dequantize(const uint32_t* wq, const void* scales, const void* biases, 
  * and biases to their result type); fp32 accumulation.  Only transpose=1 (y = x . W^T, the only
  * form the reference uses) is implemented; transpose=0 returns MLXQ_EUNSUPPORTED.
  * Dispatch: bf16 x and scales with M > 8 run the MFMA GEMM (weights dequantized to bf16 tiles);
- * bf16 with M <= 8 runs the bandwidth-bound GEMV (weights dequantized exactly in f32, factored per
- * group); an f32 operand runs the f32 kernels (exact f32 dequant, f32 result).
+ * bf16 with M <= 8 runs the bandwidth-bound GEMV (weights dequantized in f32, factored per
+ * group); an f32 operand, or fp16 x (which MLX promotes to f32 against bf16 or f32 scales), runs
+ * the f32 kernels (exact f32 dequant, f32 result).
  */
 int mlxq_quantized_matmul(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
                           const void* scales, const void* biases, int sb_dtype, int64_t N,
@@ -122,7 +132,7 @@ int mlxq_embedding(const int32_t* ids, int64_t T, const uint32_t* wq, const void
 int mlxq_qmm(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
              const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
              int bits, void* y, void* stream);
-/* GEMV; bf16 or f32 x; 1 <= M <= 8; y in promote(x_dtype, sb_dtype). */
+/* GEMV; bf16, f32 or fp16 x; 1 <= M <= 8; y in promote(x_dtype, sb_dtype). */
 int mlxq_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
              const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
              int bits, void* y, void* stream);

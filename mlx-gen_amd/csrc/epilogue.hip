@@ -166,8 +166,8 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
   }
 }
 
-// DR = f32 (an f32 activation or f32 factors): xa[M,R] = x . A and lbt[N,R] = B^T in f32, x and
-// the factors widened exactly (MLX promotes the bf16 operand of a mixed matmul to f32).
+// DR = f32 (an f32 or fp16 activation, or f32 factors): xa[M,R] = x . A and lbt[N,R] = B^T in f32,
+// x and the factors widened exactly (MLX promotes the 16-bit operands of a mixed matmul to f32).
 template <typename XT, typename FT>
 __global__ void lora_prep_f32_kernel(const XT* __restrict__ x, int64_t M, int64_t K,
                                      const FT* __restrict__ A, const FT* __restrict__ B, int64_t N,
@@ -198,7 +198,14 @@ int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* 
   if (blocks > 0x7fffffff) return set_error(MLXQ_EINVAL, "lora: problem too large");
   if (x_dtype != MLXQ_BFLOAT16 || lora_dtype != MLXQ_BFLOAT16) {
     const dim3 g((unsigned)blocks), b(256);
-    if (x_dtype == MLXQ_BFLOAT16)
+    if (x_dtype == MLXQ_FLOAT16) {
+      if (lora_dtype == MLXQ_BFLOAT16)
+        hipLaunchKernelGGL((lora_prep_f32_kernel<_Float16, uint16_t>), g, b, 0, st, (const _Float16*)x, M, K,
+                           (const uint16_t*)A, (const uint16_t*)B, N, rank, R, (float*)xa, (float*)lbt);
+      else
+        hipLaunchKernelGGL((lora_prep_f32_kernel<_Float16, float>), g, b, 0, st, (const _Float16*)x, M, K,
+                           (const float*)A, (const float*)B, N, rank, R, (float*)xa, (float*)lbt);
+    } else if (x_dtype == MLXQ_BFLOAT16)
       hipLaunchKernelGGL((lora_prep_f32_kernel<uint16_t, float>), g, b, 0, st, (const uint16_t*)x, M, K,
                          (const float*)A, (const float*)B, N, rank, R, (float*)xa, (float*)lbt);
     else if (lora_dtype == MLXQ_BFLOAT16)

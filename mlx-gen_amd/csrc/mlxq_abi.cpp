@@ -38,10 +38,19 @@ static int check_pack(const char* op, int64_t N, int64_t K, int gs, int bits) {
   return MLXQ_OK;
 }
 
+// Storage dtypes: f32 and bf16 for every operand; fp16 only as the activations x of the entry
+// points that take it (check_x_dtype), MLXQ_EUNSUPPORTED elsewhere.
 static int check_dtype(const char* op, const char* what, int dt) {
+  if (dt == MLXQ_FLOAT16)
+    return set_error(MLXQ_EUNSUPPORTED, "%s: %s dtype float16 is not supported (float16 is taken as "
+                                        "activations only)", op, what);
   if (dt != MLXQ_FLOAT32 && dt != MLXQ_BFLOAT16)
-    return set_error(MLXQ_EINVAL, "%s: %s dtype %d is not float32 or bfloat16", op, what, dt);
+    return set_error(MLXQ_EINVAL, "%s: %s dtype %d is not float32, bfloat16 or float16", op, what, dt);
   return MLXQ_OK;
+}
+
+static int check_x_dtype(const char* op, int dt) {
+  return dt == MLXQ_FLOAT16 ? MLXQ_OK : check_dtype(op, "x", dt);
 }
 
 static int check_aligned(const char* op, const char* what, const void* p, uintptr_t align = 16) {
@@ -57,7 +66,7 @@ static int check_mm(const char* op, const void* x, int x_dtype, int64_t M, int64
   int rc;
   if ((rc = check_pack(op, N, K, gs, bits))) return rc;
   if (M < 0) return set_error(MLXQ_EINVAL, "%s: M=%lld < 0", op, (long long)M);
-  if ((rc = check_dtype(op, "x", x_dtype)) || (rc = check_dtype(op, "scales", sb_dtype))) return rc;
+  if ((rc = check_x_dtype(op, x_dtype)) || (rc = check_dtype(op, "scales", sb_dtype))) return rc;
   if (M == 0 || N == 0) return MLXQ_OK;
   if ((rc = check_aligned(op, "x", x)) || (rc = check_aligned(op, "wq", wq)) ||
       (rc = check_aligned(op, "y", y)))
@@ -99,7 +108,7 @@ struct LinearPlan {
 static int plan_linear(const char* op, int x_dtype, int sb_dtype, const mlxq_epilogue* ep,
                        int64_t M, int64_t N, LinearPlan& p) {
   int rc;
-  if ((rc = check_dtype(op, "x", x_dtype)) || (rc = check_dtype(op, "scales", sb_dtype))) return rc;
+  if ((rc = check_x_dtype(op, x_dtype)) || (rc = check_dtype(op, "scales", sb_dtype))) return rc;
   p = LinearPlan{};
   p.d0_bf16 = x_dtype == MLXQ_BFLOAT16 && sb_dtype == MLXQ_BFLOAT16;
   if (ep) {
@@ -413,7 +422,7 @@ int mlxq_lora_residual(const void* x, int x_dtype, int64_t M, int64_t K, const v
                        void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   int rc;
-  if ((rc = check_dtype("lora_residual", "x", x_dtype)) ||
+  if ((rc = check_x_dtype("lora_residual", x_dtype)) ||
       (rc = check_dtype("lora_residual", "LoRA factors", lora_dtype)) ||
       (rc = check_dtype("lora_residual", "y", y_dtype)))
     return rc;
@@ -484,7 +493,7 @@ int mlxq_qmm_experts(const void* x, int x_dtype, int x_per_expert, int64_t E, in
                                           "stacked packs carry bfloat16 biases)");
   }
   if (E == 0 || M == 0 || N == 0) return MLXQ_OK;
-  const int xb = x_dtype == MLXQ_BFLOAT16 ? 2 : 4;
+  const int xb = x_dtype == MLXQ_FLOAT32 ? 4 : 2;
   const int yb = d0_bf16 ? 2 : 4;
   const int sbb = sb_dtype == MLXQ_BFLOAT16 ? 2 : 4;
   const int bb = bias_dtype == MLXQ_BFLOAT16 ? 2 : 4;

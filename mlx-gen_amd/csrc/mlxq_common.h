@@ -114,6 +114,20 @@ struct Act<float> {
   static __device__ __forceinline__ void st(float* p, int64_t i, float v) { p[i] = v; }
   static __device__ __forceinline__ float rnd(float v) { return v; }
 };
+// fp16 activations (MLXQ_FLOAT16): widened exactly to f32.  MLX promotes fp16 against bf16 or f32
+// operands to f32, so every product with fp16 x is an f32 product.
+template <>
+struct Act<_Float16> {
+  static __device__ __forceinline__ float ld(const _Float16* p, int64_t i) { return (float)p[i]; }
+  static __device__ __forceinline__ void st(_Float16* p, int64_t i, float v) { p[i] = (_Float16)v; }
+  static __device__ __forceinline__ float rnd(float v) { return (float)(_Float16)v; }
+};
+
+// The two fp16 values of a 32-bit word (element 0 in the low half), widened exactly to f32.
+__device__ __forceinline__ float f16_lo(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+}
+__device__ __forceinline__ float f16_hi(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
 
 // Exact-erf GELU, 0.5*v*(1+erf(v/sqrt(2))), branch-free so it can run on values held in the
 // MFMA accumulators without forcing them out of registers.  With z = |v|/sqrt(2):
@@ -166,7 +180,18 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return rnd(rnd(x * 0.5f) * gate);
 }
 
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+// bf16 SiLU as the reference's two ops, multiply(x, sigmoid(x)) (src/nn.rs:301-303): the sigmoid
+// rounded to bf16, then the product (exact in f32: two 8-bit significands) rounded to bf16.  g is
+// a bf16 value.  The f32 sigmoid is the correctly rounded one: 1 / (1 + expf(-g)) is within ~2 ulp
+// of it, so only where that lands within 8 ulp of a bf16 rounding midpoint (low 16 bits near
+// 0x8000), or below the f32 normal range (expf overflows for g < -88.7), is it recomputed in
+// double.  Every bf16 input then rounds as the correctly rounded f32 sigmoid does.
+__device__ __forceinline__ float silu_bf16(float g) {
+  float s = 1.0f / (1.0f + expf(-g));
+  const uint32_t lo = __float_as_uint(s) & 0xffffu;
+  if (lo - 0x7ff8u < 0x10u || s < 1.17549435e-38f) s = (float)(1.0 / (1.0 + exp(-(double)g)));
+  return round_bf16(g * round_bf16(s));
+}
 
 // ---- MFMA GEMM weight dequantization (shared by the GEMM kernels)
 // v_cvt_f32_ubyteN: byte N of v as an exact f32.

@@ -1,6 +1,8 @@
 // qmm_f32.hip — large-M quantized GEMM in f32 (y[M,N] = x[M,K] . W^T, M > 8) on gfx950 matrix
 // cores, for the operand mixes MLX computes in f32: f32 activations (FLUX.1's f32 residual stream,
-// reference mlx-gen-flux/src/model.rs:407-410 into src/adapters.rs:301-317) and/or f32 scales.
+// reference mlx-gen-flux/src/model.rs:407-410 into src/adapters.rs:301-317), fp16 activations
+// against bf16 scales (SDXL's fp16 U-Net and CLIP encoders over bf16-packed weights,
+// mlx-gen-sdxl/src/model.rs:216,283-296: promote(fp16, bf16) is f32) and/or f32 scales.
 //
 // Semantics: MLX's quantized_matmul casts x, scales and biases to their result type (f32 here),
 // dequantizes every weight in f32 and accumulates in f32.  gfx950 has no f32 matrix rate worth
@@ -11,7 +13,9 @@
 //     x.w ~= x_hi.w_hi + x_hi.w_lo + x_lo.w_hi
 // The dropped x_lo.w_lo term and the two representation errors are each below 2^-16 of |x.w|, so
 // the result is within ~1e-5 relative (Frobenius) of the f32 product, against ~1e-3 for a plain
-// bf16 product.  With bf16 activations (f32 scales) x_lo is zero and the third pass is skipped.
+// bf16 product.  With bf16 activations (f32 scales) x_lo is zero and the third pass is skipped;
+// fp16 activations split exactly (x_hi + x_lo == x), so against exact bf16 code operands (the
+// factored kernel) their products are exact.
 // Weights are dequantized exactly as fma(code, scale, bias) in f32 (scale and bias widened
 // exactly from bf16), then split.  That three-pass kernel serves group size 32 and the LoKr dense
 // product; group sizes 64 and 128 take the factored kernel further down (qmm_f32c_kernel: the
@@ -56,6 +60,28 @@ __device__ __forceinline__ u32x2 split2(float v0, float v1) {
   return u32x2{hi, pack_bf16x2(v0 - __uint_as_float(hi << 16), v1 - __uint_as_float(hi & 0xffff0000u))};
 }
 
+// Activation storage: f32 and fp16 values do not fit bf16 and carry a low part in the two-term
+// split (for fp16 the split is exact: 11 significant bits are hi's 8 plus a remainder of at most
+// 4); an 8-value chunk is W 16-byte loads (2 for f32, 1 for bf16 and fp16).
+template <typename XT>
+struct XStore {
+  static constexpr bool LO = !std::is_same<XT, uint16_t>::value;
+  static constexpr int W = std::is_same<XT, float>::value ? 2 : 1;
+  // Values 2e and 2e + 1 of a chunk, as f32.
+  static __device__ __forceinline__ void pair(const u32x4 (&a)[W], int e, float& v0, float& v1) {
+    if constexpr (std::is_same<XT, float>::value) {
+      v0 = __uint_as_float(a[e >> 1][2 * (e & 1)]);
+      v1 = __uint_as_float(a[e >> 1][2 * (e & 1) + 1]);
+    } else if constexpr (std::is_same<XT, _Float16>::value) {
+      v0 = f16_lo(a[0][e]);
+      v1 = f16_hi(a[0][e]);
+    } else {
+      v0 = __uint_as_float(a[0][e] << 16);
+      v1 = __uint_as_float(a[0][e] & 0xffff0000u);
+    }
+  }
+};
+
 __device__ __forceinline__ void f32_tile_coords(int64_t bid, int64_t tiles_m, int64_t tiles_n,
                                                 int64_t& tm, int64_t& tn) {
   const int64_t T = tiles_m * tiles_n;
@@ -73,7 +99,8 @@ __device__ __forceinline__ void f32_tile_coords(int64_t bid, int64_t tiles_m, in
 
 }  // namespace
 
-// XT: activation storage (float, or uint16_t bf16 bits); SB: scale/bias storage.  y is f32.
+// XT: activation storage (float, _Float16, or uint16_t bf16 bits); SB: scale/bias storage.  y is
+// f32.
 // WAVES: 4 (2 x 2 waves of 64 x 64) or 8 (2 x 4 waves of 64 x 32, two per SIMD).  EPI: the f32
 // epilogue (dense bias in its own dtype, then the f32 activation) is applied before the store.
 // WT: uint32_t for packed codes (wq, scales, biases); uint16_t (bf16) or float for a dense [N, K]
@@ -87,7 +114,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
                                                          const SB* __restrict__ scales,
                                                          const SB* __restrict__ biases, int64_t N,
                                                          float* __restrict__ y, F32Epilogue epi) {
-  constexpr bool XLO = std::is_same<XT, float>::value;  // activations carry a low part
+  constexpr bool XLO = XStore<XT>::LO;  // activations carry a low part
   constexpr bool DENSE = !std::is_same<WT, uint32_t>::value;
   // Weights carry a low part unless they are bf16 values: dequantized codes are f32, and a dense
   // f32 matrix keeps its low part against f32 activations.
@@ -122,7 +149,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
   // bias.  The loads are unconditional (rows past M / N are clamped; their products only reach
   // outputs that are never stored, and every step's k range lies inside K), so the loop is
   // straight-line code and each wait covers exactly the loads it needs.
-  u32x4 a_reg[2][A_LD][XLO ? 2 : 1];
+  u32x4 a_reg[2][A_LD][XStore<XT>::W];
   uint32_t b_reg[2][WPT];
   float s_reg[2], z_reg[2];
   [[maybe_unused]] u32x4 d_reg[2][DV];
@@ -137,7 +164,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
       const int64_t m = bm0 + row < M ? bm0 + row : M - 1;
       const int64_t k = k0 + c * 8;  // K % 32 == 0: a chunk never straddles K
 #pragma unroll
-      for (int h = 0; h < (XLO ? 2 : 1); ++h) a_reg[sl][i][h] = reinterpret_cast<const u32x4*>(x + m * K + k)[h];
+      for (int h = 0; h < XStore<XT>::W; ++h) a_reg[sl][i][h] = reinterpret_cast<const u32x4*>(x + m * K + k)[h];
     }
     const int row = tid / PPR, part = tid % PPR;
     const int64_t n = bn0 + row < N ? bn0 + row : N - 1;
@@ -178,8 +205,9 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
         u32x4 hi, lo;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const u32x4& src = a_reg[sl][i][e >> 1];
-          const u32x2 p = split2(__uint_as_float(src[2 * (e & 1)]), __uint_as_float(src[2 * (e & 1) + 1]));
+          float v0, v1;
+          XStore<XT>::pair(a_reg[sl][i], e, v0, v1);
+          const u32x2 p = split2(v0, v1);
           hi[e] = p[0];
           lo[e] = p[1];
         }
@@ -403,7 +431,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void qmm_f32c_kernel(const X
                                                    const SB* __restrict__ scales,
                                                    const SB* __restrict__ biases, int64_t N,
                                                    float* __restrict__ y, F32Epilogue epi) {
-  constexpr bool XLO = std::is_same<XT, float>::value;  // activations carry a low part
+  constexpr bool XLO = XStore<XT>::LO;  // activations carry a low part
   constexpr int BK = 32;
   constexpr int BM = kF32BM, NT = WAVES * 64;
   constexpr int WGN = WAVES / 2;
@@ -443,7 +471,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void qmm_f32c_kernel(const X
   // Staging registers, two slots (see qmm_f32_kernel): thread tid stages activation chunks
   // id = tid + NT i (row id / 4, chunk id % 4), and codes CPT of weight row tid / 2 with that row's
   // scale and bias.
-  u32x4 a_reg[2][A_LD][XLO ? 2 : 1];
+  u32x4 a_reg[2][A_LD][XStore<XT>::W];
   uint32_t b_reg[2][WPT];
   float s_reg[2], z_reg[2];
   float xrun[A_LD];  // each staged row's activation sum over the current group's steps so far
@@ -457,7 +485,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void qmm_f32c_kernel(const X
       const int row = id / CPR, c = id % CPR;
       const int64_t m = bm0 + row < M ? bm0 + row : M - 1;
 #pragma unroll
-      for (int h = 0; h < (XLO ? 2 : 1); ++h)
+      for (int h = 0; h < XStore<XT>::W; ++h)
         a_reg[sl][i][h] = reinterpret_cast<const u32x4*>(x + m * K + k0 + c * 8)[h];
     }
     const int row = tid / PPR, part = tid % PPR;
@@ -495,8 +523,8 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void qmm_f32c_kernel(const X
         u32x4 hi, lo;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const u32x4& src = a_reg[sl][i][e >> 1];
-          const float v0 = __uint_as_float(src[2 * (e & 1)]), v1 = __uint_as_float(src[2 * (e & 1) + 1]);
+          float v0, v1;
+          XStore<XT>::pair(a_reg[sl][i], e, v0, v1);
           t += v0 + v1;
           const u32x2 p = split2(v0, v1);
           hi[e] = p[0];
@@ -789,6 +817,11 @@ int run_qmm_f32(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t
     if (sb_dtype == MLXQ_BFLOAT16)
       return qmm_f32_bits_gs<float, uint16_t>(x, M, K, wq, s, b, N, gs, bits, y, epi, st);
     return qmm_f32_bits_gs<float, float>(x, M, K, wq, s, b, N, gs, bits, y, epi, st);
+  }
+  if (x_dtype == MLXQ_FLOAT16) {
+    if (sb_dtype == MLXQ_BFLOAT16)
+      return qmm_f32_bits_gs<_Float16, uint16_t>(x, M, K, wq, s, b, N, gs, bits, y, epi, st);
+    return qmm_f32_bits_gs<_Float16, float>(x, M, K, wq, s, b, N, gs, bits, y, epi, st);
   }
   return qmm_f32_bits_gs<uint16_t, float>(x, M, K, wq, s, b, N, gs, bits, y, epi, st);
 }

@@ -50,6 +50,9 @@ constexpr int kBufferFlags = 0x00020000;  // raw buffer resource word 3 for gfx9
 // rounded to bf16, the constants cast to bf16 first.  The f32 value of each op is taken as the
 // correctly rounded one: the op is evaluated in double (erf and tanh to within an ulp of double)
 // and rounded to float, which for + - * / of two floats is the correctly rounded float result.
+// This is the uncompiled op sequence: the reference runs gelu_exact under compile(f, true), and
+// its comments (src/nn.rs:339-343) say the fused kernel rounds 16-bit types differently from the
+// separate ops, so bf16 parity with it is unpinned.
 // Filled once per device by act_table_kernel.
 __device__ uint16_t g_act_table[2][65536];
 

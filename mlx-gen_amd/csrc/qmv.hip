@@ -42,6 +42,19 @@ __device__ __forceinline__ void load_x32<float>(const float* p, float (&v)[32]) 
   }
 }
 
+template <>
+__device__ __forceinline__ void load_x32<_Float16>(const _Float16* p, float (&v)[32]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    u32x4 r = reinterpret_cast<const u32x4*>(p)[q];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[q * 8 + 2 * i] = f16_lo(r[i]);
+      v[q * 8 + 2 * i + 1] = f16_hi(r[i]);
+    }
+  }
+}
+
 // dot of 32 codes (one chunk of a weight row) with 32 activations.
 template <int BITS>
 __device__ __forceinline__ float dot_chunk(const uint32_t (&w)[BITS], const float (&x)[32]) {
@@ -66,9 +79,11 @@ __device__ __forceinline__ float dot_chunk(const uint32_t (&w)[BITS], const floa
   return acc;
 }
 
-// The result dtype is MLX's promote(x, scales): bf16 only when both are bf16.
+// The result dtype is MLX's promote(x, scales): bf16 only when both are bf16 (uint16_t storage);
+// fp16 x against bf16 or f32 scales promotes to f32.
 template <typename XT, typename SB>
-using QmvOut = typename std::conditional<sizeof(XT) == 2 && sizeof(SB) == 2, uint16_t, float>::type;
+using QmvOut = typename std::conditional<std::is_same<XT, uint16_t>::value && std::is_same<SB, uint16_t>::value,
+                                         uint16_t, float>::type;
 
 template <typename XT, typename SB, int BITS, int GS, int MR, int ROWS>
 __global__ __launch_bounds__(256) void qmv_kernel(const XT* __restrict__ x, int M, int64_t K,
@@ -184,6 +199,10 @@ int run_qmv_valu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_
   if (x_dtype == MLXQ_BFLOAT16) {
     if (sb_dtype == MLXQ_BFLOAT16) return qmv_bits_gs<uint16_t, uint16_t>(x, M, K, wq, s, b, N, gs, bits, y, st);
     return qmv_bits_gs<uint16_t, float>(x, M, K, wq, s, b, N, gs, bits, y, st);
+  }
+  if (x_dtype == MLXQ_FLOAT16) {
+    if (sb_dtype == MLXQ_BFLOAT16) return qmv_bits_gs<_Float16, uint16_t>(x, M, K, wq, s, b, N, gs, bits, y, st);
+    return qmv_bits_gs<_Float16, float>(x, M, K, wq, s, b, N, gs, bits, y, st);
   }
   if (sb_dtype == MLXQ_BFLOAT16) return qmv_bits_gs<float, uint16_t>(x, M, K, wq, s, b, N, gs, bits, y, st);
   return qmv_bits_gs<float, float>(x, M, K, wq, s, b, N, gs, bits, y, st);

@@ -393,7 +393,8 @@ struct GemvTile {
 // Split-K reduction of a tile's partial sums through LDS (reusing the operand area):
 // [wave][m 0..15][n 0..15], waves [0, W) of matrix 0 and [W, 2W) of matrix 1.  Only rows
 // 4q + e with e < E can be < M; the rest are never written or read.  NMAT = 2 stores
-// round(round(silu(round(g))) * round(u)) (qwen3.rs:178-181), else round(y), into y [M, N].
+// round(silu(round(g)) * round(u)) with silu(g) = round(g * round(sigmoid(g)))
+// (qwen3.rs:178-181, src/nn.rs:301-303), else round(y), into y [M, N].
 template <int NMAT, int E>
 __device__ __forceinline__ void gemv_reduce_store(unsigned char* lds, const float (&yacc)[E],
                                                   int wave_all, int W, int lane, int tid, int NT,
@@ -412,9 +413,7 @@ __device__ __forceinline__ void gemv_reduce_store(unsigned char* lds, const floa
       float u = 0.0f;
       for (int w = 0; w < W; ++w) u += red[((W + w) * 16 + m) * 17 + nl];
       // each op rounded to bf16 as the reference's separate ops are (qwen3.rs:178-181)
-      const float g = round_bf16(v);
-      const float sg = round_bf16(g / (1.0f + expf(-g)));
-      v = sg * round_bf16(u);
+      v = silu_bf16(round_bf16(v)) * round_bf16(u);
     }
     if (n0 + nl < N) y[m * N + n0 + nl] = f32_to_bf16_bits(v);
   }
@@ -506,8 +505,9 @@ __device__ __forceinline__ float dpp_f32(float v) {
 
 // Contract (checked on the host by qmv_row_fits): M = 1, 1024 (LS - 1) < K <= 1024 LS, an even
 // number of groups per row, bf16 x/scales/biases, Q4 codes, group 64 or 128, 8..16 waves per
-// workgroup, dynamic LDS of qmv_row_lds bytes, every buffer < 2 GiB.  NMAT = 2: wave f streams gate row f and up row f and writes
-// round(round(silu(round(g))) * round(u)) (qwen3.rs:178-181); else round(y).
+// workgroup, dynamic LDS of qmv_row_lds bytes, every buffer < 2 GiB.  NMAT = 2: wave f streams
+// gate row f and up row f and writes round(silu(round(g)) * round(u)) with
+// silu(g) = round(g * round(sigmoid(g))) (qwen3.rs:178-181, src/nn.rs:301-303); else round(y).
 template <bool G64, int LS, int NMAT>
 __global__ __launch_bounds__(1024) void qmv_row_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const uint16_t* __restrict__ scales,
@@ -685,9 +685,7 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
     float v = tot[0];
     if constexpr (NMAT == 2) {
       // each op rounded to bf16 as the reference's separate ops are (qwen3.rs:178-181)
-      const float g = round_bf16(v);
-      const float sg = round_bf16(g / (1.0f + expf(-g)));
-      v = sg * round_bf16(tot[1]);
+      v = silu_bf16(round_bf16(v)) * round_bf16(tot[1]);
     }
     y[row] = f32_to_bf16_bits(v);
   }

@@ -19,10 +19,14 @@ void hip_check(hipError_t e, const char* what) {
   if (e != hipSuccess) throw Error(MLXQ_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// The ABI code of a float dtype.  float16 is taken by the ABI as activations only; where an entry
+// point does not take it, the library reports MLXQ_EUNSUPPORTED.
 int abi_dtype(Dtype dt, const char* op) {
   if (dt == Dtype::Float32) return MLXQ_FLOAT32;
   if (dt == Dtype::Bfloat16) return MLXQ_BFLOAT16;
-  throw Error(MLXQ_EINVAL, std::string(op) + ": expected a float32 or bfloat16 array, got " + dtype_name(dt));
+  if (dt == Dtype::Float16) return MLXQ_FLOAT16;
+  throw Error(MLXQ_EINVAL, std::string(op) + ": expected a float32, bfloat16 or float16 array, got " +
+                               dtype_name(dt));
 }
 
 void need_packed(const Array& wq, const char* op) {
@@ -31,11 +35,15 @@ void need_packed(const Array& wq, const char* op) {
   if (wq.ndim() != 2) throw Error(MLXQ_EINVAL, std::string(op) + ": packed weights must be 2-D");
 }
 
-Dtype from_abi(int dt) { return dt == MLXQ_BFLOAT16 ? Dtype::Bfloat16 : Dtype::Float32; }
+Dtype from_abi(int dt) {
+  return dt == MLXQ_BFLOAT16 ? Dtype::Bfloat16 : dt == MLXQ_FLOAT16 ? Dtype::Float16 : Dtype::Float32;
+}
 
-// MLX's result type over float operands: bf16 only when both are bf16.
+// MLX's result type over float operands: a 16-bit type only when both have it; f32 otherwise
+// (bf16 meeting fp16 included).
 Dtype promote(Dtype a, Dtype b) {
-  return a == Dtype::Bfloat16 && b == Dtype::Bfloat16 ? Dtype::Bfloat16 : Dtype::Float32;
+  if (a == b && (a == Dtype::Bfloat16 || a == Dtype::Float16)) return a;
+  return Dtype::Float32;
 }
 
 // The packed triple against x's width K, as MLX's quantized_matmul checks it

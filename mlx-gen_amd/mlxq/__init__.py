@@ -6,7 +6,7 @@ src/adapters.rs) and the ``QuantizedLinear`` / ``AdaptableLinear`` layer surface
 All compute runs in libmlxq_hip.so (hand-written HIP for gfx950) through its C ABI.
 """
 from ._lib import (MLXQ_ACT_GELU, MLXQ_ACT_GELU_EXACT, MLXQ_ACT_GELU_TANH, MLXQ_ACT_NONE,
-                   MLXQ_BFLOAT16, MLXQ_FLOAT32, MlxqError, LIB_PATH, load)
+                   MLXQ_BFLOAT16, MLXQ_FLOAT16, MLXQ_FLOAT32, MlxqError, LIB_PATH, load)
 from .ops import (DEFAULT_GROUP_SIZE, dequantize, embedding, linear, linear_out_dtype,
                   linear_workspace_size, lokr_residual, lora_residual, packed_bits, promote, qmm, qmm_experts, qmv,
                   qmv_valu, quantize, quantized_matmul, swiglu)
@@ -16,7 +16,7 @@ from . import io
 
 __all__ = [
     "MLXQ_ACT_GELU", "MLXQ_ACT_GELU_EXACT", "MLXQ_ACT_GELU_TANH", "MLXQ_ACT_NONE", "MLXQ_BFLOAT16",
-    "MLXQ_FLOAT32", "MlxqError", "LIB_PATH", "load", "DEFAULT_GROUP_SIZE", "dequantize", "embedding",
+    "MLXQ_FLOAT16", "MLXQ_FLOAT32", "MlxqError", "LIB_PATH", "load", "DEFAULT_GROUP_SIZE", "dequantize", "embedding",
     "linear", "linear_out_dtype", "linear_workspace_size", "lokr_residual", "lora_residual", "packed_bits", "promote",
     "qmm", "qmm_experts", "qmv", "qmv_valu", "quantize",
     "quantized_matmul", "swiglu", "Adapter", "AdaptableLinear", "LokrAdapter", "QuantizedLinear", "StackedExperts",

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmlxq_hip
 
 MLXQ_FLOAT32 = 0
 MLXQ_BFLOAT16 = 1
+MLXQ_FLOAT16 = 2  # activations only (SDXL's fp16 stream); promotes to f32 against bf16 / f32
 
 MLXQ_OK = 0
 MLXQ_EINVAL = 1

@@ -7,9 +7,10 @@ Reference call sites (mlx_rs::ops, MLX 0.31.2 via pmetal-mlx-rs 0.25.8):
                    group_size, bits)                     src/adapters.rs:309-317
 
 Tensors are torch tensors on the GPU (torch only supplies device memory and the current
-stream).  bf16 and f32 are supported and dtypes follow MLX's promotion: scales/biases in the
-weight dtype; a matmul returns promote(x, scales) (bf16 only when both are bf16); a bias add or a
-LoRA residual in f32 promotes the result to f32.  Every operand's shape and dtype is checked
+stream).  bf16 and f32 are supported everywhere, fp16 as activations (SDXL's dtype, reference
+mlx-gen-sdxl/src/model.rs:216), and dtypes follow MLX's promotion: scales/biases in the weight
+dtype; a matmul returns promote(x, scales) (bf16 only when both are bf16; fp16 against bf16 or f32
+is f32); a bias add or a LoRA residual in f32 promotes the result to f32.  Every operand's shape and dtype is checked
 against x before anything is launched, as MLX's quantized_matmul checks them; failures raise
 ``MlxqError`` with status MLXQ_EINVAL, and library errors carry the library's status and message.
 """
@@ -20,26 +21,35 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import MLXQ_BFLOAT16, MLXQ_EINVAL, MLXQ_FLOAT32, Epilogue, MlxqError, check
+from ._lib import MLXQ_BFLOAT16, MLXQ_EINVAL, MLXQ_FLOAT16, MLXQ_FLOAT32, Epilogue, MlxqError, check
 
 DEFAULT_GROUP_SIZE = 64  # src/quant.rs:32
 
 
+_CODES = {torch.float32: MLXQ_FLOAT32, torch.bfloat16: MLXQ_BFLOAT16, torch.float16: MLXQ_FLOAT16}
+
+
 def _dt(t: torch.Tensor) -> int:
-    if t.dtype == torch.bfloat16:
-        return MLXQ_BFLOAT16
-    if t.dtype == torch.float32:
-        return MLXQ_FLOAT32
-    raise TypeError(f"mlxq supports bfloat16 and float32 tensors, got {t.dtype}")
+    return _dt_of(t.dtype)
+
+
+def _dt_of(dtype) -> int:
+    if dtype not in _CODES:
+        raise TypeError(f"mlxq supports bfloat16, float32 and float16 tensors, got {dtype}")
+    return _CODES[dtype]
 
 
 def _torch_dtype(dt: int):
-    return torch.bfloat16 if dt == MLXQ_BFLOAT16 else torch.float32
+    return {MLXQ_BFLOAT16: torch.bfloat16, MLXQ_FLOAT16: torch.float16}.get(dt, torch.float32)
 
 
 def promote(*dtypes) -> torch.dtype:
-    """MLX's result type over bf16/f32 operands: bf16 only when every operand is bf16."""
-    return torch.bfloat16 if all(d == torch.bfloat16 for d in dtypes) else torch.float32
+    """MLX's result type over f32 / bf16 / fp16 operands: a 16-bit type only when every operand
+    has it; any f32 operand, or bf16 meeting fp16, gives f32."""
+    first = dtypes[0]
+    if first in (torch.bfloat16, torch.float16) and all(d == first for d in dtypes):
+        return first
+    return torch.float32
 
 
 def _ptr(t):
@@ -65,8 +75,10 @@ def _bad(op: str, msg: str):
 
 
 def _float_dtype(op: str, what: str, t: torch.Tensor):
-    if t.dtype not in (torch.bfloat16, torch.float32):
-        _bad(op, f"{what} must be bfloat16 or float32, got {t.dtype}")
+    """A float dtype MLX has.  fp16 is passed through: the library takes it as activations and
+    reports MLXQ_EUNSUPPORTED for any other operand."""
+    if t.dtype not in (torch.bfloat16, torch.float32, torch.float16):
+        _bad(op, f"{what} must be bfloat16, float32 or float16, got {t.dtype}")
 
 
 def _check_pack(op: str, wq, scales, biases, K: int, group_size: int, bits: int, lead=()):
@@ -284,10 +296,6 @@ def _epilogue(bias, lora_a, lora_b, lora_scale, activation, x_dtype):
                     lora_rank=rank, lora_scale=float(lora_scale), activation=int(activation),
                     bias_dtype=_dt(bias) if bias is not None else _dt_of(x_dtype),
                     lora_dtype=_dt(lora_a) if lora_a is not None else _dt_of(x_dtype))
-
-
-def _dt_of(dtype) -> int:
-    return MLXQ_BFLOAT16 if dtype == torch.bfloat16 else MLXQ_FLOAT32
 
 
 def linear_out_dtype(x_dtype, scales_dtype, bias_dtype=None, lora_dtype=None, activation: int = 0):

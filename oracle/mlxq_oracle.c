@@ -29,7 +29,12 @@
  *                      a bit-exact no-op, LoRA + LoKr stacks sum their residuals) and the
  *                      closed form x . delta^T of a rank-1 (kron of vectors) delta; the bf16
  *                      rounding points are parity unpinned (MLX per-op rounding, as elsewhere).
- *   oracle_gelu_erf / oracle_silu: textbook closed forms (special values tested).
+ *   oracle_gelu_erf    textbook closed form (special values tested).
+ *   oracle_silu        the op sequence of src/nn.rs:301-303 (sigmoid, then multiply, each rounded
+ *                      to the activation dtype); in f32 pinned by the closed form x / (1 + e^-x)
+ *                      and its special values; in bf16 parity unpinned (MLX's internal sigmoid
+ *                      precision is not fixed by any golden; the correctly rounded f32 sigmoid is
+ *                      taken).
  *   oracle_gelu_exact  the op sequence of src/nn.rs:344-355 in the input dtype; in f32 pinned by
  *                      its distance to the closed form, in bf16 parity unpinned (rounding points).
  *   oracle_gelu_tanh   pinned in f32 by the closed form (the reference test points of
@@ -52,6 +57,30 @@
 
 #define ORACLE_OK 0
 #define ORACLE_EINVAL 1
+
+/*
+ * Round-to-nearest-even f32 -> IEEE binary16 (fp16), returned widened back to f32: the value an
+ * fp16 activation holds (SDXL runs fp16, reference mlx-gen-sdxl/src/model.rs:216).  Magnitudes
+ * from 65520 up round to infinity; subnormals (steps of 2^-24) are kept; NaN stays NaN.  fp16
+ * activations then enter every function below as these f32 values with the bf16 flags off: MLX
+ * promotes fp16 against bf16 or f32 scales to f32, so the product is the f32 one.
+ */
+float oracle_fp16_round(float x) {
+    if (isnan(x) || isinf(x)) return x;
+    const double ax = fabs((double)x);
+    if (ax >= 65520.0) return x > 0 ? INFINITY : -INFINITY;
+    if (ax == 0.0) return x;
+    int e2;
+    frexp(ax, &e2);                    /* ax = m * 2^e2, m in [0.5, 1): leading bit at 2^(e2-1) */
+    int e = e2 - 1;
+    if (e < -14) e = -14;              /* subnormal range: fixed step 2^-24 */
+    const double ulp = ldexp(1.0, e - 10);
+    return (float)(nearbyint((double)x / ulp) * ulp);
+}
+
+void oracle_fp16_round_array(float* a, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) a[i] = oracle_fp16_round(a[i]);
+}
 
 /* Round-to-nearest-even f32 -> bf16, returned widened back to f32 (NaN kept quiet). */
 float oracle_bf16_round(float x) {
@@ -259,10 +288,16 @@ float oracle_gelu_tanh(float v, int out_bf16) {
     return rnd(rnd(v * 0.5f, out_bf16) * gate, out_bf16);
 }
 
-/* SiLU v * sigmoid(v), as in the SwiGLU of reference mlx-gen-sensenova/src/qwen3.rs:179. */
+/*
+ * SiLU as the reference's two ops, multiply(v, sigmoid(v)) (src/nn.rs:301-303, used by the SwiGLU
+ * of mlx-gen-sensenova/src/qwen3.rs:179): the sigmoid is computed in double, rounded to f32 (the
+ * correctly rounded f32 sigmoid) and then to the activation dtype; the product of the two is
+ * rounded to the activation dtype.
+ */
 float oracle_silu(float v, int out_bf16) {
-    double d = (double)v;
-    return rnd((float)(d / (1.0 + exp(-d))), out_bf16);
+    const double d = (double)v;
+    const float sig = rnd((float)(1.0 / (1.0 + exp(-d))), out_bf16);
+    return rnd(v * sig, out_bf16);
 }
 
 /*

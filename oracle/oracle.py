@@ -5,7 +5,9 @@ TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()`` an
 library never imports it.
 
 All tensors are numpy arrays.  bf16 tensors travel as float32 arrays holding bf16-representable
-values; the ``*_bf16`` flags choose where the oracle rounds to bf16 (see ``mlxq_oracle.c``).
+values; the ``*_bf16`` flags choose where the oracle rounds to bf16 (see ``mlxq_oracle.c``).  fp16
+activations travel as float32 arrays of fp16-representable values (``fp16_round``) with the bf16
+flags off: MLX promotes fp16 against bf16 or f32 to f32.
 """
 from __future__ import annotations
 
@@ -39,6 +41,9 @@ def lib():
         l = ctypes.CDLL(_LIB_PATH)
         l.oracle_bf16_round.argtypes = [ctypes.c_float]
         l.oracle_bf16_round.restype = ctypes.c_float
+        l.oracle_fp16_round.argtypes = [ctypes.c_float]
+        l.oracle_fp16_round.restype = ctypes.c_float
+        l.oracle_fp16_round_array.argtypes = [_f32p, _i64]
         l.oracle_quantize.argtypes = [_f32p, _i64, _i64, _int, _int, _int, _u32p, _f32p, _f32p]
         l.oracle_dequantize.argtypes = [_u32p, _f32p, _f32p, _i64, _i64, _int, _int, _int, _f32p]
         l.oracle_qmm.argtypes = [_f32p, _i64, _i64, _u32p, _f32p, _f32p, _i64, _int, _int, _int,
@@ -96,6 +101,13 @@ def bf16_round(a) -> np.ndarray:
     r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
     r = np.where(nan, (u.astype(np.uint32) | 0x00400000) & 0xFFFF0000, r).astype(np.uint32)
     return r.view(np.float32).reshape(a.shape)
+
+
+def fp16_round(a) -> np.ndarray:
+    """Round float32 values to the nearest-even fp16, returned as float32 (oracle_fp16_round)."""
+    a = np.array(a, dtype=np.float32, copy=True, order="C")
+    lib().oracle_fp16_round_array(a.ctypes.data_as(_f32p), a.size)
+    return a
 
 
 def quantize(w, group_size=64, bits=4, sb_bf16=False):

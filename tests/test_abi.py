@@ -170,6 +170,40 @@ def test_linear_out_dtype_follows_mlx_promotion(lib):
     assert ops.promote(torch.bfloat16, torch.float32) == torch.float32
 
 
+def test_fp16_activations_promote_to_f32_and_fp16_elsewhere_is_unsupported(lib):
+    """fp16 (MLXQ_FLOAT16) is taken as activations: MLX promotes it against bf16 or f32 to f32
+    (SDXL's fp16 stream over bf16 packs, mlx-gen-sdxl/src/model.rs:216,283-296), so every linear
+    with fp16 x is f32.  fp16 anywhere else is valid for MLX but not implemented: EUNSUPPORTED,
+    before any device work.  Unknown dtype codes stay EINVAL."""
+    from mlxq import _lib, ops
+    import torch
+    bf, f32, f16 = _lib.MLXQ_BFLOAT16, _lib.MLXQ_FLOAT32, _lib.MLXQ_FLOAT16
+    od = lambda xd, sd, ep: lib.mlxq_linear_out_dtype(xd, sd, ctypes.byref(ep))
+    assert od(f16, bf, _ep(lib)) == f32
+    assert od(f16, f32, _ep(lib)) == f32
+    assert od(f16, bf, _ep(lib, bias_dt=bf, lora_dt=bf, act=_lib.MLXQ_ACT_GELU_EXACT)) == f32
+    assert od(f16, bf, _ep(lib, bias_dt=f16)) == -1 and b"float16" in lib.mlxq_last_error()
+    assert od(bf, f16, _ep(lib)) == -1 and b"float16" in lib.mlxq_last_error()
+    ws = lambda xd, sd, M, N, ep: lib.mlxq_linear_workspace_size(xd, sd, M, N, ctypes.byref(ep))
+    assert ws(f16, bf, 64, 128, _ep(lib, bias_dt=bf, act=_lib.MLXQ_ACT_GELU)) == 0  # f32 product, no staging
+    null = ctypes.c_void_p(0)
+    assert lib.mlxq_quantize(null, f16, 4, 128, 64, 4, null, null, null, null) == _lib.MLXQ_EUNSUPPORTED
+    assert lib.mlxq_dequantize(null, null, null, f16, 4, 128, 64, 4, null, null) == _lib.MLXQ_EUNSUPPORTED
+    p = ctypes.c_void_p(4096)
+    st = lib.mlxq_quantized_matmul(p, f16, 4, 128, p, p, p, f16, 8, 1, 64, 4, p, null)
+    assert st == _lib.MLXQ_EUNSUPPORTED and b"scales" in lib.mlxq_last_error()
+    st = lib.mlxq_lokr_residual(p, f16, 4, 64, p, bf, 8, 0.5, p, f32, p, p, 1 << 20, None)
+    assert st == _lib.MLXQ_EUNSUPPORTED
+    st = lib.mlxq_cast(p, f16, p, bf, 8, None)
+    assert st == _lib.MLXQ_EUNSUPPORTED
+    st = lib.mlxq_quantized_matmul(p, 3, 4, 128, p, p, p, bf, 8, 1, 64, 4, p, null)
+    assert st == _lib.MLXQ_EINVAL and b"dtype" in lib.mlxq_last_error()
+    assert ops.promote(torch.float16, torch.bfloat16) == torch.float32
+    assert ops.promote(torch.float16, torch.float16) == torch.float16
+    assert ops.promote(torch.float16, torch.float32) == torch.float32
+    assert ops.linear_out_dtype(torch.float16, torch.bfloat16, bias_dtype=torch.bfloat16) == torch.float32
+
+
 def test_wrappers_reject_bad_shapes_before_launch():
     """MLX's quantized_matmul rejects inconsistent operands; the wrappers raise MLXQ_EINVAL before
     anything is launched (CPU tensors: a launch would have failed differently)."""

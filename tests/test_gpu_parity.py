@@ -523,7 +523,7 @@ def test_swiglu_group32(mlxq, M, K, F, bits):
     ref = oracle.bf16_round(oracle.bf16_round(np.vectorize(oracle.silu)(gr).astype(np.float32)) * ur)
     assert_close(h, ref, f"swiglu group 32 M={M} K={K} F={F}")
     print(f"    bit-identical outputs: {np.mean(h == ref) * 100:.2f} %", flush=True)
-    assert np.mean(h == ref) > 0.95
+    assert np.mean(h == ref) > 0.99
 
 
 @pytest.mark.parametrize("M", [2, 3, 4, 5, 8])
@@ -552,7 +552,7 @@ def test_swiglu_tile_kernel_long_and_ragged_k(mlxq, M, K, F, gs, bits):
     ref = oracle.bf16_round(oracle.bf16_round(np.vectorize(oracle.silu)(gr).astype(np.float32)) * ur)
     assert_close(h, ref, f"swiglu tile long K M={M} K={K} F={F} b={bits}")
     print(f"    bit-identical outputs: {np.mean(h == ref) * 100:.2f} %", flush=True)
-    assert np.mean(h == ref) > 0.95
+    assert np.mean(h == ref) > 0.99
 
 
 @pytest.mark.parametrize("K,F,gs", [(3584, 300, 64), (2560, 129, 128), (15488, 24, 64)])
@@ -569,7 +569,7 @@ def test_swiglu_one_row_kernel_ragged_k(mlxq, K, F, gs):
     ref = oracle.bf16_round(oracle.bf16_round(np.vectorize(oracle.silu)(gr).astype(np.float32)) * ur)
     assert_close(h, ref, f"swiglu one row ragged K={K} F={F}")
     print(f"    bit-identical outputs: {np.mean(h == ref) * 100:.2f} %", flush=True)
-    assert np.mean(h == ref) > 0.95
+    assert np.mean(h == ref) > 0.99
 
 
 @pytest.mark.parametrize("K,N,gs", [(3072, 8192, 64), (8192, 3072, 64), (4096, 520, 128)])
@@ -605,7 +605,7 @@ def test_swiglu_one_row_kernel_vs_exact(mlxq, M, K, F, gs):
     ref = oracle.bf16_round(oracle.bf16_round(np.vectorize(oracle.silu)(gr).astype(np.float32)) * ur)
     assert_close(h, ref, f"swiglu one row M={M} K={K} F={F}")
     print(f"    bit-identical outputs: {np.mean(h == ref) * 100:.2f} %", flush=True)
-    assert np.mean(h == ref) > 0.95
+    assert np.mean(h == ref) > 0.99
 
 
 @pytest.mark.parametrize("M", [1, 2, 4, 8])

@@ -380,3 +380,42 @@ def test_lokr_residual_matches_torch_promotion(x_dt, y_dt, delta_dt):
     out = t(y, tdt[y_dt]) + r
     assert out_bf16 == (out.dtype == bf)
     np.testing.assert_array_equal(got, out.float().numpy())
+
+
+def test_bf16_silu_is_sigmoid_then_multiply():
+    """The bf16 SiLU of the reference is two ops, multiply(x, sigmoid(x)) (src/nn.rs:301-303): the
+    sigmoid is rounded to bf16 before the product.  Checked on every finite bf16 input against
+    torch's CPU bf16 ops doing the same two steps (an independent f32 sigmoid); the two may part
+    only where torch's f32 sigmoid lands on the other side of a bf16 rounding midpoint.  The
+    single-rounded form x / (1 + e^-x) must differ on a visible share of inputs, so a rounding
+    point dropped from the oracle would fail here."""
+    h = np.arange(65536, dtype=np.uint32)
+    h = h[((h >> 7) & 0xFF) != 0xFF]  # finite bf16 bit patterns
+    v = (h << 16).view(np.float32)
+    got = np.array([oracle.silu(float(a)) for a in v], dtype=np.float32)
+    xt = torch.from_numpy(v).to(torch.bfloat16)
+    two_op = (xt * torch.sigmoid(xt)).float().numpy()
+    one_op = torch.from_numpy((v.astype(np.float64) / (1.0 + np.exp(-v.astype(np.float64))))
+                              .astype(np.float32)).to(torch.bfloat16).float().numpy()
+    same = (got == two_op) | (np.isnan(got) & np.isnan(two_op))
+    assert np.count_nonzero(~same) <= 16, np.count_nonzero(~same)
+    assert np.count_nonzero(got != one_op) > 500
+    assert oracle.silu(0.0) == 0.0 and oracle.silu(100.0) == 100.0 and oracle.silu(-200.0) == 0.0
+
+
+def test_fp16_round_matches_numpy():
+    """oracle_fp16_round against numpy's float32 -> float16 conversion (round to nearest even):
+    random values over the whole fp16 range and beyond, the overflow threshold (65504 stays,
+    65520 and up become inf), ties at both the normal and the subnormal step, and specials."""
+    rng = np.random.default_rng(5)
+    v = (rng.standard_normal(200000) * 10.0 ** rng.uniform(-9, 5.2, 200000)).astype(np.float32)
+    edge = np.array([0.0, -0.0, 65504.0, 65519.996, 65520.0, -65520.0, 1e9, 2.0 ** -24,
+                     2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -14, 2.0 ** -14 - 2.0 ** -25, 1.0 + 2.0 ** -11,
+                     1.0 + 3 * 2.0 ** -11, 2048.0 + 1.0, np.inf, -np.inf, np.nan], np.float32)
+    v = np.concatenate([v, edge])
+    with np.errstate(over="ignore"):
+        want = v.astype(np.float16).astype(np.float32)
+    got = oracle.fp16_round(v)
+    same = (got == want) | (np.isnan(got) & np.isnan(want))
+    assert same.all(), v[~same][:10]
+    assert np.array_equal(np.signbit(got[v == 0]), np.signbit(v[v == 0]))

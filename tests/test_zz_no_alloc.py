@@ -83,12 +83,18 @@ def test_noalloc_rejects_oversized_scratch(mlxq):
     lib = _lib.load()
     banner("noalloc oversized")
     M, N, rank = 1 << 16, 1 << 14, 64
-    ep = _lib.Epilogue(None, 16, 16, rank, 1.0, 0, _lib.MLXQ_BFLOAT16, _lib.MLXQ_BFLOAT16)
+    # Fail-safe call: real (small) device buffers, and K = 96 is not a multiple of the group size,
+    # which mlxq_linear itself rejects before any launch.  The scratch-size check runs first, so
+    # the error must name the static buffer; were it to move behind argument validation, the call
+    # would still end in an error (naming K), never in a kernel on undersized buffers.
+    buf = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    p = ctypes.c_void_p(buf.data_ptr())
+    ep = _lib.Epilogue(None, buf.data_ptr(), buf.data_ptr(), rank, 1.0, 0, _lib.MLXQ_BFLOAT16,
+                       _lib.MLXQ_BFLOAT16)
     need = int(lib.mlxq_linear_workspace_size(_lib.MLXQ_BFLOAT16, _lib.MLXQ_BFLOAT16, M, N,
                                               ctypes.byref(ep)))
     assert need > _lib.MLXQ_NOALLOC_SCRATCH_BYTES
-    p = ctypes.c_void_p(16)
-    st = lib.mlxq_linear_noalloc(p, _lib.MLXQ_BFLOAT16, M, 512, p, p, p, _lib.MLXQ_BFLOAT16, N, 64, 4,
+    st = lib.mlxq_linear_noalloc(p, _lib.MLXQ_BFLOAT16, M, 96, p, p, p, _lib.MLXQ_BFLOAT16, N, 64, 4,
                                  ctypes.byref(ep), p, None)
     assert st == _lib.MLXQ_EINVAL
     assert b"static buffer" in lib.mlxq_last_error()
