@@ -283,21 +283,44 @@ def bench_quantize(mlxq, torch, iters=10):
     # the traffic of a real conversion).
     ms = graph_ms(torch, run, inner=1, reps=iters) / QUANT_SETS
     nbytes = 4 * (5120 * 5120 * 2 + 5120 * 5120 + 5120 * 80 * 4)
-    # Reference point: a plain device copy of each weight into its own buffer, same method.
-    dsts = [torch.empty_like(w) for w in ws]
-
-    def copy():
-        for w, d in zip(ws, dsts):
-            d.copy_(w)
-    ms_c = graph_ms(torch, copy, inner=1, reps=iters) / QUANT_SETS
-    cbytes = 4 * 2 * 5120 * 5120 * 2
+    # Reference point: the same memory pattern and launch shape with trivial arithmetic (the
+    # stream kernel of libmlxq_bench.so), reading the same weights and writing the Q8 code bytes
+    # into buffers of their own, same timing.
+    ref = stream_reference(torch, ws, 8, iters) / QUANT_SETS
+    rbytes = 4 * (5120 * 5120 * 2 + 5120 * 5120)
     return {"us_per_pass": ms * 1e3, "GBs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes,
             "frac_of_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "copy_GBs": round(cbytes / (ms_c * 1e-3) / 1e9, 1),
-            "frac_of_copy_rate": round(nbytes / (ms * 1e-3) / (cbytes / (ms_c * 1e-3)), 4),
+            "stream_reference_us_per_pass": round(ref * 1e3, 2),
+            "stream_reference_GBs": round(rbytes / (ref * 1e-3) / 1e9, 1),
+            "frac_of_stream_reference_time": round(ref / ms, 4),
             "note": "4 launches per pass, each weight into its own outputs, passes rotated over "
-                    f"{QUANT_SETS} weight sets; copy_GBs: torch copy_ of the same weights into their "
-                    "own buffers, same timing"}
+                    f"{QUANT_SETS} weight sets; stream_reference: quantize's load/store pattern and "
+                    "grid with trivial arithmetic on the same weights (reads the weights, writes the "
+                    "code bytes; no scales), same timing"}
+
+
+def stream_reference(torch, ws, words, reps):
+    """Milliseconds per pass of the bench stream kernel over the weights ws (each 64-byte chunk of
+    a weight read, 4 * words bytes written into its own output), with quantize's grid: one
+    256-thread workgroup per 256 chunks, one chunk per thread."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "mlx-gen_amd", "mlxq", "libmlxq_bench.so"))
+    lib.mlxq_bench_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                      ctypes.c_int64, ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    chunks = [w.numel() * w.element_size() // 64 for w in ws]
+    outs = [torch.empty(c * 4 * words, dtype=torch.uint8, device=dev) for c in chunks]
+
+    for w, c, o in zip(ws, chunks, outs):  # host-side shape check before any launch
+        assert w.is_contiguous() and w.numel() * w.element_size() == c * 64 and o.numel() == c * 4 * words
+
+    def run():
+        sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        for w, c, o in zip(ws, chunks, outs):
+            blocks = (c + 255) // 256
+            if lib.mlxq_bench_stream(w.data_ptr(), c, o.data_ptr(), words, blocks, sp) != 0:
+                raise RuntimeError("bench stream kernel failed")
+    return graph_ms(torch, run, inner=1, reps=reps)
 
 
 def graph_ms(torch, fn, inner=8, reps=5):
@@ -430,10 +453,12 @@ def bench_config1(mlxq, torch):
     qbytes = 3072 * 3072 * 2 + 3072 * 3072 // 2 + 3072 * 48 * 4
     n = len(ws)
     t_q = graph_ms(torch, quant, inner=1, reps=10) / n
+    t_r = stream_reference(torch, ws, 4, 10) / n
     t_d = graph_ms(torch, deq, inner=1, reps=10) / n
     t_m = graph_ms(torch, mm, inner=1, reps=10) / n
     flop = 2.0 * 256 * 3072 * 3072
     return {"quantize_us": round(t_q * 1e3, 2), "quantize_GBs": round(qbytes / (t_q * 1e-3) / 1e9, 1),
+            "quantize_stream_reference_us": round(t_r * 1e3, 2),
             "dequantize_us": round(t_d * 1e3, 2), "dequantize_GBs": round(qbytes / (t_d * 1e-3) / 1e9, 1),
             "qmm_us": round(t_m * 1e3, 2), "qmm_TFLOPs": round(flop / (t_m * 1e-3) / 1e12, 1),
             "note": f"per launch, rotated over {CONFIG1_COPIES} distinct weights (HIP graph, gaps "
