@@ -196,6 +196,10 @@ static int qmv_bits_gs(const void* x, int64_t M, int64_t K, const uint32_t* wq, 
 
 int run_qmv_valu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                  const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st) {
+  // bf16 decode shapes at M = 1: the one-row kernel's loads with VALU dot products, so the A/B
+  // against the matrix cores compares the arithmetic alone.
+  if (qmv_row_valu_applicable(x_dtype, sb_dtype, M, K, N, gs, bits))
+    return run_qmv_row_valu(x, K, wq, s, b, N, gs, y, st);
   if (x_dtype == MLXQ_BFLOAT16) {
     if (sb_dtype == MLXQ_BFLOAT16) return qmv_bits_gs<uint16_t, uint16_t>(x, M, K, wq, s, b, N, gs, bits, y, st);
     return qmv_bits_gs<uint16_t, float>(x, M, K, wq, s, b, N, gs, bits, y, st);

@@ -508,7 +508,11 @@ __device__ __forceinline__ float dpp_f32(float v) {
 // workgroup, dynamic LDS of qmv_row_lds bytes, every buffer < 2 GiB.  NMAT = 2: wave f streams
 // gate row f and up row f and writes round(silu(round(g)) * round(u)) with
 // silu(g) = round(g * round(sigmoid(g))) (qwen3.rs:178-181, src/nn.rs:301-303); else round(y).
-template <bool G64, int LS, int NMAT>
+// VALU: the same loads, staging and fold with the matrix cores left out — each lane forms the
+// dot product of its 16 codes with their activations by VALU FMAs (y += s * dot, plus b * X once
+// per column), and all 64 lanes' partial sums are added at the end.  It exists for the
+// kernel-choice A/B (mlxq_qmv_valu), not for quantized_matmul.
+template <bool G64, int LS, int NMAT, bool VALU = false>
 __global__ __launch_bounds__(1024) void qmv_row_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint32_t* __restrict__ wq2,
@@ -607,7 +611,7 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
         const float s0 = __uint_as_float(cs[mat][i] << 16), s1 = __uint_as_float(cs[mat][i] & 0xffff0000u);
         const float b0 = __uint_as_float(cb[mat][i] << 16), b1 = __uint_as_float(cb[mat][i] & 0xffff0000u);
         *reinterpret_cast<f32x4*>(tab + (mat * G + g0) * 2) =
-            f32x4{s0, fmaf(-128.0f, s0, b0), s1, fmaf(-128.0f, s1, b1)};
+            VALU ? f32x4{s0, b0, s1, b1} : f32x4{s0, fmaf(-128.0f, s0, b0), s1, fmaf(-128.0f, s1, b1)};
       }
     }
   }
@@ -638,19 +642,46 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
   auto mfma_step = [&](int d) {
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat) {
-      const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][0], unpack_q4(wv[mat][d][0]),
-                                                              f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-      acc[d][mat] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][1], unpack_q4(wv[mat][d][1]), c, 0, 0, 0);
+      if constexpr (VALU) {
+        // codes of word h: bytes of (w & 0x0f0f0f0f) are codes 0, 2, 4, 6 and of (w >> 4) &
+        // 0x0f0f0f0f codes 1, 3, 5, 7 — the order of the permuted activation run.
+        float dot = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t w = wv[mat][d][h];
+          const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+          const u32x4 xr = __builtin_bit_cast(u32x4, a[d][h]);
+          dot = fmaf(__uint_as_float(xr[0] << 16), ubyte<0>(lo), dot);
+          dot = fmaf(__uint_as_float(xr[0] & 0xffff0000u), ubyte<1>(lo), dot);
+          dot = fmaf(__uint_as_float(xr[1] << 16), ubyte<2>(lo), dot);
+          dot = fmaf(__uint_as_float(xr[1] & 0xffff0000u), ubyte<3>(lo), dot);
+          dot = fmaf(__uint_as_float(xr[2] << 16), ubyte<0>(hi), dot);
+          dot = fmaf(__uint_as_float(xr[2] & 0xffff0000u), ubyte<1>(hi), dot);
+          dot = fmaf(__uint_as_float(xr[3] << 16), ubyte<2>(hi), dot);
+          dot = fmaf(__uint_as_float(xr[3] & 0xffff0000u), ubyte<3>(hi), dot);
+        }
+        acc[d][mat][0] = dot;
+      } else {
+        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][0], unpack_q4(wv[mat][d][0]),
+                                                                f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        acc[d][mat] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][1], unpack_q4(wv[mat][d][1]), c, 0, 0, 0);
+      }
     }
   };
   auto fold_step = [&](int d) {
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat) {
-      const f32x4 c = acc[d][mat];
-      float v = e == 1 ? c[1] : c[0];
-      v = e == 2 ? c[2] : v;
-      v = e == 3 ? c[3] : v;
-      ya[mat] = fmaf(p[d][mat][0], v, fmaf(p[d][mat][1], xg[d], ya[mat]));
+      if constexpr (VALU) {
+        // lane (m, q): s times its 16 codes' dot product; b times the column's activation sum
+        // once per column (q == 0)
+        ya[mat] = fmaf(p[d][mat][0], acc[d][mat][0], fmaf(q == 0 ? p[d][mat][1] : 0.0f, xg[d], ya[mat]));
+      } else {
+        const f32x4 c = acc[d][mat];
+        float v = e == 1 ? c[1] : c[0];
+        v = e == 2 ? c[2] : v;
+        v = e == 3 ? c[3] : v;
+        ya[mat] = fmaf(p[d][mat][0], v, fmaf(p[d][mat][1], xg[d], ya[mat]));
+      }
       asm volatile("" : "+v"(ya[mat]));
     }
   };
@@ -665,9 +696,9 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
   __builtin_amdgcn_sched_barrier(0);
   fold_step(LS - 1);
 
-  // The 16 diagonal lanes (n + 16 (n >> 2)) hold the partial sums: a row-shift scan leaves each
-  // 16-lane row's sum in its lane 15.
-  const bool diag = q == (m >> 2);
+  // The 16 diagonal lanes (n + 16 (n >> 2)) hold the partial sums (every lane in the VALU form):
+  // a row-shift scan leaves each 16-lane row's sum in its lane 15.
+  const bool diag = VALU || q == (m >> 2);
   float tot[NMAT];
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat) {
@@ -883,31 +914,32 @@ static int qmv_row_wpb(int64_t N, int nmat) {
   return best;
 }
 
-template <bool G64, int LS, int NMAT>
+template <bool G64, int LS, int NMAT, bool VALU = false>
 static int launch_qmv_row(const QmvArgs& a, hipStream_t st) {
   static_assert(qmv_row_lds(LS, G64, NMAT, 16) <= kMaxLds, "one-row workgroup exceeds the LDS");
   static std::atomic<bool> attr_set[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return set_error(MLXQ_EDEVICE, "qmv: no current device");
   if (dev < 0 || dev >= 64 || !attr_set[dev].load(std::memory_order_acquire)) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_row_kernel<G64, LS, NMAT>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&qmv_row_kernel<G64, LS, NMAT, VALU>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds) != hipSuccess)
       return set_error(MLXQ_EDEVICE, "qmv: hipFuncSetAttribute failed");
     if (dev >= 0 && dev < 64) attr_set[dev].store(true, std::memory_order_release);
   }
   const int wpb = qmv_row_wpb(a.N, NMAT);
   const int lds = qmv_row_lds(LS, G64, NMAT, wpb);
-  hipLaunchKernelGGL((qmv_row_kernel<G64, LS, NMAT>), dim3((unsigned)((a.N + wpb - 1) / wpb)), dim3(wpb * 64),
-                     lds, st, (const uint16_t*)a.x, a.wq, (const uint16_t*)a.s, (const uint16_t*)a.b, a.wq2,
-                     (const uint16_t*)a.s2, (const uint16_t*)a.b2, (int)a.K, (int)a.N, (uint16_t*)a.y);
-  return check_launch(NMAT == 2 ? "swiglu_qmv_row" : "qmv_row");
+  hipLaunchKernelGGL((qmv_row_kernel<G64, LS, NMAT, VALU>), dim3((unsigned)((a.N + wpb - 1) / wpb)),
+                     dim3(wpb * 64), lds, st, (const uint16_t*)a.x, a.wq, (const uint16_t*)a.s,
+                     (const uint16_t*)a.b, a.wq2, (const uint16_t*)a.s2, (const uint16_t*)a.b2, (int)a.K,
+                     (int)a.N, (uint16_t*)a.y);
+  return check_launch(NMAT == 2 ? "swiglu_qmv_row" : VALU ? "qmv_row_valu" : "qmv_row");
 }
 
 // Launchers by loads per row (1 .. kRowMaxLoads).
-template <bool G64, int NMAT, int... L>
+template <bool G64, int NMAT, bool VALU = false, int... L>
 static int qmv_row_ls(const QmvArgs& a, hipStream_t st, std::integer_sequence<int, L...>) {
   using Launch = int (*)(const QmvArgs&, hipStream_t);
-  static constexpr Launch launch[] = {&launch_qmv_row<G64, L + 1, NMAT>...};
+  static constexpr Launch launch[] = {&launch_qmv_row<G64, L + 1, NMAT, VALU>...};
   return launch[(a.K + 1023) / 1024 - 1](a, st);
 }
 
@@ -943,6 +975,22 @@ int run_qmv_mfma(const void* x, int64_t M, int64_t K, const uint32_t* wq, const 
     if (rc != MLXQ_OK) return rc;
   }
   return MLXQ_OK;
+}
+
+// The VALU form of the one-row kernel (the kernel-choice A/B behind mlxq_qmv_valu): bf16 x and
+// scales, M = 1, Q4 group 64/128, K up to kRowValuMaxLoads * 1024 (the decode shapes).
+constexpr int kRowValuMaxLoads = 8;
+
+bool qmv_row_valu_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int64_t N, int gs, int bits) {
+  return x_dtype == MLXQ_BFLOAT16 && sb_dtype == MLXQ_BFLOAT16 && buffers_fit(M, K, N) &&
+         qmv_row_fits(M, K, gs, bits, 1) && K <= 1024 * kRowValuMaxLoads;
+}
+
+int run_qmv_row_valu(const void* x, int64_t K, const uint32_t* wq, const void* s, const void* b, int64_t N,
+                     int gs, void* y, hipStream_t st) {
+  const QmvArgs a = {x, 1, K, N, wq, s, b, nullptr, nullptr, nullptr, y};
+  constexpr auto ls = std::make_integer_sequence<int, kRowValuMaxLoads>{};
+  return gs == 64 ? qmv_row_ls<true, 1, true>(a, st, ls) : qmv_row_ls<false, 1, true>(a, st, ls);
 }
 
 bool swiglu_qmv_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int64_t F, int gs, int bits) {

@@ -31,6 +31,7 @@ int oracle_dequantize(const uint32_t* wq, const float* scales, const float* bias
 int oracle_qmm(const float* x, int64_t M, int64_t K, const uint32_t* wq, const float* scales,
                const float* biases, int64_t N, int gs, int bits, int w_bf16, int out_bf16, float* y);
 float oracle_silu(float v, int out_bf16);
+float oracle_fp16_round(float x);
 int oracle_linear(const float* x, int64_t M, int64_t K, const uint32_t* wq, const float* scales,
                   const float* biases, int64_t N, int gs, int bits, int w_bf16, int x_bf16,
                   int sb_bf16, const float* bias, int bias_bf16, const float* lora_a,
@@ -96,6 +97,19 @@ static std::vector<float> host_f32(const Array& a) {
     return from_bf16_bits(b.data(), b.size());
   }
   return host<float>(a);
+}
+// IEEE binary16 bits of a value that fp16 represents exactly (oracle_fp16_round's outputs).
+static uint16_t fp16_bits_exact(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const float a = std::fabs(f);
+  if (a == 0.0f) return sign;
+  int e;
+  std::frexp(a, &e);  // a = m 2^e, m in [0.5, 1)
+  if (e - 1 < -14) return (uint16_t)(sign | (uint16_t)std::ldexp(a, 24));  // subnormal: a / 2^-24
+  const uint32_t mant = (uint32_t)std::ldexp(a, 11 - e) - 1024u;           // 10 fraction bits
+  return (uint16_t)(sign | (uint16_t)(((e - 1 + 15) << 10) | mant));
 }
 static Array bf16_array(const std::vector<float>& v, std::vector<int64_t> shape) {
   auto b = to_bf16_bits(v);
@@ -286,6 +300,39 @@ static void gpu_cases(const fs::path& root) {
       threw = err.status == 2;  // MLXQ_EUNSUPPORTED
     }
     EXPECT(threw, "transpose=false accepted");
+  }
+
+  banner("AdaptableLinear on an fp16 stream (SDXL): bf16-cast base and bias, f32 result");
+  {
+    // mlx-gen-sdxl/src/model.rs:216,283-296: fp16 activations through AdaptableLinear::quantize's
+    // bf16 packs; MLX promotes fp16 against bf16 to f32, so the product, bias add and result are f32.
+    std::mt19937 rng(11);
+    const int64_t M = 77, K = 768, N = 320;
+    std::vector<float> wf(N * K), bias(N), x(M * K);
+    std::normal_distribution<float> nw(0.0f, 0.02f), nx(0.0f, 1.0f);
+    for (auto& v : wf) v = nw(rng);
+    for (auto& v : bias) v = nw(rng) * 10.0f;
+    for (auto& v : x) v = oracle_fp16_round(nx(rng));
+    std::vector<uint16_t> xh(x.size());
+    for (size_t i = 0; i < x.size(); ++i) xh[i] = fp16_bits_exact(x[i]);
+    AdaptableLinear l = AdaptableLinear::dense(Array::from_host(wf.data(), {N, K}, Dtype::Float32),
+                                               Array::from_host(bias.data(), {N}, Dtype::Float32));
+    l.quantize(4, std::nullopt);
+    EXPECT(l.out_dtype(Dtype::Float16) == Dtype::Float32, "fp16 x promotes to f32");
+    Array y = l.forward(Array::from_host(xh.data(), {M, K}, Dtype::Float16));
+    EXPECT(y.dtype() == Dtype::Float32 && y.shape() == std::vector<int64_t>({M, N}), "fp16 forward output");
+    std::vector<float> wb(wf.size()), bias_b(N), ref(M * N);
+    for (size_t i = 0; i < wf.size(); ++i) wb[i] = oracle_bf16_round(wf[i]);
+    for (int64_t n = 0; n < N; ++n) bias_b[n] = oracle_bf16_round(bias[n]);
+    std::vector<uint32_t> wq(N * K / 8);
+    std::vector<float> sc(N * K / 64), zb(N * K / 64);
+    oracle_quantize(wb.data(), N, K, 64, 4, 1, wq.data(), sc.data(), zb.data());
+    int out_bf16 = -1;
+    oracle_linear(x.data(), M, K, wq.data(), sc.data(), zb.data(), N, 64, 4, 0, 0, 1, bias_b.data(), 1,
+                  nullptr, nullptr, 0, 1, 1.0f, 0, ref.data(), &out_bf16);
+    EXPECT(out_bf16 == 0, "oracle result dtype");
+    const double e = rel_fro(host<float>(y), ref);
+    EXPECT(e < 2e-5, "relFro %.3e", e);
   }
 
   banner("AdaptableLinear: bf16 cast + quantize, bias, two LoRA adapters");

@@ -1,9 +1,9 @@
 """GPU parity of the forced VALU GEMV (mlxq_qmv_valu) on bf16 decode shapes.
 
 The VALU kernel serves f32 activations, f32 scales and group size 32; forced on bf16 operands it
-is the kernel the matrix-core GEMV replaced on the decode path, measured against it in bench.py's
-gemv leg.  Both have the exact-f32 semantics of MLX's qmv, checked against the oracle and against
-each other.
+is the VALU side of the kernel-choice A/B against the matrix-core GEMV in bench.py's gemv leg (at
+M = 1 on the one-row kernel's own loads with VALU dot products).  Both have the f32 semantics of
+MLX's qmv, checked against the oracle and against each other.
 """
 import numpy as np
 import pytest
@@ -21,8 +21,13 @@ def mlxq():
     return m
 
 
+# M = 1 bf16 Q4 with group 64/128 and K <= 8192 runs the one-row kernel's loads with VALU dot
+# products (ragged last load at K = 3584, ragged N, group 128); K = 16384 and the other rows the
+# VALU GEMV proper.
 @pytest.mark.parametrize("M,K,N,gs,bits", [(1, 3072, 8192, 64, 4), (8, 8192, 3072, 64, 4),
-                                          (3, 1024, 200, 128, 8), (2, 512, 96, 32, 4)])
+                                          (3, 1024, 200, 128, 8), (2, 512, 96, 32, 4),
+                                          (1, 8192, 3072, 64, 4), (1, 3584, 300, 64, 4),
+                                          (1, 2048, 520, 128, 4), (1, 16384, 64, 64, 4)])
 def test_qmv_valu_bf16_vs_oracle(mlxq, M, K, N, gs, bits):
     """The VALU GEMV forced on bf16 operands (the kernel the matrix-core GEMV replaced there):
     exact-f32 semantics like qmv, against the oracle and against the matrix-core GEMV."""
