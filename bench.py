@@ -61,6 +61,9 @@ def parse():
     p.add_argument("--trace-skip", type=int, default=0, metavar="N",
                    help="with --summarize-trace: leave out each launch shape's first N launches "
                         "(the warm-up steps), so the averages cover the timed launches")
+    p.add_argument("--trace-last", type=int, default=0, metavar="N",
+                   help="with --summarize-trace: keep only each launch shape's last N launches "
+                        "(the timed steps after the clock pre-run and warm-up)")
     p.add_argument("--summarize-pmc", metavar="DIR",
                    help="print the counter summary of the rocprofv3 --pmc runs under DIR (one "
                         "subdirectory per counter set, see summarize_pmc) and exit")
@@ -699,10 +702,10 @@ def summarize_pmc(d, sets=None):
     print("\n".join(lines))
 
 
-def summarize_trace(d, skip=0):
+def summarize_trace(d, skip=0, last=0):
     """Per mlxq kernel and launch shape (grid in workgroups x workgroup size) of the rocprofv3
     --kernel-trace csv files under d: launch count and average / median / minimum duration, over
-    the launches after each shape's first `skip` (in start-time order)."""
+    the launches after each shape's first `skip` (in start-time order), or its last `last`."""
     import csv
     import glob
     shapes = {}
@@ -721,6 +724,8 @@ def summarize_trace(d, skip=0):
     for key, ts in shapes.items():
         ts.sort()
         kept = ts[skip:] if len(ts) > skip else ts
+        if last > 0:
+            kept = kept[-last:]
         durs[key] = [(e - b) / 1e3 for b, e in kept]
     for (name, grid, wg), v in sorted(durs.items(), key=lambda kv: -sum(kv[1]) / len(kv[1])):
         lines.append(f"  {name}  grid {grid} x {wg}: launches {len(v)}  avg {sum(v) / len(v):.2f} us  "
@@ -742,7 +747,7 @@ def read_traffic():
 def main():
     args = parse()
     if args.summarize_trace:
-        summarize_trace(args.summarize_trace, args.trace_skip)
+        summarize_trace(args.summarize_trace, args.trace_skip, args.trace_last)
         return
     if args.summarize_pmc:
         summarize_pmc(args.summarize_pmc, args.pmc_sets)
