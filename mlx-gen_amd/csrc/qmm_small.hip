@@ -178,7 +178,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
       (void)kt;
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const bf16x8 b = dequant8<BITS>(c.w[j], kk, s, s * 0.0625f, z);
+        const bf16x8 b = dequant8<BITS>(c.w[j], kk, s, z);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(

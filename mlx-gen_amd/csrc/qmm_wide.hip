@@ -22,9 +22,9 @@
 //     and the epilogue writes 8-byte (4 x bf16) row segments directly.
 // Within a K step, lane half h (lane >> 5) covers k in [8(4h+kk), 8(4h+kk)+8) for MFMA kk = 0..3,
 // i.e. packed words 4h..4h+3 of the row's 8-word (Q4) K step — one contiguous load.
-// Q4 dequant: lo = w & 0x0f0f0f0f holds the even codes in its bytes, w & 0xf0f0f0f0 the odd codes
-// times 16, so each code is one v_cvt_f32_ubyteN and one FMA (with scale/16 for the odd codes —
-// an exact power-of-two rescale, so fma(16c, s/16, b) == fma(c, s, b) bit for bit).
+// Q4 dequant: w & 0x0f0f0f0f holds the even codes in its bytes, (w >> 4) & 0x0f0f0f0f the odd
+// ones; each pair of codes becomes two exact f32 values in one fp8 convert (a byte 0..15 read as
+// E4M3 is c * 2^-9, rescaled by 2^9), then one FMA per code and one bf16 pack per pair.
 //
 // Tile order is XCD-aware: workgroups are dispatched round-robin over the 8 XCDs, so consecutive
 // ids are remapped to give each XCD a contiguous slice of a grouped (4 M-tiles x all N-tiles)
@@ -387,7 +387,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   // A(0) W(0) A(1) W(1) ...; a scheduling fence keeps the weight take (VALU on loaded
   // registers) from being hoisted across the barrier, where it would force an early wait.
   uint32_t bcur[TNW][WPL];
-  float scur[TNW], s16cur[TNW], zcur[TNW];
+  float scur[TNW], zcur[TNW];
   auto take_b = [&](auto SLOT, int ktn) {  // ktn: the step these weights belong to
     constexpr int sl = decltype(SLOT)::value;
 #pragma unroll
@@ -404,7 +404,6 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
         scur[j] = sb_to_f32<SB>(bs[sl][j]);
         zcur[j] = sb_to_f32<SB>(bz[sl][j]);
       }
-      s16cur[j] = scur[j] * 0.0625f;
     }
   };
   bf16x8 af[2][TMW], bfr[2][TNW];
@@ -414,7 +413,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
   };
   auto deq_b = [&](int slot, int kk) {
 #pragma unroll
-    for (int j = 0; j < TNW; ++j) bfr[slot][j] = dequant8<BITS>(bcur[j], kk, scur[j], s16cur[j], zcur[j]);
+    for (int j = 0; j < TNW; ++j) bfr[slot][j] = dequant8<BITS>(bcur[j], kk, scur[j], zcur[j]);
   };
   auto mfma_group = [&](int slot) {
 #pragma unroll
