@@ -137,9 +137,12 @@ int mlxq_qmv(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* w
              const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
              int bits, void* y, void* stream);
 
-/* The VALU GEMV (no matrix cores; exact f32 dequant); any x / scales dtype; 1 <= M <= 8; y in
- * promote(x_dtype, sb_dtype).  The kernel quantized_matmul uses for f32 operands and group size
- * 32; forced here so it can be measured against the matrix-core GEMV on bf16 decode shapes. */
+/* A GEMV on the VALU only (no matrix cores); any x / scales dtype; 1 <= M <= 8; y in
+ * promote(x_dtype, sb_dtype).  The VALU GEMV with exact f32 dequant (the kernel quantized_matmul
+ * uses for f32 operands and group size 32), except at M = 1 with bf16 x and scales, Q4, group
+ * 64/128 and K <= 8192, where it is the M = 1 matrix-core kernel's loads and fold with VALU dot
+ * products.  Forced here so it can be measured against the matrix-core GEMV on bf16 decode
+ * shapes. */
 int mlxq_qmv_valu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq,
                   const void* scales, const void* biases, int sb_dtype, int64_t N, int group_size,
                   int bits, void* y, void* stream);

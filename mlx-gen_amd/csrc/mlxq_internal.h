@@ -89,7 +89,8 @@ bool swiglu_qmv_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int6
 int run_swiglu_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq_g, const void* s_g,
                    const void* b_g, const uint32_t* wq_u, const void* s_u, const void* b_u, int64_t F,
                    int gs, int bits, void* h, hipStream_t st);
-// The one-row GEMV (M = 1) with its MFMA dot products replaced by VALU FMAs, same loads and fold:
+// The one-row GEMV (M = 1) with its MFMA dot products replaced by VALU v_dot2_f32_bf16, same
+// loads, unpack and fold:
 // the VALU side of the kernel-choice A/B for bf16 operands at M = 1, Q4 group 64/128, K <= 8192.
 bool qmv_row_valu_applicable(int x_dtype, int sb_dtype, int64_t M, int64_t K, int64_t N, int gs, int bits);
 int run_qmv_row_valu(const void* x, int64_t K, const uint32_t* wq, const void* s, const void* b, int64_t N,

@@ -508,10 +508,11 @@ __device__ __forceinline__ float dpp_f32(float v) {
 // workgroup, dynamic LDS of qmv_row_lds bytes, every buffer < 2 GiB.  NMAT = 2: wave f streams
 // gate row f and up row f and writes round(silu(round(g)) * round(u)) with
 // silu(g) = round(g * round(sigmoid(g))) (qwen3.rs:178-181, src/nn.rs:301-303); else round(y).
-// VALU: the same loads, staging and fold with the matrix cores left out — each lane forms the
-// dot product of its 16 codes with their activations by VALU FMAs (y += s * dot, plus b * X once
-// per column), and all 64 lanes' partial sums are added at the end.  It exists for the
-// kernel-choice A/B (mlxq_qmv_valu), not for quantized_matmul.
+// VALU: the same loads, unpack, staging and fold with the matrix cores left out — each lane forms
+// the dot product of its 16 codes (as 128 + c) with their activations by v_dot2_f32_bf16, two
+// products per instruction with f32 accumulation (y += s * dot, plus (b - 128 s) * X once per
+// column), and all 64 lanes' partial sums are added at the end.  It exists for the kernel-choice
+// A/B (mlxq_qmv_valu), not for quantized_matmul.
 template <bool G64, int LS, int NMAT, bool VALU = false>
 __global__ __launch_bounds__(1024) void qmv_row_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const uint16_t* __restrict__ scales,
@@ -611,7 +612,7 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
         const float s0 = __uint_as_float(cs[mat][i] << 16), s1 = __uint_as_float(cs[mat][i] & 0xffff0000u);
         const float b0 = __uint_as_float(cb[mat][i] << 16), b1 = __uint_as_float(cb[mat][i] & 0xffff0000u);
         *reinterpret_cast<f32x4*>(tab + (mat * G + g0) * 2) =
-            VALU ? f32x4{s0, b0, s1, b1} : f32x4{s0, fmaf(-128.0f, s0, b0), s1, fmaf(-128.0f, s1, b1)};
+            f32x4{s0, fmaf(-128.0f, s0, b0), s1, fmaf(-128.0f, s1, b1)};
       }
     }
   }
@@ -643,23 +644,24 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat) {
       if constexpr (VALU) {
-        // codes of word h: bytes of (w & 0x0f0f0f0f) are codes 0, 2, 4, 6 and of (w >> 4) &
-        // 0x0f0f0f0f codes 1, 3, 5, 7 — the order of the permuted activation run.
-        float dot = 0.0f;
+        // unpack_q4's pairs line up with the activation run's bf16 pairs (the MFMA operands'
+        // element order), so each v_dot2 adds two code-activation products.
+        float part[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const uint32_t w = wv[mat][d][h];
-          const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+          const u32x4 wb = __builtin_bit_cast(u32x4, unpack_q4(wv[mat][d][h]));
           const u32x4 xr = __builtin_bit_cast(u32x4, a[d][h]);
-          dot = fmaf(__uint_as_float(xr[0] << 16), ubyte<0>(lo), dot);
-          dot = fmaf(__uint_as_float(xr[0] & 0xffff0000u), ubyte<1>(lo), dot);
-          dot = fmaf(__uint_as_float(xr[1] << 16), ubyte<2>(lo), dot);
-          dot = fmaf(__uint_as_float(xr[1] & 0xffff0000u), ubyte<3>(lo), dot);
-          dot = fmaf(__uint_as_float(xr[2] << 16), ubyte<0>(hi), dot);
-          dot = fmaf(__uint_as_float(xr[2] & 0xffff0000u), ubyte<1>(hi), dot);
-          dot = fmaf(__uint_as_float(xr[3] << 16), ubyte<2>(hi), dot);
-          dot = fmaf(__uint_as_float(xr[3] & 0xffff0000u), ubyte<3>(hi), dot);
+          float t = 0.0f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            // Elements copied out first: __builtin_bit_cast of a vector subscript (xr[j]) reads
+            // element 0 for every j with this compiler.
+            const uint32_t xj = xr[j], wj = wb[j];
+            t = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xj), __builtin_bit_cast(bf16x2, wj), t, false);
+          }
+          part[h] = t;
         }
+        const float dot = part[0] + part[1];
         acc[d][mat][0] = dot;
       } else {
         const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][0], unpack_q4(wv[mat][d][0]),
@@ -672,8 +674,8 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat) {
       if constexpr (VALU) {
-        // lane (m, q): s times its 16 codes' dot product; b times the column's activation sum
-        // once per column (q == 0)
+        // lane (m, q): s times its 16 codes' dot product; b - 128 s times the column's
+        // activation sum once per column (q == 0)
         ya[mat] = fmaf(p[d][mat][0], acc[d][mat][0], fmaf(q == 0 ? p[d][mat][1] : 0.0f, xg[d], ya[mat]));
       } else {
         const f32x4 c = acc[d][mat];
