@@ -12,10 +12,8 @@
 //
 // Semantics are the exact-f32 factored form (no bf16 rounding of dequantized weights):
 //   y[m,n] = sum_g ( s[n,g] * sum_{k in g} x[m,k]*c[n,k]  +  b[n,g] * X[m,g] ),  X = sum_{k in g} x.
-// Q4 codes enter the MFMA as the exact bf16 value 128+c (bf16 bits 0x4300|c, built with byte
-// permutes), so acc = sum x*(128+c) and the fold per group is
-//   y += s*acc + (b - 128*s)*X.
-// Q8 codes enter as bf16(c) (exact for c < 256) and fold as y += s*acc + b*X.
+// Q4 codes enter the MFMA as exact bf16 values c, two per fp8 scaled convert (unpack_q4), and
+// Q8 codes as bf16(c) (exact for c < 256); both fold per group as y += s*acc + b*X.
 // X comes from the same activation fragments multiplied by an all-ones operand on the MFMA.
 //
 // v_mfma_f32_16x16x32_bf16 with A = activations (rows m = lane&15; rows >= M read row 0 and are
@@ -53,17 +51,18 @@ constexpr int kCopySlots = 8;  // 16-byte activation chunks a lane stages (regis
 constexpr int kMaxLds = 160 * 1024;
 constexpr uint32_t kOob = 0x7ffffff0u;  // buffer offset past every resource: loads return zero
 
-// Q4 word (codes c0..c7, c_i at bits 4i) -> bf16 pairs (128+c0, 128+c2), (128+c4, 128+c6),
-// (128+c1, 128+c3), (128+c5, 128+c7): bf16 bits 0x4300|c are exactly 128+c.  The low and high
-// nibbles are split into bytes once, then v_perm_b32 pairs two code bytes with two 0x43 bytes.
+// Q4 word (codes c0..c7, c_i at bits 4i) -> bf16 pairs (c0, c2), (c4, c6), (c1, c3), (c5, c7).
+// The low and high nibbles are split into bytes once; a byte c <= 15 read as OCP fp8 E4M3 is
+// exactly c * 2^-9, so v_cvt_scalef32_pk_bf16_fp8 with scale 2^9 turns two code bytes into two
+// exact bf16 values.
 __device__ __forceinline__ bf16x8 unpack_q4(uint32_t w) {
   const uint32_t lo = w & 0x0f0f0f0fu;          // bytes c0, c2, c4, c6
   const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;   // bytes c1, c3, c5, c7
   u32x4 o;
-  o[0] = __builtin_amdgcn_perm(0x43434343u, lo, 0x04010400u);
-  o[1] = __builtin_amdgcn_perm(0x43434343u, lo, 0x04030402u);
-  o[2] = __builtin_amdgcn_perm(0x43434343u, hi, 0x04010400u);
-  o[3] = __builtin_amdgcn_perm(0x43434343u, hi, 0x04030402u);
+  o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, false));
+  o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, true));
+  o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, false));
+  o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, true));
   return __builtin_bit_cast(bf16x8, o);
 }
 
@@ -244,7 +243,7 @@ struct GemvTile {
 
   // Operands into the wave's LDS region.  Q4 activation runs are stored permuted to
   // [0,2,4,6,1,3,5,7] so they pair with the unpacked code layout; scales and biases become
-  // f32 pairs (s, b - 128 s) for Q4 and (s, b) for Q8, ready for the fold.  Only this wave
+  // f32 pairs (s, b), ready for the fold.  Only this wave
   // reads them back, so a wave-level ordering point replaces a workgroup barrier.
   __device__ __forceinline__ void stage() {
 #pragma unroll
@@ -264,7 +263,7 @@ struct GemvTile {
       if (e < 16 * NGW) {
         const int r = e / NGW, gl = e - r * NGW;
         const float sv = __uint_as_float(cs[j] << 16), zv = __uint_as_float(cz[j] << 16);
-        *reinterpret_cast<f32x2*>(szw + r * PW + 2 * gl) = f32x2{sv, BITS == 4 ? fmaf(-128.0f, sv, zv) : zv};
+        *reinterpret_cast<f32x2*>(szw + r * PW + 2 * gl) = f32x2{sv, zv};
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -470,13 +469,13 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
 // n = L & 15, q = L >> 4: codes [16q, 16q + 16) of column n, i.e. its two words feed two MFMAs
 // (v_mfma_f32_16x16x32_bf16) whose B column n is column n's 64 codes.  The A operand's row m is
 // the activation run of column m (16 different K slices of the one activation row), so the
-// product's diagonal C[n][n] is column n's dot product sum x*(128+c), and the off-diagonal
+// product's diagonal C[n][n] is column n's dot product sum x*c, and the off-diagonal
 // entries are discarded.  A row of K codes takes LS = ceil(K / 1024) loads; when K is not a
 // multiple of 1024 the last load's upper columns reach into the next row (or past the buffer end,
 // where the loads return zero), and those columns fold exactly zero: their staged activations,
-// activation sums and (s, b - 128 s) table entries are all zero.  C[n][n] sits in lane n + 16 (n >> 2), register n & 3: 16 lanes of the
+// activation sums and (s, b) table entries are all zero.  C[n][n] sits in lane n + 16 (n >> 2), register n & 3: 16 lanes of the
 // wave fold one column each per load,
-//   y += s*C[n][n] + (b - 128 s)*X[column],
+//   y += s*C[n][n] + b*X[column],
 // with X the column's activation sum (computed once per workgroup while staging).  The wave's
 // 16 partial sums are added at the end with row shifts and lane reads.
 constexpr int kRowColPitch = 144;  // LDS bytes per 64-element activation column (128 + pad)
@@ -509,9 +508,8 @@ __device__ __forceinline__ float dpp_f32(float v) {
 // gate row f and up row f and writes round(silu(round(g)) * round(u)) with
 // silu(g) = round(g * round(sigmoid(g))) (qwen3.rs:178-181, src/nn.rs:301-303); else round(y).
 // VALU: the same loads, unpack, staging and fold with the matrix cores left out — each lane forms
-// the dot product of its 16 codes (as 128 + c) with their activations by v_dot2_f32_bf16, two
-// products per instruction with f32 accumulation (y += s * dot, plus (b - 128 s) * X once per
-// column), and all 64 lanes' partial sums are added at the end.  It exists for the kernel-choice
+// the dot product of its 16 codes with their activations by v_dot2_f32_bf16, two products per
+// instruction with f32 accumulation (y += s * dot, plus b * X once per column), and all 64 lanes' partial sums are added at the end.  It exists for the kernel-choice
 // A/B (mlxq_qmv_valu), not for quantized_matmul.
 template <bool G64, int LS, int NMAT, bool VALU = false>
 __global__ __launch_bounds__(1024) void qmv_row_kernel(
@@ -600,7 +598,7 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-  // The wave's (s, b - 128 s) pairs per group, f32, after the barrier: only this wave reads them,
+  // The wave's (s, b) pairs per group, f32, after the barrier: only this wave reads them,
   // so the workgroup waits for the activations alone, not for every wave's scale loads.  Groups
   // past the row's end get (0, 0) (their loads returned zero).
 #pragma unroll
@@ -611,8 +609,7 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
       if (g0 < G) {
         const float s0 = __uint_as_float(cs[mat][i] << 16), s1 = __uint_as_float(cs[mat][i] & 0xffff0000u);
         const float b0 = __uint_as_float(cb[mat][i] << 16), b1 = __uint_as_float(cb[mat][i] & 0xffff0000u);
-        *reinterpret_cast<f32x4*>(tab + (mat * G + g0) * 2) =
-            f32x4{s0, fmaf(-128.0f, s0, b0), s1, fmaf(-128.0f, s1, b1)};
+        *reinterpret_cast<f32x4*>(tab + (mat * G + g0) * 2) = f32x4{s0, b0, s1, b1};
       }
     }
   }
@@ -674,8 +671,8 @@ __global__ __launch_bounds__(1024) void qmv_row_kernel(
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat) {
       if constexpr (VALU) {
-        // lane (m, q): s times its 16 codes' dot product; b - 128 s times the column's
-        // activation sum once per column (q == 0)
+        // lane (m, q): s times its 16 codes' dot product; b times the column's activation sum
+        // once per column (q == 0)
         ya[mat] = fmaf(p[d][mat][0], acc[d][mat][0], fmaf(q == 0 ? p[d][mat][1] : 0.0f, xg[d], ya[mat]));
       } else {
         const f32x4 c = acc[d][mat];

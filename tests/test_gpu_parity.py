@@ -440,6 +440,28 @@ def test_qmv_one_row_kernel_vs_exact(mlxq, M, K, N, gs):
     assert_close(y, oracle.bf16_round(exact), f"one-row M={M} K={K} N={N} gs={gs}")
 
 
+# Biases far below their scales: every code 0, scales +-1, biases 2^-40 .. 2^-20, so each output is
+# sum_g b_g * X_g alone.  The GEMVs fold s * sum(x * c) + b * X with the codes as exact bf16 values,
+# so the bias term keeps its own precision; a fold through an offset code (128 + c, with
+# b - 128 s) would round the bias away entirely.  One-row kernel (M = 1, Q4 g64/g128), tile
+# kernel (M = 2, 8, Q4 g32 and Q8), held to the one-ulp bound of the exact product.
+@pytest.mark.parametrize("M", [1, 2, 8])
+@pytest.mark.parametrize("bits,gs", [(4, 64), (4, 128), (4, 32), (8, 64)])
+def test_qmv_bias_far_below_scale(mlxq, M, bits, gs):
+    banner("qmv small bias", M, bits, gs)
+    K, N = 3072, 520
+    rng = np.random.default_rng(7 * M + bits + gs)
+    x = bf16_normal(rng, (M, K))
+    rwq = np.zeros((N, K * bits // 32), dtype=np.uint32)
+    rs = oracle.bf16_round(rng.choice([-1.0, 1.0], size=(N, K // gs)).astype(np.float32))
+    rb = oracle.bf16_round((np.exp2(rng.uniform(-40, -20, size=(N, K // gs)))
+                            * rng.choice([-1.0, 1.0], size=(N, K // gs))).astype(np.float32))
+    y = to_np(mlxq.quantized_matmul(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), True, gs, bits))
+    exact = oracle.quantized_matmul(x, rwq, rs, rb, gs, bits, w_bf16=False, out_bf16=False)
+    assert np.abs(exact).max() < 1e-3  # the outputs are the bias terms alone
+    _close_to_exact(y, exact, f"small bias M={M} Q{bits} gs={gs}")
+
+
 @pytest.mark.parametrize("K,N,gs", [(1152, 33, 64), (11008, 300, 64), (8960, 257, 128), (13824, 130, 64),
                                     (18944, 100, 64), (29568, 48, 64), (32768, 40, 128), (2560, 4097, 128)])
 def test_qmv_one_row_kernel_ragged_k(mlxq, K, N, gs):

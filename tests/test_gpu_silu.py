@@ -6,8 +6,7 @@ silu as two ops (src/nn.rs:301-303).  The products are made exact so that only t
 under test: x = c * e_0 (one non-zero element, c a power of two), every code 0, scales 0 and the
 biases of row f equal to the f-th bf16 value, so gate row f is exactly c * b_f (or its overflow to
 +-inf, the same in every implementation) and up row f is c * u_f for a chosen bf16 value u_f.
-(Scales are 0 rather than 1: the Q4 GEMV folds each group as s * sum(x * (128 + c)) + (b - 128 s)
-* sum(x), exact for b = 0 or s = 0 but not for a tiny b against s = 1.)  Every normal
+(With every code 0 the scale does not enter the product.)  Every normal
 bf16 value and both zeros appear as b_f; subnormal values are left out (the rounding of the exact
 product's subnormal tail is not what this test is about).
 """
