@@ -266,7 +266,10 @@ def bench_quantize(mlxq, torch, iters=10):
     """Config 3 quantize pass: 4 x [5120,5120] bf16 -> Q8 g64 (321.1 MB algorithmic), timed over
     QUANT_SETS distinct sets of four weights so the Infinity Cache cannot hold one pass's data."""
     dev = torch.device("cuda:0")
-    ws = [gen_bf16((5120, 5120), 0.02, 200 + i, dev) for i in range(4 * QUANT_SETS)]
+    # Each set's four weights are consecutive row blocks of one tensor, so the batched legs can
+    # stream a set as one buffer; the per-weight legs see four ordinary contiguous weights.
+    sets = [gen_bf16((4 * 5120, 5120), 0.02, 200 + i, dev) for i in range(QUANT_SETS)]
+    ws = [t[5120 * j:5120 * (j + 1)] for t in sets for j in range(4)]
     outs = [(torch.empty((5120, 1280), dtype=torch.int32, device=dev),
              torch.empty((5120, 80), dtype=torch.bfloat16, device=dev),
              torch.empty((5120, 80), dtype=torch.bfloat16, device=dev)) for _ in ws]
@@ -279,6 +282,16 @@ def bench_quantize(mlxq, torch, iters=10):
         for w, (q, s, b) in zip(ws, outs):
             _lib.check(lib.mlxq_quantize(w.data_ptr(), 1, 5120, 5120, 64, 8, q.data_ptr(), s.data_ptr(),
                                          b.data_ptr(), sp))
+
+    arr4 = ctypes.c_void_p * 4
+
+    def run_batched():  # one mlxq_quantize_batched launch per set of four
+        sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        for i in range(QUANT_SETS):
+            sw, so = ws[4 * i:4 * i + 4], outs[4 * i:4 * i + 4]
+            _lib.check(lib.mlxq_quantize_batched(
+                arr4(*[w.data_ptr() for w in sw]), 4, 1, 5120, 5120, 64, 8, arr4(*[o[0].data_ptr() for o in so]),
+                arr4(*[o[1].data_ptr() for o in so]), arr4(*[o[2].data_ptr() for o in so]), sp))
     # Replayed from a HIP graph like the GEMV leg, so the ~17 us launches are not spaced out by
     # the host's per-call overhead (the rate still includes the gaps between the four kernels).
     # Every weight writes its own preallocated outputs: outputs allocated per call inside a graph
@@ -291,15 +304,26 @@ def bench_quantize(mlxq, torch, iters=10):
     # into buffers of their own, same timing.
     ref = stream_reference(torch, ws, 8, iters) / QUANT_SETS
     rbytes = 4 * (5120 * 5120 * 2 + 5120 * 5120)
+    # The same pass as one launch per set (mlxq_quantize_batched), against the stream kernel over
+    # each set's four weights in one launch.
+    mb = graph_ms(torch, run_batched, inner=1, reps=iters) / QUANT_SETS
+    refb = stream_reference(torch, sets, 8, iters) / QUANT_SETS
     return {"us_per_pass": ms * 1e3, "GBs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes,
             "frac_of_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "stream_reference_us_per_pass": round(ref * 1e3, 2),
             "stream_reference_GBs": round(rbytes / (ref * 1e-3) / 1e9, 1),
             "frac_of_stream_reference_time": round(ref / ms, 4),
-            "note": "4 launches per pass, each weight into its own outputs, passes rotated over "
-                    f"{QUANT_SETS} weight sets; stream_reference: quantize's load/store pattern and "
-                    "grid with trivial arithmetic on the same weights (reads the weights, writes the "
-                    "code bytes; no scales), same timing"}
+            "batched_us_per_pass": round(mb * 1e3, 2),
+            "batched_GBs": round(nbytes / (mb * 1e-3) / 1e9, 1),
+            "batched_frac_of_hbm_peak": round(nbytes / (mb * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "batched_stream_reference_us_per_pass": round(refb * 1e3, 2),
+            "batched_stream_reference_GBs": round(rbytes / (refb * 1e-3) / 1e9, 1),
+            "note": "4 launches per pass (the reference's weight-by-weight calls), each weight into its "
+                    f"own outputs, passes rotated over {QUANT_SETS} weight sets; stream_reference: "
+                    "quantize's load/store pattern and grid with trivial arithmetic on the same weights "
+                    "(reads the weights, writes the code bytes; no scales), same timing; batched_*: the "
+                    "same pass as one mlxq_quantize_batched launch per set of four, against the stream "
+                    "kernel over the four weights in one launch"}
 
 
 def stream_reference(torch, ws, words, reps):

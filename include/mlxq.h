@@ -93,6 +93,17 @@ int mlxq_quantize(const void* w, int w_dtype, int64_t N, int64_t K, int group_si
                   uint32_t* wq, void* scales, void* biases, void* stream);
 
 /*
+ * quantize over `count` weights of one shape [N,K] and dtype: the same outputs as `count`
+ * mlxq_quantize calls (w[i] -> wq[i], scales[i], biases[i]), in launches of up to 16 weights,
+ * which pay a launch's ramp and its partly filled last round once for all of them.  No single
+ * counterpart in the reference, which quantizes weight by weight (quantize_map, src/quant.rs:125-149,
+ * calling a-1 per target); for converters that pack many same-shaped weights.  The pointer arrays
+ * are host memory; count == 0 does nothing.
+ */
+int mlxq_quantize_batched(const void* const* w, int count, int w_dtype, int64_t N, int64_t K, int group_size,
+                          int bits, uint32_t* const* wq, void* const* scales, void* const* biases, void* stream);
+
+/*
  * dequantize — replaces mlx_rs::ops::dequantize(wq, scales, biases, group_size, bits)
  * (src/nn.rs:55).  out [N,K] in sb_dtype (the scales dtype, as MLX returns).
  */

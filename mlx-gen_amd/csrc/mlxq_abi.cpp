@@ -222,6 +222,23 @@ int mlxq_quantize(const void* w, int w_dtype, int64_t N, int64_t K, int group_si
   return run_quantize(w, w_dtype, N, K, group_size, bits, wq, scales, biases, (hipStream_t)stream);
 }
 
+int mlxq_quantize_batched(const void* const* w, int count, int w_dtype, int64_t N, int64_t K, int group_size,
+                          int bits, uint32_t* const* wq, void* const* scales, void* const* biases, void* stream) {
+  g_err[0] = 0;
+  int rc;
+  if (count < 0) return set_error(MLXQ_EINVAL, "quantize_batched: count %d < 0", count);
+  if ((rc = check_pack("quantize_batched", N, K, group_size, bits))) return rc;
+  if ((rc = check_dtype("quantize_batched", "w", w_dtype))) return rc;
+  if (count == 0 || N == 0) return MLXQ_OK;
+  if (!w || !wq || !scales || !biases) return set_error(MLXQ_EINVAL, "quantize_batched: a pointer array is null");
+  for (int e = 0; e < count; ++e) {
+    if ((rc = check_aligned("quantize_batched", "w", w[e])) || (rc = check_aligned("quantize_batched", "wq", wq[e])))
+      return rc;
+    if (!scales[e] || !biases[e]) return set_error(MLXQ_EINVAL, "quantize_batched: scales/biases %d are null", e);
+  }
+  return run_quantize_batched(w, count, w_dtype, N, K, group_size, bits, wq, scales, biases, (hipStream_t)stream);
+}
+
 int mlxq_dequantize(const uint32_t* wq, const void* scales, const void* biases, int sb_dtype,
                     int64_t N, int64_t K, int group_size, int bits, void* out, void* stream) {
   g_err[0] = 0;

@@ -62,6 +62,8 @@ int check_launch(const char* what);
 
 int run_quantize(const void* w, int dtype, int64_t N, int64_t K, int gs, int bits, uint32_t* wq,
                  void* s, void* b, hipStream_t st);
+int run_quantize_batched(const void* const* w, int count, int dtype, int64_t N, int64_t K, int gs, int bits,
+                         uint32_t* const* wq, void* const* s, void* const* b, hipStream_t st);
 int run_dequantize(const uint32_t* wq, const void* s, const void* b, int dtype, int64_t N, int64_t K,
                    int gs, int bits, void* out, hipStream_t st);
 // The f32-dequant product; y in promote(x_dtype, sb_dtype): the GEMV for M <= 8 (exact f32), the

@@ -82,6 +82,10 @@ struct Packed {
 // `as_dtype` between f32 and bf16 (round to nearest even); returns `a` itself when equal.
 Array as_dtype(const Array& a, Dtype dt, hipStream_t s = nullptr);
 Packed quantize(const Array& w, int group_size, int bits, hipStream_t s = nullptr);
+// quantize over weights of one shape and dtype, several per launch (mlxq_quantize_batched): the
+// same triples as one quantize per weight.
+std::vector<Packed> quantize_batched(const std::vector<Array>& ws, int group_size, int bits,
+                                     hipStream_t s = nullptr);
 Array dequantize(const Array& wq, const Array& scales, const Array& biases, int group_size, int bits,
                  hipStream_t s = nullptr);
 // x [..., K] -> [..., N]; only transpose = true exists in the reference and here.

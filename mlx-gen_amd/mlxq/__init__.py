@@ -9,7 +9,7 @@ from ._lib import (MLXQ_ACT_GELU, MLXQ_ACT_GELU_EXACT, MLXQ_ACT_GELU_TANH, MLXQ_
                    MLXQ_BFLOAT16, MLXQ_FLOAT16, MLXQ_FLOAT32, MlxqError, LIB_PATH, load)
 from .ops import (DEFAULT_GROUP_SIZE, dequantize, embedding, linear, linear_out_dtype,
                   linear_workspace_size, lokr_residual, lora_residual, packed_bits, promote, qmm, qmm_experts, qmv,
-                  qmv_valu, quantize, quantized_matmul, swiglu)
+                  qmv_valu, quantize, quantize_batched, quantized_matmul, swiglu)
 from .nn import (Adapter, AdaptableLinear, LokrAdapter, QuantizedLinear, StackedExperts, TokenEmbedding,
                  has_packed_experts, lin, load_packed_experts, quantize_map)
 from . import io
@@ -18,7 +18,7 @@ __all__ = [
     "MLXQ_ACT_GELU", "MLXQ_ACT_GELU_EXACT", "MLXQ_ACT_GELU_TANH", "MLXQ_ACT_NONE", "MLXQ_BFLOAT16",
     "MLXQ_FLOAT16", "MLXQ_FLOAT32", "MlxqError", "LIB_PATH", "load", "DEFAULT_GROUP_SIZE", "dequantize", "embedding",
     "linear", "linear_out_dtype", "linear_workspace_size", "lokr_residual", "lora_residual", "packed_bits", "promote",
-    "qmm", "qmm_experts", "qmv", "qmv_valu", "quantize",
+    "qmm", "qmm_experts", "qmv", "qmv_valu", "quantize", "quantize_batched",
     "quantized_matmul", "swiglu", "Adapter", "AdaptableLinear", "LokrAdapter", "QuantizedLinear", "StackedExperts",
     "TokenEmbedding", "has_packed_experts", "lin", "load_packed_experts", "quantize_map", "io",
 ]

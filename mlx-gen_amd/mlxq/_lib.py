@@ -33,6 +33,7 @@ EXPORTS = (
     "mlxq_last_error",
     "mlxq_version",
     "mlxq_quantize",
+    "mlxq_quantize_batched",
     "mlxq_dequantize",
     "mlxq_quantized_matmul",
     "mlxq_qmm",
@@ -95,6 +96,8 @@ def load():
     lib.mlxq_last_error.restype = ctypes.c_char_p
     lib.mlxq_version.restype = ctypes.c_char_p
     lib.mlxq_quantize.argtypes = [_vp, _int, _i64, _i64, _int, _int, _vp, _vp, _vp, _vp]
+    _pp = ctypes.POINTER(ctypes.c_void_p)
+    lib.mlxq_quantize_batched.argtypes = [_pp, _int, _int, _i64, _i64, _int, _int, _pp, _pp, _pp, _vp]
     lib.mlxq_dequantize.argtypes = [_vp, _vp, _vp, _int, _i64, _i64, _int, _int, _vp, _vp]
     lib.mlxq_quantized_matmul.argtypes = [_vp, _int, _i64, _i64, _vp, _vp, _vp, _int, _i64, _int,
                                           _int, _int, _vp, _vp]
@@ -125,7 +128,7 @@ def load():
                                 _int, _vp, _vp]
     lib.mlxq_embedding.argtypes = [_vp, _i64, _vp, _vp, _vp, _int, _i64, _i64, _int, _int, _vp, _int,
                                    _vp]
-    for name in ("mlxq_quantize", "mlxq_dequantize", "mlxq_quantized_matmul", "mlxq_qmm",
+    for name in ("mlxq_quantize", "mlxq_quantize_batched", "mlxq_dequantize", "mlxq_quantized_matmul", "mlxq_qmm",
                  "mlxq_qmv", "mlxq_qmv_valu", "mlxq_linear", "mlxq_linear_noalloc", "mlxq_packed_bits", "mlxq_embedding",
                  "mlxq_lora_residual", "mlxq_lokr_residual", "mlxq_cast", "mlxq_swiglu",
                  "mlxq_qmm_experts"):

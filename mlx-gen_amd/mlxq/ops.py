@@ -132,6 +132,32 @@ def quantize(w: torch.Tensor, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 
     return wq, s, b
 
 
+def quantize_batched(ws, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4):
+    """quantize() over a list of weights of one shape and dtype, in launches of up to 16 weights
+    (mlxq_quantize_batched): the same (wq, scales, biases) triples as one quantize() per weight."""
+    ws = [w.contiguous() for w in ws]
+    if not ws:
+        return []
+    _need_gpu(*ws)
+    w0 = ws[0]
+    if w0.dim() != 2:
+        raise ValueError(f"quantize_batched expects 2-D weights, got shape {tuple(w0.shape)}")
+    for w in ws[1:]:
+        if w.shape != w0.shape or w.dtype != w0.dtype or w.device != w0.device:
+            _bad("quantize_batched", "every weight must have the first one's shape, dtype and device")
+    N, K = w0.shape
+    gcols = K // group_size if group_size > 0 else 0
+    outs = [(torch.empty((N, max(K * bits // 32, 0)), dtype=torch.int32, device=w0.device),
+             torch.empty((N, gcols), dtype=w0.dtype, device=w0.device),
+             torch.empty((N, gcols), dtype=w0.dtype, device=w0.device)) for _ in ws]
+    arr = ctypes.c_void_p * len(ws)
+    check(_lib.load().mlxq_quantize_batched(
+        arr(*[_ptr(w) for w in ws]), len(ws), _dt(w0), N, K, group_size, bits,
+        arr(*[_ptr(o[0]) for o in outs]), arr(*[_ptr(o[1]) for o in outs]), arr(*[_ptr(o[2]) for o in outs]),
+        _stream(w0.device)))
+    return outs
+
+
 def _k_of(wq: torch.Tensor, bits: int) -> int:
     return wq.shape[-1] * 32 // bits
 

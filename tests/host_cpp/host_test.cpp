@@ -586,6 +586,20 @@ static void gpu_cases(const fs::path& root) {
     Weights packed = quantize_map(m, 4, 32, [](const std::string& b) { return b != "blk.norm"; });
     EXPECT(packed.count("blk.q.scales") && packed.count("embed.biases") && !packed.count("blk.norm.scales"),
            "quantize_map keys");
+    {  // two targets of one shape: packed in one batched launch, the same triples as quantize()
+      Weights m2;
+      std::vector<float> wa = bf16_normal(rng, 64 * 128, 0.02f), wb = bf16_normal(rng, 64 * 128, 0.05f);
+      m2["a.weight"] = bf16_array(wa, {64, 128});
+      m2["b.weight"] = bf16_array(wb, {64, 128});
+      Weights p2 = quantize_map(m2, 8, 64, [](const std::string&) { return true; });
+      for (const char* base : {"a", "b"}) {
+        Packed one = quantize(m2.at(std::string(base) + ".weight"), 64, 8);
+        EXPECT(host<uint32_t>(p2.at(std::string(base) + ".weight")) == host<uint32_t>(one.wq) &&
+                   host<uint16_t>(p2.at(std::string(base) + ".scales")) == host<uint16_t>(one.scales) &&
+                   host<uint16_t>(p2.at(std::string(base) + ".biases")) == host<uint16_t>(one.biases),
+               "batched quantize_map differs from quantize");
+      }
+    }
     save_map((dir / "model.safetensors").string(), packed);
     HostMap raw = read_safetensors((dir / "model.safetensors").string());
     EXPECT(raw.at("blk.q.weight").dtype == Dtype::Uint32, "codes stored as U32");

@@ -103,6 +103,28 @@ def test_qmv_valu_validation(lib):
     assert st == _lib.MLXQ_EINVAL and b"multiple of group_size" in lib.mlxq_last_error()
 
 
+def test_quantize_batched_validation(lib):
+    """mlxq_quantize_batched: argument errors come back before any device work."""
+    from mlxq import _lib
+    arr = ctypes.c_void_p * 2
+    good = arr(4096, 8192)
+    odd = arr(4096, 4100)  # second weight not 16-byte aligned
+    null = ctypes.c_void_p(0)
+    st = lib.mlxq_quantize_batched(good, -1, 1, 8, 128, 64, 4, good, good, good, null)
+    assert st == _lib.MLXQ_EINVAL and b"count" in lib.mlxq_last_error()
+    st = lib.mlxq_quantize_batched(good, 2, 1, 8, 100, 64, 4, good, good, good, null)
+    assert st == _lib.MLXQ_EINVAL and b"multiple of group_size" in lib.mlxq_last_error()
+    st = lib.mlxq_quantize_batched(good, 2, 7, 8, 128, 64, 4, good, good, good, null)
+    assert st == _lib.MLXQ_EINVAL and b"dtype" in lib.mlxq_last_error()
+    st = lib.mlxq_quantize_batched(odd, 2, 1, 8, 128, 64, 4, good, good, good, null)
+    assert st == _lib.MLXQ_EINVAL and b"aligned" in lib.mlxq_last_error()
+    st = lib.mlxq_quantize_batched(good, 2, 1, 8, 128, 64, 4, good, arr(4096, 0), good, null)
+    assert st == _lib.MLXQ_EINVAL and b"null" in lib.mlxq_last_error()
+    st = lib.mlxq_quantize_batched(None, 2, 1, 8, 128, 64, 4, good, good, good, null)
+    assert st == _lib.MLXQ_EINVAL and b"null" in lib.mlxq_last_error()
+    assert lib.mlxq_quantize_batched(None, 0, 1, 8, 128, 64, 4, None, None, None, null) == _lib.MLXQ_OK
+
+
 def test_linear_workspace_size(lib):
     from mlxq import _lib
     bf, f32 = _lib.MLXQ_BFLOAT16, _lib.MLXQ_FLOAT32
@@ -251,20 +273,24 @@ def test_quantize_map_host_logic(monkeypatch):
 
     calls = []
 
-    def fake_quantize(w, gs, bits):
-        calls.append((tuple(w.shape), w.dtype, gs, bits))
-        return (torch.zeros(1), torch.zeros(1), torch.zeros(1))
+    def fake_quantize_batched(ws, gs, bits):
+        calls.append(([tuple(w.shape) for w in ws], [w.dtype for w in ws], gs, bits))
+        # each triple carries its weight's first element, so the test can see which went where
+        return [(w.flatten()[:1].clone(), torch.zeros(1), torch.zeros(1)) for w in ws]
 
-    monkeypatch.setattr(ops, "quantize", fake_quantize)
+    monkeypatch.setattr(ops, "quantize_batched", fake_quantize_batched)
     m = {
-        "a.weight": torch.zeros(8, 128),
+        "a.weight": torch.full((8, 128), 1.0),
         "a.bias": torch.zeros(8),
         "b.weight": torch.zeros(8, 100),     # K not divisible by gs -> dense
         "c.weight": torch.zeros(8, 32),      # K < gs -> dense
         "norm.weight": torch.zeros(128),     # 1-D -> dense
         "skip.weight": torch.zeros(8, 128),  # not a target -> dense
+        "d.weight": torch.full((16, 64), 3.0),
+        "e.weight": torch.full((8, 128), 2.0),  # same shape as a: packed in a's launch
     }
     out = nn.quantize_map(m, 4, 64, lambda base: base != "skip")
-    assert set(out) == {"a.weight", "a.scales", "a.biases", "a.bias", "b.weight", "c.weight",
-                        "norm.weight", "skip.weight"}
-    assert calls == [((8, 128), torch.bfloat16, 64, 4)]
+    assert list(out) == ["a.weight", "a.scales", "a.biases", "a.bias", "b.weight", "c.weight", "norm.weight",
+                         "skip.weight", "d.weight", "d.scales", "d.biases", "e.weight", "e.scales", "e.biases"]
+    assert calls == [([(8, 128), (8, 128)], [torch.bfloat16] * 2, 64, 4), ([(16, 64)], [torch.bfloat16], 64, 4)]
+    assert [float(out[k][0]) for k in ("a.weight", "d.weight", "e.weight")] == [1.0, 3.0, 2.0]

@@ -75,6 +75,29 @@ def test_quantize_bit_exact(mlxq, N, K, gs, bits, dtype):
     assert np.array_equal(deq, oracle.dequantize(rwq, rs, rb, gs, bits, out_bf16=(dtype == "bf16")))
 
 
+# mlxq_quantize_batched: several weights of one shape per launch (up to 16; 17 takes two launches),
+# bit for bit what one quantize per weight gives, and the oracle's packing for the first weight.
+@pytest.mark.parametrize("count,N,K,gs,bits,dtype", [(1, 40, 256, 64, 4, "bf16"), (4, 640, 5120, 64, 8, "bf16"),
+                                                     (17, 33, 384, 128, 4, "bf16"), (3, 257, 96, 32, 8, "f32"),
+                                                     (5, 1, 64, 64, 4, "f32"), (16, 96, 1024, 32, 4, "bf16")])
+def test_quantize_batched_matches_per_weight(mlxq, count, N, K, gs, bits, dtype):
+    banner("quantize batched", count, N, K, gs, bits, dtype)
+    rng = np.random.default_rng(count * 31 + N + K + gs + bits)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    ws = [(rng.standard_normal((N, K)) * 0.02 * (i + 1)).astype(np.float32) for i in range(count)]
+    if dtype == "bf16":
+        ws = [oracle.bf16_round(w) for w in ws]
+    gws = [to_gpu(w, tdt) for w in ws]
+    got = mlxq.quantize_batched(gws, gs, bits)
+    assert len(got) == count
+    for gw, (wq, s, b) in zip(gws, got):
+        rwq, rs, rb = mlxq.quantize(gw, gs, bits)
+        assert torch.equal(wq, rwq) and torch.equal(s, rs) and torch.equal(b, rb)
+    owq, os_, ob = oracle.quantize(ws[0], gs, bits, sb_bf16=(dtype == "bf16"))
+    assert np.array_equal(to_np(got[0][0]), owq)
+    assert np.array_equal(to_np(got[0][1]), os_) and np.array_equal(to_np(got[0][2]), ob)
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_quantize_special_groups(mlxq, bits):
     """Zero, constant, all-negative, tiny-range and huge-range groups."""
