@@ -35,7 +35,8 @@ __global__ void lora_prep_kernel(const XT* __restrict__ x, int64_t M, int64_t K,
 }
 
 // bf16 x.A on the matrix cores: xa[M,R] = round_bf16(x[M,K] . A[K,rank]), columns >= rank zero.
-// A workgroup owns 16 rows of x and 16 columns of xa; its 8 waves split K (32 per MFMA step,
+// A workgroup owns `rows` rows of x (NB blocks of 16 rows on the MFMA; rows past its share repeat
+// its last row and are not stored) and 16 columns of xa; its 8 waves split K (32 per MFMA step,
 // K % 32 == 0 because K is a multiple of the group size) and reduce through LDS.  The MFMA's B
 // operand needs 8 consecutive k of one column of the k-major A: 8 two-byte loads per lane and
 // step, L1/L2 hits (A is at most K x 256 x 2 bytes and every workgroup reads it).  Each wave
@@ -49,13 +50,21 @@ constexpr int kXaChunk = 4;
 // A16 (rank 16, one 16-column block): a chunk of A (4 steps x 32 rows x 16 columns) is 4 KB of
 // contiguous memory, fetched with four 16-byte loads per lane and transposed through the wave's
 // 4 KB LDS buffer, instead of 32 two-byte gathers per lane.
-template <bool A16>
+// Rows per workgroup: 16, except from 4097 to 8192 rows, where ceil(M / 256) (17-32 rows, two
+// MFMA blocks) spreads the x stream evenly over at most 256 workgroups, one per CU.  With 16-row
+// workgroups M = 4608 made 288 of them, and the 32 CUs that ran two read twice the bytes: same-
+// process A/B through mlxq_lora_residual (K = 3072, rank 16), 16-row against balanced workgroups:
+// M = 4608 24.0 -> 20.9 us, 5120 23.8 -> 21.3, 6144 26.0 -> 24.3, 8192 29.9 / 30.1 (even);
+// 512 balanced workgroups of up to 16 rows (two per CU) gained about half as much, and 32-row
+// workgroups past 8192 rows lost (M = 12288 51.5 -> 53.1).
+template <bool A16, int NB>
 __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* __restrict__ x, int M,
                                                                 int K, const uint16_t* __restrict__ A,
                                                                 int rank, int R, uint16_t* __restrict__ xa,
-                                                                int xa_blocks, const uint16_t* __restrict__ B,
+                                                                int xa_blocks, int rows,
+                                                                const uint16_t* __restrict__ B,
                                                                 int64_t N, uint16_t* __restrict__ lbt) {
-  __shared__ float red[kXaWaves][16 * 16];
+  __shared__ float red[NB][kXaWaves][16 * 16];
   __shared__ __attribute__((aligned(16))) uint16_t abuf[A16 ? kXaWaves * 2048 : 8];
   // wave is made scalar so the K-range branches below are uniform scalar branches.
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -70,17 +79,22 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
     return;
   }
   const int c16 = lane & 15, q = lane >> 4;
-  const int m0 = blockIdx.x * 16, r0 = blockIdx.y * 16;
-  const int xrow = m0 + c16 < M ? m0 + c16 : M - 1;
+  const int m0 = blockIdx.x * rows, r0 = blockIdx.y * 16;
+  const int m_end = m0 + rows < M ? m0 + rows : M;  // this workgroup's rows [m0, m_end)
   const int r = r0 + c16;
   const bool rvalid = r < rank;
   const int KS = K / 32, per = (KS + kXaWaves - 1) / kXaWaves;
   const int ks0 = __builtin_amdgcn_readfirstlane(wave * per);
   const int ks1 = __builtin_amdgcn_readfirstlane(ks0 + per < KS ? ks0 + per : KS);
-  const uint16_t* xp = x + (int64_t)xrow * K + 8 * q;
+  const uint16_t* xp[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int row = m0 + 16 * b + c16;
+    xp[b] = x + (int64_t)(row < m_end ? row : m_end - 1) * K + 8 * q;
+  }
   const uint16_t* ap = A + (int64_t)(8 * q) * rank + (rvalid ? r : 0);
   struct Chunk {
-    bf16x8 a[kXaChunk];
+    bf16x8 a[NB][kXaChunk];
     uint16_t w[A16 ? 1 : kXaChunk][8];
     u32x4 araw[A16 ? kXaChunk : 1];  // A16: lane l's 64 bytes of the chunk (rows 2l, 2l+1)
   };
@@ -92,7 +106,8 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
 #pragma unroll
     for (int u = 0; u < kXaChunk; ++u) {
       const int k = ks + u < ks1 ? ks + u : ks1 - 1;
-      c.a[u] = *reinterpret_cast<const bf16x8*>(xp + k * 32);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) c.a[b][u] = *reinterpret_cast<const bf16x8*>(xp[b] + k * 32);
       if constexpr (!A16) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) c.w[u][j] = ap[(int64_t)(k * 32 + j) * rank];  // column 0 if !rvalid
@@ -114,7 +129,9 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
       for (int p = 0; p < kXaChunk; ++p) *reinterpret_cast<u32x4*>(wbuf + lane * 32 + p * 8) = c.araw[p];
     }
   };
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4 acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   // Every MFMA of a chunk is issued; steps past the wave's range and padding columns get a zero B
   // operand through a mask the compiler cannot see through.  MFMA does not honour the EXEC mask:
   // given a visible "operand is zero" condition the compiler predicated the MFMA on EXEC without
@@ -137,7 +154,9 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
         }
         bw[j] = (lo | (hi << 16)) & keep;
       }
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c.a[u], __builtin_bit_cast(bf16x8, bw), acc, 0, 0, 0);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c.a[b][u], __builtin_bit_cast(bf16x8, bw), acc[b], 0, 0, 0);
     }
   };
   if (ks0 < ks1) {
@@ -155,14 +174,17 @@ __global__ __launch_bounds__(kXaWaves * 64) void lora_xa_kernel(const uint16_t* 
     }
   }
 #pragma unroll
-  for (int e = 0; e < 4; ++e) red[wave][(4 * q + e) * 16 + c16] = acc[e];
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[b][wave][(4 * q + e) * 16 + c16] = acc[b][e];
   __syncthreads();
-  if (tid < 256) {
-    const int m = tid >> 4, n = tid & 15;
+  if (tid < 256 * NB) {
+    const int b = tid >> 8, m = (tid >> 4) & 15, n = tid & 15;
     float v = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kXaWaves; ++w) v += red[w][m * 16 + n];
-    if (m0 + m < M) xa[(int64_t)(m0 + m) * R + r0 + n] = f32_to_bf16_bits(v);
+    for (int w = 0; w < kXaWaves; ++w) v += red[b][w][m * 16 + n];
+    const int row = m0 + 16 * b + m;
+    if (row < m_end) xa[(int64_t)row * R + r0 + n] = f32_to_bf16_bits(v);
   }
 }
 
@@ -218,17 +240,29 @@ int run_lora_prep(const void* x, int x_dtype, int64_t M, int64_t K, const void* 
   }
   const int64_t bt_blocks = (N * R + kXaWaves * 64 - 1) / (kXaWaves * 64);
   if (K % 32 == 0 && M < (1LL << 31) / 16 && K < (1LL << 31) && bt_blocks < (1LL << 30)) {
-    // x.A workgroups (16 rows x 16 columns each), then the B^T workgroups.
-    const int xa_blocks = (int)((M + 15) / 16);
+    // x.A workgroups (`rows` rows x 16 columns each), then the B^T workgroups.
+    const int rows = M > 16 * 256 && M <= 32 * 256 ? (int)((M + 255) / 256) : 16;
+    const int xa_blocks = (int)((M + rows - 1) / rows);
     const dim3 grid((unsigned)(xa_blocks + bt_blocks), (unsigned)(R / 16));
-    if (rank == 16 && R == 16)
-      hipLaunchKernelGGL(lora_xa_kernel<true>, grid, dim3(kXaWaves * 64), 0, st, (const uint16_t*)x,
-                         (int)M, (int)K, (const uint16_t*)A, rank, R, (uint16_t*)xa, xa_blocks,
-                         (const uint16_t*)B, N, (uint16_t*)lbt);
-    else
-      hipLaunchKernelGGL(lora_xa_kernel<false>, grid, dim3(kXaWaves * 64), 0, st, (const uint16_t*)x,
-                         (int)M, (int)K, (const uint16_t*)A, rank, R, (uint16_t*)xa, xa_blocks,
-                         (const uint16_t*)B, N, (uint16_t*)lbt);
+    if (rows <= 16) {
+      if (rank == 16 && R == 16)
+        hipLaunchKernelGGL((lora_xa_kernel<true, 1>), grid, dim3(kXaWaves * 64), 0, st, (const uint16_t*)x,
+                           (int)M, (int)K, (const uint16_t*)A, rank, R, (uint16_t*)xa, xa_blocks, rows,
+                           (const uint16_t*)B, N, (uint16_t*)lbt);
+      else
+        hipLaunchKernelGGL((lora_xa_kernel<false, 1>), grid, dim3(kXaWaves * 64), 0, st, (const uint16_t*)x,
+                           (int)M, (int)K, (const uint16_t*)A, rank, R, (uint16_t*)xa, xa_blocks, rows,
+                           (const uint16_t*)B, N, (uint16_t*)lbt);
+    } else {
+      if (rank == 16 && R == 16)
+        hipLaunchKernelGGL((lora_xa_kernel<true, 2>), grid, dim3(kXaWaves * 64), 0, st, (const uint16_t*)x,
+                           (int)M, (int)K, (const uint16_t*)A, rank, R, (uint16_t*)xa, xa_blocks, rows,
+                           (const uint16_t*)B, N, (uint16_t*)lbt);
+      else
+        hipLaunchKernelGGL((lora_xa_kernel<false, 2>), grid, dim3(kXaWaves * 64), 0, st, (const uint16_t*)x,
+                           (int)M, (int)K, (const uint16_t*)A, rank, R, (uint16_t*)xa, xa_blocks, rows,
+                           (const uint16_t*)B, N, (uint16_t*)lbt);
+    }
   } else {
     hipLaunchKernelGGL(lora_prep_kernel<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
                        (const uint16_t*)x, M, K, (const uint16_t*)A, (const uint16_t*)B, N, rank, R,

@@ -777,6 +777,31 @@ def test_linear_lora_short_k_ranks(mlxq, K, rank, scale):
     assert_close(y, ref, f"lora K={K} rank={rank}")
 
 
+# The x.A preparation from 4097 to 8192 rows spreads the rows over at most 256 workgroups of 17-32
+# (two MFMA blocks; rows past a workgroup's share repeat its last row and are never stored):
+# M just past 4096 (17 rows each), the config-5 M = 4608 (18), 8192 (32) and beyond (16-row
+# workgroups again), ranks 16 (the 4 KB A-chunk form) and 24 (the general form, two column
+# blocks).  y = 0, so the outputs are the LoRA term alone: each row's x.A is checked, not hidden
+# under a base product.
+@pytest.mark.parametrize("M", [4097, 4608, 8192, 8229])
+@pytest.mark.parametrize("rank", [16, 24])
+def test_lora_xa_rows_per_workgroup(mlxq, M, rank):
+    banner("lora x.A rows", M, rank)
+    rng = np.random.default_rng(M + rank)
+    K, N = 256, 64
+    x = bf16_normal(rng, (M, K))
+    A = bf16_normal(rng, (K, rank), 0.05)
+    B = bf16_normal(rng, (rank, N), 0.05)
+    y = torch.zeros((M, N), dtype=torch.bfloat16, device="cuda")
+    out = to_np(mlxq.ops.lora_residual(to_gpu(x), y, to_gpu(A), to_gpu(B), 1.0))
+    xa = oracle.bf16_round((x.astype(np.float64) @ A.astype(np.float64)).astype(np.float32))
+    want = oracle.bf16_round((xa.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+    assert_close(out, want, f"lora x.A M={M} rank={rank}")
+    # every row carries its own term: a row computed from a neighbour's x would be off by O(1)
+    rowerr = np.abs(out - want).max(axis=1) / (np.abs(want).max(axis=1) + 1e-30)
+    assert rowerr.max() < 0.05, int(rowerr.argmax())
+
+
 # ---------------------------------------------------------------- errors never crash
 
 def test_invalid_arguments_return_errors(mlxq):
