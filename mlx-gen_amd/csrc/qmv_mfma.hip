@@ -32,7 +32,8 @@
 //     (quarter, word), after which word i of every lane belongs to group 4t+i.
 // Each lane reads the activation run matching its code run from LDS (per-lane offsets below).
 // The 16x16 result holds column n = lane&15 for rows m = 4q + e.
-// A workgroup owns 16 weight rows; its waves split K and reduce through LDS at the end.
+// A workgroup owns up to 16 weight rows (one MFMA tile); its waves split K and reduce through LDS
+// at the end.
 // Q4 k-order inside an 8-run is [0,2,4,6,1,3,5,7] (low nibbles first, see unpack_q4); the
 // activation rows are permuted to match with v_perm_b32 as they are copied into LDS.
 #include <atomic>
@@ -175,7 +176,7 @@ struct GemvTile {
   static constexpr int SBL = (16 * NGW + 63) / 64;  // scale entries per lane
   static constexpr int XW = T * CPL * 2 + 16;       // LDS pitch of the wave's activation rows
 
-  int lane, c16, q, n0, M, K, N, G, ls0, kb, g0;
+  int lane, c16, q, n0, nr, M, K, N, G, ls0, kb, g0;
   unsigned char* wl;  // this wave's LDS region: activation rows, then the (s, zc) table
   float* szw;
   u32x4 cx[MR][XSL];
@@ -185,13 +186,15 @@ struct GemvTile {
   uint32_t w_base;
 
   // wave_all: the wave's index in the workgroup (selects its LDS region); wave: its index among
-  // the waves of its matrix (selects its K range); rows [n0, n0 + 16) of an [N, K] matrix.
-  __device__ __forceinline__ GemvTile(int lane_, int wave_all, int wave, int n0_, int M_, int K_,
+  // the waves of its matrix (selects its K range); rows [n0, n0 + nr) of an [N, K] matrix, nr <= 16
+  // (MFMA columns past nr load nothing and are never stored).
+  __device__ __forceinline__ GemvTile(int lane_, int wave_all, int wave, int n0_, int nr_, int M_, int K_,
                                       int N_, unsigned char* lds) {
     lane = lane_;
     c16 = lane & 15;
     q = lane >> 4;
     n0 = n0_;
+    nr = nr_;
     M = M_;
     K = K_;
     N = N_;
@@ -223,20 +226,18 @@ struct GemvTile {
     for (int j = 0; j < SBL; ++j) {
       const int e = lane + 64 * j;
       const int r = e / NGW, gl = e - r * NGW;  // constant divisor
-      const bool ok = e < 16 * NGW && n0 + r < N && g0 + gl < G;
+      const bool ok = e < 16 * NGW && r < nr && g0 + gl < G;
       const uint32_t off = ok ? ((uint32_t)(n0 + r) * (uint32_t)G + (uint32_t)(g0 + gl)) * 2u : kOob;
       cs[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
       cz[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rz, off, 0, 0);
     }
   }
 
-  // The wave's first STEPS weight loads: 16 rows x 64 contiguous bytes per load, rows past N
-  // clamped (never stored).
+  // The wave's first STEPS weight loads: 16 rows x 64 contiguous bytes per load; the lanes of
+  // rows past the workgroup's nr read past every buffer (zero, no memory traffic).
   __device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t rw_) {
     rw = rw_;
-    const int n = n0 + c16;
-    const int nn = n < N ? n : N - 1;
-    w_base = (uint32_t)nn * (uint32_t)(K * BITS / 8) + (uint32_t)(ls0 * 64 + q * 16);
+    w_base = c16 < nr ? (uint32_t)(n0 + c16) * (uint32_t)(K * BITS / 8) + (uint32_t)(ls0 * 64 + q * 16) : kOob;
 #pragma unroll
     for (int d = 0; d < STEPS; ++d) wv[d] = load16(rw, w_base + (uint32_t)d * 64u);
   }
@@ -397,7 +398,7 @@ struct GemvTile {
 template <int NMAT, int E>
 __device__ __forceinline__ void gemv_reduce_store(unsigned char* lds, const float (&yacc)[E],
                                                   int wave_all, int W, int lane, int tid, int NT,
-                                                  int M, int n0, int N, uint16_t* __restrict__ y) {
+                                                  int M, int n0, int nr, int N, uint16_t* __restrict__ y) {
   const int c16 = lane & 15, q = lane >> 4;
   __syncthreads();
   float* red = reinterpret_cast<float*>(lds);
@@ -414,11 +415,11 @@ __device__ __forceinline__ void gemv_reduce_store(unsigned char* lds, const floa
       // each op rounded to bf16 as the reference's separate ops are (qwen3.rs:178-181)
       v = silu_bf16(round_bf16(v)) * round_bf16(u);
     }
-    if (n0 + nl < N) y[m * N + n0 + nl] = f32_to_bf16_bits(v);
+    if (nl < nr) y[m * N + n0 + nl] = f32_to_bf16_bits(v);
   }
 }
 
-// The GEMV launch: a workgroup owns 16 weight rows and its waves split K.  NMAT = 2 is the
+// The GEMV launch: a workgroup owns `rows` <= 16 weight rows and its waves split K.  NMAT = 2 is the
 // SwiGLU decode form: the second wave half streams the same 16 rows of a second matrix (up).
 // Each wave stages only its own operands (its K range of the activations, the scales and biases
 // of its groups) into its own LDS region, so it starts on its weights as soon as its own operands
@@ -428,7 +429,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
     const uint16_t* __restrict__ x, int M, int K, const uint32_t* __restrict__ wq,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const uint32_t* __restrict__ wq2, const uint16_t* __restrict__ scales2,
-    const uint16_t* __restrict__ biases2, int N, uint16_t* __restrict__ y) {
+    const uint16_t* __restrict__ biases2, int N, int rows, uint16_t* __restrict__ y) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int NT = blockDim.x;
   const int tid = threadIdx.x;
@@ -436,9 +437,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int W = (NT >> 6) / NMAT;  // waves per matrix
   const int mat = NMAT == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave_all / W);
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * rows;
+  const int nr = N - n0 < rows ? N - n0 : rows;
   using Tile = GemvTile<BITS, GS, STEPS, MR, STEPS * RING>;
-  Tile t(lane, wave_all, wave_all - mat * W, n0, M, K, N, lds);
+  Tile t(lane, wave_all, wave_all - mat * W, n0, nr, M, K, N, lds);
   const int sb_total = (int)(((uint32_t)N * (uint32_t)t.G * 2u + 3u) & ~3u);  // whole dwords
   t.issue_x(make_rsrc(x, M * K * 2));
   t.issue_sb(make_rsrc(mat ? scales2 : scales, sb_total), make_rsrc(mat ? biases2 : biases, sb_total));
@@ -453,7 +455,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void qmv_mfma_kernel(
   t.stage();
   float yacc[Tile::E];
   t.fold(yacc);
-  gemv_reduce_store<NMAT>(lds, yacc, wave_all, W, lane, tid, NT, M, n0, N, y);
+  gemv_reduce_store<NMAT>(lds, yacc, wave_all, W, lane, tid, NT, M, n0, nr, N, y);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -811,6 +813,12 @@ struct QmvArgs {
 
 }  // namespace
 
+static int qmv_row_wpb(int64_t N, int nmat);
+
+// Rows per tile workgroup: 16 for SwiGLU; for one matrix, of 16, 12 and 8 the count whose
+// busiest CU streams the fewest rows, the rule of the one-row kernel (the MFMA columns past the
+// count load nothing).  The down projection of a decode MLP (N = 3072) takes 12 rows: 256
+// workgroups, every CU, where 16-row tiles left 64 CUs idle.
 template <int BITS, int GS, int STEPS, int MR, int NMAT, int RING>
 static int launch_qmv_mfma(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
   // The dynamic-LDS limit is raised once per device (any thread may get here first; setting it
@@ -824,10 +832,11 @@ static int launch_qmv_mfma(const QmvArgs& a, const QmvPlan& p, hipStream_t st) {
       return set_error(MLXQ_EDEVICE, "qmv: hipFuncSetAttribute failed");
     if (dev >= 0 && dev < 64) attr_set[dev].store(true, std::memory_order_release);
   }
-  hipLaunchKernelGGL((qmv_mfma_kernel<BITS, GS, STEPS, MR, NMAT, RING>), dim3((unsigned)((a.N + 15) / 16)),
+  const int rows = NMAT == 1 ? qmv_row_wpb(a.N, 1) : 16;
+  hipLaunchKernelGGL((qmv_mfma_kernel<BITS, GS, STEPS, MR, NMAT, RING>), dim3((unsigned)((a.N + rows - 1) / rows)),
                      dim3(p.waves * 64), p.lds, st, (const uint16_t*)a.x, (int)a.M, (int)a.K, a.wq,
                      (const uint16_t*)a.s, (const uint16_t*)a.b, a.wq2, (const uint16_t*)a.s2,
-                     (const uint16_t*)a.b2, (int)a.N, (uint16_t*)a.y);
+                     (const uint16_t*)a.b2, (int)a.N, rows, (uint16_t*)a.y);
   return check_launch(NMAT == 2 ? "swiglu_qmv" : "qmv_mfma");
 }
 
