@@ -46,20 +46,24 @@ __device__ __forceinline__ void round_bf16x2(float& a, float& b) {
 }
 
 // The fused bias / LoRA epilogue on two outputs, rounded to bf16 after each op as the
-// reference's separate ops round: o = rnd(rnd(rnd(acc) + bias) + rnd(rnd(r) * scale)).  With
-// scale == 1 the product's rounding is the identity and is skipped.
-__device__ __forceinline__ void epilogue_bias_lora2(float& o0, float& o1, bool has_bias, float b0,
-                                                    float b1, bool lora, float r0, float r1,
-                                                    float scale) {
+// reference's separate ops round: o = rnd(rnd(rnd(acc) + bias) + rnd(rnd(r) * scale)); with
+// scale == 1 the product's rounding is the identity and is skipped.  Each term (HB bias, HL LoRA,
+// HS LoRA scale != 1) is either fixed at compile time (kTermOff / kTermOn) or read from its
+// runtime flag (kTermRuntime): epilogues that choose the combination once per tile avoid the
+// three uniform branches per output pair that runtime flags cost.
+enum : int { kTermOff = 0, kTermOn = 1, kTermRuntime = 2 };
+template <int HB, int HL, int HS>
+__device__ __forceinline__ void epilogue_terms2(float& o0, float& o1, bool has_bias, float b0, float b1,
+                                                bool lora, float r0, float r1, float scale) {
   round_bf16x2(o0, o1);
-  if (has_bias) {
+  if (HB == kTermOn || (HB == kTermRuntime && has_bias)) {
     o0 += b0;
     o1 += b1;
     round_bf16x2(o0, o1);
   }
-  if (lora) {
+  if (HL == kTermOn || (HL == kTermRuntime && lora)) {
     round_bf16x2(r0, r1);
-    if (scale != 1.0f) {
+    if (HS == kTermOn || (HS == kTermRuntime && scale != 1.0f)) {
       r0 *= scale;
       r1 *= scale;
       round_bf16x2(r0, r1);

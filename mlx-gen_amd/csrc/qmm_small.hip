@@ -291,7 +291,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qmm_small_kernel(
         const int e = 4 * a + b;
         const float b0 = bv[e], b1 = bv[e + 1];
         float o0 = v[e], o1 = v[e + 1];
-        epilogue_bias_lora2(o0, o1, epi.bias != nullptr, b0, b1, lora, r[e], r[e + 1], epi.lora_scale);
+        epilogue_terms2<kTermRuntime, kTermRuntime, kTermRuntime>(o0, o1, epi.bias != nullptr, b0, b1, lora,
+                                                                 r[e], r[e + 1], epi.lora_scale);
         v[e] = o0;
         v[e + 1] = o1;
         if constexpr (ACT != kFusedActNone) {  // bf16 values: the table's entries for them
