@@ -607,12 +607,14 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     constexpr int j = decltype(J)::value;
     constexpr int kB = decltype(HB)::value, kL = decltype(HL)::value, kS = decltype(HS)::value;
     const int cb = wave * (BN / WAVES) + j * 32 + 4 * half;
+    // Without a bias the GELU pass adds -0, the identity for every value (-0 and NaN included),
+    // instead of branching on the bias.
     float bias_v[16] = {};
     if constexpr (kB != kTermOff) {
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) bias_v[4 * a + b] = epi.bias ? bias_lds[cb + 8 * a + b] : 0.0f;
+        for (int b = 0; b < 4; ++b) bias_v[4 * a + b] = epi.bias ? bias_lds[cb + 8 * a + b] : -0.0f;
     }
 #pragma unroll
     for (int i = 0; i < TMW; ++i) {
@@ -649,10 +651,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(
     first_pass(Off{}, Off{}, Off{});
   } else if constexpr (TABLE) {
     // With neither term the lookup pass rounds the products itself (FLUX up with GELU 337.9 ->
-    // 328.7 us against the pass with runtime conditions, outputs identical).  The terms stay
-    // runtime conditions here: a second copy of the pass (one per combination, or a bias-only
-    // one beside the general one) pushes the GELU kernels past 256 VGPRs into scratch.
-    if (epi.bias || lora) first_pass(Rt{}, Rt{}, Rt{});
+    // 328.7 us against the pass with runtime conditions, outputs identical).  Otherwise one pass
+    // adds the bias unconditionally (-0 without one: 350.8 -> 348.8 us with a bias) and keeps
+    // LoRA a runtime condition: a second copy of the pass (one per combination, or a bias-only one
+    // beside the general one) pushes the GELU kernels past 256 VGPRs into scratch.
+    if (epi.bias || lora) first_pass(On{}, Rt{}, Rt{});
   } else {
     // Bias and LoRA without an activation (the host sends no launch with neither term):
     // measured on M = 4608, K = 3072 with rank-16 LoRA and bias, 98.7 -> 97.2 us (N = 3072) and

@@ -343,6 +343,40 @@ def test_linear_wide_bias_lora_act(mlxq, act, scale, M, N):
     assert_close(y, ref, f"linear wide act={act} scale={scale}")
 
 
+# Every bias / LoRA / LoRA-scale / activation combination of the wide kernel's epilogue: without
+# an activation each combination has its own compile-time pass, with a GELU the terms are runtime
+# conditions and a launch with neither term skips the first pass (the lookup rounds the products).
+@pytest.mark.parametrize("bias,lora,scale,act", [
+    (True, False, 1.0, 0), (False, True, 1.0, 0), (False, True, 0.5, 0), (True, True, 1.0, 0),
+    (True, True, 0.5, 0), (False, False, 1.0, 3), (True, False, 1.0, 3), (False, True, 0.5, 3),
+    (True, True, 1.5, 2)])
+@pytest.mark.parametrize("M,N", [(2048, 4096), (1024, 3000)])
+def test_linear_wide_epilogue_combinations(mlxq, bias, lora, scale, act, M, N):
+    """256x256 tiles of 8 waves (M = 2048, N = 4096: 128 tiles) and 128x128 tiles of 4 waves
+    (M = 1024, N = 3000, ragged N), sampled rows in every tile band against the oracle."""
+    banner("linear wide epilogue combination", bias, lora, scale, act, M, N)
+    rng = np.random.default_rng(M + N + 7 * act + (3 if bias else 0) + (5 if lora else 0) + int(4 * scale))
+    K, r = 512, 16
+    x = bf16_normal(rng, (M, K))
+    w = bf16_normal(rng, (N, K), 0.02)
+    bv = bf16_normal(rng, (N,), 0.5) if bias else None
+    A = bf16_normal(rng, (K, r), 0.01) if lora else None
+    B = bf16_normal(rng, (r, N), 0.01) if lora else None
+    rwq, rs, rb = oracle.quantize(w, 64, 4, sb_bf16=True)
+    kw = {}
+    if bias:
+        kw["bias"] = to_gpu(bv)
+    if lora:
+        kw.update(lora_a=to_gpu(A), lora_b=to_gpu(B), lora_scale=scale)
+    y = to_np(mlxq.linear(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), 64, 4, activation=act, **kw))
+    rows = _band_rows(rng, M, heights=(128, 256))
+    okw = {"bias": bv} if bias else {}
+    if lora:
+        okw.update(lora_a=A, lora_b=B, lora_scale=scale)
+    ref = oracle.linear(x[rows], rwq, rs, rb, 64, 4, w_bf16=True, act_bf16=True, act=act, **okw)
+    assert_close(y[rows], ref, f"wide epilogue bias={bias} lora={lora} scale={scale} act={act}")
+
+
 def _band_rows(rng, M, heights=(224, 256)):
     """At least one row in every M-tile band of each tile height (a random row per band, plus the
     band edges of the first and last bands)."""
