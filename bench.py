@@ -477,17 +477,35 @@ def bench_config1(mlxq, torch):
     def mm():
         for q in qs:
             mlxq.quantized_matmul(x, *q, True, 64, 4, out=yo)
+    # The vendor's dense bf16 GEMM on the same shape (torch.mm, hipBLASLt), W^T made contiguous
+    # [K, N], rotated over the same number of distinct weights and timed the same way (a HIP
+    # graph, since a ~10 us launch from the host would be launch-bound): context for the
+    # small-grid kernel, not a measure of it (it reads 18.9 MB of bf16 weights where the Q4 GEMM
+    # reads 5.3 MB).  The graph's last output is checked against an eager call.
+    wts = [w.t().contiguous() for w in ws]
+    yd = torch.empty((256, 3072), dtype=torch.bfloat16, device=dev)
+
+    def dense():
+        for wt in wts:
+            torch.mm(x, wt, out=yd)
     qbytes = 3072 * 3072 * 2 + 3072 * 3072 // 2 + 3072 * 48 * 4
     n = len(ws)
     t_q = graph_ms(torch, quant, inner=1, reps=10) / n
     t_r = stream_reference(torch, ws, 4, 10) / n
     t_d = graph_ms(torch, deq, inner=1, reps=10) / n
     t_m = graph_ms(torch, mm, inner=1, reps=10) / n
+    t_dense = graph_ms(torch, dense, inner=1, reps=10) / n
+    torch.cuda.synchronize()
+    dense_ok = bool(torch.equal(yd, torch.mm(x, wts[-1])))
+    del wts
     flop = 2.0 * 256 * 3072 * 3072
     return {"quantize_us": round(t_q * 1e3, 2), "quantize_GBs": round(qbytes / (t_q * 1e-3) / 1e9, 1),
             "quantize_stream_reference_us": round(t_r * 1e3, 2),
             "dequantize_us": round(t_d * 1e3, 2), "dequantize_GBs": round(qbytes / (t_d * 1e-3) / 1e9, 1),
             "qmm_us": round(t_m * 1e3, 2), "qmm_TFLOPs": round(flop / (t_m * 1e-3) / 1e12, 1),
+            "dense_bf16_reference_us": round(t_dense * 1e3, 2),
+            "dense_bf16_reference_TFLOPs": round(flop / (t_dense * 1e-3) / 1e12, 1),
+            "dense_bf16_reference_graph_matches_eager": dense_ok,
             "note": f"per launch, rotated over {CONFIG1_COPIES} distinct weights (HIP graph, gaps "
                     "included); 24.2 MB per quantize/dequantize: latency-bound at this size"}
 
