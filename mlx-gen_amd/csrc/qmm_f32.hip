@@ -45,6 +45,33 @@ namespace {
 constexpr int kF32BM = 128;
 constexpr int kF32GroupM = 8;
 
+// The f32 epilogue of LinearBase::forward and the caller's activation (reference
+// src/adapters.rs:318-320, mlx-gen-flux/src/transformer.rs:975) on one output: y + bias in f32 (a
+// -0 bias when there is none, the identity for every value), then the activation ACT in f32 —
+// the elementwise epilogue kernel's arithmetic.
+template <bool EPI, int ACT>
+__device__ __forceinline__ float f32_finish(float o, float bv) {
+  if constexpr (EPI) {
+    o += bv;
+    if constexpr (ACT == MLXQ_ACT_GELU || ACT == MLXQ_ACT_GELU_EXACT) o = gelu_erf(o);
+    else if constexpr (ACT == MLXQ_ACT_GELU_TANH) o = gelu_tanh<false>(o);
+  }
+  return o;
+}
+
+// Runs the tile's store loop once, instantiated for the launch's activation, so the activation
+// is chosen once per tile rather than tested per output (a branch per output before).
+template <bool EPI, typename Store>
+__device__ __forceinline__ void f32_store_dispatch(int act, Store&& store) {
+  if constexpr (EPI) {
+    if (act == MLXQ_ACT_GELU || act == MLXQ_ACT_GELU_EXACT) store(std::integral_constant<int, MLXQ_ACT_GELU_EXACT>{});
+    else if (act == MLXQ_ACT_GELU_TANH) store(std::integral_constant<int, MLXQ_ACT_GELU_TANH>{});
+    else store(std::integral_constant<int, MLXQ_ACT_NONE>{});
+  } else {
+    store(std::integral_constant<int, MLXQ_ACT_NONE>{});
+  }
+}
+
 // Byte offset of 16-byte chunk `chunk` of tile row `row` for rows of BK bf16: 128-byte rows XOR
 // the chunk with row & 7, 64-byte rows with (row >> 1) & 3, so the fragment reads (one chunk of 8
 // or more consecutive rows) fall on distinct banks.
@@ -364,9 +391,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
   // 4 half + (v & 3) of B's fragment: the weight operand is MFMA's A side, so each lane holds four
   // runs of 4 consecutive n for one m and stores them as 16-byte rows.
   const bool vec_ok = (N % 4) == 0;
-  // The f32 epilogue of LinearBase::forward + the caller's activation (reference
-  // src/adapters.rs:318-320, mlx-gen-flux/src/transformer.rs:975): y + bias in f32, then the
-  // activation evaluated in f32 — the same arithmetic as the elementwise epilogue kernel.
+  // The f32 epilogue (f32_finish): y + bias in f32, then the activation in f32.
   [[maybe_unused]] float bcol[TN][16];
   if constexpr (EPI) {
 #pragma unroll
@@ -375,42 +400,37 @@ __global__ __launch_bounds__(WAVES * 64) void qmm_f32_kernel(const XT* __restric
       for (int v = 0; v < 16; ++v) {
         const int64_t n = bn0 + wn * WN + j * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
         const int64_t nc = n < N ? n : N - 1;  // columns past N are never stored
-        bcol[j][v] = epi.bias == nullptr ? 0.0f
+        bcol[j][v] = epi.bias == nullptr ? -0.0f
                      : epi.bias_bf16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(epi.bias)[nc])
                                      : static_cast<const float*>(epi.bias)[nc];
       }
   }
-  auto finish = [&](float o, float bv) {
-    if constexpr (EPI) {
-      if (epi.bias) o += bv;
-      if (epi.act == MLXQ_ACT_GELU || epi.act == MLXQ_ACT_GELU_EXACT) o = gelu_erf(o);
-      else if (epi.act == MLXQ_ACT_GELU_TANH) o = gelu_tanh<false>(o);
-    }
-    return o;
-  };
+  auto store = [&](auto A) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int64_t m = bm0 + wm * WM + i * 32 + r32;
-    if (m >= M) continue;
-    float* yrow = y + m * N;
+    for (int i = 0; i < TM; ++i) {
+      const int64_t m = bm0 + wm * WM + i * 32 + r32;
+      if (m >= M) continue;
+      float* yrow = y + m * N;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
+      for (int j = 0; j < TN; ++j) {
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int64_t n = bn0 + wn * WN + j * 32 + 8 * a + 4 * half;
-        f32x4 v;
+        for (int a = 0; a < 4; ++a) {
+          const int64_t n = bn0 + wn * WN + j * 32 + 8 * a + 4 * half;
+          f32x4 v;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) v[b] = finish(acc[i][j][4 * a + b], EPI ? bcol[j][4 * a + b] : 0.0f);
-        if (vec_ok && n + 3 < N) {
-          *reinterpret_cast<f32x4*>(yrow + n) = v;
-        } else {
+          for (int b = 0; b < 4; ++b) v[b] = f32_finish<EPI, decltype(A)::value>(acc[i][j][4 * a + b], EPI ? bcol[j][4 * a + b] : 0.0f);
+          if (vec_ok && n + 3 < N) {
+            *reinterpret_cast<f32x4*>(yrow + n) = v;
+          } else {
 #pragma unroll
-          for (int b = 0; b < 4; ++b)
-            if (n + b < N) yrow[n + b] = v[b];
+            for (int b = 0; b < 4; ++b)
+              if (n + b < N) yrow[n + b] = v[b];
+          }
         }
       }
     }
-  }
+  };
+  f32_store_dispatch<EPI>(epi.act, store);
 }
 
 // The factored form for group sizes 64 and 128: since
@@ -719,42 +739,37 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void qmm_f32c_kernel(const X
       for (int v = 0; v < 16; ++v) {
         const int64_t n = bn0 + wn * WN + j * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
         const int64_t nc = n < N ? n : N - 1;  // columns past N are never stored
-        bcol[j][v] = epi.bias == nullptr ? 0.0f
+        bcol[j][v] = epi.bias == nullptr ? -0.0f
                      : epi.bias_bf16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(epi.bias)[nc])
                                      : static_cast<const float*>(epi.bias)[nc];
       }
   }
-  auto finish = [&](float o, float bv) {
-    if constexpr (EPI) {
-      if (epi.bias) o += bv;
-      if (epi.act == MLXQ_ACT_GELU || epi.act == MLXQ_ACT_GELU_EXACT) o = gelu_erf(o);
-      else if (epi.act == MLXQ_ACT_GELU_TANH) o = gelu_tanh<false>(o);
-    }
-    return o;
-  };
+  auto store = [&](auto A) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int64_t m = bm0 + wm * WM + i * 32 + r32;
-    if (m >= M) continue;
-    float* yrow = y + m * N;
+    for (int i = 0; i < TM; ++i) {
+      const int64_t m = bm0 + wm * WM + i * 32 + r32;
+      if (m >= M) continue;
+      float* yrow = y + m * N;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
+      for (int j = 0; j < TN; ++j) {
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int64_t n = bn0 + wn * WN + j * 32 + 8 * a + 4 * half;
-        f32x4 v;
+        for (int a = 0; a < 4; ++a) {
+          const int64_t n = bn0 + wn * WN + j * 32 + 8 * a + 4 * half;
+          f32x4 v;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) v[b] = finish(yv[i][j][4 * a + b], EPI ? bcol[j][4 * a + b] : 0.0f);
-        if (vec_ok && n + 3 < N) {
-          *reinterpret_cast<f32x4*>(yrow + n) = v;
-        } else {
+          for (int b = 0; b < 4; ++b) v[b] = f32_finish<EPI, decltype(A)::value>(yv[i][j][4 * a + b], EPI ? bcol[j][4 * a + b] : 0.0f);
+          if (vec_ok && n + 3 < N) {
+            *reinterpret_cast<f32x4*>(yrow + n) = v;
+          } else {
 #pragma unroll
-          for (int b = 0; b < 4; ++b)
-            if (n + b < N) yrow[n + b] = v[b];
+            for (int b = 0; b < 4; ++b)
+              if (n + b < N) yrow[n + b] = v[b];
+          }
         }
       }
     }
-  }
+  };
+  f32_store_dispatch<EPI>(epi.act, store);
 }
 
 template <typename XT, typename SB, int BITS, int GS>
