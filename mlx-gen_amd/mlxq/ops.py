@@ -115,8 +115,21 @@ def _check_out(op: str, out, dtype, numel: int, device):
         _bad(op, f"out must be a contiguous {dtype} tensor of {numel} elements on {device}")
 
 
+def _scales_biases(N: int, gcols: int, dtype, device):
+    """Empty scales and biases [N, gcols] as two views of one allocation, the biases starting 256
+    bytes past the scales' end rounded up: the large-M GEMM stages bf16 scales and biases through
+    one buffer resource, which needs both arrays within 4 GiB of each other (two separate
+    allocations of a large process can lie further apart, which costs that GEMM its fast path)."""
+    n = N * gcols
+    esz = torch.empty((), dtype=dtype).element_size()
+    off = (n * esz + 511) // 256 * 256 // esz
+    buf = torch.empty((off + n,), dtype=dtype, device=device)
+    return buf[:n].view(N, gcols), buf[off:off + n].view(N, gcols)
+
+
 def quantize(w: torch.Tensor, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4):
-    """Affine group quantization of w [N, K] -> (wq u32-as-int32 [N, K*bits/32], scales, biases)."""
+    """Affine group quantization of w [N, K] -> (wq u32-as-int32 [N, K*bits/32], scales, biases).
+    scales and biases are views of one allocation (_scales_biases)."""
     _need_gpu(w)
     if w.dim() != 2:
         raise ValueError(f"quantize expects a 2-D weight, got shape {tuple(w.shape)}")
@@ -125,8 +138,7 @@ def quantize(w: torch.Tensor, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 
     # Packed words are stored in an int32 tensor (same bits as MLX's uint32 array).
     wq = torch.empty((N, max(K * bits // 32, 0)), dtype=torch.int32, device=w.device)
     gcols = K // group_size if group_size > 0 else 0
-    s = torch.empty((N, gcols), dtype=w.dtype, device=w.device)
-    b = torch.empty((N, gcols), dtype=w.dtype, device=w.device)
+    s, b = _scales_biases(N, gcols, w.dtype, w.device)
     check(_lib.load().mlxq_quantize(_ptr(w), _dt(w), N, K, group_size, bits, _ptr(wq), _ptr(s),
                                     _ptr(b), _stream(w.device)))
     return wq, s, b
@@ -148,8 +160,7 @@ def quantize_batched(ws, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4):
     N, K = w0.shape
     gcols = K // group_size if group_size > 0 else 0
     outs = [(torch.empty((N, max(K * bits // 32, 0)), dtype=torch.int32, device=w0.device),
-             torch.empty((N, gcols), dtype=w0.dtype, device=w0.device),
-             torch.empty((N, gcols), dtype=w0.dtype, device=w0.device)) for _ in ws]
+             *_scales_biases(N, gcols, w0.dtype, w0.device)) for _ in ws]
     arr = ctypes.c_void_p * len(ws)
     check(_lib.load().mlxq_quantize_batched(
         arr(*[_ptr(w) for w in ws]), len(ws), _dt(w0), N, K, group_size, bits,
