@@ -145,6 +145,25 @@ Array Array::empty(std::vector<int64_t> shape, Dtype dt) {
   return a;
 }
 
+std::pair<Array, Array> Array::empty_pair(std::vector<int64_t> shape, Dtype dt) {
+  Array a, b;
+  a.shape_ = b.shape_ = std::move(shape);
+  a.dtype_ = b.dtype_ = dt;
+  for (int64_t d : a.shape_)
+    if (d < 0) throw Error(MLXQ_EINVAL, "Array: negative dimension");
+  const size_t n = a.nbytes();
+  if (n > 0) {
+    const size_t off = (n + 511) / 256 * 256;
+    void* p = nullptr;
+    hip_check(hipMalloc(&p, off + n), "hipMalloc");
+    a.buf_ = std::shared_ptr<void>(p, [](void* q) { (void)hipFree(q); });
+    b.buf_ = a.buf_;
+    a.ptr_ = p;
+    b.ptr_ = static_cast<unsigned char*>(p) + off;
+  }
+  return {a, b};
+}
+
 Array Array::from_host(const void* data, std::vector<int64_t> shape, Dtype dt) {
   Array a = empty(std::move(shape), dt);
   if (a.nbytes() > 0) hip_check(hipMemcpy(a.ptr_, data, a.nbytes(), hipMemcpyHostToDevice), "hipMemcpy");
@@ -195,8 +214,8 @@ Packed quantize(const Array& w, int group_size, int bits, hipStream_t s) {
   const int dt = abi_dtype(w.dtype(), "quantize");
   const int64_t N = w.dim(0), K = w.dim(1);
   const int64_t gcols = group_size > 0 ? K / group_size : 0;
-  Packed p{Array::empty({N, bits > 0 ? K * bits / 32 : 0}, Dtype::Uint32),
-           Array::empty({N, gcols}, w.dtype()), Array::empty({N, gcols}, w.dtype())};
+  auto sb = Array::empty_pair({N, gcols}, w.dtype());
+  Packed p{Array::empty({N, bits > 0 ? K * bits / 32 : 0}, Dtype::Uint32), sb.first, sb.second};
   check(mlxq_quantize(w.data(), dt, N, K, group_size, bits, (uint32_t*)p.wq.data(), p.scales.data(),
                       p.biases.data(), s));
   return p;
@@ -217,8 +236,8 @@ std::vector<Packed> quantize_batched(const std::vector<Array>& ws, int group_siz
   std::vector<uint32_t*> qp;
   std::vector<void*> sp, bp;
   for (const Array& w : ws) {
-    out.push_back(Packed{Array::empty({N, bits > 0 ? K * bits / 32 : 0}, Dtype::Uint32),
-                         Array::empty({N, gcols}, w0.dtype()), Array::empty({N, gcols}, w0.dtype())});
+    auto sb = Array::empty_pair({N, gcols}, w0.dtype());
+    out.push_back(Packed{Array::empty({N, bits > 0 ? K * bits / 32 : 0}, Dtype::Uint32), sb.first, sb.second});
     wp.push_back(w.data());
     qp.push_back((uint32_t*)out.back().wq.data());
     sp.push_back(out.back().scales.data());

@@ -25,6 +25,7 @@
 #include <optional>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace mlxq {
@@ -52,6 +53,10 @@ class Array {
   static Array from_host(const void* data, std::vector<int64_t> shape, Dtype dt);
   // Wraps memory owned elsewhere (e.g. a framework tensor); the caller keeps it alive.
   static Array borrow(void* device_ptr, std::vector<int64_t> shape, Dtype dt);
+  // Two arrays of one shape in one allocation, the second starting 256 bytes past the first's
+  // end rounded up: quantize's scales and biases, which the large-M GEMM stages through one
+  // buffer resource reaching both (separate allocations may lie more than 4 GiB apart).
+  static std::pair<Array, Array> empty_pair(std::vector<int64_t> shape, Dtype dt);
 
   void to_host(void* dst) const;  // synchronous device-to-host copy of nbytes()
   Array reshape(std::vector<int64_t> shape) const;  // same buffer, new shape (same size)
