@@ -1,0 +1,96 @@
+"""Seeded random shapes through every dispatch path of the quantized linear, against the oracle.
+
+The other GPU tests pin each kernel at chosen shapes and edges; this one draws (M, N, K, group
+size, bits, bias, LoRA, activation) at random from fixed seeds, so shapes nobody picked by hand
+reach the GEMV (M <= 8), the small-grid, generic and wide GEMMs (bf16 x) and the f32 GEMM (f32 x),
+each checked with the quantized_matmul tolerance (relFro <= 2e-3, per-element |delta| <= 1e-2 of
+max|y|) against the oracle on a sample of rows, and the f32 products at the exact-f32 bar.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import assert_close, banner, bf16_normal, errors, to_gpu, to_np, wq_to_gpu
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+# M buckets: GEMV, small grids, mid-size prefill, wide grids.
+M_BUCKETS = [(1, 8), (9, 96), (97, 700), (701, 2400)]
+
+
+@pytest.fixture(scope="module")
+def mlxq():
+    import mlxq as m
+    m.load()
+    return m
+
+
+def _draw(seed):
+    rng = np.random.default_rng(1000 + seed)
+    lo, hi = M_BUCKETS[seed % len(M_BUCKETS)]
+    M = int(rng.integers(lo, hi + 1))
+    gs = int(rng.choice([32, 64, 128]))
+    bits = int(rng.choice([4, 8]))
+    K = gs * int(rng.integers(2, max(3, 4096 // gs) + 1))
+    N = int(rng.integers(1, 3000)) if rng.random() < 0.5 else 8 * int(rng.integers(1, 400))
+    bias = bool(rng.random() < 0.5)
+    lora = bool(rng.random() < 0.4)
+    scale = float(rng.choice([1.0, 0.5, 1.25]))
+    act = int(rng.choice([0, 0, 2, 3]))
+    return rng, M, N, K, gs, bits, bias, lora, scale, act
+
+
+def _rows(rng, M):
+    if M <= 64:
+        return np.arange(M)
+    return np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, 46)]))
+
+
+@pytest.mark.parametrize("seed", range(96))
+def test_random_bf16_linear_vs_oracle(mlxq, seed):
+    rng, M, N, K, gs, bits, bias, lora, scale, act = _draw(seed)
+    banner("random bf16 linear", seed, M, N, K, gs, bits, bias, lora, scale, act)
+    x = bf16_normal(rng, (M, K))
+    w = bf16_normal(rng, (N, K), 0.02)
+    rwq, rs, rb = oracle.quantize(w, gs, bits, sb_bf16=True)
+    kw, okw = {}, {}
+    if bias:
+        bv = bf16_normal(rng, (N,), 0.5)
+        kw["bias"] = to_gpu(bv)
+        okw["bias"] = bv
+    if lora:
+        A = bf16_normal(rng, (K, 16), 0.01)
+        B = bf16_normal(rng, (16, N), 0.01)
+        kw.update(lora_a=to_gpu(A), lora_b=to_gpu(B), lora_scale=scale)
+        okw.update(lora_a=A, lora_b=B, lora_scale=scale)
+    y = to_np(mlxq.linear(to_gpu(x), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb), gs, bits, activation=act, **kw))
+    rows = _rows(rng, M)
+    ref = oracle.linear(x[rows], rwq, rs, rb, gs, bits, w_bf16=M > 8, act_bf16=True, act=act, **okw)
+    assert_close(y[rows], ref, f"seed {seed}")
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_f32_quantized_matmul_vs_exact(mlxq, seed):
+    rng = np.random.default_rng(5000 + seed)
+    M = int(rng.integers(9, 900))
+    gs = int(rng.choice([32, 64, 128]))
+    bits = int(rng.choice([4, 8]))
+    K = gs * int(rng.integers(2, max(3, 3072 // gs) + 1))
+    N = int(rng.integers(1, 2000))
+    sdt = "bf16" if rng.random() < 0.7 else "f32"
+    banner("random f32 qmm", seed, M, N, K, gs, bits, sdt)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    if sdt == "bf16":
+        w = oracle.bf16_round(w)
+    rwq, rs, rb = oracle.quantize(w, gs, bits, sb_bf16=sdt == "bf16")
+    tdt = torch.bfloat16 if sdt == "bf16" else torch.float32
+    y = mlxq.quantized_matmul(to_gpu(x, torch.float32), wq_to_gpu(rwq), to_gpu(rs, tdt), to_gpu(rb, tdt),
+                              True, gs, bits)
+    assert y.dtype == torch.float32
+    rows = _rows(rng, M)
+    ref = oracle.quantized_matmul(x[rows], rwq, rs, rb, gs, bits, w_bf16=False, out_bf16=False)
+    rel, peak = errors(to_np(y)[rows], ref)
+    print(f"    seed {seed} relFro={rel:.3e} peak={peak:.3e}", flush=True)
+    assert rel < 1e-4 and peak < 1e-3
