@@ -94,3 +94,48 @@ def test_random_f32_quantized_matmul_vs_exact(mlxq, seed):
     rel, peak = errors(to_np(y)[rows], ref)
     print(f"    seed {seed} relFro={rel:.3e} peak={peak:.3e}", flush=True)
     assert rel < 1e-4 and peak < 1e-3
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_quantize_dequantize_bit_exact(mlxq, seed):
+    """quantize and dequantize at random shapes, bf16 or f32 weights: codes, scales, biases and the
+    dequantized matrix bit for bit against the oracle."""
+    rng = np.random.default_rng(7000 + seed)
+    gs = int(rng.choice([32, 64, 128]))
+    bits = int(rng.choice([4, 8]))
+    K = gs * int(rng.integers(1, max(2, 4096 // gs) + 1))
+    N = int(rng.integers(1, 2000))
+    bf = bool(rng.random() < 0.6)
+    banner("random quantize", seed, N, K, gs, bits, "bf16" if bf else "f32")
+    w = (rng.standard_normal((N, K)) * float(rng.choice([0.02, 1.0, 30.0]))).astype(np.float32)
+    if bf:
+        w = oracle.bf16_round(w)
+    dt = torch.bfloat16 if bf else torch.float32
+    wq, s, b = mlxq.quantize(to_gpu(w, dt), gs, bits)
+    rwq, rs, rb = oracle.quantize(w, gs, bits, sb_bf16=bf)
+    assert np.array_equal(to_np(wq), rwq)
+    assert np.array_equal(to_np(s), rs) and np.array_equal(to_np(b), rb)
+    d = mlxq.dequantize(wq, s, b, gs, bits)
+    assert np.array_equal(to_np(d), oracle.dequantize(rwq, rs, rb, gs, bits, out_bf16=bf))
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_swiglu_vs_oracle(mlxq, seed):
+    """The fused decode SwiGLU (M <= 8) at random shapes against the oracle's op-by-op h."""
+    rng = np.random.default_rng(9000 + seed)
+    M = int(rng.integers(1, 9))
+    gs = int(rng.choice([32, 64, 128]))
+    bits = int(rng.choice([4, 8]))
+    step = max(gs, 512 // bits)
+    K = step * int(rng.integers(1, 4096 // step + 1))
+    F = int(rng.integers(1, 3000))
+    banner("random swiglu", seed, M, K, F, gs, bits)
+    x = bf16_normal(rng, (M, K))
+    tg, tu = [oracle.quantize(bf16_normal(rng, (F, K), 0.02), gs, bits, sb_bf16=True) for _ in range(2)]
+    g, u = [(wq_to_gpu(t[0]), to_gpu(t[1]), to_gpu(t[2])) for t in (tg, tu)]
+    h = to_np(mlxq.swiglu(to_gpu(x), g, u, gs, bits))
+    gr = oracle.quantized_matmul(x, *tg, gs, bits, w_bf16=False, out_bf16=True)
+    ur = oracle.quantized_matmul(x, *tu, gs, bits, w_bf16=False, out_bf16=True)
+    ref_h = oracle.bf16_round(oracle.bf16_round(np.vectorize(oracle.silu)(gr).astype(np.float32)) * ur)
+    assert_close(h, ref_h, f"seed {seed}")
+    print(f"    bit-identical h: {np.mean(h == ref_h) * 100:.2f} %", flush=True)
