@@ -231,7 +231,11 @@ int mlxq_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, const 
  * f32 bias over a bf16 product would need a promoted second pass and returns MLXQ_EUNSUPPORTED.
  * x is [M, K] shared by every expert when x_per_expert == 0 (the gate_up projection of
  * gpt_oss.rs:702), else [E, M, K] (the down projection of :714).  Each expert's result equals the
- * single-matrix mlxq_linear with that bias; bf16 x with M > 8 runs every expert in one GEMM launch.
+ * single-matrix mlxq_linear with that bias.  bf16 x and scales with M > 8, K a multiple of 64 and at
+ * least 128 GEMM tiles over all experts run every expert in one launch; otherwise the experts run
+ * one after another through mlxq_linear, which needs each expert's slices aligned: M*N elements of
+ * y a multiple of 16 bytes and N*K/group_size scales (biases) a multiple of 4 bytes, else
+ * MLXQ_EUNSUPPORTED (the Python and C++ hosts then run those experts on aligned copies).
  */
 int mlxq_qmm_experts(const void* x, int x_dtype, int x_per_expert, int64_t E, int64_t M, int64_t K,
                      const uint32_t* wq, const void* scales, const void* biases, int sb_dtype,

@@ -532,7 +532,14 @@ int mlxq_qmm_experts(const void* x, int x_dtype, int x_per_expert, int64_t E, in
     return run_qmm_wide(x, M, K, wq, scales, biases, sb_dtype, N, group_size, bits, y, qe, st, bat);
   }
   // Otherwise expert by expert through the single-matrix paths (same rounding points; no
-  // workspace: without LoRA nothing is staged and the result never promotes past D0).
+  // workspace: without LoRA nothing is staged and the result never promotes past D0).  Each
+  // expert's slices must meet mlxq_linear's alignment: y 16 bytes, scales and biases 4 bytes.
+  if (E > 1 && ((M * N * yb) % 16 != 0 || (bat.sb * sbb) % 4 != 0))
+    return set_error(MLXQ_EUNSUPPORTED,
+                     "qmm_experts: expert by expert, each expert's y slice (M*N = %lld elements of %d "
+                     "bytes) must be a multiple of 16 bytes and its scales/biases slice (N*K/group_size "
+                     "= %lld of %d bytes) a multiple of 4 bytes; run such packs one expert at a time "
+                     "on aligned copies", (long long)(M * N), yb, (long long)bat.sb, sbb);
   for (int64_t e = 0; e < E; ++e) {
     mlxq_epilogue ep = {};
     ep.bias = bias ? (const char*)bias + e * bat.bias * bb : nullptr;

@@ -306,9 +306,20 @@ Array swiglu(const Array& x, const QuantizedLinear& gate, const QuantizedLinear&
 }
 
 std::vector<QuantizedLinear> StackedExperts::split() const {
+  // Views of the stack, as the reference's split; an expert's scales/biases slice that does not
+  // start on a 4-byte boundary (N * K/group_size odd in bf16) is copied instead, since the library
+  // reads scales and biases as whole words.
+  const int64_t E = num_experts();
+  const bool copy_sb = E > 0 && (scales.nbytes() / (size_t)E) % 4 != 0;
+  auto copy_of = [](const Array& a) {
+    Array c = Array::empty(a.shape(), a.dtype());
+    if (c.nbytes() > 0) hip_check(hipMemcpy(c.data(), a.data(), c.nbytes(), hipMemcpyDeviceToDevice), "hipMemcpy");
+    return c;
+  };
   std::vector<QuantizedLinear> out;
-  for (int64_t e = 0; e < num_experts(); ++e)
-    out.push_back(QuantizedLinear{weight.index0(e), scales.index0(e), biases.index0(e),
+  for (int64_t e = 0; e < E; ++e)
+    out.push_back(QuantizedLinear{weight.index0(e), copy_sb ? copy_of(scales.index0(e)) : scales.index0(e),
+                                  copy_sb ? copy_of(biases.index0(e)) : biases.index0(e),
                                   bias ? std::optional<Array>(bias->index0(e)) : std::nullopt,
                                   group_size, bits});
   return out;
@@ -334,11 +345,39 @@ Array StackedExperts::forward(const Array& x, bool per_expert, hipStream_t s) co
   Dtype ydt = promote(x.dtype(), scales.dtype());
   if (bias) ydt = promote(ydt, bias->dtype());
   Array y = Array::empty(shape, ydt);
-  check(mlxq_qmm_experts(x.data(), abi_dtype(x.dtype(), "experts"), per_expert ? 1 : 0, E, M, K,
-                         (const uint32_t*)weight.data(), scales.data(), biases.data(),
-                         abi_dtype(scales.dtype(), "experts"), bias ? bias->data() : nullptr,
-                         bias ? abi_dtype(bias->dtype(), "experts") : MLXQ_BFLOAT16, N, group_size,
-                         bits, y.data(), s));
+  const int xdt = abi_dtype(x.dtype(), "experts"), sdt = abi_dtype(scales.dtype(), "experts");
+  const int bdt = bias ? abi_dtype(bias->dtype(), "experts") : MLXQ_BFLOAT16;
+  const int rc = mlxq_qmm_experts(x.data(), xdt, per_expert ? 1 : 0, E, M, K, (const uint32_t*)weight.data(),
+                                  scales.data(), biases.data(), sdt, bias ? bias->data() : nullptr, bdt, N,
+                                  group_size, bits, y.data(), s);
+  const size_t ysz = dtype_size(ydt), ssz = dtype_size(scales.dtype());
+  const int64_t G = K / group_size;
+  const bool misaligned = E > 1 && ((M * N * (int64_t)ysz) % 16 != 0 || (N * G * (int64_t)ssz) % 4 != 0);
+  if (rc != MLXQ_EUNSUPPORTED || !misaligned) {
+    check(rc);
+    return y;
+  }
+  // The library runs these experts one at a time and an expert's slice of y or of the
+  // scales/biases is unaligned for it: run them here on aligned copies.
+  const size_t xsz = dtype_size(x.dtype());
+  Array se = Array::empty({N, G}, scales.dtype()), be = Array::empty({N, G}, scales.dtype());
+  Array ye = Array::empty({M, N}, ydt);
+  for (int64_t e = 0; e < E; ++e) {
+    hip_check(hipMemcpyAsync(se.data(), static_cast<const char*>(scales.data()) + e * N * G * ssz, se.nbytes(),
+                             hipMemcpyDeviceToDevice, s), "hipMemcpyAsync");
+    hip_check(hipMemcpyAsync(be.data(), static_cast<const char*>(biases.data()) + e * N * G * ssz, be.nbytes(),
+                             hipMemcpyDeviceToDevice, s), "hipMemcpyAsync");
+    mlxq_epilogue ep = {};
+    ep.lora_scale = 1.0f;
+    ep.bias_dtype = bias ? bdt : xdt;
+    ep.lora_dtype = xdt;
+    if (bias) ep.bias = static_cast<const char*>(bias->data()) + e * N * dtype_size(bias->dtype());
+    check(mlxq_linear(static_cast<const char*>(x.data()) + (per_expert ? e * M * K * xsz : 0), xdt, M, K,
+                      static_cast<const uint32_t*>(weight.data()) + e * N * (K * bits / 32), se.data(), be.data(),
+                      sdt, N, group_size, bits, &ep, ye.data(), nullptr, 0, s));
+    hip_check(hipMemcpyAsync(static_cast<char*>(y.data()) + e * M * N * ysz, ye.data(), ye.nbytes(),
+                             hipMemcpyDeviceToDevice, s), "hipMemcpyAsync");
+  }
   return y;
 }
 

@@ -212,7 +212,8 @@ struct StackedExperts {
   int bits = 4;
 
   int64_t num_experts() const { return weight.dim(0); }
-  // Per-expert layers sharing the stack's buffers (the axis-0 split of quant.rs:111-137).
+  // Per-expert layers sharing the stack's buffers (the axis-0 split of quant.rs:111-137); an
+  // expert's scales/biases slice that starts mid-word is copied instead.
   std::vector<QuantizedLinear> split() const;
   // Proj::forward of every expert (gpt_oss.rs:412-425) in one call: x [..., in] shared by all
   // experts, or [E, ..., in] with per_expert; returns [E, ..., out].

@@ -251,7 +251,9 @@ class StackedExperts:
         return self.weight.shape[0]
 
     def split(self) -> List[QuantizedLinear]:
-        """Per-expert packs, the axis-0 split of mlx-gen-lens/src/quant.rs:111-137 (views, no copy)."""
+        """Per-expert packs, the axis-0 split of mlx-gen-lens/src/quant.rs:111-137 (views, no copy;
+        the ops copy a view whose start the library cannot take, such as a scales slice that
+        starts mid-word)."""
         return [QuantizedLinear(self.weight[e], self.scales[e], self.biases[e], self.bias[e],
                                 self.group_size, self.bits) for e in range(self.num_experts)]
 

@@ -70,6 +70,19 @@ def _contig(t):
     return None if t is None else t.contiguous()
 
 
+def _aligned(t, align: int):
+    """t when its data pointer is `align`-byte aligned, else an aligned copy: views such as one
+    expert's slice of a stacked pack can start mid-word, and the library requires 16-byte aligned
+    activations and packed codes and 4-byte aligned scales and biases."""
+    return t if t is None or t.data_ptr() % align == 0 else t.clone()
+
+
+def _pack3(wq, scales, biases):
+    """A (wq, scales, biases) pack made contiguous and aligned for the library."""
+    return (_aligned(wq.contiguous(), 16), _aligned(scales.contiguous(), 4),
+            _aligned(biases.contiguous(), 4))
+
+
 def _bad(op: str, msg: str):
     raise MlxqError(MLXQ_EINVAL, f"{op}: {msg}")
 
@@ -176,7 +189,7 @@ def _k_of(wq: torch.Tensor, bits: int) -> int:
 def dequantize(wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4):
     if bits not in (4, 8):
         _bad("dequantize", f"bits must be 4 or 8 (got {bits})")
-    wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
+    wq, scales, biases = _pack3(wq, scales, biases)
     K = _k_of(wq, bits)
     N = _check_pack("dequantize", wq, scales, biases, K, group_size, bits)
     _need_gpu(wq, scales, biases)
@@ -192,8 +205,8 @@ def _mm(entry, x, wq, scales, biases, group_size, bits, *extra, out=None):
     _float_dtype(entry, "x", x)
     K = x.shape[-1]
     lead = x.shape[:-1]
-    x2 = x.reshape(-1, K).contiguous()
-    wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
+    x2 = _aligned(x.reshape(-1, K).contiguous(), 16)
+    wq, scales, biases = _pack3(wq, scales, biases)
     N = _check_pack(entry, wq, scales, biases, K, group_size, bits)
     M = x2.shape[0]
     # The forced bf16-tile GEMM returns bf16; the others MLX's promote(x, scales).
@@ -244,7 +257,7 @@ def embedding(ids, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bit
         raise TypeError(f"embedding: out_dtype must be bfloat16 or float32, got {out_dtype}")
     if bits not in (4, 8):
         _bad("embedding", f"bits must be 4 or 8 (got {bits})")
-    wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
+    wq, scales, biases = _pack3(wq, scales, biases)
     hidden = _k_of(wq, bits)
     vocab = _check_pack("embedding", wq, scales, biases, hidden, group_size, bits)
     _need_gpu(ids, wq, scales, biases)
@@ -264,9 +277,9 @@ def swiglu(x, gate, up, group_size: int = DEFAULT_GROUP_SIZE, bits: int = 4, out
     _float_dtype("swiglu", "x", x)
     K = x.shape[-1]
     lead = x.shape[:-1]
-    x2 = x.reshape(-1, K).contiguous()
-    g = [t.contiguous() for t in gate]
-    u = [t.contiguous() for t in up]
+    x2 = _aligned(x.reshape(-1, K).contiguous(), 16)
+    g = list(_pack3(*gate))
+    u = list(_pack3(*up))
     F = _check_pack("swiglu", *g, K, group_size, bits)
     if _check_pack("swiglu", *u, K, group_size, bits) != F or u[1].dtype != g[1].dtype:
         _bad("swiglu", "gate and up must be packed alike")
@@ -296,7 +309,7 @@ def qmm_experts(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bit
         _bad("qmm_experts", "wq must be a stacked [E, N, K*bits/32] pack")
     E = wq.shape[0]
     K = x.shape[-1]
-    wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
+    wq, scales, biases = _pack3(wq, scales, biases)
     N = _check_pack("qmm_experts", wq, scales, biases, K, group_size, bits, lead=(E,))
     if per_expert:
         if x.dim() < 2 or x.shape[0] != E:
@@ -318,10 +331,23 @@ def qmm_experts(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bit
         _check_out("qmm_experts", out, ydt, E * M * N, x.device)
     _need_gpu(x, wq, scales, biases, bias)
     y = out if out is not None else torch.empty((E, M, N), dtype=ydt, device=x.device)
-    check(_lib.load().mlxq_qmm_experts(_ptr(x2), _dt(x2), int(per_expert), E, M, K, _ptr(wq),
-                                       _ptr(scales), _ptr(biases), _dt(scales), _ptr(b),
-                                       MLXQ_BFLOAT16 if b is None else _dt(b), N, group_size, bits,
-                                       _ptr(y), _stream(x.device)))
+    rc = _lib.load().mlxq_qmm_experts(_ptr(x2), _dt(x2), int(per_expert), E, M, K, _ptr(wq),
+                                      _ptr(scales), _ptr(biases), _dt(scales), _ptr(b),
+                                      MLXQ_BFLOAT16 if b is None else _dt(b), N, group_size, bits,
+                                      _ptr(y), _stream(x.device))
+    misaligned = E > 1 and ((M * N * y.element_size()) % 16 or (N * (K // group_size) * scales.element_size()) % 4)
+    if rc == _lib.MLXQ_EUNSUPPORTED and misaligned:
+        # The library runs these experts one at a time and each expert's slice of y or of the
+        # scales/biases is unaligned for it: run them here (linear aligns its operands, and each
+        # expert's result goes through an aligned output).
+        y3 = y.view(E, M, N)
+        xs = x2.reshape(E, M, K) if per_expert else x2.reshape(M, K)
+        for e in range(E):
+            ye = linear(xs[e] if per_expert else xs, wq[e], scales[e], biases[e], group_size, bits,
+                        bias=None if b is None else b[e])
+            y3[e].copy_(ye)
+    else:
+        check(rc)
     return y.reshape(E, *lead, N)
 
 
@@ -363,8 +389,8 @@ def linear(x, wq, scales, biases, group_size: int = DEFAULT_GROUP_SIZE, bits: in
     _float_dtype("linear", "x", x)
     K = x.shape[-1]
     lead = x.shape[:-1]
-    x2 = x.reshape(-1, K).contiguous()
-    wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
+    x2 = _aligned(x.reshape(-1, K).contiguous(), 16)
+    wq, scales, biases = _pack3(wq, scales, biases)
     bias, lora_a, lora_b = _contig(bias), _contig(lora_a), _contig(lora_b)
     N = _check_pack("linear", wq, scales, biases, K, group_size, bits)
     M = x2.shape[0]
@@ -405,7 +431,7 @@ def lora_residual(x, y, lora_a, lora_b, lora_scale: float = 1.0, workspace=None)
     _float_dtype("lora_residual", "x", x)
     _float_dtype("lora_residual", "y", y)
     K = x.shape[-1]
-    x2 = x.reshape(-1, K).contiguous()
+    x2 = _aligned(x.reshape(-1, K).contiguous(), 16)
     M = x2.shape[0]
     N = y.shape[-1]
     if y.numel() != M * N:
@@ -440,7 +466,7 @@ def lokr_residual(x, y, delta, scale: float = 1.0, workspace=None):
     _float_dtype("lokr_residual", "y", y)
     _float_dtype("lokr_residual", "delta", delta)
     K = x.shape[-1]
-    x2 = x.reshape(-1, K).contiguous()
+    x2 = _aligned(x.reshape(-1, K).contiguous(), 16)
     M = x2.shape[0]
     N = y.shape[-1]
     if y.numel() != M * N:

@@ -554,6 +554,21 @@ static void gpu_cases(const fs::path& root) {
       e = rel_fro(mine, one);
       EXPECT(e < 2e-3, "expert %lld relFro %.3e", (long long)ex, e);
     }
+    // Odd N with one group per row (K = 64) and M = 3: every expert's y and scales slices are
+    // unaligned for the expert-by-expert launches, so the host runs them on aligned copies.
+    const int64_t No = 37, Ko = 64, Mo = 3;
+    std::vector<float> wo = bf16_normal(rng, E * No * Ko, 0.02f), bo = bf16_normal(rng, E * No, 0.5f);
+    Packed po = quantize(bf16_array(wo, {E * No, Ko}), 64, 4);
+    StackedExperts so{po.wq.reshape({E, No, Ko / 8}), po.scales.reshape({E, No, 1}),
+                      po.biases.reshape({E, No, 1}), bf16_array(bo, {E, No}), 64, 4};
+    std::vector<float> xo = bf16_normal(rng, Mo * Ko, 1.0f);
+    std::vector<float> yo = host_f32(so.forward(bf16_array(xo, {Mo, Ko})));
+    std::vector<QuantizedLinear> po_parts = so.split();
+    for (int64_t ex = 0; ex < E; ++ex) {
+      std::vector<float> one = host_f32(po_parts[ex].forward(bf16_array(xo, {Mo, Ko})));
+      std::vector<float> mine(yo.begin() + ex * Mo * No, yo.begin() + (ex + 1) * Mo * No);
+      EXPECT(mine == one, "unaligned expert %lld differs from its own layer", (long long)ex);
+    }
   }
 
   banner("TokenEmbedding quantize + forward, and the snapshot round trip");

@@ -125,6 +125,22 @@ def test_quantize_batched_validation(lib):
     assert lib.mlxq_quantize_batched(None, 0, 1, 8, 128, 64, 4, None, None, None, null) == _lib.MLXQ_OK
 
 
+def test_qmm_experts_unaligned_slices_rejected(lib):
+    """mlxq_qmm_experts run expert by expert (M <= 8) with expert slices the single-matrix path
+    cannot take: an odd M*N (y slices mid-word) or odd N*K/group_size (scales slices mid-word)
+    return MLXQ_EUNSUPPORTED before any device work; aligned slices pass these checks."""
+    from mlxq import _lib
+    p = ctypes.c_void_p(1 << 20)
+    null = ctypes.c_void_p(0)
+    bf = _lib.MLXQ_BFLOAT16
+    # E=2, M=3, K=64, N=37, Q4 g64: y slice 3*37 elements (odd), scales slice 37 elements (odd)
+    st = lib.mlxq_qmm_experts(p, bf, 0, 2, 3, 64, p, p, p, bf, None, bf, 37, 64, 4, p, null)
+    assert st == _lib.MLXQ_EUNSUPPORTED and b"aligned copies" in lib.mlxq_last_error()
+    # N=36: y slice 108 elements = 216 bytes (not 16-byte), scales 36 elements = 72 bytes (4-byte)
+    st = lib.mlxq_qmm_experts(p, bf, 0, 2, 3, 64, p, p, p, bf, None, bf, 36, 64, 4, p, null)
+    assert st == _lib.MLXQ_EUNSUPPORTED and b"16 bytes" in lib.mlxq_last_error()
+
+
 def test_linear_workspace_size(lib):
     from mlxq import _lib
     bf, f32 = _lib.MLXQ_BFLOAT16, _lib.MLXQ_FLOAT32

@@ -139,3 +139,32 @@ def test_random_swiglu_vs_oracle(mlxq, seed):
     ref_h = oracle.bf16_round(oracle.bf16_round(np.vectorize(oracle.silu)(gr).astype(np.float32)) * ur)
     assert_close(h, ref_h, f"seed {seed}")
     print(f"    bit-identical h: {np.mean(h == ref_h) * 100:.2f} %", flush=True)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_stacked_experts_vs_oracle(mlxq, seed):
+    """Stacked-expert projections (qmm_experts) at random expert counts and shapes, shared or
+    per-expert x, with or without a bf16 bias, each expert against the oracle's linear."""
+    rng = np.random.default_rng(11000 + seed)
+    E = int(rng.integers(1, 9))
+    M = int(rng.choice([int(rng.integers(1, 9)), int(rng.integers(9, 700))]))
+    gs = int(rng.choice([32, 64, 128]))
+    bits = int(rng.choice([4, 8]))
+    K = gs * int(rng.integers(2, max(3, 3072 // gs) + 1))
+    N = int(rng.integers(1, 2400))
+    per_expert = bool(rng.random() < 0.5)
+    with_bias = bool(rng.random() < 0.6)
+    banner("random experts", seed, E, M, N, K, gs, bits, per_expert, with_bias)
+    packs = [oracle.quantize(bf16_normal(rng, (N, K), 0.02), gs, bits, sb_bf16=True) for _ in range(E)]
+    wq, s, b = (np.stack([p[i] for p in packs]) for i in range(3))
+    bias = bf16_normal(rng, (E, N), 0.5) if with_bias else None
+    x = bf16_normal(rng, (E, M, K) if per_expert else (M, K))
+    y = to_np(mlxq.qmm_experts(to_gpu(x), wq_to_gpu(wq), to_gpu(s), to_gpu(b), gs, bits,
+                               bias=None if bias is None else to_gpu(bias), per_expert=per_expert))
+    assert y.shape == (E, M, N)
+    rows = _rows(rng, M)
+    for e, p in enumerate(packs):
+        xe = x[e] if per_expert else x
+        ref = oracle.linear(xe[rows], *p, gs, bits, w_bf16=M > 8, act_bf16=True,
+                            bias=None if bias is None else bias[e])
+        assert_close(y[e][rows], ref, f"seed {seed} expert {e}")
