@@ -168,3 +168,73 @@ def test_random_stacked_experts_vs_oracle(mlxq, seed):
         ref = oracle.linear(xe[rows], *p, gs, bits, w_bf16=M > 8, act_bf16=True,
                             bias=None if bias is None else bias[e])
         assert_close(y[e][rows], ref, f"seed {seed} expert {e}")
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_f32_fp16_linear_vs_oracle(mlxq, seed):
+    """linear with f32 or fp16 activations (FLUX.1's f32 stream, SDXL's fp16 stream) at random
+    shapes, bf16 scales, with a bias in either dtype, a bf16 LoRA adapter and an activation: the
+    f32 result against the oracle's f32 linear."""
+    rng = np.random.default_rng(13000 + seed)
+    lo, hi = M_BUCKETS[seed % len(M_BUCKETS)]
+    M = int(rng.integers(lo, min(hi, 1200) + 1))
+    gs = int(rng.choice([32, 64, 128]))
+    bits = int(rng.choice([4, 8]))
+    K = gs * int(rng.integers(2, max(3, 2048 // gs) + 1))
+    N = int(rng.integers(1, 2000))
+    fp16 = bool(rng.random() < 0.5)
+    bias_dt = str(rng.choice(["none", "bf16", "f32"]))
+    lora = bool(rng.random() < 0.4)
+    act = int(rng.choice([0, 1, 2, 3]))
+    banner("random f32/fp16 linear", seed, M, N, K, gs, bits, "fp16" if fp16 else "f32", bias_dt, lora, act)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x = x.astype(np.float16).astype(np.float32) if fp16 else x
+    rwq, rs, rb = oracle.quantize(bf16_normal(rng, (N, K), 0.02), gs, bits, sb_bf16=True)
+    kw, okw = {}, {}
+    if bias_dt != "none":
+        bv = (rng.standard_normal(N) * 0.5).astype(np.float32)
+        if bias_dt == "bf16":
+            bv = oracle.bf16_round(bv)
+        kw["bias"] = to_gpu(bv, torch.bfloat16 if bias_dt == "bf16" else torch.float32)
+        okw.update(bias=bv, bias_bf16=bias_dt == "bf16")
+    if lora:
+        A = bf16_normal(rng, (K, 16), 0.05)
+        B = bf16_normal(rng, (16, N), 0.05)
+        kw.update(lora_a=to_gpu(A), lora_b=to_gpu(B), lora_scale=0.75)
+        okw.update(lora_a=A, lora_b=B, lora_bf16=True, lora_scale=0.75)
+    y = mlxq.linear(to_gpu(x, torch.float16 if fp16 else torch.float32), wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb),
+                    gs, bits, activation=act, **kw)
+    assert y.dtype == torch.float32
+    rows = _rows(rng, M)
+    ref = oracle.linear(x[rows], rwq, rs, rb, gs, bits, w_bf16=False, x_bf16=False, sb_bf16=True, act=act, **okw)
+    rel, peak = errors(to_np(y)[rows], ref)
+    print(f"    seed {seed} relFro={rel:.3e} peak={peak:.3e}", flush=True)
+    assert rel < 1e-4 and peak < 1e-3
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_embedding_bit_exact(mlxq, seed):
+    """The quantized TokenEmbedding gather at random table shapes and id batches, bf16 or f32
+    scales, bf16 or f32 output: bit for bit the oracle's dequantized rows."""
+    rng = np.random.default_rng(15000 + seed)
+    gs = int(rng.choice([32, 64, 128]))
+    bits = int(rng.choice([4, 8]))
+    hidden = gs * int(rng.integers(1, max(2, 2048 // gs) + 1))
+    vocab = int(rng.integers(1, 5000))
+    sb_bf16 = bool(rng.random() < 0.6)
+    out_dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float32
+    shape = tuple(int(d) for d in rng.integers(1, 40, size=int(rng.integers(1, 3))))
+    banner("random embedding", seed, vocab, hidden, gs, bits, sb_bf16, out_dtype, shape)
+    w = (rng.standard_normal((vocab, hidden)) * 0.02).astype(np.float32)
+    if sb_bf16:
+        w = oracle.bf16_round(w)
+    wq, s, b = oracle.quantize(w, gs, bits, sb_bf16=sb_bf16)
+    ids = rng.integers(0, vocab, size=shape).astype(np.int32)
+    sdt = torch.bfloat16 if sb_bf16 else torch.float32
+    y = mlxq.embedding(torch.from_numpy(ids).cuda(), wq_to_gpu(wq), to_gpu(s, sdt), to_gpu(b, sdt), gs, bits,
+                       out_dtype)
+    assert y.shape == (*shape, hidden) and y.dtype == out_dtype
+    ref = oracle.dequantize(wq, s, b, gs, bits, out_bf16=sb_bf16)[ids]
+    if out_dtype == torch.bfloat16:
+        ref = oracle.bf16_round(ref)
+    assert np.array_equal(to_np(y), ref)
