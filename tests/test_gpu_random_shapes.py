@@ -238,3 +238,28 @@ def test_random_embedding_bit_exact(mlxq, seed):
     if out_dtype == torch.bfloat16:
         ref = oracle.bf16_round(ref)
     assert np.array_equal(to_np(y), ref)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_lora_residual_vs_reference(mlxq, seed):
+    """One more LoRA adapter on a computed bf16 y (Adapter::residual, src/adapters.rs:260-270) at
+    random M, K, N, rank (1-64) and scale: round(y + round(round(round(x.A).B) * scale)), each op
+    rounded to bf16, from fp64 products."""
+    rng = np.random.default_rng(17000 + seed)
+    M = int(rng.choice([int(rng.integers(1, 9)), int(rng.integers(9, 600)), int(rng.integers(4000, 6000))]))
+    K = 8 * int(rng.integers(1, 384))
+    N = int(rng.integers(1, 1500))
+    rank = int(rng.integers(1, 65))
+    scale = float(rng.choice([1.0, 0.5, 1.25, 2.0]))
+    banner("random lora residual", seed, M, K, N, rank, scale)
+    x = bf16_normal(rng, (M, K))
+    y = bf16_normal(rng, (M, N))
+    A = bf16_normal(rng, (K, rank), 0.05)
+    B = bf16_normal(rng, (rank, N), 0.05)
+    out = to_np(mlxq.ops.lora_residual(to_gpu(x), to_gpu(y), to_gpu(A), to_gpu(B), scale))
+    xa = oracle.bf16_round((x.astype(np.float64) @ A.astype(np.float64)).astype(np.float32))
+    r = oracle.bf16_round((xa.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+    if scale != 1.0:
+        r = oracle.bf16_round(r * np.float32(scale))
+    want = oracle.bf16_round(y + r)
+    assert_close(out, want, f"seed {seed}")
