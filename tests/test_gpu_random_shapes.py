@@ -263,3 +263,23 @@ def test_random_lora_residual_vs_reference(mlxq, seed):
         r = oracle.bf16_round(r * np.float32(scale))
     want = oracle.bf16_round(y + r)
     assert_close(out, want, f"seed {seed}")
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_quantize_batched_matches_per_weight(mlxq, seed):
+    """mlxq_quantize_batched over 1-20 weights of a random shape: bit for bit one quantize per
+    weight (launches of up to 16 weights)."""
+    rng = np.random.default_rng(19000 + seed)
+    gs = int(rng.choice([32, 64, 128]))
+    bits = int(rng.choice([4, 8]))
+    K = gs * int(rng.integers(1, max(2, 2048 // gs) + 1))
+    N = int(rng.integers(1, 1500))
+    count = int(rng.integers(1, 21))
+    dt = torch.bfloat16 if rng.random() < 0.6 else torch.float32
+    banner("random quantize batched", seed, count, N, K, gs, bits, dt)
+    ws = [to_gpu((rng.standard_normal((N, K)) * 0.02).astype(np.float32), dt) for _ in range(count)]
+    got = mlxq.quantize_batched(ws, gs, bits)
+    assert len(got) == count
+    for w, (wq, s, b) in zip(ws, got):
+        rq, rs, rb = mlxq.quantize(w, gs, bits)
+        assert torch.equal(wq, rq) and torch.equal(s, rs) and torch.equal(b, rb)
