@@ -283,3 +283,29 @@ def test_random_quantize_batched_matches_per_weight(mlxq, seed):
     for w, (wq, s, b) in zip(ws, got):
         rq, rs, rb = mlxq.quantize(w, gs, bits)
         assert torch.equal(wq, rq) and torch.equal(s, rs) and torch.equal(b, rb)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_forced_kernels_vs_oracle(mlxq, seed):
+    """The forced entry points at random shapes: mlxq_qmm (the bf16-tile GEMM at any M, small M
+    included) against the GEMM oracle, mlxq_qmv (the matrix-core GEMV) and mlxq_qmv_valu (the
+    VALU GEMV) at M <= 8 against the exact-f32 oracle."""
+    rng = np.random.default_rng(21000 + seed)
+    gs = int(rng.choice([32, 64, 128]))
+    bits = int(rng.choice([4, 8]))
+    K = gs * int(rng.integers(1, max(2, 3072 // gs) + 1))
+    N = int(rng.integers(1, 2500))
+    Mg = int(rng.integers(1, 600))
+    Mv = int(rng.integers(1, 9))
+    banner("random forced kernels", seed, Mg, Mv, N, K, gs, bits)
+    rwq, rs, rb = oracle.quantize(bf16_normal(rng, (N, K), 0.02), gs, bits, sb_bf16=True)
+    g = (wq_to_gpu(rwq), to_gpu(rs), to_gpu(rb))
+    x = bf16_normal(rng, (Mg, K))
+    rows = _rows(rng, Mg)
+    y = to_np(mlxq.qmm(to_gpu(x), *g, gs, bits))
+    assert_close(y[rows], oracle.quantized_matmul(x[rows], rwq, rs, rb, gs, bits, w_bf16=True, out_bf16=True),
+                 f"qmm seed {seed}")
+    xv = bf16_normal(rng, (Mv, K))
+    ref = oracle.quantized_matmul(xv, rwq, rs, rb, gs, bits, w_bf16=False, out_bf16=True)
+    assert_close(to_np(mlxq.qmv(to_gpu(xv), *g, gs, bits)), ref, f"qmv seed {seed}")
+    assert_close(to_np(mlxq.qmv_valu(to_gpu(xv), *g, gs, bits)), ref, f"qmv_valu seed {seed}")
