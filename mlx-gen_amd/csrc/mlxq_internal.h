@@ -101,6 +101,8 @@ int run_qmv_row_valu(const void* x, int64_t K, const uint32_t* wq, const void* s
 // point for measuring it against the matrix-core GEMV).
 int run_qmv_valu(const void* x, int x_dtype, int64_t M, int64_t K, const uint32_t* wq, const void* s,
                  const void* b, int sb_dtype, int64_t N, int gs, int bits, void* y, hipStream_t st);
+// Compute units of the current device (cached per device; 256 if the query fails).
+int64_t device_cu_count();
 // The f32 epilogue the f32 GEMM can fuse: y + bias (bias in its own dtype, the sum in f32), then
 // an activation evaluated in f32 (mlxq_activation; the sequence of linear_epilogue_kernel in f32).
 struct F32Epilogue {

@@ -791,8 +791,7 @@ const uint16_t* act_table_ptr(int fused_act, hipStream_t st) {
   return reinterpret_cast<const uint16_t*>(a) + (fused_act == kFusedActGeluExact ? 0 : 65536);
 }
 
-// Workgroups that run at once: one per CU (the kernel's LDS and registers allow no second).
-static int64_t resident_workgroups() {
+int64_t device_cu_count() {
   static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
@@ -804,6 +803,9 @@ static int64_t resident_workgroups() {
   }
   return cus;
 }
+
+// Workgroups that run at once: one per CU (the kernel's LDS and registers allow no second).
+static int64_t resident_workgroups() { return device_cu_count(); }
 
 // Tile height for a problem.  A launch takes ceil(tiles / CUs) rounds (one workgroup per CU).
 // Fewer rounds win.  At equal round counts, 224-row tiles win when there are several rounds

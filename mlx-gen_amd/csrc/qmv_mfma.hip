@@ -886,19 +886,8 @@ static int qmv_kind(const QmvArgs& a, int gs, int bits, const QmvPlan& p, hipStr
   return qmv_steps<4, 128, NMAT>(a, p, st);
 }
 
-// CUs of the current device (cached per device).
-static int64_t gemv_cus() {
-  static std::atomic<int> cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int cus = cached[dev].load(std::memory_order_relaxed);
-  if (cus <= 0) {
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-    cached[dev].store(cus, std::memory_order_relaxed);
-  }
-  return cus;
-}
+// CUs of the current device.
+static int64_t gemv_cus() { return device_cu_count(); }
 
 // Waves (rows) per one-row workgroup.  SwiGLU (two rows per wave): 8, i.e. the staging barrier
 // among fewer waves (K = 3072, F = 8192: 7.7 -> 7.1 us against 16 waves; 4 measured slower).
