@@ -122,3 +122,31 @@ def test_quantize_weight_past_4gib(mlxq):
     d = mlxq.dequantize(wq, s, b, 64, 4)
     torch.cuda.synchronize()
     assert np.array_equal(to_np(d[rows]), oracle.dequantize(rwq, rs, rb, 64, 4, out_bf16=True))
+
+
+def test_stacked_experts_pack_past_4gib(mlxq):
+    """A stacked Q4 g64 pack of 80 experts [14336, 8192] (codes 4.7 GB) in one qmm_experts launch
+    (grid.y = expert, each expert's operands addressed from its own base): the first expert and the
+    last one, whose codes start past 4 GiB, against the bf16-tile GEMM oracle on two rows."""
+    E, M, N, K = 80, 256, 14336, 8192
+    banner("large stacked experts", E, M, N, K)
+    gen = torch.Generator(device="cuda").manual_seed(15)
+    wq = torch.empty((E, N, K // 8), dtype=torch.int32, device="cuda")
+    s = torch.empty((E, N, K // 64), dtype=torch.bfloat16, device="cuda")
+    b = torch.empty_like(s)
+    for e in range(E):
+        pe = mlxq.quantize(_bf16_rows(gen, N, K, 0.02), 64, 4)
+        wq[e].copy_(pe[0])
+        s[e].copy_(pe[1])
+        b[e].copy_(pe[2])
+    assert wq.numel() * 4 > GIB4
+    x = _bf16_rows(gen, M, K, 1.0)
+    y = mlxq.qmm_experts(x, wq, s, b, 64, 4)
+    torch.cuda.synchronize()
+    assert y.shape == (E, M, N)
+    rows = [0, M - 1]
+    xr = x[rows].float().cpu().numpy()
+    for e in (0, E - 1):
+        ref = oracle.quantized_matmul(xr, to_np(wq[e]), to_np(s[e]), to_np(b[e]), 64, 4, w_bf16=True,
+                                      out_bf16=True)
+        assert_close(to_np(y[e, rows]), ref, f"stacked experts past 4 GiB, expert {e}")
